@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""bench.py — q4 decode GEMV HBM GB/s at Qwen3-4B shapes on one MI355X (+ the other BASELINE configs).
+
+Headline (``value``): the full Qwen3-4B q4 GEMV layer set at M=1 (K=2560 -> N in {4096, 1024, 1024,
+9728, 9728}; K=9728 -> N=2560) for all 36 layers — 216 matrices, 2.04 GB of distinct packed weights,
+8x the 256 MB Infinity Cache, so every step streams from HBM — executed as one grouped GEMV plan
+(one kernel launch per step). A step = one pass over the 216 matrices. ``value`` = algorithmic bytes
+(packed W + x + y) per step / step time.
+
+Also measured and reported under ``extra`` (same run, same process): the per-matrix single-launch
+GEMV at each Qwen3-4B shape, the q8 GEMV (cfg 1), the q3 LM head (cfg 3), the prefill q4 GEMM
+TFLOP/s (cfg 4) and the MoE expert-grouped q4 GEMM (cfg 5); every one rotates enough distinct weight
+copies to exceed the Infinity Cache.
+
+``cpu_baseline``: the reference's CPU matmul restated in JavaScript (oracle/cpuref.js: dequantize the
+tensor, f64-accumulated dot per output), run by node on this host on one Qwen3-4B layer set (M=1,
+the same six shapes), single-threaded.
+
+Timing: HIP events on the library's stream bracket exactly ``--steps`` steps after ``--warmup``
+untimed ones, with a device synchronization on both sides.
+"""
+import argparse
+import json
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
+QWEN3_4B = [("q", 2560, 4096), ("k", 2560, 1024), ("v", 2560, 1024),
+            ("gate", 2560, 9728), ("up", 2560, 9728), ("down", 9728, 2560)]
+LAYERS = 36
+
+
+def q_bytes(fmt, N, K):
+    from brimkern_amd import layout
+    return layout.byte_length(fmt, N * K)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Replicas:
+    """``count`` device copies (distinct addresses) of one packed tensor; returns plane addresses."""
+
+    def __init__(self, ctx, fmt, t, count):
+        from brimkern_amd import layout
+        self.fmt, self.N, self.K = fmt, t["N"], t["K"]
+        blob = layout.pack(fmt, t)
+        self.stride = (blob.size + 255) // 256 * 256
+        self.buf = ctx.alloc(self.stride * count)
+        ctx.h2d(self.buf, blob)
+        for i in range(1, count):
+            ctx._check(ctx.lib.brik_d2d(ctx.handle, ctx_p(self.buf.ptr + i * self.stride), ctx_p(self.buf.ptr),
+                                        blob.size))
+        self.offs = layout.plane_offsets(fmt, self.N * self.K)
+        self.count = count
+
+    def planes(self, i):
+        base = self.buf.ptr + i * self.stride
+        names = {"q8": ("codes", "sc"), "q4": ("nib", "sc", "mn"), "q3": ("lo", "hi", "sc", "mn")}[self.fmt]
+        return [base + self.offs[k][0] for k in names]
+
+
+def ctx_p(v):
+    import ctypes
+    return ctypes.c_void_p(v)
+
+
+def time_loop(ctx, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    ctx.sync()
+    ctx.timer_begin()
+    for i in range(steps):
+        fn(i)
+    ms = ctx.timer_end()
+    ctx.sync()
+    return ms / steps
+
+
+def gemv_layer_set(ctx, steps, warmup, layers):
+    from brimkern_amd import synth
+    reps, jobs, nbytes = {}, [], 0
+    xa = ctx.upload(synth.normal(101, 2560))
+    xd = ctx.upload(synth.normal(102, 9728))
+    ybuf = ctx.alloc(4 * layers * sum(n for _, _, n in QWEN3_4B))
+    yo = 0
+    for si, (name, K, N) in enumerate(QWEN3_4B):
+        reps[name] = Replicas(ctx, "q4", synth.q4_tensor(200 + si, N, K), layers)
+    for l in range(layers):
+        for name, K, N in QWEN3_4B:
+            nib, sc, mn = reps[name].planes(l)
+            jobs.append({"x": xd if K == 9728 else xa, "p0": nib, "sc": sc, "mn": mn,
+                         "y": ybuf.ptr + 4 * yo, "K": K, "N": N})
+            yo += N
+            nbytes += q_bytes("q4", N, K) + 4 * K + 4 * N
+    plan = ctx.gemv_plan("q4", jobs)
+    ms = time_loop(ctx, lambda i: plan.run(), steps, warmup)
+    # per-shape single launches, rotating over the layers' copies
+    single = {}
+    for name, K, N in QWEN3_4B:
+        r = reps[name]
+        yb = ctx.alloc(4 * N)
+        x = xd if K == 9728 else xa
+
+        def one(i, r=r, x=x, yb=yb, K=K, N=N):
+            nib, sc, mn = r.planes(i % layers)
+            ctx.matmul_t_q4(x, nib, sc, mn, yb, 1, K, N)
+        lms = time_loop(ctx, one, 4 * layers, layers)
+        b = q_bytes("q4", N, K) + 4 * K + 4 * N
+        single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1)}
+        ctx.free(yb)
+    plan.destroy()
+    for r in reps.values():
+        ctx.free(r.buf)
+    ctx.free(ybuf)
+    return ms, nbytes, single
+
+
+def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
+    from brimkern_amd import synth
+    t = synth.tensor(fmt, seed, N, K)
+    tb = q_bytes(fmt, N, K)
+    copies = max(2, -(-cache_bytes // tb))
+    r = Replicas(ctx, fmt, t, copies)
+    x = ctx.upload(synth.normal(seed + 1, K))
+    y = ctx.alloc(4 * N)
+    fn = {"q8": ctx.matmul_t_q8, "q4": ctx.matmul_t_q4, "q3": ctx.matmul_t_q3}[fmt]
+    ms = time_loop(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies), copies)
+    b = tb + 4 * K + 4 * N
+    for bb in (r.buf, x, y):
+        ctx.free(bb)
+    return {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+
+
+def gemm_cfg4(ctx, steps, warmup):
+    from brimkern_amd import synth
+    M, K, N = 512, 2560, 9728
+    copies = 36
+    r = Replicas(ctx, "q4", synth.q4_tensor(300, N, K), copies)
+    x = ctx.upload(synth.normal(301, M * K))
+    y = ctx.alloc(4 * M * N)
+    ms = time_loop(ctx, lambda i: ctx.matmul_t_q4(x, *r.planes(i % copies), y, M, K, N), max(steps, copies), 4)
+    flops = 2.0 * M * N * K
+    for bb in (r.buf, x, y):
+        ctx.free(bb)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
+def moe_cfg5(ctx, steps, warmup):
+    from brimkern_amd import synth
+    T, H, E, F, TOPK = 256, 2048, 64, 768, 8
+    rows, row_off = synth.moe_routing(77, T, E, TOPK)
+    R = rows.size
+    copies = 3
+    reps = {w: Replicas(ctx, "q4", synth.q4_tensor(400 + i, E * (F if w != "down" else H), F if w == "down" else H),
+                        copies) for i, w in enumerate(("gate", "up", "down"))}
+    xg = ctx.upload(np.ascontiguousarray(synth.normal(401, T * H).reshape(T, H)[rows]))
+    xd = ctx.upload(synth.normal(402, R * F))
+    ro = ctx.upload(row_off)
+    yg = ctx.alloc(4 * R * F)
+    yu = ctx.alloc(4 * R * F)
+    yd = ctx.alloc(4 * R * H)
+
+    def step(i):
+        c = i % copies
+        ctx.moe_matmul_t_q4(xg, ro, *reps["gate"].planes(c), yg, E, R, H, F)
+        ctx.moe_matmul_t_q4(xg, ro, *reps["up"].planes(c), yu, E, R, H, F)
+        ctx.moe_matmul_t_q4(xd, ro, *reps["down"].planes(c), yd, E, R, F, H)
+    ms = time_loop(ctx, step, max(steps, 6), 3)
+    wbytes = 2 * q_bytes("q4", E * F, H) + q_bytes("q4", E * H, F)
+    flops = 2.0 * R * (2 * H * F + F * H)
+    for bb in list(r.buf for r in reps.values()) + [xg, xd, ro, yg, yu, yd]:
+        ctx.free(bb)
+    return {"us": round(ms * 1e3, 2), "weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2), "rows": int(R),
+            "max_rows_per_expert": int(np.diff(row_off).max()), "min_rows_per_expert": int(np.diff(row_off).min())}
+
+
+def cpu_baseline():
+    """JS restatement of the reference CPU matmul on one Qwen3-4B q4 layer set (M=1), 1 thread."""
+    node = shutil.which("node")
+    if node is None:
+        return None
+    from brimkern_amd import synth, layout
+    total_ms, nbytes = 0.0, 0
+    with tempfile.TemporaryDirectory() as d:
+        for si, (name, K, N) in enumerate(QWEN3_4B):
+            t = synth.q4_tensor(200 + si, N, K)
+            x = synth.normal(500 + si, K)
+            inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
+            with open(inp, "wb") as f:
+                f.write(x.tobytes())
+                f.write(layout.pack("q4", t).tobytes())
+            res = json.loads(subprocess.check_output([node, os.path.join(ROOT, "oracle", "cpuref.js"), "q4", "1",
+                                                      str(K), str(N), inp, out, "2"]))
+            total_ms += res["ms"]
+            nbytes += q_bytes("q4", N, K) + 4 * K + 4 * N
+    import platform
+    return {"value": round(nbytes / (total_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"one Qwen3-4B q4 layer set (6 matrices, M=1, {nbytes / 1e6:.1f} MB), node "
+                      f"{subprocess.check_output([node, '--version']).decode().strip()}, best of 2 per matrix, "
+                      f"{total_ms / 1e3:.2f} s, cpu {platform.processor() or platform.machine()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this path has no multi-GPU form in this build "
+              "(sharding along N is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from brimkern_amd import Context
+    ctx = Context(0)
+    log("bench: q4 GEMV layer set")
+    ms, nbytes, single = gemv_layer_set(ctx, args.steps, args.warmup, args.layers)
+    value = nbytes / (ms * 1e-3) / 1e9
+    extra = {"per_matrix_single_launch": single}
+    if not args.no_extra:
+        log("bench: cfg1 q8 GEMV")
+        extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)
+        log("bench: cfg3 q3 LM head")
+        extra["cfg3_q3_gemv_K2560_N151936"] = gemv_single_cfg(ctx, "q3", 2560, 151936, 700, args.steps, args.warmup)
+        log("bench: cfg4 q4 GEMM")
+        extra["cfg4_q4_gemm_M512_K2560_N9728"] = gemm_cfg4(ctx, args.steps, args.warmup)
+        log("bench: cfg5 MoE")
+        extra["cfg5_moe_q4_gate_up_down"] = moe_cfg5(ctx, args.steps, args.warmup)
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": "q4 GEMV HBM GB/s (% of peak) at Qwen3-4B shapes; prefill q4 GEMM TFLOP/s",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "q4 weights, f32 activations and accumulation", "data": "synthetic (seeded SplitMix64)",
+        "config": {"workload": f"matmul_t_q4 decode GEMV, Qwen3-4B layer set x {args.layers} layers "
+                               f"(216 matrices, M=1), grouped plan, one launch per step",
+                   "bytes_per_step": nbytes, "layers": args.layers},
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "brik_gemv_grouped_q4_t16"},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

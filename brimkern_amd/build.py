@@ -1,0 +1,80 @@
+"""Build recipe for the native parts of brimkern_amd (no cmake / node-gyp needed).
+
+1. ``csrc/kernels/brik_kernels.hip`` -> ``_build/brik_gfx950.hsaco``  (hipcc --genco, gfx950 only)
+2. ``csrc/brik_runtime.cpp`` + ``csrc/brik_embed.S`` (embeds the code object) -> ``libbrik.so``
+   (the C ABI declared in ``include/brik.h``)
+3. ``csrc/brik_napi.cc`` -> ``js/brik.node`` (Node N-API addon over libbrik.so, rpath $ORIGIN/..)
+
+Run ``python -m brimkern_amd.build`` or call :func:`build`.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+NODE_INC = "/usr/include/node"
+
+HSACO = os.path.join(BUILD, "brik_gfx950.hsaco")
+LIB = os.path.join(PKG, "libbrik.so")
+ADDON = os.path.join(PKG, "js", "brik.node")
+
+# Device flags. packed-fp32-ops is switched off: the compiler would otherwise fuse pairs of f32
+# operations into v_pk_* forms.
+HIP_DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-ffp-contract=fast",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print("+", " ".join(cmd), flush=True)
+    subprocess.check_call(cmd)
+
+
+def build_hsaco(verbose=False):
+    os.makedirs(BUILD, exist_ok=True)
+    src = os.path.join(CSRC, "kernels", "brik_kernels.hip")
+    tmp = HSACO + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", "--no-gpu-bundle-output", *HIP_DEVICE_FLAGS,
+          "-o", tmp, src], verbose)
+    os.replace(tmp, HSACO)
+    return HSACO
+
+
+def build_lib(verbose=False):
+    tmp = LIB + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
+          f'-DBRIK_HSACO_PATH="{HSACO}"',
+          os.path.join(CSRC, "brik_runtime.cpp"), os.path.join(CSRC, "brik_embed.S"),
+          "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+          "-Wl,--no-undefined", "-o", tmp], verbose)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_addon(verbose=False):
+    src = os.path.join(CSRC, "brik_napi.cc")
+    if not os.path.exists(src) or not os.path.exists(os.path.join(NODE_INC, "node_api.h")):
+        return None
+    tmp = ADDON + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
+          "-I", NODE_INC, "-I", os.path.join(ROOT, "include"), src,
+          "-L", PKG, "-lbrik", "-Wl,-rpath,$ORIGIN/..", "-o", tmp], verbose)
+    os.replace(tmp, ADDON)
+    return ADDON
+
+
+def build(verbose=False):
+    build_hsaco(verbose)
+    build_lib(verbose)
+    build_addon(verbose)
+
+
+if __name__ == "__main__":
+    build(verbose="-q" not in sys.argv)

@@ -1,0 +1,249 @@
+"""ctypes binding of ``libbrik.so`` (the C ABI in ``include/brik.h``).
+
+This is the Python-side host of the drop-in boundary (tests, bench, smoke); the JavaScript host is
+``brimkern_amd/js`` over the N-API addon. Both call the same C entry points. Nothing here falls
+back to CPU: if the library is missing or no gfx950 device is present, construction raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "libbrik.so")
+
+BRIK_OK, BRIK_EINVAL, BRIK_EALIGN, BRIK_EHIP, BRIK_ENOMEM, BRIK_ENODEV, BRIK_EMODULE = 0, -1, -2, -3, -4, -5, -6
+BRIK_OPT_PATH, BRIK_OPT_GEMV_TEAM = 1, 2
+PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+
+# every exported symbol of include/brik.h with (restype, argtypes)
+_P, _I, _Z, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(ctypes.c_float)
+SIGNATURES = {
+    "brik_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "brik_destroy": (None, [_P]),
+    "brik_last_error": (ctypes.c_char_p, [_P]),
+    "brik_strerror": (ctypes.c_char_p, [_I]),
+    "brik_device_count": (_I, [ctypes.POINTER(_I)]),
+    "brik_alloc": (_I, [_P, _Z, ctypes.POINTER(_P)]),
+    "brik_free": (_I, [_P, _P]),
+    "brik_h2d": (_I, [_P, _P, _P, _Z]),
+    "brik_d2h": (_I, [_P, _P, _P, _Z]),
+    "brik_d2d": (_I, [_P, _P, _P, _Z]),
+    "brik_sync": (_I, [_P]),
+    "brik_matmul_t_q8": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "brik_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    "brik_matmul_t_q3": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    "brik_moe_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    "brik_dequant_q8_f32": (_I, [_P, _P, _P, _P, _Z]),
+    "brik_dequant_q4_f32": (_I, [_P, _P, _P, _P, _P, _Z]),
+    "brik_dequant_q3_f32": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
+    "brik_timer_begin": (_I, [_P]),
+    "brik_timer_end": (_I, [_P, _F]),
+    "brik_set_option": (_I, [_P, _I, _I]),
+    "brik_gemv_plan_create": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
+    "brik_gemv_plan_run": (_I, [_P, _P]),
+    "brik_gemv_plan_destroy": (None, [_P, _P]),
+}
+
+FMT_CODES = {"q8": 8, "q4": 4, "q3": 3}
+
+
+class GemvJob(ctypes.Structure):
+    """``brik_gemv_job`` of include/brik.h."""
+    _fields_ = [("x", _P), ("p0", _P), ("p1", _P), ("scales", _P), ("mins", _P), ("y", _P),
+                ("K", ctypes.c_int32), ("N", ctypes.c_int32)]
+
+
+class BrikError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"brik error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libbrik.so and declare every entry point. Raises if it was never built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing: run `python -m brimkern_amd.build` (no CPU fallback exists)")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    load_library().brik_device_count(ctypes.byref(n))
+    return n.value
+
+
+class DeviceBuffer:
+    """A device allocation owned by a :class:`Context`."""
+
+    __slots__ = ("ctx", "ptr", "nbytes")
+
+    def __init__(self, ctx: "Context", ptr: int, nbytes: int):
+        self.ctx, self.ptr, self.nbytes = ctx, ptr, nbytes
+
+    def offset(self, nbytes: int) -> int:
+        """Raw device address ``nbytes`` into the buffer (for plane views into a packed blob)."""
+        assert 0 <= nbytes <= self.nbytes
+        return self.ptr + nbytes
+
+    def free(self):
+        if self.ptr:
+            self.ctx._check(self.ctx.lib.brik_free(self.ctx.handle, _P(self.ptr)))
+            self.ptr = 0
+
+    def __int__(self):
+        return self.ptr
+
+
+def _addr(p) -> _P:
+    if p is None:
+        return _P(None)
+    if isinstance(p, DeviceBuffer):
+        return _P(p.ptr)
+    return _P(int(p))
+
+
+class Context:
+    """One device + one stream (``brik_ctx``)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = _P()
+        rc = self.lib.brik_create(device, ctypes.byref(h))
+        if rc != BRIK_OK:
+            raise BrikError(rc, f"brik_create({device}): {self.lib.brik_strerror(rc).decode()}")
+        self.handle = h
+        self._buffers = []
+
+    def _check(self, rc: int):
+        if rc != BRIK_OK:
+            raise BrikError(rc, self.lib.brik_last_error(self.handle).decode())
+        return rc
+
+    def close(self):
+        if getattr(self, "handle", None):
+            for b in self._buffers:
+                b.free()
+            self._buffers.clear()
+            self.lib.brik_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- memory -----------------------------------------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        p = _P()
+        self._check(self.lib.brik_alloc(self.handle, max(int(nbytes), 1), ctypes.byref(p)))
+        b = DeviceBuffer(self, p.value, int(nbytes))
+        self._buffers.append(b)
+        return b
+
+    def free(self, buf: DeviceBuffer):
+        buf.free()
+        if buf in self._buffers:
+            self._buffers.remove(buf)
+
+    def upload(self, arr: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(arr)
+        b = self.alloc(a.nbytes)
+        self.h2d(b, a)
+        return b
+
+    def h2d(self, dst, arr: np.ndarray, dst_offset: int = 0):
+        a = np.ascontiguousarray(arr)
+        self._check(self.lib.brik_h2d(self.handle, _P(int(_addr(dst).value or 0) + dst_offset),
+                                      _P(a.ctypes.data), a.nbytes))
+
+    def download(self, src, dtype, count: int, src_offset: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        self._check(self.lib.brik_d2h(self.handle, _P(out.ctypes.data),
+                                      _P(int(_addr(src).value or 0) + src_offset), out.nbytes))
+        return out
+
+    def sync(self):
+        self._check(self.lib.brik_sync(self.handle))
+
+    def set_option(self, key: int, value: int):
+        self._check(self.lib.brik_set_option(self.handle, key, value))
+
+    def timer_begin(self):
+        self._check(self.lib.brik_timer_begin(self.handle))
+
+    def timer_end(self) -> float:
+        ms = ctypes.c_float(0)
+        self._check(self.lib.brik_timer_end(self.handle, ctypes.byref(ms)))
+        return ms.value
+
+    # ---- compute (device pointers, enqueue only) -------------------------------------------
+    def matmul_t_q8(self, x, codes, sc, y, M, K, N):
+        self._check(self.lib.brik_matmul_t_q8(self.handle, _addr(x), _addr(codes), _addr(sc), _addr(y), M, K, N))
+
+    def matmul_t_q4(self, x, nib, sc, mn, y, M, K, N):
+        self._check(self.lib.brik_matmul_t_q4(self.handle, _addr(x), _addr(nib), _addr(sc), _addr(mn),
+                                              _addr(y), M, K, N))
+
+    def matmul_t_q3(self, x, lo, hi, sc, mn, y, M, K, N):
+        self._check(self.lib.brik_matmul_t_q3(self.handle, _addr(x), _addr(lo), _addr(hi), _addr(sc),
+                                              _addr(mn), _addr(y), M, K, N))
+
+    def moe_matmul_t_q4(self, x, row_off, nib, sc, mn, y, E, R, K, N):
+        self._check(self.lib.brik_moe_matmul_t_q4(self.handle, _addr(x), _addr(row_off), _addr(nib),
+                                                  _addr(sc), _addr(mn), _addr(y), E, R, K, N))
+
+    def gemv_plan(self, fmt: str, jobs) -> "GemvPlan":
+        """jobs: iterable of dicts with x, p0, p1, sc, mn, y (device addresses), K, N."""
+        jobs = list(jobs)
+        arr = (GemvJob * len(jobs))()
+        for i, j in enumerate(jobs):
+            arr[i] = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]),
+                             _addr(j.get("mn")), _addr(j["y"]), j["K"], j["N"])
+        h = _P()
+        self._check(self.lib.brik_gemv_plan_create(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
+                                                   ctypes.byref(h)))
+        return GemvPlan(self, h)
+
+    def dequant_q8(self, codes, sc, out, n):
+        self._check(self.lib.brik_dequant_q8_f32(self.handle, _addr(codes), _addr(sc), _addr(out), n))
+
+    def dequant_q4(self, nib, sc, mn, out, n):
+        self._check(self.lib.brik_dequant_q4_f32(self.handle, _addr(nib), _addr(sc), _addr(mn), _addr(out), n))
+
+    def dequant_q3(self, lo, hi, sc, mn, out, n):
+        self._check(self.lib.brik_dequant_q3_f32(self.handle, _addr(lo), _addr(hi), _addr(sc), _addr(mn),
+                                                 _addr(out), n))
+
+
+class GemvPlan:
+    def __init__(self, ctx: Context, handle):
+        self.ctx, self.handle = ctx, handle
+
+    def run(self):
+        self.ctx._check(self.ctx.lib.brik_gemv_plan_run(self.ctx.handle, self.handle))
+
+    def destroy(self):
+        if self.handle:
+            self.ctx.lib.brik_gemv_plan_destroy(self.ctx.handle, self.handle)
+            self.handle = None

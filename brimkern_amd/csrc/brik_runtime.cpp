@@ -1,0 +1,460 @@
+// libbrik.so — C-ABI runtime over the gfx950 code object of the quantized matmul kernels.
+//
+// The code object (brik_gfx950.hsaco, built with `hipcc --genco --offload-arch=gfx950`) is
+// embedded in this library by brik_embed.S and loaded with hipModuleLoadData; kernels are launched
+// with hipModuleLaunchKernel on the context's own stream. Host API surface: device selection,
+// hipMalloc/hipFree, hipMemcpy(Async), module load + launch, events for timing.
+#include "../../include/brik.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+extern "C" const unsigned char brik_hsaco_begin[];
+extern "C" const unsigned char brik_hsaco_end[];
+
+namespace {
+
+enum Kern {
+    K_DEQ_Q8, K_DEQ_Q4, K_DEQ_Q3,
+    K_GEMV_Q4_16, K_GEMV_Q4_32, K_GEMV_Q4_64,
+    K_GEMV_Q8_16, K_GEMV_Q8_32, K_GEMV_Q8_64,
+    K_GEMV_Q3_16, K_GEMV_Q3_32, K_GEMV_Q3_64,
+    K_GEMM_Q4, K_GEMM_Q8, K_GEMM_Q3,
+    K_GRP_Q4_16, K_GRP_Q4_32, K_GRP_Q4_64,
+    K_GRP_Q8_16, K_GRP_Q8_32, K_GRP_Q8_64,
+    K_GRP_Q3_16, K_GRP_Q3_32, K_GRP_Q3_64,
+    K_COUNT
+};
+
+const char* const kKernelNames[K_COUNT] = {
+    "brik_dequant_q8", "brik_dequant_q4", "brik_dequant_q3",
+    "brik_gemv_q4_t16", "brik_gemv_q4_t32", "brik_gemv_q4_t64",
+    "brik_gemv_q8_t16", "brik_gemv_q8_t32", "brik_gemv_q8_t64",
+    "brik_gemv_q3_t16", "brik_gemv_q3_t32", "brik_gemv_q3_t64",
+    "brik_gemm_q4", "brik_gemm_q8", "brik_gemm_q3",
+    "brik_gemv_grouped_q4_t16", "brik_gemv_grouped_q4_t32", "brik_gemv_grouped_q4_t64",
+    "brik_gemv_grouped_q8_t16", "brik_gemv_grouped_q8_t32", "brik_gemv_grouped_q8_t64",
+    "brik_gemv_grouped_q3_t16", "brik_gemv_grouped_q3_t32", "brik_gemv_grouped_q3_t64",
+};
+
+constexpr int kGroup = 32;
+constexpr int kGemmTile = 64;                  // BM = BN of brik_gemm_*
+constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
+
+enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
+
+}  // namespace
+
+struct brik_gemv_plan {
+    Kern kernel;
+    void* dev = nullptr;          // [jobs | block_start]
+    int njobs = 0;
+    int rows_per_block = 0;
+    unsigned blocks = 0;
+    size_t lds = 0;
+};
+
+struct brik_ctx {
+    int device = -1;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[K_COUNT] = {};
+    hipStream_t stream = nullptr;
+    hipEvent_t ev_begin = nullptr, ev_end = nullptr;
+    int opt_path = 0;
+    int opt_team = 0;
+    char err[512] = {0};
+};
+
+namespace {
+
+int fail(brik_ctx* c, int code, const char* fmt, ...)
+{
+    if (c) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(c->err, sizeof c->err, fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+#define HIP_TRY(ctx, call)                                                                    \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess)                                                                 \
+            return fail((ctx), e_ == hipErrorOutOfMemory ? BRIK_ENOMEM : BRIK_EHIP, "%s: %s", \
+                        #call, hipGetErrorString(e_));                                        \
+    } while (0)
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int launch(brik_ctx* c, Kern k, unsigned gx, unsigned gy, unsigned bx, size_t lds, void** args)
+{
+    if (gx == 0 || gy == 0) return BRIK_OK;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipModuleLaunchKernel(c->fn[k], gx, gy, 1, bx, 1, 1, (unsigned)lds, c->stream, args, nullptr));
+    return BRIK_OK;
+}
+
+// Shape + pointer validation shared by the three matmuls.
+int check_mm(brik_ctx* c, const char* who, const float* x, const void* p0, const void* p1,
+             const void* sc, const void* mn, const float* y, int M, int K, int N, Fmt f)
+{
+    if (!c) return BRIK_EINVAL;
+    if (M < 0 || K < 0 || N < 0) return fail(c, BRIK_EINVAL, "%s: negative shape M=%d K=%d N=%d", who, M, K, N);
+    if (K % kGroup) return fail(c, BRIK_EINVAL, "%s: K=%d is not a multiple of 32", who, K);
+    if (M == 0 || N == 0) return BRIK_OK;
+    if (!y) return fail(c, BRIK_EINVAL, "%s: y is null", who);
+    if (!aligned(y, 4)) return fail(c, BRIK_EALIGN, "%s: y must be 4-byte aligned", who);
+    if (K == 0) return BRIK_OK;
+    if (!x || !p0 || !sc || (f != F_Q8 && !mn) || (f == F_Q3 && !p1))
+        return fail(c, BRIK_EINVAL, "%s: null operand pointer", who);
+    if (!aligned(x, 16)) return fail(c, BRIK_EALIGN, "%s: x must be 16-byte aligned", who);
+    if (!aligned(p0, 16)) return fail(c, BRIK_EALIGN, "%s: code plane must be 16-byte aligned", who);
+    if (f == F_Q3 && !aligned(p1, 8)) return fail(c, BRIK_EALIGN, "%s: q3 hi plane must be 8-byte aligned", who);
+    if (!aligned(sc, 2) || (mn && !aligned(mn, 2)))
+        return fail(c, BRIK_EALIGN, "%s: scales/mins must be 2-byte aligned", who);
+    if ((long long)N * K / kGroup > 0x7fffffffLL * 8)
+        return fail(c, BRIK_EINVAL, "%s: tensor too large", who);
+    return BRIK_OK;
+}
+
+int gemv_team(brik_ctx* c, int K)
+{
+    if (c->opt_team == 16 || c->opt_team == 32 || c->opt_team == 64) return c->opt_team;
+    const int G = K / kGroup;
+    if (G >= 256) return 64;
+    if (G >= 96) return 32;
+    return 16;
+}
+
+Kern gemv_kernel(Fmt f, int team)
+{
+    const int t = team == 16 ? 0 : team == 32 ? 1 : 2;
+    switch (f) {
+    case F_Q4: return Kern(K_GEMV_Q4_16 + t);
+    case F_Q8: return Kern(K_GEMV_Q8_16 + t);
+    default:   return Kern(K_GEMV_Q3_16 + t);
+    }
+}
+
+int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
+           const void* mn, float* y, int M, int K, int N)
+{
+    const size_t lds = ((size_t)K + K / kGroup) * sizeof(float);
+    const bool gemv_fits = lds <= kGemvMaxLds;
+    bool use_gemv = (M == 1 && gemv_fits);
+    if (c->opt_path == 1) {
+        if (!gemv_fits) return fail(c, BRIK_EINVAL, "forced GEMV: K=%d exceeds the LDS staging limit", K);
+        use_gemv = true;
+    } else if (c->opt_path == 2) {
+        use_gemv = false;
+    }
+    int Mi = M, Ki = K, Ni = N;
+    if (use_gemv) {
+        const int team = gemv_team(c, K);
+        const int rpb = 256 / team;
+        unsigned gx = (unsigned)((N + rpb - 1) / rpb);
+        if (gx > 65535u * 4) gx = 65535u * 4;
+        void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni};
+        return launch(c, gemv_kernel(f, team), gx, (unsigned)M, 256, lds, args);
+    }
+    const int* row_off = nullptr;
+    int E = 0;
+    const Kern k = f == F_Q4 ? K_GEMM_Q4 : f == F_Q8 ? K_GEMM_Q8 : K_GEMM_Q3;
+    void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &E};
+    return launch(c, k, (unsigned)((N + kGemmTile - 1) / kGemmTile), (unsigned)((M + kGemmTile - 1) / kGemmTile),
+                  256, 0, args);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* brik_strerror(int code)
+{
+    switch (code) {
+    case BRIK_OK: return "ok";
+    case BRIK_EINVAL: return "invalid argument";
+    case BRIK_EALIGN: return "misaligned pointer";
+    case BRIK_EHIP: return "HIP runtime error";
+    case BRIK_ENOMEM: return "out of device memory";
+    case BRIK_ENODEV: return "no such device";
+    case BRIK_EMODULE: return "code object load failed";
+    default: return "unknown error";
+    }
+}
+
+const char* brik_last_error(const brik_ctx* c) { return c ? c->err : "null context"; }
+
+int brik_device_count(int* count)
+{
+    if (!count) return BRIK_EINVAL;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return BRIK_OK;
+}
+
+int brik_create(int device, brik_ctx** out)
+{
+    if (!out) return BRIK_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return BRIK_ENODEV;
+    brik_ctx* c = new (std::nothrow) brik_ctx();
+    if (!c) return BRIK_ENOMEM;
+    c->device = device;
+    auto bail = [&](int code) { brik_destroy(c); return code; };
+    if (hipSetDevice(device) != hipSuccess) return bail(BRIK_ENODEV);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return bail(BRIK_ENODEV);
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return bail(BRIK_ENODEV);
+    if (hipModuleLoadData(&c->module, brik_hsaco_begin) != hipSuccess) return bail(BRIK_EMODULE);
+    for (int k = 0; k < K_COUNT; ++k)
+        if (hipModuleGetFunction(&c->fn[k], c->module, kKernelNames[k]) != hipSuccess) return bail(BRIK_EMODULE);
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);
+    if (hipEventCreate(&c->ev_begin) != hipSuccess || hipEventCreate(&c->ev_end) != hipSuccess)
+        return bail(BRIK_EHIP);
+    *out = c;
+    return BRIK_OK;
+}
+
+void brik_destroy(brik_ctx* c)
+{
+    if (!c) return;
+    // best-effort teardown: errors here have no caller to report to
+    if (c->device >= 0) (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
+    if (c->ev_end) (void)hipEventDestroy(c->ev_end);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->module) (void)hipModuleUnload(c->module);
+    delete c;
+}
+
+int brik_alloc(brik_ctx* c, size_t bytes, void** dptr)
+{
+    if (!c || !dptr) return BRIK_EINVAL;
+    *dptr = nullptr;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMalloc(dptr, bytes ? bytes : 1));
+    return BRIK_OK;
+}
+
+int brik_free(brik_ctx* c, void* dptr)
+{
+    if (!c) return BRIK_EINVAL;
+    if (!dptr) return BRIK_OK;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    HIP_TRY(c, hipFree(dptr));
+    return BRIK_OK;
+}
+
+static int copy(brik_ctx* c, void* dst, const void* src, size_t n, hipMemcpyKind kind)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n == 0) return BRIK_OK;
+    if (!dst || !src) return fail(c, BRIK_EINVAL, "copy: null pointer");
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMemcpyAsync(dst, src, n, kind, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return BRIK_OK;
+}
+
+int brik_h2d(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyHostToDevice); }
+int brik_d2h(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyDeviceToHost); }
+int brik_d2d(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyDeviceToDevice); }
+
+int brik_sync(brik_ctx* c)
+{
+    if (!c) return BRIK_EINVAL;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return BRIK_OK;
+}
+
+int brik_matmul_t_q8(brik_ctx* c, const float* x, const int8_t* codes, const uint16_t* sc, float* y,
+                     int M, int K, int N)
+{
+    int r = check_mm(c, "matmul_t_q8", x, codes, nullptr, sc, nullptr, y, M, K, N, F_Q8);
+    if (r != BRIK_OK || M == 0 || N == 0) return r;
+    return matmul(c, F_Q8, x, codes, nullptr, sc, nullptr, y, M, K, N);
+}
+
+int brik_matmul_t_q4(brik_ctx* c, const float* x, const uint8_t* nib, const uint16_t* sc,
+                     const uint16_t* mn, float* y, int M, int K, int N)
+{
+    int r = check_mm(c, "matmul_t_q4", x, nib, nullptr, sc, mn, y, M, K, N, F_Q4);
+    if (r != BRIK_OK || M == 0 || N == 0) return r;
+    return matmul(c, F_Q4, x, nib, nullptr, sc, mn, y, M, K, N);
+}
+
+int brik_matmul_t_q3(brik_ctx* c, const float* x, const uint32_t* lo, const uint32_t* hi,
+                     const uint16_t* sc, const uint16_t* mn, float* y, int M, int K, int N)
+{
+    int r = check_mm(c, "matmul_t_q3", x, lo, hi, sc, mn, y, M, K, N, F_Q3);
+    if (r != BRIK_OK || M == 0 || N == 0) return r;
+    return matmul(c, F_Q3, x, lo, hi, sc, mn, y, M, K, N);
+}
+
+int brik_moe_matmul_t_q4(brik_ctx* c, const float* x, const int32_t* row_off, const uint8_t* nib,
+                         const uint16_t* sc, const uint16_t* mn, float* y, int E, int R, int K, int N)
+{
+    if (!c) return BRIK_EINVAL;
+    if (E < 0 || R < 0) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: negative E=%d or R=%d", E, R);
+    int r = check_mm(c, "moe_matmul_t_q4", x, nib, nullptr, sc, mn, y, R, K, N, F_Q4);
+    if (r != BRIK_OK || R == 0 || N == 0 || E == 0) return r;
+    if (!row_off) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: row_off is null");
+    if (!aligned(row_off, 4)) return fail(c, BRIK_EALIGN, "moe_matmul_t_q4: row_off must be 4-byte aligned");
+    const void* p1 = nullptr;
+    int Mi = R, Ki = K, Ni = N, Ei = E;
+    void* args[] = {&x, &nib, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
+    const unsigned gy = (unsigned)((R + kGemmTile - 1) / kGemmTile + E);
+    return launch(c, K_GEMM_Q4, (unsigned)((N + kGemmTile - 1) / kGemmTile), gy, 256, 0, args);
+}
+
+static int dequant(brik_ctx* c, Kern k, const char* who, void** args, size_t n, const void* p0,
+                   const void* out, size_t p0_align)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n % kGroup) return fail(c, BRIK_EINVAL, "%s: n=%zu is not a multiple of 32", who, n);
+    if (n == 0) return BRIK_OK;
+    if (!p0 || !out) return fail(c, BRIK_EINVAL, "%s: null pointer", who);
+    if (!aligned(out, 16) || !aligned(p0, p0_align)) return fail(c, BRIK_EALIGN, "%s: misaligned pointer", who);
+    const uint64_t n8 = n / 8;
+    (void)n8;
+    const unsigned gx = (unsigned)((n / 8 + 255) / 256);
+    return launch(c, k, gx, 1, 256, 0, args);
+}
+
+int brik_dequant_q8_f32(brik_ctx* c, const int8_t* codes, const uint16_t* sc, float* out, size_t n)
+{
+    uint64_t n8 = n / 8;
+    if (n && !sc) return fail(c, BRIK_EINVAL, "dequant_q8: null scales");
+    void* args[] = {&codes, &sc, &out, &n8};
+    return dequant(c, K_DEQ_Q8, "dequant_q8", args, n, codes, out, 8);
+}
+
+int brik_dequant_q4_f32(brik_ctx* c, const uint8_t* nib, const uint16_t* sc, const uint16_t* mn,
+                        float* out, size_t n)
+{
+    uint64_t n8 = n / 8;
+    if (n && (!sc || !mn)) return fail(c, BRIK_EINVAL, "dequant_q4: null scales/mins");
+    void* args[] = {&nib, &sc, &mn, &out, &n8};
+    return dequant(c, K_DEQ_Q4, "dequant_q4", args, n, nib, out, 4);
+}
+
+int brik_dequant_q3_f32(brik_ctx* c, const uint32_t* lo, const uint32_t* hi, const uint16_t* sc,
+                        const uint16_t* mn, float* out, size_t n)
+{
+    uint64_t n8 = n / 8;
+    if (n && (!hi || !sc || !mn)) return fail(c, BRIK_EINVAL, "dequant_q3: null plane");
+    void* args[] = {&lo, &hi, &sc, &mn, &out, &n8};
+    return dequant(c, K_DEQ_Q3, "dequant_q3", args, n, lo, out, 4);
+}
+
+int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int njobs, brik_gemv_plan** out)
+{
+    if (!c || !out) return BRIK_EINVAL;
+    *out = nullptr;
+    if (fmt != BRIK_FMT_Q8 && fmt != BRIK_FMT_Q4 && fmt != BRIK_FMT_Q3)
+        return fail(c, BRIK_EINVAL, "gemv_plan: unknown format %d", fmt);
+    if (njobs <= 0 || !jobs) return fail(c, BRIK_EINVAL, "gemv_plan: need at least one job");
+    const Fmt f = Fmt(fmt);
+    int kmax = 0, kmin = 1 << 30;
+    for (int j = 0; j < njobs; ++j) {
+        const brik_gemv_job& b = jobs[j];
+        if (b.K < 32 || b.N < 1)
+            return fail(c, BRIK_EINVAL, "gemv_plan: job %d has K=%d N=%d (need K >= 32, N >= 1)", j, b.K, b.N);
+        int r = check_mm(c, "gemv_plan", b.x, b.p0, b.p1, b.scales, b.mins, b.y, 1, b.K, b.N, f);
+        if (r != BRIK_OK) return r;
+        if (((size_t)b.K + b.K / kGroup) * sizeof(float) > kGemvMaxLds)
+            return fail(c, BRIK_EINVAL, "gemv_plan: job %d K=%d exceeds the LDS staging limit", j, b.K);
+        kmax = b.K > kmax ? b.K : kmax;
+        kmin = b.K < kmin ? b.K : kmin;
+    }
+    const int team = gemv_team(c, kmin);
+    const int rpb = 4 * (256 / team);
+    std::vector<uint32_t> start(njobs + 1, 0);
+    for (int j = 0; j < njobs; ++j) start[j + 1] = start[j] + (uint32_t)((jobs[j].N + rpb - 1) / rpb);
+    brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();
+    if (!p) return BRIK_ENOMEM;
+    const size_t jb = sizeof(brik_gemv_job) * (size_t)njobs;
+    const size_t bytes = jb + sizeof(uint32_t) * start.size();
+    std::vector<unsigned char> host(bytes);
+    std::memcpy(host.data(), jobs, jb);
+    std::memcpy(host.data() + jb, start.data(), sizeof(uint32_t) * start.size());
+    int r = brik_alloc(c, bytes, &p->dev);
+    if (r == BRIK_OK) r = brik_h2d(c, p->dev, host.data(), bytes);
+    if (r != BRIK_OK) { brik_free(c, p->dev); delete p; return r; }
+    const int t = team == 16 ? 0 : team == 32 ? 1 : 2;
+    p->kernel = Kern((f == F_Q4 ? K_GRP_Q4_16 : f == F_Q8 ? K_GRP_Q8_16 : K_GRP_Q3_16) + t);
+    p->njobs = njobs;
+    p->rows_per_block = rpb;
+    p->blocks = start[njobs];
+    p->lds = ((size_t)kmax + kmax / kGroup) * sizeof(float);
+    *out = p;
+    return BRIK_OK;
+}
+
+int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
+{
+    if (!c || !p) return BRIK_EINVAL;
+    const brik_gemv_job* jobs = (const brik_gemv_job*)p->dev;
+    const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job) * (size_t)p->njobs);
+    int nj = p->njobs, rpb = p->rows_per_block;
+    void* args[] = {&jobs, &start, &nj, &rpb};
+    return launch(c, p->kernel, p->blocks, 1, 256, p->lds, args);
+}
+
+void brik_gemv_plan_destroy(brik_ctx* c, brik_gemv_plan* p)
+{
+    if (!p) return;
+    if (c) brik_free(c, p->dev);
+    delete p;
+}
+
+int brik_timer_begin(brik_ctx* c)
+{
+    if (!c) return BRIK_EINVAL;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipEventRecord(c->ev_begin, c->stream));
+    return BRIK_OK;
+}
+
+int brik_timer_end(brik_ctx* c, float* ms)
+{
+    if (!c || !ms) return BRIK_EINVAL;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipEventRecord(c->ev_end, c->stream));
+    HIP_TRY(c, hipEventSynchronize(c->ev_end));
+    HIP_TRY(c, hipEventElapsedTime(ms, c->ev_begin, c->ev_end));
+    return BRIK_OK;
+}
+
+int brik_set_option(brik_ctx* c, int key, int value)
+{
+    if (!c) return BRIK_EINVAL;
+    switch (key) {
+    case BRIK_OPT_PATH:
+        if (value < 0 || value > 2) return fail(c, BRIK_EINVAL, "BRIK_OPT_PATH: %d not in 0..2", value);
+        c->opt_path = value;
+        return BRIK_OK;
+    case BRIK_OPT_GEMV_TEAM:
+        if (value != 0 && value != 16 && value != 32 && value != 64)
+            return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMV_TEAM: %d not in {0,16,32,64}", value);
+        c->opt_team = value;
+        return BRIK_OK;
+    default:
+        return fail(c, BRIK_EINVAL, "unknown option %d", key);
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,4 @@
+// Single translation unit of the gfx950 code object embedded in libbrik.so.
+#include "dequant.hip"
+#include "gemv.hip"
+#include "gemm.hip"

@@ -1,0 +1,116 @@
+"""Host-side mirror of the reference engine's quantized-matmul interface (Python host).
+
+Mirrors the subset of ``WebGpuEngine`` (``src/lib/webgpu/kernels.ts``) that the quantized matmul
+path exposes, with the same names, argument meaning and error behaviour, over ``libbrik.so``:
+
+=========================  ===================================================  ==================
+reference                  here                                                 reference lines
+=========================  ===================================================  ==================
+``uploadGpuRaw(bytes)``    :meth:`Engine.upload_gpu_raw` (pads to 4 bytes)       kernels.ts:1032-1042
+``matmulQ4(a,nib,sc,mn,    :meth:`Engine.matmul_q4` (+ ``_tiled``/``_shared``)   kernels.ts:1046-1075
+m,k,n)``
+``matmulQ8(a,codes,sc,     :meth:`Engine.matmul_q8` (+ ``_tiled``/``_shared``)   kernels.ts:1140-1169
+m,k,n)``
+``matmulQ3(a,lo,hi,sc,mn,  :meth:`Engine.matmul_q3`                              kernels.ts:1080-1087
+m,k,n)``
+``dequantGpuQ4/Q3/Q8``     :meth:`Engine.weight` (one upload, planes in place)   model.ts:214-270
+``recMM(enc,trash,a,w,     :meth:`Engine.mm` (dispatch on the handle's shape)    kernels.ts:1562-1567
+m,k,n)``
+=========================  ===================================================  ==================
+
+The readback ops take host ``float32`` activations and return a host ``float32`` array of
+``m*n`` (the reference returns ``Promise<Float32Array>``). The reference validates nothing and lets
+WebGPU fail silently; here invalid shapes raise :class:`~brimkern_amd.capi.BrikError` before any
+launch. The ``_tiled``/``_shared`` variants exist in the reference only to pick a kernel by M; here
+one entry point picks the MI355X kernel by M, so they are aliases with the same output contract.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import layout
+from .capi import BrikError, Context, DeviceBuffer, BRIK_EINVAL
+
+
+class QWeight(dict):
+    """A quantized weight handle: ``{nib, sc, mn}`` (q4), ``{codes, sc}`` (q8) or
+    ``{q3: True, lo, hi, sc, mn}`` (q3) of device addresses, like ``model.ts:214-270`` builds."""
+
+    @property
+    def fmt(self) -> str:
+        return "q3" if self.get("q3") else "q4" if "nib" in self else "q8"
+
+
+class Engine:
+    def __init__(self, device: int = 0):
+        self.ctx = Context(device)
+
+    def close(self):
+        self.ctx.close()
+
+    # ---- uploads ---------------------------------------------------------------------
+    def upload_gpu_raw(self, data) -> DeviceBuffer:
+        """Persistent device copy of raw bytes, padded to a 4-byte multiple (kernels.ts:1032-1042)."""
+        b = np.frombuffer(memoryview(np.ascontiguousarray(data)).cast("B"), dtype=np.uint8)
+        pad = (-b.size) % 4
+        if pad:
+            b = np.concatenate([b, np.zeros(pad, np.uint8)])
+        return self.ctx.upload(b)
+
+    def weight(self, fmt: str, blob, n_elems: int) -> QWeight:
+        """Upload a packed .brik blob once and address its planes in place."""
+        offs = layout.plane_offsets(fmt, n_elems)
+        buf = self.upload_gpu_raw(np.asarray(blob, np.uint8)[: layout.byte_length(fmt, n_elems)])
+        h = QWeight({k: buf.offset(o) for k, (o, _) in offs.items()})
+        if fmt == "q3":
+            h["q3"] = True
+        h["_buf"] = buf
+        return h
+
+    # ---- readback ops ------------------------------------------------------------------
+    def _run(self, fn, a, planes, m, k, n):
+        a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+        if a.size != m * k:
+            raise BrikError(BRIK_EINVAL, f"activation has {a.size} floats, expected m*k={m * k}")
+        xa = self.ctx.upload(a) if a.size else None
+        out = self.ctx.alloc(max(m * n, 1) * 4)
+        try:
+            fn(xa, *planes, out, m, k, n)
+            res = self.ctx.download(out, np.float32, m * n)
+        finally:
+            self.ctx.free(out)
+            if xa is not None:
+                self.ctx.free(xa)
+        return res
+
+    def matmul_q4(self, a, nib, sc, mn, m, k, n) -> np.ndarray:
+        return self._run(self.ctx.matmul_t_q4, a, (nib, sc, mn), m, k, n)
+
+    matmul_q4_tiled = matmul_q4
+    matmul_q4_shared = matmul_q4
+
+    def matmul_q8(self, a, codes, sc, m, k, n) -> np.ndarray:
+        return self._run(self.ctx.matmul_t_q8, a, (codes, sc), m, k, n)
+
+    matmul_q8_tiled = matmul_q8
+    matmul_q8_shared = matmul_q8
+
+    def matmul_q3(self, a, lo, hi, sc, mn, m, k, n) -> np.ndarray:
+        return self._run(self.ctx.matmul_t_q3, a, (lo, hi, sc, mn), m, k, n)
+
+    # ---- recorded form ------------------------------------------------------------------
+    def mm(self, a, w: QWeight, m: int, k: int, n: int, out=None) -> DeviceBuffer:
+        """Device-resident ``recMM``: ``a`` and the result are device buffers; the kernel follows
+        the handle's shape (q3 flag, nib, codes) as kernels.ts:1562-1567 does."""
+        if out is None:
+            out = self.ctx.alloc(max(m * n, 1) * 4)
+        if w.get("q3"):
+            self.ctx.matmul_t_q3(a, w["lo"], w["hi"], w["sc"], w["mn"], out, m, k, n)
+        elif "nib" in w:
+            self.ctx.matmul_t_q4(a, w["nib"], w["sc"], w["mn"], out, m, k, n)
+        elif "codes" in w:
+            self.ctx.matmul_t_q8(a, w["codes"], w["sc"], out, m, k, n)
+        else:
+            raise BrikError(BRIK_EINVAL, "mm: weight handle is not a q3/q4/q8 handle (f32/f16 weights are "
+                                         "outside this library)")
+        return out

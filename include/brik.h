@@ -1,0 +1,147 @@
+/*
+ * brik.h — C ABI of the MI355X (gfx950) quantized matmul library, libbrik.so.
+ *
+ * Drop-in for the quantized matmul path of Brimkern's WebGPU engine:
+ *   y[M, N] = x[M, K] . deq(W[N, K])^T
+ * with W in the exact .brik q8web / q4web / q3web planes (src/lib/brik/q8web.ts, q4web.ts,
+ * q3web.ts; BRIK_FORMAT.md "Tensor encoding"), per-32-group f16 scales (and mins), x and y f32
+ * row-major. Plain pointers and sizes only; every pointer argument named x, y, out, or a plane is a
+ * DEVICE pointer (from brik_alloc or any hipMalloc'd buffer of the same device).
+ *
+ * Execution model: one context = one device + one HIP stream (default priority). Compute entry
+ * points enqueue on that stream and return; brik_sync() waits. Copies are synchronous.
+ * A context is not thread-safe: use it from one thread at a time.
+ *
+ * Error model: every int-returning function returns BRIK_OK (0) or a negative BRIK_E* code and
+ * leaves a message for brik_last_error(). Shapes are validated before any launch:
+ *   K % 32 == 0 (the reference's documented precondition, src/lib/webgpu/kernels.ts:1045, 1139),
+ *   M, K, N >= 0, non-null pointers when the operand is non-empty, plane alignment as listed.
+ * M == 0 or N == 0 is a no-op. K == 0 writes y = 0.
+ *
+ * Alignment (what a 16-byte aligned packed .brik blob guarantees, BRIK_ALIGN = 16,
+ * src/lib/brik/format.ts:8): x, y, out 16 B; q8 codes 16 B; q4 nibbles 16 B; q3 lo 16 B,
+ * q3 hi 8 B; scales and mins 2 B.
+ */
+#ifndef BRIK_H
+#define BRIK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BRIK_OK 0
+#define BRIK_EINVAL (-1)   /* bad shape / null pointer / K % 32 != 0 */
+#define BRIK_EALIGN (-2)   /* a plane or activation pointer breaks the alignment contract */
+#define BRIK_EHIP (-3)     /* a HIP runtime call failed (message holds hipGetErrorString) */
+#define BRIK_ENOMEM (-4)   /* device allocation failed */
+#define BRIK_ENODEV (-5)   /* no such device / no gfx950 device */
+#define BRIK_EMODULE (-6)  /* the embedded gfx950 code object failed to load */
+
+typedef struct brik_ctx brik_ctx;
+
+/* ---- context, memory, copies ------------------------------------------------------------
+ * Replace the engine runtime primitives the reference drives through WebGPU:
+ * init (src/lib/webgpu/kernels.ts:158-229), buffers + readBack (:231-274), uploadGpuRaw
+ * (:1032-1042), queue submit (:360-390). */
+
+/* Create a context on HIP device `device`, loading the embedded gfx950 code object. */
+int brik_create(int device, brik_ctx **out);
+void brik_destroy(brik_ctx *ctx);
+const char *brik_last_error(const brik_ctx *ctx);
+const char *brik_strerror(int code);
+int brik_device_count(int *count);
+
+int brik_alloc(brik_ctx *ctx, size_t bytes, void **dptr);
+int brik_free(brik_ctx *ctx, void *dptr);
+int brik_h2d(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
+int brik_d2h(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
+int brik_d2d(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Wait for all work enqueued on the context's stream. */
+int brik_sync(brik_ctx *ctx);
+
+/* ---- quantized matmuls --------------------------------------------------------------------
+ * Replace matmulQ8 / matmulQ8Tiled / matmulQ8Shared (kernels.ts:1140-1169), matmulQ4 /
+ * matmulQ4Tiled / matmulQ4Shared (kernels.ts:1046-1075), matmulQ3 (kernels.ts:1080-1087) and the
+ * recorded forms recMatmulQ8/Q4/Q3 behind recMM (kernels.ts:1521-1567). The kernel is chosen by
+ * M as recMatmulQ4 does (kernels.ts:1524-1531): M == 1 -> streaming GEMV; M >= 2 -> f16 MFMA GEMM.
+ * Planes are the unpackQ8/Q4/Q3 sub-arrays (q8web.ts:99-106, q4web.ts:187-197, q3web.ts:293-308),
+ * i.e. the packed blob split at the offsets those functions use. */
+
+int brik_matmul_t_q8(brik_ctx *ctx, const float *x, const int8_t *codes, const uint16_t *scales,
+                     float *y, int M, int K, int N);
+
+int brik_matmul_t_q4(brik_ctx *ctx, const float *x, const uint8_t *nibbles, const uint16_t *scales,
+                     const uint16_t *mins, float *y, int M, int K, int N);
+
+int brik_matmul_t_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const uint32_t *hi,
+                     const uint16_t *scales, const uint16_t *mins, float *y, int M, int K, int N);
+
+/* Expert-grouped q4 matmul (MoE). No counterpart exists in the reference (it has no MoE); this is
+ * the per-expert application of matmul_t_q4 over a token list sorted by expert:
+ *   for e in [0, E): y_sorted[r, :] = x_sorted[r, :] . deq(W_e)^T  for r in [row_off[e], row_off[e+1])
+ * W is ONE stacked q4 tensor [E, N, K] in .brik layout (nElems = E*N*K; expert e's nibbles start at
+ * e*N*K/2 bytes, its scales and mins at index e*N*K/32 of their planes).
+ * row_off: DEVICE int32[E + 1], non-decreasing, row_off[0] == 0, row_off[E] == R, the number of
+ * rows of x_sorted and y_sorted. The grid is sized from R and E alone (ceil(R/64) + E row tiles),
+ * so routing can stay on the device. */
+int brik_moe_matmul_t_q4(brik_ctx *ctx, const float *x_sorted, const int32_t *row_off,
+                         const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
+                         float *y_sorted, int E, int R, int K, int N);
+
+/* ---- grouped decode GEMV plans -------------------------------------------------------------
+ * The reference records a whole decoder layer, 7 recMM calls, into one command encoder and submits
+ * once (recordLayerKV, src/lib/webgpu/kernels.ts:1690-1744; decodeTopKQ8 :1908-1969). A plan is the
+ * MI355X form of that batching for the M == 1 matmuls: a table of independent GEMV jobs (e.g. q/k/v
+ * sharing one x, gate/up sharing another, or every projection of every layer) validated and uploaded
+ * once, then executed by ONE kernel launch per brik_gemv_plan_run. Jobs keep their pointers; the
+ * contents of x / W may change between runs. All jobs of a plan have the same format. */
+#define BRIK_FMT_Q8 8
+#define BRIK_FMT_Q4 4
+#define BRIK_FMT_Q3 3
+
+typedef struct brik_gemv_job {
+    const float *x;          /* [K] activation row (16 B aligned) */
+    const void *p0;          /* q8 codes / q4 nibbles / q3 lo plane */
+    const void *p1;          /* q3 hi plane; NULL for q8 and q4 */
+    const uint16_t *scales;  /* f16 per group */
+    const uint16_t *mins;    /* f16 per group; NULL for q8 */
+    float *y;                /* [N] output */
+    int32_t K, N;            /* K % 32 == 0, K >= 32, N >= 1 */
+} brik_gemv_job;
+
+typedef struct brik_gemv_plan brik_gemv_plan;
+int brik_gemv_plan_create(brik_ctx *ctx, int fmt, const brik_gemv_job *jobs, int njobs,
+                          brik_gemv_plan **out);
+int brik_gemv_plan_run(brik_ctx *ctx, const brik_gemv_plan *plan);
+void brik_gemv_plan_destroy(brik_ctx *ctx, brik_gemv_plan *plan);
+
+/* ---- dequantization (the bit-exactness check) ----------------------------------------------
+ * out[i] = deq(W)[i] in f32 for n_elems elements (n_elems % 32 == 0), bit-identical to
+ * dequantizeQ8 / dequantizeQ4 / dequantizeQ3 (q8web.ts:108-117, q4web.ts:199-213,
+ * q3web.ts:310-323) for every normal (non-subnormal, finite) scale and min. */
+int brik_dequant_q8_f32(brik_ctx *ctx, const int8_t *codes, const uint16_t *scales, float *out,
+                        size_t n_elems);
+int brik_dequant_q4_f32(brik_ctx *ctx, const uint8_t *nibbles, const uint16_t *scales,
+                        const uint16_t *mins, float *out, size_t n_elems);
+int brik_dequant_q3_f32(brik_ctx *ctx, const uint32_t *lo, const uint32_t *hi, const uint16_t *scales,
+                        const uint16_t *mins, float *out, size_t n_elems);
+
+/* ---- timing and tuning -------------------------------------------------------------------
+ * The reference has no kernel timing (it times whole tokens with performance.now(),
+ * src/app/page.tsx:1313-1376). brik_timer_begin/end record HIP events on the context stream
+ * around whatever was enqueued between them and return the elapsed GPU time in ms. */
+int brik_timer_begin(brik_ctx *ctx);
+int brik_timer_end(brik_ctx *ctx, float *ms);
+
+/* Kernel-selection overrides, for tests and tuning sweeps (0 restores automatic choice). */
+#define BRIK_OPT_PATH 1        /* 0 auto, 1 force GEMV (any M), 2 force MFMA GEMM (any M) */
+#define BRIK_OPT_GEMV_TEAM 2   /* 0 auto, else lanes per weight row: 16, 32 or 64 */
+int brik_set_option(brik_ctx *ctx, int key, int value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BRIK_H */

@@ -1,0 +1,264 @@
+"""GPU parity: the HIP kernels through the C ABI against the CPU oracle on identical seeded inputs.
+
+Bars (from the task): dequantized weights bit-exact; outputs within max relative error 1e-3 with
+f32 accumulation, measured normwise (max|y - r| / max|r|) and componentwise
+(|y - r| <= 1e-3 * sum_k |x_k w_k|). The M == 1 GEMV keeps f32 arithmetic end to end and is held
+to a tighter 1e-5; the MFMA GEMM rounds operands to f16 and is held to the 1e-3 bar.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from brimkern_amd import synth, layout
+from brimkern_amd.capi import BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_TEAM
+from helpers import Gpu, load_golden, normwise_rel, componentwise_ok, PLANES, REL_TOL
+
+pytestmark = pytest.mark.gpu
+GEMV_TOL = 1e-5
+CASES, MOE = load_golden()
+
+
+@pytest.fixture()
+def gpu(ctx):
+    g = Gpu(ctx)
+    yield g
+    ctx.set_option(BRIK_OPT_PATH, 0)
+    ctx.set_option(BRIK_OPT_GEMV_TEAM, 0)
+    g.free()
+
+
+def oracle_mm(fmt, x, t, M, K, N, absden=True):
+    args = [t[k] for k in PLANES[fmt]]
+    return {"q8": O.matmul_t_q8, "q4": O.matmul_t_q4, "q3": O.matmul_t_q3}[fmt](x, *args, M, K, N, absden=absden)
+
+
+def oracle_deq(fmt, t):
+    args = [t[k] for k in PLANES[fmt]]
+    return {"q8": O.dequant_q8, "q4": O.dequant_q4, "q3": O.dequant_q3}[fmt](*args)
+
+
+def check(y, r, den, tol):
+    rel = normwise_rel(y, r)
+    assert rel <= tol, f"normwise rel {rel:.3e} > {tol}"
+    assert componentwise_ok(y, r, den, tol), "componentwise bound violated"
+    return rel
+
+
+# ---- golden fixtures (reference selfValidate shapes) -----------------------------------
+
+@pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
+def test_golden_fixture(gpu, case):
+    fmt, M, K, N = case["fmt"], case["M"], case["K"], case["N"]
+    planes = gpu.planes(fmt, case)
+    assert np.array_equal(gpu.dequant(fmt, planes, N * K), case["deq"])
+    y = gpu.matmul(fmt, case["x"], planes, M, K, N)
+    r = case["y"].reshape(M, N)
+    assert normwise_rel(y, r) <= (GEMV_TOL if M == 1 else REL_TOL)
+    if M == 1:
+        # the reference's own gate, |got - ref| < 1e-3 absolute (kernels.ts:2263-2264), holds for the
+        # f32 GEMV; the f16-operand MFMA path (M >= 2) is held to the 1e-3 relative bar instead
+        assert np.abs(y - r).max() < 1e-3
+
+
+def test_golden_moe(gpu):
+    m = MOE
+    E, K, N, R = m["E"], m["K"], m["N"], m["R"]
+    planes = gpu.planes("q4", dict(m, N=E * N))
+    xb, rb = gpu.up(m["x"]), gpu.up(m["row_off"])
+    yb = gpu.up(np.zeros(R * N, np.float32))
+    gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
+    y = gpu.ctx.download(yb, np.float32, R * N)
+    assert normwise_rel(y, m["y"]) <= REL_TOL
+
+
+# ---- dequant bit-exactness at full BASELINE sizes ----------------------------------------
+
+@pytest.mark.parametrize("fmt,N,K,seed", [
+    ("q8", 4864, 896, 1),        # cfg 1
+    ("q4", 9728, 2560, 2),       # cfg 2 gate/up, cfg 4
+    ("q4", 2560, 9728, 3),       # cfg 2 down
+    ("q3", 151936, 2560, 4),     # cfg 3 LM head
+])
+def test_dequant_bit_exact(gpu, fmt, N, K, seed):
+    t = synth.tensor(fmt, seed, N, K)
+    planes = gpu.planes(fmt, t)
+    got = gpu.dequant(fmt, planes, N * K)
+    assert np.array_equal(got.view(np.uint32), oracle_deq(fmt, t).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_one_hot_gemv_is_dequant_column(gpu, fmt):
+    """x = e_k makes the GEMV output column k of deq(W) exactly: pins the in-register dequant."""
+    N, K = 300, 2560
+    t = synth.tensor(fmt, 9, N, K)
+    planes = gpu.planes(fmt, t)
+    deq = oracle_deq(fmt, t).reshape(N, K)
+    for k in (0, 1, 7, 31, 32, 1000, 2559):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        y = gpu.matmul(fmt, x, planes, 1, K, N)
+        assert np.array_equal(y.ravel().view(np.uint32), deq[:, k].copy().view(np.uint32)), f"k={k}"
+
+
+# ---- decode GEMV at the BASELINE shapes -------------------------------------------------
+
+GEMV_SHAPES = [
+    ("q8", 896, 4864),                                     # cfg 1 (Qwen2.5-0.5B FFN)
+    ("q4", 2560, 4096), ("q4", 2560, 1024), ("q4", 2560, 9728), ("q4", 9728, 2560),   # cfg 2
+    ("q3", 2560, 151936),                                  # cfg 3 (Qwen3-4B LM head)
+]
+
+
+@pytest.mark.parametrize("fmt,K,N", GEMV_SHAPES)
+def test_gemv_baseline_shapes(gpu, fmt, K, N):
+    t = synth.tensor(fmt, 17 + N, N, K)
+    x = synth.normal(5 + K, K)
+    planes = gpu.planes(fmt, t)
+    y = gpu.matmul(fmt, x, planes, 1, K, N)
+    r, den = oracle_mm(fmt, x, t, 1, K, N)
+    check(y, r, den, GEMV_TOL)
+
+
+@pytest.mark.parametrize("team", [16, 32, 64])
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_gemv_team_variants(gpu, fmt, team):
+    K, N = 1024, 777
+    t = synth.tensor(fmt, 23, N, K)
+    x = synth.normal(24, K)
+    planes = gpu.planes(fmt, t)
+    gpu.ctx.set_option(BRIK_OPT_GEMV_TEAM, team)
+    y = gpu.matmul(fmt, x, planes, 1, K, N)
+    r, den = oracle_mm(fmt, x, t, 1, K, N)
+    check(y, r, den, GEMV_TOL)
+
+
+# ---- prefill GEMM and small-M -----------------------------------------------------------
+
+@pytest.mark.parametrize("fmt,M,K,N", [
+    ("q4", 512, 2560, 9728),     # cfg 4
+    ("q8", 64, 896, 4864),
+    ("q3", 48, 2560, 4096),
+    ("q4", 2, 2560, 1024), ("q4", 5, 128, 6), ("q4", 17, 96, 65), ("q8", 3, 64, 130), ("q3", 65, 160, 33),
+])
+def test_gemm_parity(gpu, fmt, M, K, N):
+    t = synth.tensor(fmt, 31 + M, N, K)
+    x = synth.normal(32 + M, M * K)
+    planes = gpu.planes(fmt, t)
+    y = gpu.matmul(fmt, x, planes, M, K, N)
+    r, den = oracle_mm(fmt, x, t, M, K, N)
+    check(y, r, den, REL_TOL)
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_forced_paths_agree(gpu, fmt):
+    M, K, N = 6, 512, 200
+    t = synth.tensor(fmt, 41, N, K)
+    x = synth.normal(42, M * K)
+    planes = gpu.planes(fmt, t)
+    r, den = oracle_mm(fmt, x, t, M, K, N)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 1)
+    check(gpu.matmul(fmt, x, planes, M, K, N), r, den, GEMV_TOL)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
+    check(gpu.matmul(fmt, x[:K], planes, 1, K, N), r[:1], den[:1], REL_TOL)
+
+
+# ---- MoE expert-grouped q4 (cfg 5) ------------------------------------------------------
+
+@pytest.mark.parametrize("which", ["gate", "down"])
+def test_moe_cfg5(gpu, which):
+    T, H, E, F, TOPK = 256, 2048, 64, 768, 8
+    K, N = (H, F) if which == "gate" else (F, H)
+    rows, row_off = synth.moe_routing(77, T, E, TOPK)
+    R = rows.size
+    assert R == T * TOPK and np.diff(row_off).min() >= 0
+    t = synth.q4_tensor(78 if which == "gate" else 79, E * N, K)
+    if which == "gate":
+        x = synth.normal(80, T * H).reshape(T, H)[rows]        # gathered token rows
+    else:
+        x = synth.normal(81, R * K).reshape(R, K)
+    planes = gpu.planes("q4", t)
+    xb, rb = gpu.up(np.ascontiguousarray(x)), gpu.up(row_off)
+    yb = gpu.up(np.zeros(R * N, np.float32))
+    gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
+    y = gpu.ctx.download(yb, np.float32, R * N)
+    r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
+    assert normwise_rel(y, r) <= REL_TOL
+
+
+def test_moe_empty_experts(gpu):
+    E, K, N = 6, 64, 40
+    row_off = np.array([0, 0, 5, 5, 5, 9, 9], np.int32)
+    t = synth.q4_tensor(90, E * N, K)
+    x = synth.normal(91, 9 * K)
+    planes = gpu.planes("q4", t)
+    xb, rb = gpu.up(x), gpu.up(row_off)
+    yb = gpu.up(np.full(9 * N, np.nan, np.float32))
+    gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, 9, K, N)
+    y = gpu.ctx.download(yb, np.float32, 9 * N)
+    r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
+    assert normwise_rel(y, r) <= REL_TOL
+
+
+# ---- edge cases and error behaviour --------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_empty_and_degenerate_shapes(gpu, fmt):
+    K, N = 64, 10
+    t = synth.tensor(fmt, 50, N, K)
+    planes = gpu.planes(fmt, t)
+    x = synth.normal(51, 3 * K)
+    # M == 0 and N == 0 are no-ops: y untouched
+    yb = gpu.up(np.full(30, 7.0, np.float32))
+    fn = {"q8": gpu.ctx.matmul_t_q8, "q4": gpu.ctx.matmul_t_q4, "q3": gpu.ctx.matmul_t_q3}[fmt]
+    xb = gpu.up(x)
+    fn(xb, *planes, yb, 0, K, N)
+    fn(xb, *planes, yb, 3, K, 0)
+    assert np.all(gpu.ctx.download(yb, np.float32, 30) == 7.0)
+    # K == 0 writes zeros
+    fn(xb, *planes, yb, 3, 0, N)
+    assert np.all(gpu.ctx.download(yb, np.float32, 30) == 0.0)
+    # ragged N and M around the tile sizes
+    for M, N2 in ((1, 1), (1, 17), (2, 1), (3, 65), (64, 64), (65, 63)):
+        t2 = synth.tensor(fmt, 52 + M + N2, N2, 96)
+        x2 = synth.normal(53, M * 96)
+        y = gpu.matmul(fmt, x2, gpu.planes(fmt, t2), M, 96, N2)
+        r, den = oracle_mm(fmt, x2, t2, M, 96, N2)
+        check(y, r, den, REL_TOL)
+
+
+def test_invalid_arguments(gpu):
+    K, N = 64, 8
+    t = synth.q4_tensor(60, N, K)
+    planes = gpu.planes("q4", t)
+    xb = gpu.up(synth.normal(61, 2 * K))
+    yb = gpu.up(np.zeros(2 * N, np.float32))
+    with pytest.raises(BrikError) as e:
+        gpu.ctx.matmul_t_q4(xb, *planes, yb, 2, 48, N)          # K % 32 != 0
+    assert e.value.code == BRIK_EINVAL
+    with pytest.raises(BrikError) as e:
+        gpu.ctx.matmul_t_q4(xb, *planes, yb, -1, K, N)
+    assert e.value.code == BRIK_EINVAL
+    with pytest.raises(BrikError) as e:
+        gpu.ctx.matmul_t_q4(None, *planes, yb, 2, K, N)
+    assert e.value.code == BRIK_EINVAL
+    with pytest.raises(BrikError) as e:
+        gpu.ctx.matmul_t_q4(xb.ptr + 4, *planes, yb, 1, K, N)     # misaligned activation
+    assert e.value.code == BRIK_EALIGN
+    with pytest.raises(BrikError) as e:
+        gpu.ctx.matmul_t_q4(xb, planes[0] + 8, planes[1], planes[2], yb, 1, K, N)   # misaligned nibbles
+    assert e.value.code == BRIK_EALIGN
+    with pytest.raises(BrikError):
+        gpu.ctx.set_option(BRIK_OPT_GEMV_TEAM, 48)
+
+
+def test_bit_flip_is_detected(gpu):
+    """Negative control: corrupting one nibble byte must break parity (the check is not vacuous)."""
+    K, N = 256, 64
+    t = synth.q4_tensor(70, N, K)
+    x = synth.normal(71, K)
+    bad = dict(t, nib=t["nib"].copy())
+    bad["nib"][5 * K // 2 + 3] ^= 0x11
+    y = gpu.matmul("q4", x, gpu.planes("q4", bad), 1, K, N)
+    r, _ = oracle_mm("q4", x, t, 1, K, N)
+    assert np.abs(y.ravel() - r.ravel()).max() > 0
+    assert np.argmax(np.abs(y.ravel() - r.ravel())) == 5
