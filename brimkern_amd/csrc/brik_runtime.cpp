@@ -13,6 +13,8 @@
 #include <cstring>
 #include <new>
 #include <vector>
+#include <algorithm>
+#include <cmath>
 
 extern "C" const unsigned char brik_hsaco_begin[];
 extern "C" const unsigned char brik_hsaco_end[];
@@ -21,40 +23,44 @@ namespace {
 
 enum Kern {
     K_DEQ_Q8, K_DEQ_Q4, K_DEQ_Q3,
-    K_GEMV_Q4_16, K_GEMV_Q4_32, K_GEMV_Q4_64,
-    K_GEMV_Q8_16, K_GEMV_Q8_32, K_GEMV_Q8_64,
-    K_GEMV_Q3_16, K_GEMV_Q3_32, K_GEMV_Q3_64,
     K_GEMM_Q4, K_GEMM_Q8, K_GEMM_Q3,
-    K_GRP_Q4_16, K_GRP_Q4_32, K_GRP_Q4_64,
-    K_GRP_Q8_16, K_GRP_Q8_32, K_GRP_Q8_64,
-    K_GRP_Q3_16, K_GRP_Q3_32, K_GRP_Q3_64,
     K_COUNT
 };
 
 const char* const kKernelNames[K_COUNT] = {
     "brik_dequant_q8", "brik_dequant_q4", "brik_dequant_q3",
-    "brik_gemv_q4_t16", "brik_gemv_q4_t32", "brik_gemv_q4_t64",
-    "brik_gemv_q8_t16", "brik_gemv_q8_t32", "brik_gemv_q8_t64",
-    "brik_gemv_q3_t16", "brik_gemv_q3_t32", "brik_gemv_q3_t64",
     "brik_gemm_q4", "brik_gemm_q8", "brik_gemm_q3",
-    "brik_gemv_grouped_q4_t16", "brik_gemv_grouped_q4_t32", "brik_gemv_grouped_q4_t64",
-    "brik_gemv_grouped_q8_t16", "brik_gemv_grouped_q8_t32", "brik_gemv_grouped_q8_t64",
-    "brik_gemv_grouped_q3_t16", "brik_gemv_grouped_q3_t32", "brik_gemv_grouped_q3_t64",
 };
+
+// GEMV variants (lanes per row team, rows per team, groups per pipeline step), in the order of
+// BRIK_GEMV_FMT in gemv.hip. Kernels: brik_gemv_<fmt>_t<T>_r<R>_u<U> (one matrix) and
+// brik_gemvg_<fmt>_t<T>_r<R>_u<U> (grouped job table).
+struct GemvVariant { int team, r, u, d; };
+constexpr GemvVariant kGemvVariants[] = {{16, 2, 1, 2}, {16, 2, 1, 3}, {16, 2, 1, 4}, {16, 4, 1, 2},
+                                         {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}};
+constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]);
+const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 
 constexpr int kGroup = 32;
 constexpr int kGemmTile = 64;                  // BM = BN of brik_gemm_*
 constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
+constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loop over row sets
+constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
+constexpr long kPlanMaxSets = 4;               // row sets per grouped-plan block, at most
+
+// LDS bytes of a staged activation row (xprep.h): three int8 limbs per element, then per group an
+// f32 sum and an int32 exponent, then a flag.
+size_t gemv_lds(int K) { return (size_t)3 * K + (size_t)(K / kGroup) * 8 + 16; }
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
+int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 }  // namespace
 
 struct brik_gemv_plan {
-    Kern kernel;
+    hipFunction_t kernel;
     void* dev = nullptr;          // [jobs | block_start]
     int njobs = 0;
-    int rows_per_block = 0;
     unsigned blocks = 0;
     size_t lds = 0;
 };
@@ -63,10 +69,12 @@ struct brik_ctx {
     int device = -1;
     hipModule_t module = nullptr;
     hipFunction_t fn[K_COUNT] = {};
+    hipFunction_t gemv[3][kNumGemvVariants] = {};
+    hipFunction_t gemvg[3][kNumGemvVariants] = {};
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     int opt_path = 0;
-    int opt_team = 0;
+    int opt_variant = 0;   // 0 auto, else 1 + index into kGemvVariants
     char err[512] = {0};
 };
 
@@ -93,12 +101,17 @@ int fail(brik_ctx* c, int code, const char* fmt, ...)
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
-int launch(brik_ctx* c, Kern k, unsigned gx, unsigned gy, unsigned bx, size_t lds, void** args)
+int launch_fn(brik_ctx* c, hipFunction_t f, unsigned gx, unsigned gy, unsigned bx, size_t lds, void** args)
 {
     if (gx == 0 || gy == 0) return BRIK_OK;
     HIP_TRY(c, hipSetDevice(c->device));
-    HIP_TRY(c, hipModuleLaunchKernel(c->fn[k], gx, gy, 1, bx, 1, 1, (unsigned)lds, c->stream, args, nullptr));
+    HIP_TRY(c, hipModuleLaunchKernel(f, gx, gy, 1, bx, 1, 1, (unsigned)lds, c->stream, args, nullptr));
     return BRIK_OK;
+}
+
+int launch(brik_ctx* c, Kern k, unsigned gx, unsigned gy, unsigned bx, size_t lds, void** args)
+{
+    return launch_fn(c, c->fn[k], gx, gy, bx, lds, args);
 }
 
 // Shape + pointer validation shared by the three matmuls.
@@ -119,34 +132,30 @@ int check_mm(brik_ctx* c, const char* who, const float* x, const void* p0, const
     if (f == F_Q3 && !aligned(p1, 8)) return fail(c, BRIK_EALIGN, "%s: q3 hi plane must be 8-byte aligned", who);
     if (!aligned(sc, 2) || (mn && !aligned(mn, 2)))
         return fail(c, BRIK_EALIGN, "%s: scales/mins must be 2-byte aligned", who);
-    if ((long long)N * K / kGroup > 0x7fffffffLL * 8)
-        return fail(c, BRIK_EINVAL, "%s: tensor too large", who);
+    // each plane is addressed through one buffer resource (32-bit byte offsets); the largest
+    // plane is the q8 code plane, N*K bytes
+    if ((unsigned long long)N * (unsigned long long)K >= (1ull << 32))
+        return fail(c, BRIK_EINVAL, "%s: N*K = %lld elements exceeds the 2^32 per-tensor limit", who, (long long)N * K);
     return BRIK_OK;
 }
 
-int gemv_team(brik_ctx* c, int K)
+// GEMV variant for a given K (index into kGemvVariants).
+int gemv_variant(brik_ctx* c, int K)
 {
-    if (c->opt_team == 16 || c->opt_team == 32 || c->opt_team == 64) return c->opt_team;
-    const int G = K / kGroup;
-    if (G >= 256) return 64;
-    if (G >= 96) return 32;
-    return 16;
-}
-
-Kern gemv_kernel(Fmt f, int team)
-{
-    const int t = team == 16 ? 0 : team == 32 ? 1 : 2;
-    switch (f) {
-    case F_Q4: return Kern(K_GEMV_Q4_16 + t);
-    case F_Q8: return Kern(K_GEMV_Q8_16 + t);
-    default:   return Kern(K_GEMV_Q3_16 + t);
-    }
+    if (c->opt_variant > 0) return c->opt_variant - 1;
+    (void)K;
+    return 0;
 }
 
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N)
 {
-    const size_t lds = ((size_t)K + K / kGroup) * sizeof(float);
+    // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
+    const int v = gemv_variant(c, K);
+    const int rpi = (256 / kGemvVariants[v].team) * kGemvVariants[v].r;
+    const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
+    const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
+    const size_t lds = gemv_lds(K) + sizeof(float) * (size_t)rpi * kGemvVariants[v].team * ((sets + gx - 1) / gx);
     const bool gemv_fits = lds <= kGemvMaxLds;
     bool use_gemv = (M == 1 && gemv_fits);
     if (c->opt_path == 1) {
@@ -157,12 +166,8 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     }
     int Mi = M, Ki = K, Ni = N;
     if (use_gemv) {
-        const int team = gemv_team(c, K);
-        const int rpb = 256 / team;
-        unsigned gx = (unsigned)((N + rpb - 1) / rpb);
-        if (gx > 65535u * 4) gx = 65535u * 4;
         void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni};
-        return launch(c, gemv_kernel(f, team), gx, (unsigned)M, 256, lds, args);
+        return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
     const int* row_off = nullptr;
     int E = 0;
@@ -218,6 +223,15 @@ int brik_create(int device, brik_ctx** out)
     if (hipModuleLoadData(&c->module, brik_hsaco_begin) != hipSuccess) return bail(BRIK_EMODULE);
     for (int k = 0; k < K_COUNT; ++k)
         if (hipModuleGetFunction(&c->fn[k], c->module, kKernelNames[k]) != hipSuccess) return bail(BRIK_EMODULE);
+    for (int f = 0; f < 3; ++f)
+        for (int v = 0; v < kNumGemvVariants; ++v) {
+            char name[64];
+            const GemvVariant& gv = kGemvVariants[v];
+            snprintf(name, sizeof name, "brik_gemv_%s_t%d_r%d_u%d_d%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d);
+            if (hipModuleGetFunction(&c->gemv[f][v], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+            snprintf(name, sizeof name, "brik_gemvg_%s_t%d_r%d_u%d_d%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d);
+            if (hipModuleGetFunction(&c->gemvg[f][v], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+        }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);
     if (hipEventCreate(&c->ev_begin) != hipSuccess || hipEventCreate(&c->ev_end) != hipSuccess)
         return bail(BRIK_EHIP);
@@ -375,31 +389,49 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d has K=%d N=%d (need K >= 32, N >= 1)", j, b.K, b.N);
         int r = check_mm(c, "gemv_plan", b.x, b.p0, b.p1, b.scales, b.mins, b.y, 1, b.K, b.N, f);
         if (r != BRIK_OK) return r;
-        if (((size_t)b.K + b.K / kGroup) * sizeof(float) > kGemvMaxLds)
+        if (gemv_lds(b.K) + 16384 > kGemvMaxLds)
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d K=%d exceeds the LDS staging limit", j, b.K);
         kmax = b.K > kmax ? b.K : kmax;
         kmin = b.K < kmin ? b.K : kmin;
     }
-    const int team = gemv_team(c, kmin);
-    const int rpb = 4 * (256 / team);
-    std::vector<uint32_t> start(njobs + 1, 0);
-    for (int j = 0; j < njobs; ++j) start[j + 1] = start[j] + (uint32_t)((jobs[j].N + rpb - 1) / rpb);
+    const int v = gemv_variant(c, kmin);
+    const int rpi = (256 / kGemvVariants[v].team) * kGemvVariants[v].r;
+    // Blocks of about equal cost: rows per block ~ kPlanGroupRows / (K/32), in whole row sets of rpi
+    // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). Jobs are laid out in order
+    // of decreasing K, so the most expensive blocks are dispatched first and the tail of the launch
+    // consists of the cheapest ones.
+    std::vector<int> order(njobs);
+    for (int j = 0; j < njobs; ++j) order[j] = j;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return jobs[a].K > jobs[b].K; });
+    std::vector<brik_gemv_job> sorted(njobs);
+    std::vector<uint32_t> start(njobs + 1, 0), rpbs(njobs);
+    size_t lds = 0;
+    for (int k = 0; k < njobs; ++k) {
+        const brik_gemv_job& b = jobs[order[k]];
+        sorted[k] = b;
+        long sets = lround((double)kPlanGroupRows / ((double)(b.K / kGroup) * rpi));
+        sets = sets < 1 ? 1 : sets > kPlanMaxSets ? kPlanMaxSets : sets;
+        rpbs[k] = (uint32_t)(sets * rpi);
+        start[k + 1] = start[k] + (uint32_t)((b.N + rpbs[k] - 1) / rpbs[k]);
+        const size_t need = gemv_lds(b.K) + sizeof(float) * (size_t)rpbs[k] * kGemvVariants[v].team;
+        lds = need > lds ? need : lds;
+    }
+    if (lds > kGemvMaxLds) return fail(c, BRIK_EINVAL, "gemv_plan: K=%d too large for LDS staging", kmax);
     brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();
     if (!p) return BRIK_ENOMEM;
     const size_t jb = sizeof(brik_gemv_job) * (size_t)njobs;
-    const size_t bytes = jb + sizeof(uint32_t) * start.size();
+    const size_t bytes = jb + sizeof(uint32_t) * (start.size() + rpbs.size());
     std::vector<unsigned char> host(bytes);
-    std::memcpy(host.data(), jobs, jb);
+    std::memcpy(host.data(), sorted.data(), jb);
     std::memcpy(host.data() + jb, start.data(), sizeof(uint32_t) * start.size());
+    std::memcpy(host.data() + jb + sizeof(uint32_t) * start.size(), rpbs.data(), sizeof(uint32_t) * rpbs.size());
     int r = brik_alloc(c, bytes, &p->dev);
     if (r == BRIK_OK) r = brik_h2d(c, p->dev, host.data(), bytes);
     if (r != BRIK_OK) { brik_free(c, p->dev); delete p; return r; }
-    const int t = team == 16 ? 0 : team == 32 ? 1 : 2;
-    p->kernel = Kern((f == F_Q4 ? K_GRP_Q4_16 : f == F_Q8 ? K_GRP_Q8_16 : K_GRP_Q3_16) + t);
+    p->kernel = c->gemvg[fmt_index(f)][v];
     p->njobs = njobs;
-    p->rows_per_block = rpb;
     p->blocks = start[njobs];
-    p->lds = ((size_t)kmax + kmax / kGroup) * sizeof(float);
+    p->lds = lds;
     *out = p;
     return BRIK_OK;
 }
@@ -409,9 +441,10 @@ int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
     if (!c || !p) return BRIK_EINVAL;
     const brik_gemv_job* jobs = (const brik_gemv_job*)p->dev;
     const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job) * (size_t)p->njobs);
-    int nj = p->njobs, rpb = p->rows_per_block;
-    void* args[] = {&jobs, &start, &nj, &rpb};
-    return launch(c, p->kernel, p->blocks, 1, 256, p->lds, args);
+    const uint32_t* rpbs = start + p->njobs + 1;
+    int nj = p->njobs;
+    void* args[] = {&jobs, &start, &rpbs, &nj};
+    return launch_fn(c, p->kernel, p->blocks, 1, 256, p->lds, args);
 }
 
 void brik_gemv_plan_destroy(brik_ctx* c, brik_gemv_plan* p)
@@ -447,10 +480,10 @@ int brik_set_option(brik_ctx* c, int key, int value)
         if (value < 0 || value > 2) return fail(c, BRIK_EINVAL, "BRIK_OPT_PATH: %d not in 0..2", value);
         c->opt_path = value;
         return BRIK_OK;
-    case BRIK_OPT_GEMV_TEAM:
-        if (value != 0 && value != 16 && value != 32 && value != 64)
-            return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMV_TEAM: %d not in {0,16,32,64}", value);
-        c->opt_team = value;
+    case BRIK_OPT_GEMV_VARIANT:
+        if (value < 0 || value > kNumGemvVariants)
+            return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMV_VARIANT: %d not in 0..%d", value, kNumGemvVariants);
+        c->opt_variant = value;
         return BRIK_OK;
     default:
         return fail(c, BRIK_EINVAL, "unknown option %d", key);

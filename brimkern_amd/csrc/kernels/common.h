@@ -31,3 +31,52 @@ __device__ __forceinline__ T ld_stream(const T* p)
 }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int b) { return (w >> (8 * b)) & 0xffu; }
+
+// ---- buffer addressing ------------------------------------------------------------------------
+// A raw buffer resource over [p, p + bytes): loads take a 32-bit VGPR offset, a uniform SGPR offset
+// and an immediate, so per-load address arithmetic is free, and reads past `bytes` return 0
+// instead of faulting. Planes are limited to < 4 GiB per resource (checked on the host).
+typedef __amdgpu_buffer_rsrc_t brsrc_t;
+#define BRIK_BUF_DWORD3 0x00020000   // raw (untyped) buffer, 32-bit data format, gfx9 family
+
+__device__ __forceinline__ brsrc_t make_rsrc(const void* p, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, BRIK_BUF_DWORD3);
+}
+
+// Cache policy of streamed weight loads: non-temporal (nt).
+#define BRIK_AUX_STREAM 2
+
+// ---- DPP cross-lane sums (within 16-lane rows) ---------------------------------------------------
+
+#define BRIK_DPP_ADD(v, CTRL) \
+    ((v) + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (CTRL), 0xF, 0xF, false)))
+#define BRIK_DPP_MAX(v, CTRL) \
+    fmaxf((v), __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (CTRL), 0xF, 0xF, false)))
+#define DPP_QUAD_1032 0xB1      // quad_perm [1,0,3,2]
+#define DPP_QUAD_2301 0x4E      // quad_perm [2,3,0,1]
+#define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_ROR4 0x124
+#define DPP_ROW_ROR8 0x128
+
+// Sum / max over aligned groups of 8 lanes; every lane of the group receives the result.
+__device__ __forceinline__ float sum8(float v)
+{
+    v = BRIK_DPP_ADD(v, DPP_QUAD_1032);
+    v = BRIK_DPP_ADD(v, DPP_QUAD_2301);
+    return BRIK_DPP_ADD(v, DPP_ROW_HALF_MIRROR);
+}
+__device__ __forceinline__ float max8(float v)
+{
+    v = BRIK_DPP_MAX(v, DPP_QUAD_1032);
+    v = BRIK_DPP_MAX(v, DPP_QUAD_2301);
+    return BRIK_DPP_MAX(v, DPP_ROW_HALF_MIRROR);
+}
+// Sum over aligned groups of 16 lanes (one DPP row); every lane receives the result.
+__device__ __forceinline__ float sum16(float v)
+{
+    v = BRIK_DPP_ADD(v, DPP_QUAD_1032);
+    v = BRIK_DPP_ADD(v, DPP_QUAD_2301);
+    v = BRIK_DPP_ADD(v, DPP_ROW_ROR4);
+    return BRIK_DPP_ADD(v, DPP_ROW_ROR8);
+}

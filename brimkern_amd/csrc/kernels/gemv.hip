@@ -1,168 +1,356 @@
-// Decode GEMV: y[m, :] = x[m, :] . deq(W)^T for one activation row per grid.y, streaming the
-// packed .brik planes once. Replaces the reference's 1-row WGSL kernels matmul_t_q8 / _q4 / _q3
-// (src/lib/webgpu/shaders.ts:376-418, 77-114, 323-369), which give each output to one thread
-// and walk its weight row serially with 32-bit loads.
+// Decode GEMV: y[m, :] = x[m, :] . deq(W)^T for one activation row per grid.y, streaming the packed
+// .brik planes once. Replaces the reference's 1-row WGSL kernels matmul_t_q8 / _q4 / _q3
+// (src/lib/webgpu/shaders.ts:376-418, 77-114, 323-369), which give each output to one thread and
+// walk its weight row serially with 32-bit loads.
+//
+// Arithmetic. The group scale factors out of the dot product:
+//   y_n = sum_g [ s_ng * sum_{k in g} x_k q_nk + m_ng * sum_{k in g} x_k ].
+// x is staged once per block as 24-bit block floating point (xprep.h), so sum x_k q_nk is an exact
+// int32 dot product of int8 limbs with the integer codes (v_dot4_i32_i8), rescaled once per group.
+// A one-hot x reproduces deq(W) bit-exactly: the single product s*q*2^21 and its rescale are exact
+// and the final fmaf(m, 1, s*q) rounds q*s + m once, as the reference's dequantize does.
 //
 // Mapping (wave64, 256-thread blocks):
-//   * a "team" of TEAM lanes (16, 32 or 64; a DPP row is 16 lanes) owns one weight row at a time;
-//     lane l of the team handles the row's groups g = l, l + TEAM, ... so the team's loads of one
-//     step are TEAM consecutive groups: TEAM x 16 contiguous bytes for q4 (one 128-bit load per
-//     lane per group), fully coalesced.
-//   * the activation row is staged once per block in LDS, 16-byte chunks XOR-swizzled inside each
-//     32-float group so the lanes of a team (stride of one group) hit distinct banks.
-//   * the per-group scale factors out of the dot: y = sum_g s_g * (sum_{k in g} x_k q_k)
-//     + m_g * (sum_{k in g} x_k). The group sums of x are computed once at staging.
-//   * the TEAM partial sums of a row are reduced with cross-lane shuffles; lane 0 writes y.
+//   * a team of TEAM lanes (16, 32 or 64) owns R adjacent weight rows; lane l handles groups
+//     g = l, l + TEAM, ... so one step of a team loads TEAM consecutive groups per row: for q4,
+//     TEAM x 16 contiguous bytes, one 128-bit load per lane per group;
+//   * each lane reads a group's x limbs from LDS once and applies them to its R rows;
+//   * software pipeline: a lane's work is a sequence of steps of U groups x R rows; the loads of
+//     step i + 1 are issued before step i is consumed, and the first step's loads before x is staged;
+//   * team partial sums are reduced with cross-lane shuffles; lane 0 writes y.
 #include "common.h"
+#include "xprep.h"
 #include "../../../include/brik.h"   // brik_gemv_job
 
 namespace {
 
-// x chunk c (4 floats) of group g lives at float offset g*32 + ((c ^ (g & 7)) * 4).
-__device__ __forceinline__ int xsw(int g, int c) { return g * 32 + ((c ^ (g & 7)) << 2); }
+using brik::XStage;
 
-// Stage one activation row (K floats) into LDS and compute its 32-element group sums.
-__device__ __forceinline__ void stage_x(const float* __restrict__ xrow, float* xl, float* xsum, int K)
+// Raw data of one (row, group) as loaded from the planes.
+template <int FMT> struct Grp;
+// Scale and min stay raw 16-bit values (v_cvt_f32_f16 reads the low half of the register), so no
+// zero-extension consumes a load before the step that uses it.
+template <> struct Grp<FMT_Q4> { u32x4_t w; uint16_t s, m; };
+template <> struct Grp<FMT_Q8> { u32x4_t w0, w1; uint16_t s; };
+template <> struct Grp<FMT_Q3> { u32x2_t l; uint32_t h; uint16_t s, m; };
+
+// Bytes per group in the code plane (p0).
+template <int FMT> struct CodeBytes { static constexpr int v = FMT == FMT_Q4 ? 16 : FMT == FMT_Q8 ? 32 : 8; };
+
+struct Planes {
+    const uint8_t* p0;
+    const uint8_t* p1;
+    const uint16_t* sc;
+    const uint16_t* mn;
+};
+
+// Buffer resources over the planes of an N x K matrix (G groups per row).
+struct Rs {
+    brsrc_t code, hi, sc, mn;
+};
+
+template <int FMT>
+__device__ __forceinline__ Rs make_rs(const Planes& P, int N, int G)
 {
-    const int nq = K >> 2;               // float4 chunks
-    for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-        f32x4_t v = *(const f32x4_t*)(xrow + 4 * i);
-        const int g = i >> 3, c = i & 7;
-        *(f32x4_t*)(xl + xsw(g, c)) = v;
-        // group sum: the 8 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0)
-        float p = (v.x + v.y) + (v.z + v.w);
-        p += __shfl_xor(p, 1, 8);
-        p += __shfl_xor(p, 2, 8);
-        p += __shfl_xor(p, 4, 8);
-        if (c == 0) xsum[g] = p;
+    const uint32_t groups = (uint32_t)N * (uint32_t)G;
+    Rs r;
+    r.code = make_rsrc(P.p0, groups * CodeBytes<FMT>::v);
+    r.hi = make_rsrc(FMT == FMT_Q3 ? (const void*)P.p1 : (const void*)P.p0, FMT == FMT_Q3 ? groups * 4 : 0);
+    r.sc = make_rsrc(P.sc, groups * 2);
+    r.mn = make_rsrc(FMT == FMT_Q8 ? (const void*)P.sc : (const void*)P.mn, FMT == FMT_Q8 ? 0 : groups * 2);
+    return r;
+}
+
+// Load group (gi + goff) where gi is per lane (VGPR) and goff = step offset (uniform) + gconst.
+template <int FMT>
+__device__ __forceinline__ void load_grp(Grp<FMT>& d, const Rs& rs, uint32_t gi, uint32_t gstep, uint32_t gconst)
+{
+    constexpr int CB = CodeBytes<FMT>::v;
+    if constexpr (FMT == FMT_Q4) {
+        d.w = __builtin_amdgcn_raw_buffer_load_b128(rs.code, (gi + gconst) * CB, gstep * CB, BRIK_AUX_STREAM);
+        d.m = __builtin_amdgcn_raw_buffer_load_b16(rs.mn, (gi + gconst) * 2, gstep * 2, 0);
+    } else if constexpr (FMT == FMT_Q8) {
+        d.w0 = __builtin_amdgcn_raw_buffer_load_b128(rs.code, (gi + gconst) * CB, gstep * CB, BRIK_AUX_STREAM);
+        d.w1 = __builtin_amdgcn_raw_buffer_load_b128(rs.code, (gi + gconst) * CB + 16, gstep * CB, BRIK_AUX_STREAM);
+    } else {
+        d.l = __builtin_amdgcn_raw_buffer_load_b64(rs.code, (gi + gconst) * CB, gstep * CB, BRIK_AUX_STREAM);
+        d.h = __builtin_amdgcn_raw_buffer_load_b32(rs.hi, (gi + gconst) * 4, gstep * 4, BRIK_AUX_STREAM);
+        d.m = __builtin_amdgcn_raw_buffer_load_b16(rs.mn, (gi + gconst) * 2, gstep * 2, 0);
+    }
+    d.s = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (gi + gconst) * 2, gstep * 2, 0);
+}
+
+// The group's 32 codes as 8 dwords of bytes, in brik::code_pos order.
+template <int FMT>
+__device__ __forceinline__ void unpack(const Grp<FMT>& d, uint32_t (&b)[8])
+{
+    if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            b[2 * j] = d.w[j] & 0x0f0f0f0fu;
+            b[2 * j + 1] = (d.w[j] >> 4) & 0x0f0f0f0fu;
+        }
+    } else if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { b[j] = d.w0[j]; b[4 + j] = d.w1[j]; }
+    } else {
+        // lo words L0 (codes 0..15) and L1 (16..31), 2 bits per code; hi word, 1 bit per code.
+        // Byte dword s holds codes s, s+8, s+16, s+24. The 2-bit fields of codes s and s+8 (s < 4)
+        // sit in bytes 0 and 2 of L0, of codes s+16 and s+24 in bytes 0 and 2 of L1; for s >= 4 in
+        // bytes 1 and 3.
+        const uint32_t p0 = __builtin_amdgcn_perm(d.l.y, d.l.x, 0x06040200u);   // L0.b0 L0.b2 L1.b0 L1.b2
+        const uint32_t p1 = __builtin_amdgcn_perm(d.l.y, d.l.x, 0x07050301u);   // L0.b1 L0.b3 L1.b1 L1.b3
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const uint32_t lo = ((s < 4 ? p0 : p1) >> (2 * (s & 3))) & 0x03030303u;
+            const uint32_t hi = ((d.h >> s) & 0x01010101u) << 2;
+            b[s] = lo | hi;
+        }
+    }
+}
+
+// sum_{k in g} x_k q_k * 2^-(e_g - 22) as exact int32 limb dot products, combined in f32.
+__device__ __forceinline__ float limb_dot(const uint32_t (&b)[8], const u32x4_t (&xl)[3][2])
+{
+    int a[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t) {
+        int v = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v = __builtin_amdgcn_sdot4((int)b[j], (int)xl[t][0][j], v, false);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v = __builtin_amdgcn_sdot4((int)b[4 + j], (int)xl[t][1][j], v, false);
+        a[t] = v;
+    }
+    const int hm = (a[0] << 8) + a[1];                   // |a0| <= 2^19, so no int32 overflow
+    return __builtin_fmaf((float)hm, 256.f, (float)a[2]);
+}
+
+// acc += s * sum(x q) + m * sum(x) for one (row, group); s and m zeroed for masked-out groups.
+template <int FMT>
+__device__ __forceinline__ float use_grp(const Grp<FMT>& d, const u32x4_t (&xl)[3][2], float2 xse, bool valid,
+                                         float acc)
+{
+    uint32_t b[8];
+    unpack<FMT>(d, b);
+    const float p = limb_dot(b, xl);
+    const float s = valid ? f16_bits_to_f32(d.s) : 0.f;
+    acc += ldexpf(s * p, __builtin_bit_cast(int, xse.y));
+    if constexpr (FMT != FMT_Q8) {
+        const float m = valid ? f16_bits_to_f32(d.m) : 0.f;
+        acc = __builtin_fmaf(m, xse.x, acc);
+    }
+    return acc;
+}
+
+// Exact f32 fallback for a row holding Inf/NaN: per-element dequant, f32 FMA.
+template <int FMT>
+__device__ __forceinline__ float deq_elem(const Planes& P, size_t e)
+{
+    const size_t fg = e / BRIK_GROUP;
+    const float s = f16_bits_to_f32(P.sc[fg]);
+    if constexpr (FMT == FMT_Q8) {
+        return (float)(int8_t)P.p0[e] * s;
+    } else {
+        uint32_t q;
+        if constexpr (FMT == FMT_Q4) {
+            q = (P.p0[e >> 1] >> (4 * (e & 1))) & 15u;
+        } else {
+            const uint32_t lw = ((const uint32_t*)P.p0)[e >> 4], hw = ((const uint32_t*)P.p1)[e >> 5];
+            q = ((lw >> ((e & 15) * 2)) & 3u) | (((hw >> (e & 31)) & 1u) << 2);
+        }
+        return __builtin_fmaf((float)q, s, f16_bits_to_f32(P.mn[fg]));
     }
 }
 
 template <int TEAM>
 __device__ __forceinline__ float team_sum(float v)
 {
-#pragma unroll
-    for (int off = TEAM / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, TEAM);
+    v = sum16(v);
+    if constexpr (TEAM >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (TEAM >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
-// sum_{k in group} x_k * q_k for one group, per format. xg points at the group's swizzled chunks.
-__device__ __forceinline__ float dot_q4(const float* xl, int g, u32x4_t w)
-{
-    float p = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {          // word j holds elements 8j .. 8j+7
-        const uint32_t wj = w[j];
-        const uint32_t lo = wj & 0x0f0f0f0fu;          // bytes: elements 8j+0, +2, +4, +6
-        const uint32_t hi = (wj >> 4) & 0x0f0f0f0fu;   // bytes: elements 8j+1, +3, +5, +7
-        const f32x4_t xa = *(const f32x4_t*)(xl + xsw(g, 2 * j));
-        const f32x4_t xb = *(const f32x4_t*)(xl + xsw(g, 2 * j + 1));
-        p = __builtin_fmaf(xa.x, (float)byte_of(lo, 0), p);
-        p = __builtin_fmaf(xa.y, (float)byte_of(hi, 0), p);
-        p = __builtin_fmaf(xa.z, (float)byte_of(lo, 1), p);
-        p = __builtin_fmaf(xa.w, (float)byte_of(hi, 1), p);
-        p = __builtin_fmaf(xb.x, (float)byte_of(lo, 2), p);
-        p = __builtin_fmaf(xb.y, (float)byte_of(hi, 2), p);
-        p = __builtin_fmaf(xb.z, (float)byte_of(lo, 3), p);
-        p = __builtin_fmaf(xb.w, (float)byte_of(hi, 3), p);
-    }
-    return p;
-}
+// Per-team schedule over one matrix. The block owns row sets p = 0 .. nsets-1; team t computes rows
+// n0(p) + [0, R) with n0(p) = r0 + t * R + p * rstep. A row set takes B steps; step b covers groups
+// lane + TEAM * (U*b + u), u < U. The S = nsets * B steps of a team run as one software pipeline of
+// depth D: the loads of step i + D - 1 are issued before step i is consumed.
+//
+// The pipelined loop body is straight-line code (no branches), which is what lets the compiler keep
+// the loads of the steps ahead in flight (s_waitcnt vmcnt(N) rather than vmcnt(0)): step indices
+// advance by scalar selects, rows past r1 and groups past G are clamped for loading and masked for
+// accumulation, and each lane stores its running partial sums to LDS every step (the value after a
+// row set's last step is the lane's final partial). The cross-lane sums and the y writes happen
+// once, after the loop.
+template <int FMT, int TEAM, int R, int U>
+struct Work {
+    static constexpr int RPI = (256 / TEAM) * R;   // rows per block iteration
+    Rs rs;
+    int G, r0, r1, rstep, B, lane, team;
+    float* part;       // LDS [nsets][RPI][TEAM] lane partials (see gemv_matrix)
 
-__device__ __forceinline__ float dot_q8(const float* xl, int g, u32x4_t w0, u32x4_t w1)
-{
-    float p = 0.f;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {          // word c holds elements 4c .. 4c+3
-        const uint32_t wc = c < 4 ? w0[c] : w1[c - 4];
-        const f32x4_t xv = *(const f32x4_t*)(xl + xsw(g, c));
-        p = __builtin_fmaf(xv.x, (float)(int8_t)byte_of(wc, 0), p);
-        p = __builtin_fmaf(xv.y, (float)(int8_t)byte_of(wc, 1), p);
-        p = __builtin_fmaf(xv.z, (float)(int8_t)byte_of(wc, 2), p);
-        p = __builtin_fmaf(xv.w, (float)(int8_t)byte_of(wc, 3), p);
-    }
-    return p;
-}
+    __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
 
-__device__ __forceinline__ float dot_q3(const float* xl, int g, u32x2_t l, uint32_t h)
-{
-    float p = 0.f;
+    // Loads of step (p, b), branch-free, every address clamped in bounds.
+    __device__ __forceinline__ void issue(Grp<FMT> (&d)[U][R], int p, int b) const
+    {
+        const int n = n0(p);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {          // chunk c: elements 4c .. 4c+3
-        const uint32_t lw = l[c >> 2] >> ((c & 3) * 8);
-        const uint32_t hw = h >> (4 * c);
-        const f32x4_t xv = *(const f32x4_t*)(xl + xsw(g, c));
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = (uint32_t)min(n + r, r1 - 1) * (uint32_t)G;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t q = ((lw >> (2 * t)) & 3u) | (((hw >> t) & 1u) << 2);
-            p = __builtin_fmaf(xv[t], (float)q, p);
+            for (int u = 0; u < U; ++u) {
+                const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
+                load_grp<FMT>(d[u][r], rs, row + g, 0u, 0u);
+            }
         }
     }
-    return p;
-}
 
-// Rows [r0, r1) of one weight matrix, TEAM lanes per row, x already staged in LDS.
-template <int FMT, int TEAM>
-__device__ __forceinline__ void gemv_rows(const float* xl, const float* xsum, const uint8_t* __restrict__ p0,
-                                          const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
-                                          const uint16_t* __restrict__ mn, float* __restrict__ yrow,
-                                          int G, int r0, int r1, int rstep)
+    // Consume step (p, b) into acc (reset first when b == 0) and store the lane partials.
+    __device__ __forceinline__ void consume(const Grp<FMT> (&d)[U][R], const XStage& S, int p, int b,
+                                            float (&acc)[R]) const
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = b == 0 ? 0.f : acc[r];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int g = lane + TEAM * (U * b + u);
+            const int gl = min(g, G - 1);
+            const bool valid = g < G;
+            u32x4_t xl[3][2];
+            const int hs = brik::half_swap(gl);
+#pragma unroll
+            for (int t = 0; t < 3; ++t) {
+                const int8_t* base = S.limbs + (size_t)t * 32 * G + 32 * gl;
+                xl[t][0] = *(const u32x4_t*)(base + hs);
+                xl[t][1] = *(const u32x4_t*)(base + (16 ^ hs));
+            }
+            const float2 xse = S.xse[gl];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = use_grp<FMT>(d[u][r], xl, xse, valid, acc[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[(p * RPI + team * R + r) * TEAM + lane] = acc[r];
+    }
+};
+
+// Exact path for a row holding Inf/NaN.
+template <int FMT, int TEAM, int R>
+__device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Planes& P, float* __restrict__ yrow,
+                                                int K, int r0, int r1, int rstep)
 {
     const int lane = threadIdx.x % TEAM;
     const int team = threadIdx.x / TEAM;
-    for (int n = r0 + team; n < r1; n += rstep) {
-        const size_t gb = (size_t)n * G;      // first flat group of row n
-        float acc = 0.f;
-        for (int g = lane; g < G; g += TEAM) {
-            float p;
-            if constexpr (FMT == FMT_Q4) {
-                const u32x4_t w = ld_stream((const u32x4_t*)p0 + gb + g);
-                p = dot_q4(xl, g, w);
-            } else if constexpr (FMT == FMT_Q8) {
-                const u32x4_t* wp = (const u32x4_t*)p0 + 2 * (gb + g);
-                const u32x4_t w0 = ld_stream(wp), w1 = ld_stream(wp + 1);
-                p = dot_q8(xl, g, w0, w1);
-            } else {
-                const u32x2_t l = ld_stream((const u32x2_t*)p0 + gb + g);
-                const uint32_t h = ld_stream((const uint32_t*)p1 + gb + g);
-                p = dot_q3(xl, g, l, h);
-            }
-            const float s = f16_bits_to_f32(sc[gb + g]);
-            acc = __builtin_fmaf(s, p, acc);
-            if constexpr (FMT != FMT_Q8) {
-                const float mm = f16_bits_to_f32(mn[gb + g]);
-                acc = __builtin_fmaf(mm, xsum[g], acc);
-            }
+    for (int n0 = r0 + team * R; n0 < r1; n0 += rstep) {
+        for (int r = 0; r < R && n0 + r < r1; ++r) {
+            float acc = 0.f;
+            for (int k = lane; k < K; k += TEAM)
+                acc = __builtin_fmaf(x[k], deq_elem<FMT>(P, (size_t)(n0 + r) * K + k), acc);
+            acc = team_sum<TEAM>(acc);
+            if (lane == 0) yrow[n0 + r] = acc;
         }
-        acc = team_sum<TEAM>(acc);
-        if (lane == 0) yrow[n] = acc;
     }
 }
 
-template <int FMT, int TEAM>
+// Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
+// then the cross-lane sums of the LDS partials are written to y. The block owns row sets
+// p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
+template <int FMT, int TEAM, int R, int U, int D>
+__device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Planes& P, float* __restrict__ yrow,
+                                            int N, int K, int r0, int r1, int rstep, unsigned char* lds)
+{
+    using W = Work<FMT, TEAM, R, U>;
+    W w;
+    w.G = K / BRIK_GROUP;
+    w.rs = make_rs<FMT>(P, N, w.G);
+    w.r0 = r0; w.r1 = r1; w.rstep = rstep;
+    w.lane = threadIdx.x % TEAM;
+    w.team = threadIdx.x / TEAM;
+    w.B = (w.G + U * TEAM - 1) / (U * TEAM);
+    const int nsets = r0 < r1 ? (r1 - r0 + rstep - 1) / rstep : 0;     // block-uniform
+    const int S = nsets * w.B;                                            // steps per team
+    Grp<FMT> d[D][U][R];
+    // prologue: steps 0 .. D-2 in flight before x is staged
+    int ip = 0, bp = 0;                      // (p, b) of the next step to issue
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) {
+        w.issue(d[k], ip, bp);
+        const bool wrap = bp + 1 == w.B;
+        bp = wrap ? 0 : bp + 1;
+        ip += wrap;
+    }
+    const XStage X = brik::xstage_layout(lds, K);
+    w.part = (float*)(lds + brik::xstage_bytes(K));
+    brik::xstage<FMT>(x, X, K);
+    if (*X.flag) {
+        gemv_rows_exact<FMT, TEAM, R>(x, P, yrow, K, r0, r1, rstep);
+        return;
+    }
+    float acc[R] = {};
+    int pc = 0, bc = 0;                      // (p, b) of the next step to consume
+    int i = 0;
+    // main loop, unrolled by D so every buffer index is static; straight-line body
+    for (; i + D <= S; i += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            w.issue(d[(k + D - 1) % D], ip, bp);
+            {
+                const bool wrap = bp + 1 == w.B;
+                bp = wrap ? 0 : bp + 1;
+                ip += wrap;
+            }
+            w.consume(d[k], X, pc, bc, acc);
+            const bool wrap = bc + 1 == w.B;
+            bc = wrap ? 0 : bc + 1;
+            pc += wrap;
+        }
+    }
+    // remaining S - i < D steps are already issued
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) {
+        if (i + k < S) {
+            w.consume(d[k], X, pc, bc, acc);
+            const bool wrap = bc + 1 == w.B;
+            bc = wrap ? 0 : bc + 1;
+            pc += wrap;
+        }
+    }
+    __syncthreads();
+    // cross-lane sums: one thread per row, TEAM partials each (rows past r1 are skipped)
+    for (int q = threadIdx.x; q < nsets * W::RPI; q += blockDim.x) {
+        const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
+        if (n < r1) {
+            const float* pp = w.part + (size_t)q * TEAM;
+            float v = 0.f;
+#pragma unroll
+            for (int l = 0; l < TEAM; ++l) v += pp[(l + q) % TEAM];
+            yrow[n] = v;
+        }
+    }
+}
+
+template <int FMT, int TEAM, int R, int U, int D>
 __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uint8_t* __restrict__ p0,
                                           const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
                                           const uint16_t* __restrict__ mn, float* __restrict__ y, int K, int N)
 {
-    extern __shared__ float lds[];
-    const int G = K / BRIK_GROUP;
-    float* xl = lds;
-    float* xsum = lds + K;
-    const int m = blockIdx.y;
-    stage_x(x + (size_t)m * K, xl, xsum, K);
-    __syncthreads();
-    constexpr int RPB = 256 / TEAM;      // rows in flight per block
-    gemv_rows<FMT, TEAM>(xl, xsum, p0, p1, sc, mn, y + (size_t)m * N, G, blockIdx.x * RPB, N, gridDim.x * RPB);
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int RPI = (256 / TEAM) * R;     // rows per block iteration
+    const Planes P{p0, p1, sc, mn};
+    gemv_matrix<FMT, TEAM, R, U, D>(x + (size_t)blockIdx.y * K, P, y + (size_t)blockIdx.y * N, N, K, blockIdx.x * RPI,
+                                    N, gridDim.x * RPI, lds);
 }
 
-// Grouped GEMV over a job table: block b runs rows [rb * rows_per_block, ...) of job j, where
+// Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
 // block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts).
-template <int FMT, int TEAM>
+template <int FMT, int TEAM, int R, int U, int D>
 __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restrict__ jobs,
-                                                  const uint32_t* __restrict__ block_start, int njobs,
-                                                  int rows_per_block)
+                                                  const uint32_t* __restrict__ block_start,
+                                                  const uint32_t* __restrict__ rows_per_block, int njobs)
 {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int RPI = (256 / TEAM) * R;
     const uint32_t b = blockIdx.x;
     int lo = 0, hi = njobs - 1;          // last j with block_start[j] <= b
     while (lo < hi) {
@@ -170,53 +358,40 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restric
         if (block_start[mid] <= b) lo = mid; else hi = mid - 1;
     }
     const brik_gemv_job job = jobs[lo];
-    const int K = job.K, G = K / BRIK_GROUP;
-    float* xl = lds;
-    float* xsum = lds + K;
-    stage_x(job.x, xl, xsum, K);
-    __syncthreads();
-    const int r0 = (int)(b - block_start[lo]) * rows_per_block;
-    const int r1 = min(job.N, r0 + rows_per_block);
-    constexpr int RPB = 256 / TEAM;
-    gemv_rows<FMT, TEAM>(xl, xsum, (const uint8_t*)job.p0, (const uint8_t*)job.p1, job.scales, job.mins,
-                         job.y, G, r0, r1, RPB);
+    const Planes P{(const uint8_t*)job.p0, (const uint8_t*)job.p1, job.scales, job.mins};
+    const int rpb = (int)rows_per_block[lo];
+    const int r0 = (int)(b - block_start[lo]) * rpb;
+    const int r1 = min(job.N, r0 + rpb);
+    gemv_matrix<FMT, TEAM, R, U, D>(job.x, P, job.y, job.N, job.K, r0, r1, RPI, lds);
 }
 
 }  // namespace
 
-#define BRIK_GEMV(NAME, FMT, TEAM)                                                                  \
-    extern "C" __global__ __launch_bounds__(256) void NAME(                                         \
+#define BRIK_GEMV(FMTN, FMT, TEAM, RR, UU, DD)                                                      \
+    extern "C" __global__ __launch_bounds__(256) void brik_gemv_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
         const float* __restrict__ x, const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1, \
         const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, float* __restrict__ y,    \
         int K, int N)                                                                               \
     {                                                                                               \
-        gemv_body<FMT, TEAM>(x, p0, p1, sc, mn, y, K, N);                                           \
-    }
-
-BRIK_GEMV(brik_gemv_q4_t16, FMT_Q4, 16)
-BRIK_GEMV(brik_gemv_q4_t32, FMT_Q4, 32)
-BRIK_GEMV(brik_gemv_q4_t64, FMT_Q4, 64)
-BRIK_GEMV(brik_gemv_q8_t16, FMT_Q8, 16)
-BRIK_GEMV(brik_gemv_q8_t32, FMT_Q8, 32)
-BRIK_GEMV(brik_gemv_q8_t64, FMT_Q8, 64)
-BRIK_GEMV(brik_gemv_q3_t16, FMT_Q3, 16)
-BRIK_GEMV(brik_gemv_q3_t32, FMT_Q3, 32)
-BRIK_GEMV(brik_gemv_q3_t64, FMT_Q3, 64)
-
-#define BRIK_GEMV_GROUPED(NAME, FMT, TEAM)                                                          \
-    extern "C" __global__ __launch_bounds__(256) void NAME(                                         \
-        const brik_gemv_job* __restrict__ jobs, const uint32_t* __restrict__ block_start, int njobs,  \
-        int rows_per_block)                                                                         \
+        gemv_body<FMT, TEAM, RR, UU, DD>(x, p0, p1, sc, mn, y, K, N);                               \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
+        const brik_gemv_job* __restrict__ jobs, const uint32_t* __restrict__ block_start,           \
+        const uint32_t* __restrict__ rows_per_block, int njobs)                                      \
     {                                                                                               \
-        gemv_grouped_body<FMT, TEAM>(jobs, block_start, njobs, rows_per_block);                     \
+        gemv_grouped_body<FMT, TEAM, RR, UU, DD>(jobs, block_start, rows_per_block, njobs);         \
     }
 
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q4_t16, FMT_Q4, 16)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q4_t32, FMT_Q4, 32)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q4_t64, FMT_Q4, 64)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q8_t16, FMT_Q8, 16)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q8_t32, FMT_Q8, 32)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q8_t64, FMT_Q8, 64)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q3_t16, FMT_Q3, 16)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q3_t32, FMT_Q3, 32)
-BRIK_GEMV_GROUPED(brik_gemv_grouped_q3_t64, FMT_Q3, 64)
+// The variant table of the runtime (brik_runtime.cpp, kGemvVariants) lists these in this order.
+#define BRIK_GEMV_FMT(FMTN, FMT)     \
+    BRIK_GEMV(FMTN, FMT, 16, 2, 1, 2) \
+    BRIK_GEMV(FMTN, FMT, 16, 2, 1, 3) \
+    BRIK_GEMV(FMTN, FMT, 16, 2, 1, 4) \
+    BRIK_GEMV(FMTN, FMT, 16, 4, 1, 2) \
+    BRIK_GEMV(FMTN, FMT, 16, 2, 2, 2) \
+    BRIK_GEMV(FMTN, FMT, 32, 2, 1, 3) \
+    BRIK_GEMV(FMTN, FMT, 64, 1, 1, 3)
+
+BRIK_GEMV_FMT(q4, FMT_Q4)
+BRIK_GEMV_FMT(q8, FMT_Q8)
+BRIK_GEMV_FMT(q3, FMT_Q3)

@@ -1,0 +1,131 @@
+// Activation staging for the decode GEMV: one f32 row x[K] -> LDS as 24-bit block floating point.
+//
+// Per 32-element group g (the quantization group of the weights), with e_g the binary exponent of
+// max|x| over the group (frexp), every element becomes the integer X = rint(x * 2^(22 - e_g)),
+// |X| < 2^22, split into three signed bytes X = h * 65536 + m * 256 + l (h, m, l in [-128, 127]).
+// The dot products with the integer weight codes then run on v_dot4_i32_i8 (four int8 MACs per lane
+// per instruction, exact int32 sums), and the group's result is rescaled by 2^(e_g - 22) in f32.
+// Relative to the group's largest element this keeps 22 bits, about f32's 24-bit significand.
+//
+// LDS layout for K = 32 * G:
+//   limbs: limb t (0 = h, 1 = m, 2 = l) of group g occupies bytes [t*32G + 32g, +32), the 32 bytes in
+//          the byte order the format's code unpacking produces (code_pos), with the two 16-byte
+//          halves swapped when bit 3 of g is set (so the lanes reading groups g and g + 8 in the same
+//          instruction hit different banks);
+//   xse[g]: {f32 sum of the group's x, int32 e_g - 22};
+//   flag:  int32, nonzero if the row holds a non-finite value (the exact f32 path then runs).
+#pragma once
+#include "common.h"
+
+namespace brik {
+
+// Byte position, inside a group's 32 limb bytes (before the half swap), of group element e.
+//   q8: codes are already bytes in element order.
+//   q4: code dword j (elements 8j..8j+7) unpacks to two byte dwords: (w & 0x0f0f0f0f) holds elements
+//       8j, 8j+2, 8j+4, 8j+6 and ((w >> 4) & 0x0f0f0f0f) holds 8j+1, 8j+3, 8j+5, 8j+7; they are
+//       byte dwords 2j and 2j+1.
+//   q3: byte dword s (0..7) holds codes s, s+8, s+16, s+24 (see unpack in gemv.hip).
+template <int FMT>
+__device__ __forceinline__ int code_pos(int e)
+{
+    if constexpr (FMT == FMT_Q8) return e;
+    else if constexpr (FMT == FMT_Q4) return ((2 * (e >> 3) + (e & 1)) << 2) + ((e & 7) >> 1);
+    else return ((e & 7) << 2) + (e >> 3);
+}
+
+__device__ __forceinline__ int half_swap(int g) { return ((g >> 3) & 1) << 4; }
+
+struct XStage {
+    int8_t* limbs;
+    float2* xse;      // {sum, bit-cast int exponent}
+    int* flag;
+    int G;
+};
+
+// Bytes of the staged row; the block's result buffer follows at this offset (16-byte aligned).
+__host__ __device__ __forceinline__ size_t xstage_bytes(int K)
+{
+    return (size_t)3 * K + (size_t)(K / BRIK_GROUP) * 8 + 16;
+}
+
+__device__ __forceinline__ XStage xstage_layout(void* lds, int K)
+{
+    XStage s;
+    s.G = K / BRIK_GROUP;
+    s.limbs = (int8_t*)lds;
+    s.xse = (float2*)((char*)lds + 3 * (size_t)K);
+    s.flag = (int*)(s.xse + s.G);
+    return s;
+}
+
+__device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h, int& m, int& l)
+{
+    const int X = finite ? (int)__builtin_rintf(ldexpf(v, sh)) : 0;
+    l = (int)(int8_t)(X & 0xff);
+    const int X1 = (X - l) >> 8;
+    m = (int)(int8_t)(X1 & 0xff);
+    h = (X1 - m) >> 8;
+}
+
+// Stage x[0..K) (16-byte aligned, K % 32 == 0). All threads of the block call it; ends with a barrier.
+template <int FMT>
+__device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K)
+{
+    if (threadIdx.x == 0) *S.flag = 0;
+    __syncthreads();
+    const int nq = K >> 2;
+    const int G = S.G;
+    // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
+    // every loop trip is entered by whole 8-lane groups, so the DPP group reductions see full groups
+    for (int i = threadIdx.x; i < nq; i += blockDim.x) {
+        const f32x4_t v = *(const f32x4_t*)(x + 4 * i);
+        const int g = i >> 3, c = i & 7;
+        const float p = sum8((v.x + v.y) + (v.z + v.w));
+        const float a = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const bool finite = __builtin_isfinite(p) && __builtin_isfinite(a);
+        int e = 0;
+        (void)frexpf(a, &e);                 // a < 2^e, so |x * 2^(22-e)| < 2^22
+        const int sh = 22 - e;
+        if (c == 0) S.xse[g] = float2{p, __builtin_bit_cast(float, -sh)};
+        if (!finite) *S.flag = 1;
+        int hh[4], mm[4], ll[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) split_limbs(v[t], sh, finite, hh[t], mm[t], ll[t]);
+        int8_t* base = S.limbs + 32 * g;
+        const int hs = half_swap(g);
+        if constexpr (FMT == FMT_Q8) {
+            // elements 4c..4c+3 are byte dword c of every limb
+            const int pos = (4 * c) ^ hs;
+            auto pack = [](const int (&b)[4]) {
+                return (uint32_t)(b[0] & 0xff) | ((uint32_t)(b[1] & 0xff) << 8) | ((uint32_t)(b[2] & 0xff) << 16) |
+                       ((uint32_t)(b[3] & 0xff) << 24);
+            };
+            *(uint32_t*)(base + pos) = pack(hh);
+            *(uint32_t*)(base + 32 * G + pos) = pack(mm);
+            *(uint32_t*)(base + 64 * G + pos) = pack(ll);
+        } else if constexpr (FMT == FMT_Q4) {
+            // elements 4c..4c+3 give bytes (c&1)*2 and +1 of byte dwords 2j (even elements) and
+            // 2j+1 (odd elements), j = c/2: two 16-bit stores per limb
+            const int j = c >> 1, bo = (c & 1) * 2;
+            const int pe = ((8 * j) + bo) ^ hs, po = ((8 * j + 4) + bo) ^ hs;
+            auto st = [&](int8_t* lb, const int (&b)[4]) {
+                *(uint16_t*)(lb + pe) = (uint16_t)((b[0] & 0xff) | ((b[2] & 0xff) << 8));
+                *(uint16_t*)(lb + po) = (uint16_t)((b[1] & 0xff) | ((b[3] & 0xff) << 8));
+            };
+            st(base, hh);
+            st(base + 32 * G, mm);
+            st(base + 64 * G, ll);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int pos = code_pos<FMT>(4 * c + t) ^ hs;
+                base[pos] = (int8_t)hh[t];
+                base[32 * G + pos] = (int8_t)mm[t];
+                base[64 * G + pos] = (int8_t)ll[t];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+}  // namespace brik

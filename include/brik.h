@@ -138,7 +138,8 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
 
 /* Kernel-selection overrides, for tests and tuning sweeps (0 restores automatic choice). */
 #define BRIK_OPT_PATH 1        /* 0 auto, 1 force GEMV (any M), 2 force MFMA GEMM (any M) */
-#define BRIK_OPT_GEMV_TEAM 2   /* 0 auto, else lanes per weight row: 16, 32 or 64 */
+#define BRIK_OPT_GEMV_VARIANT 2  /* 0 auto, else 1 + index of a GEMV tiling variant (see brik_runtime.cpp) */
+#define BRIK_GEMV_VARIANTS 7
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus

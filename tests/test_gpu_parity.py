@@ -10,7 +10,7 @@ import pytest
 
 import oracle as O
 from brimkern_amd import synth, layout
-from brimkern_amd.capi import BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_TEAM
+from brimkern_amd.capi import BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT, BRIK_GEMV_VARIANTS
 from helpers import Gpu, load_golden, normwise_rel, componentwise_ok, PLANES, REL_TOL
 
 pytestmark = pytest.mark.gpu
@@ -23,7 +23,7 @@ def gpu(ctx):
     g = Gpu(ctx)
     yield g
     ctx.set_option(BRIK_OPT_PATH, 0)
-    ctx.set_option(BRIK_OPT_GEMV_TEAM, 0)
+    ctx.set_option(BRIK_OPT_GEMV_VARIANT, 0)
     g.free()
 
 
@@ -119,17 +119,29 @@ def test_gemv_baseline_shapes(gpu, fmt, K, N):
     check(y, r, den, GEMV_TOL)
 
 
-@pytest.mark.parametrize("team", [16, 32, 64])
+@pytest.mark.parametrize("variant", range(1, BRIK_GEMV_VARIANTS + 1))
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
-def test_gemv_team_variants(gpu, fmt, team):
-    K, N = 1024, 777
+def test_gemv_variants(gpu, fmt, variant):
+    """Every GEMV tiling variant (team width, rows per team, pipeline depth), single and grouped,
+    at a ragged shape (N odd, K/32 not a multiple of the team width)."""
+    K, N = 1056, 777
     t = synth.tensor(fmt, 23, N, K)
     x = synth.normal(24, K)
     planes = gpu.planes(fmt, t)
-    gpu.ctx.set_option(BRIK_OPT_GEMV_TEAM, team)
+    gpu.ctx.set_option(BRIK_OPT_GEMV_VARIANT, variant)
     y = gpu.matmul(fmt, x, planes, 1, K, N)
     r, den = oracle_mm(fmt, x, t, 1, K, N)
     check(y, r, den, GEMV_TOL)
+    xb = gpu.up(x)
+    yb = gpu.up(np.zeros(N, np.float32))
+    names = PLANES[fmt]
+    job = {"x": xb, "p0": planes[0], "p1": planes[1] if fmt == "q3" else None, "sc": planes[names.index("sc")],
+           "mn": planes[names.index("mn")] if "mn" in names else None, "y": yb, "K": K, "N": N}
+    plan = gpu.ctx.gemv_plan(fmt, [job])
+    plan.run()
+    yg = gpu.ctx.download(yb, np.float32, N)
+    plan.destroy()
+    check(yg, r, den, GEMV_TOL)
 
 
 # ---- prefill GEMM and small-M -----------------------------------------------------------
@@ -248,7 +260,7 @@ def test_invalid_arguments(gpu):
         gpu.ctx.matmul_t_q4(xb, planes[0] + 8, planes[1], planes[2], yb, 1, K, N)   # misaligned nibbles
     assert e.value.code == BRIK_EALIGN
     with pytest.raises(BrikError):
-        gpu.ctx.set_option(BRIK_OPT_GEMV_TEAM, 48)
+        gpu.ctx.set_option(BRIK_OPT_GEMV_VARIANT, BRIK_GEMV_VARIANTS + 1)
 
 
 def test_bit_flip_is_detected(gpu):
@@ -262,3 +274,57 @@ def test_bit_flip_is_detected(gpu):
     r, _ = oracle_mm("q4", x, t, 1, K, N)
     assert np.abs(y.ravel() - r.ravel()).max() > 0
     assert np.argmax(np.abs(y.ravel() - r.ravel())) == 5
+
+
+# ---- grouped plans and non-finite activations -----------------------------------------------
+
+def test_grouped_plan_layer_set(gpu):
+    """A plan over a small 'layer set': jobs of different K and N sharing x buffers, like the
+    q/k/v + gate/up + down projections of one decoder layer."""
+    shapes = [(256, 384), (256, 96), (256, 96), (256, 700), (704, 256)]
+    xs = {256: synth.normal(301, 256), 704: synth.normal(302, 704)}
+    xb = {k: gpu.up(v) for k, v in xs.items()}
+    jobs, refs = [], []
+    for i, (K, N) in enumerate(shapes):
+        t = synth.q4_tensor(310 + i, N, K)
+        nib, sc, mn = gpu.planes("q4", t)
+        yb = gpu.up(np.zeros(N, np.float32))
+        jobs.append({"x": xb[K], "p0": nib, "sc": sc, "mn": mn, "y": yb, "K": K, "N": N})
+        refs.append(oracle_mm("q4", xs[K], t, 1, K, N))
+    plan = gpu.ctx.gemv_plan("q4", jobs)
+    for _ in range(2):                      # plans are reusable
+        plan.run()
+    for j, (r, den) in zip(jobs, refs):
+        y = gpu.ctx.download(j["y"], np.float32, j["N"])
+        check(y, r, den, GEMV_TOL)
+    plan.destroy()
+
+
+def test_grouped_plan_rejects_bad_jobs(gpu):
+    t = synth.q4_tensor(320, 8, 64)
+    nib, sc, mn = gpu.planes("q4", t)
+    xb, yb = gpu.up(synth.normal(321, 64)), gpu.up(np.zeros(8, np.float32))
+    good = {"x": xb, "p0": nib, "sc": sc, "mn": mn, "y": yb, "K": 64, "N": 8}
+    for bad in (dict(good, K=48), dict(good, N=0), dict(good, K=0), dict(good, mn=None), dict(good, x=xb.ptr + 4)):
+        with pytest.raises(BrikError):
+            gpu.ctx.gemv_plan("q4", [good, bad])
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_non_finite_activation_follows_f32_semantics(gpu, fmt):
+    """Inf/NaN in x cannot be held in the integer limbs; such a row takes the exact f32 path and
+    yields the same Inf/NaN pattern as the f64 reference sum."""
+    K, N = 256, 40
+    t = synth.tensor(fmt, 330, N, K)
+    planes = gpu.planes(fmt, t)
+    x = synth.normal(331, 3 * K).reshape(3, K)
+    x[0, 17] = np.inf
+    x[1, 200] = np.nan
+    gpu.ctx.set_option(BRIK_OPT_PATH, 1)        # GEMV for every row
+    y = gpu.matmul(fmt, x, planes, 3, K, N)
+    r, den = oracle_mm(fmt, x, t, 3, K, N)
+    for row in (0, 1):
+        assert np.array_equal(np.isnan(y[row]), np.isnan(r[row]))
+        assert np.array_equal(np.isposinf(y[row]), np.isposinf(r[row]))
+        assert np.array_equal(np.isneginf(y[row]), np.isneginf(r[row]))
+    check(y[2], r[2], den[2], GEMV_TOL)          # the finite row is unaffected
