@@ -63,7 +63,7 @@ def build_addon(verbose=False):
     if not os.path.exists(src) or not os.path.exists(os.path.join(NODE_INC, "node_api.h")):
         return None
     tmp = ADDON + ".tmp"
-    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra", "-DNODE_GYP_MODULE_NAME=brik",
           "-I", NODE_INC, "-I", os.path.join(ROOT, "include"), src,
           "-L", PKG, "-lbrik", "-Wl,-rpath,$ORIGIN/..", "-o", tmp], verbose)
     os.replace(tmp, ADDON)

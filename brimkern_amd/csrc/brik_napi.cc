@@ -1,0 +1,464 @@
+// brik.node — Node N-API binding of libbrik.so (the C ABI of include/brik.h).
+//
+// Thin by design: every function converts JS arguments, calls one brik_* entry point and throws a JS
+// Error on a negative return (err.code = "BRIK_EINVAL" etc., err.message = the library's message).
+// Device pointers cross the boundary as BigInt addresses; the engine facade in js/index.js wraps them
+// in DeviceBuffer objects with the reference engine's method names.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "brik.h"
+
+namespace {
+
+#define NAPI_CALL(env, call)                                                  \
+    do {                                                                      \
+        if ((call) != napi_ok) {                                              \
+            napi_throw_error((env), "BRIK_NAPI", "N-API call failed: " #call); \
+            return nullptr;                                                   \
+        }                                                                     \
+    } while (0)
+
+const char* code_name(int rc)
+{
+    switch (rc) {
+    case BRIK_EINVAL: return "BRIK_EINVAL";
+    case BRIK_EALIGN: return "BRIK_EALIGN";
+    case BRIK_EHIP: return "BRIK_EHIP";
+    case BRIK_ENOMEM: return "BRIK_ENOMEM";
+    case BRIK_ENODEV: return "BRIK_ENODEV";
+    case BRIK_EMODULE: return "BRIK_EMODULE";
+    default: return "BRIK_ERROR";
+    }
+}
+
+// Throw for rc < 0. Returns true if an exception is pending.
+bool check(napi_env env, brik_ctx* ctx, int rc)
+{
+    if (rc == BRIK_OK) return false;
+    std::string msg = std::string(code_name(rc)) + ": " + (ctx ? brik_last_error(ctx) : brik_strerror(rc));
+    napi_throw_error(env, code_name(rc), msg.c_str());
+    return true;
+}
+
+struct Args {
+    napi_value v[16];
+    size_t n = 16;
+};
+
+bool get_args(napi_env env, napi_callback_info info, Args& a, size_t need)
+{
+    if (napi_get_cb_info(env, info, &a.n, a.v, nullptr, nullptr) != napi_ok) return false;
+    if (a.n < need) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "too few arguments");
+        return false;
+    }
+    return true;
+}
+
+bool get_i32(napi_env env, napi_value v, int32_t* out)
+{
+    if (napi_get_value_int32(env, v, out) != napi_ok) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a number");
+        return false;
+    }
+    return true;
+}
+
+// A device pointer: BigInt address, null/undefined (-> nullptr), or an object with a BigInt `ptr`.
+bool get_ptr(napi_env env, napi_value v, void** out)
+{
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_null || t == napi_undefined) { *out = nullptr; return true; }
+    if (t == napi_object) {
+        napi_value p;
+        if (napi_get_named_property(env, v, "ptr", &p) != napi_ok) return false;
+        v = p;
+        napi_typeof(env, v, &t);
+    }
+    if (t != napi_bigint) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a device pointer (BigInt or {ptr: BigInt})");
+        return false;
+    }
+    uint64_t u;
+    bool lossless;
+    if (napi_get_value_bigint_uint64(env, v, &u, &lossless) != napi_ok) return false;
+    *out = reinterpret_cast<void*>(static_cast<uintptr_t>(u));
+    return true;
+}
+
+bool get_ctx(napi_env env, napi_value v, brik_ctx** out)
+{
+    void* p = nullptr;
+    if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a brik context");
+        return false;
+    }
+    *out = static_cast<brik_ctx*>(p);
+    return true;
+}
+
+napi_value make_ptr(napi_env env, void* p)
+{
+    napi_value r;
+    napi_create_bigint_uint64(env, static_cast<uint64_t>(reinterpret_cast<uintptr_t>(p)), &r);
+    return r;
+}
+
+napi_value undefined(napi_env env)
+{
+    napi_value u;
+    napi_get_undefined(env, &u);
+    return u;
+}
+
+// Host bytes of a TypedArray / Buffer / ArrayBuffer / DataView.
+bool get_bytes(napi_env env, napi_value v, void** data, size_t* len)
+{
+    bool is;
+    napi_is_typedarray(env, v, &is);
+    if (is) {
+        napi_typedarray_type tt;
+        size_t n, off;
+        napi_value ab;
+        if (napi_get_typedarray_info(env, v, &tt, &n, data, &ab, &off) != napi_ok) return false;
+        size_t es = 1;
+        switch (tt) {
+        case napi_int16_array: case napi_uint16_array: es = 2; break;
+        case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+        case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+        default: es = 1;
+        }
+        *len = n * es;
+        return true;
+    }
+    napi_is_arraybuffer(env, v, &is);
+    if (is) return napi_get_arraybuffer_info(env, v, data, len) == napi_ok;
+    napi_is_dataview(env, v, &is);
+    if (is) {
+        napi_value ab;
+        size_t off;
+        return napi_get_dataview_info(env, v, len, data, &ab, &off) == napi_ok;
+    }
+    napi_throw_type_error(env, "BRIK_EINVAL", "expected a TypedArray, ArrayBuffer or DataView");
+    return false;
+}
+
+void ctx_finalize(napi_env, void* data, void*) { brik_destroy(static_cast<brik_ctx*>(data)); }
+
+// ---- context / memory ------------------------------------------------------------------------
+
+napi_value DeviceCount(napi_env env, napi_callback_info)
+{
+    int n = 0;
+    brik_device_count(&n);
+    napi_value r;
+    NAPI_CALL(env, napi_create_int32(env, n, &r));
+    return r;
+}
+
+napi_value CreateContext(napi_env env, napi_callback_info info)
+{
+    Args a;
+    int32_t dev = 0;
+    if (napi_get_cb_info(env, info, &a.n, a.v, nullptr, nullptr) != napi_ok) return nullptr;
+    if (a.n >= 1 && !get_i32(env, a.v[0], &dev)) return nullptr;
+    brik_ctx* ctx = nullptr;
+    if (check(env, nullptr, brik_create(dev, &ctx))) return nullptr;
+    napi_value ext;
+    NAPI_CALL(env, napi_create_external(env, ctx, ctx_finalize, nullptr, &ext));
+    return ext;
+}
+
+napi_value Alloc(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 2)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    int64_t bytes = 0;
+    NAPI_CALL(env, napi_get_value_int64(env, a.v[1], &bytes));
+    if (bytes < 0) { napi_throw_range_error(env, "BRIK_EINVAL", "negative size"); return nullptr; }
+    void* p = nullptr;
+    if (check(env, ctx, brik_alloc(ctx, (size_t)bytes, &p))) return nullptr;
+    return make_ptr(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 2)) return nullptr;
+    brik_ctx* ctx;
+    void* p;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_ptr(env, a.v[1], &p)) return nullptr;
+    if (check(env, ctx, brik_free(ctx, p))) return nullptr;
+    return undefined(env);
+}
+
+// h2d(ctx, dstPtr, src): copy the bytes of a TypedArray / ArrayBuffer / DataView to the device
+napi_value H2D(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    brik_ctx* ctx;
+    void* dst;
+    void* src;
+    size_t len;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_ptr(env, a.v[1], &dst) || !get_bytes(env, a.v[2], &src, &len)) return nullptr;
+    if (check(env, ctx, brik_h2d(ctx, dst, src, len))) return nullptr;
+    return undefined(env);
+}
+
+// d2h(ctx, srcPtr, bytes) -> ArrayBuffer
+napi_value D2H(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    brik_ctx* ctx;
+    void* src;
+    int64_t bytes = 0;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_ptr(env, a.v[1], &src)) return nullptr;
+    NAPI_CALL(env, napi_get_value_int64(env, a.v[2], &bytes));
+    void* data = nullptr;
+    napi_value ab;
+    NAPI_CALL(env, napi_create_arraybuffer(env, (size_t)bytes, &data, &ab));
+    if (check(env, ctx, brik_d2h(ctx, data, src, (size_t)bytes))) return nullptr;
+    return ab;
+}
+
+napi_value Sync(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    if (check(env, ctx, brik_sync(ctx))) return nullptr;
+    return undefined(env);
+}
+
+napi_value SetOption(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    brik_ctx* ctx;
+    int32_t k, v;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_i32(env, a.v[1], &k) || !get_i32(env, a.v[2], &v)) return nullptr;
+    if (check(env, ctx, brik_set_option(ctx, k, v))) return nullptr;
+    return undefined(env);
+}
+
+napi_value TimerBegin(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    if (check(env, ctx, brik_timer_begin(ctx))) return nullptr;
+    return undefined(env);
+}
+
+napi_value TimerEnd(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    float ms = 0;
+    if (check(env, ctx, brik_timer_end(ctx, &ms))) return nullptr;
+    napi_value r;
+    NAPI_CALL(env, napi_create_double(env, ms, &r));
+    return r;
+}
+
+// ---- compute --------------------------------------------------------------------------------
+
+// Parse (ctx, p0 .. p{np-1}, i0 .. i{ni-1}).
+bool parse(napi_env env, napi_callback_info info, brik_ctx** ctx, void** p, int np, int32_t* iv, int ni)
+{
+    Args a;
+    if (!get_args(env, info, a, (size_t)(1 + np + ni))) return false;
+    if (!get_ctx(env, a.v[0], ctx)) return false;
+    for (int i = 0; i < np; ++i)
+        if (!get_ptr(env, a.v[1 + i], &p[i])) return false;
+    for (int i = 0; i < ni; ++i)
+        if (!get_i32(env, a.v[1 + np + i], &iv[i])) return false;
+    return true;
+}
+
+napi_value MatmulQ8(napi_env env, napi_callback_info info)   // (ctx, x, codes, sc, y, M, K, N)
+{
+    brik_ctx* c; void* p[4]; int32_t i[3];
+    if (!parse(env, info, &c, p, 4, i, 3)) return nullptr;
+    if (check(env, c, brik_matmul_t_q8(c, (const float*)p[0], (const int8_t*)p[1], (const uint16_t*)p[2], (float*)p[3],
+                                       i[0], i[1], i[2]))) return nullptr;
+    return undefined(env);
+}
+
+napi_value MatmulQ4(napi_env env, napi_callback_info info)   // (ctx, x, nib, sc, mn, y, M, K, N)
+{
+    brik_ctx* c; void* p[5]; int32_t i[3];
+    if (!parse(env, info, &c, p, 5, i, 3)) return nullptr;
+    if (check(env, c, brik_matmul_t_q4(c, (const float*)p[0], (const uint8_t*)p[1], (const uint16_t*)p[2],
+                                       (const uint16_t*)p[3], (float*)p[4], i[0], i[1], i[2]))) return nullptr;
+    return undefined(env);
+}
+
+napi_value MatmulQ3(napi_env env, napi_callback_info info)   // (ctx, x, lo, hi, sc, mn, y, M, K, N)
+{
+    brik_ctx* c; void* p[6]; int32_t i[3];
+    if (!parse(env, info, &c, p, 6, i, 3)) return nullptr;
+    if (check(env, c, brik_matmul_t_q3(c, (const float*)p[0], (const uint32_t*)p[1], (const uint32_t*)p[2],
+                                       (const uint16_t*)p[3], (const uint16_t*)p[4], (float*)p[5], i[0], i[1], i[2])))
+        return nullptr;
+    return undefined(env);
+}
+
+napi_value MoeMatmulQ4(napi_env env, napi_callback_info info)   // (ctx, x, rowOff, nib, sc, mn, y, E, R, K, N)
+{
+    brik_ctx* c; void* p[6]; int32_t i[4];
+    if (!parse(env, info, &c, p, 6, i, 4)) return nullptr;
+    if (check(env, c, brik_moe_matmul_t_q4(c, (const float*)p[0], (const int32_t*)p[1], (const uint8_t*)p[2],
+                                           (const uint16_t*)p[3], (const uint16_t*)p[4], (float*)p[5], i[0], i[1],
+                                           i[2], i[3]))) return nullptr;
+    return undefined(env);
+}
+
+napi_value DequantQ8(napi_env env, napi_callback_info info)   // (ctx, codes, sc, out, n)
+{
+    brik_ctx* c; void* p[3]; int32_t i[1];
+    if (!parse(env, info, &c, p, 3, i, 1)) return nullptr;
+    if (check(env, c, brik_dequant_q8_f32(c, (const int8_t*)p[0], (const uint16_t*)p[1], (float*)p[2], (size_t)i[0])))
+        return nullptr;
+    return undefined(env);
+}
+
+napi_value DequantQ4(napi_env env, napi_callback_info info)   // (ctx, nib, sc, mn, out, n)
+{
+    brik_ctx* c; void* p[4]; int32_t i[1];
+    if (!parse(env, info, &c, p, 4, i, 1)) return nullptr;
+    if (check(env, c, brik_dequant_q4_f32(c, (const uint8_t*)p[0], (const uint16_t*)p[1], (const uint16_t*)p[2],
+                                          (float*)p[3], (size_t)i[0]))) return nullptr;
+    return undefined(env);
+}
+
+napi_value DequantQ3(napi_env env, napi_callback_info info)   // (ctx, lo, hi, sc, mn, out, n)
+{
+    brik_ctx* c; void* p[5]; int32_t i[1];
+    if (!parse(env, info, &c, p, 5, i, 1)) return nullptr;
+    if (check(env, c, brik_dequant_q3_f32(c, (const uint32_t*)p[0], (const uint32_t*)p[1], (const uint16_t*)p[2],
+                                          (const uint16_t*)p[3], (float*)p[4], (size_t)i[0]))) return nullptr;
+    return undefined(env);
+}
+
+// ---- grouped GEMV plans ----------------------------------------------------------------------
+
+struct PlanBox {
+    brik_ctx* ctx;
+    brik_gemv_plan* plan;
+};
+
+void plan_finalize(napi_env, void* data, void*)
+{
+    PlanBox* b = static_cast<PlanBox*>(data);
+    if (b->plan) brik_gemv_plan_destroy(b->ctx, b->plan);
+    delete b;
+}
+
+// gemvPlanCreate(ctx, fmt, [{x, p0, p1, scales, mins, y, K, N}, ...]) -> plan
+napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    brik_ctx* ctx;
+    int32_t fmt;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    uint32_t n = 0;
+    NAPI_CALL(env, napi_get_array_length(env, a.v[2], &n));
+    std::vector<brik_gemv_job> jobs(n);
+    static const char* const names[6] = {"x", "p0", "p1", "scales", "mins", "y"};
+    for (uint32_t j = 0; j < n; ++j) {
+        napi_value o, f;
+        NAPI_CALL(env, napi_get_element(env, a.v[2], j, &o));
+        void* ptrs[6];
+        for (int k = 0; k < 6; ++k) {
+            NAPI_CALL(env, napi_get_named_property(env, o, names[k], &f));
+            if (!get_ptr(env, f, &ptrs[k])) return nullptr;
+        }
+        int32_t K, N;
+        NAPI_CALL(env, napi_get_named_property(env, o, "K", &f));
+        if (!get_i32(env, f, &K)) return nullptr;
+        NAPI_CALL(env, napi_get_named_property(env, o, "N", &f));
+        if (!get_i32(env, f, &N)) return nullptr;
+        jobs[j] = brik_gemv_job{(const float*)ptrs[0], ptrs[1], ptrs[2], (const uint16_t*)ptrs[3],
+                                (const uint16_t*)ptrs[4], (float*)ptrs[5], K, N};
+    }
+    brik_gemv_plan* plan = nullptr;
+    if (check(env, ctx, brik_gemv_plan_create(ctx, fmt, jobs.data(), (int)n, &plan))) return nullptr;
+    napi_value ext;
+    NAPI_CALL(env, napi_create_external(env, new PlanBox{ctx, plan}, plan_finalize, nullptr, &ext));
+    return ext;
+}
+
+napi_value GemvPlanRun(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    void* p = nullptr;
+    if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a GEMV plan");
+        return nullptr;
+    }
+    PlanBox* b = static_cast<PlanBox*>(p);
+    if (!b->plan) { napi_throw_error(env, "BRIK_EINVAL", "plan was destroyed"); return nullptr; }
+    if (check(env, b->ctx, brik_gemv_plan_run(b->ctx, b->plan))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GemvPlanDestroy(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    void* p = nullptr;
+    if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p) return nullptr;
+    PlanBox* b = static_cast<PlanBox*>(p);
+    if (b->plan) brik_gemv_plan_destroy(b->ctx, b->plan);
+    b->plan = nullptr;
+    return undefined(env);
+}
+
+napi_value Init(napi_env env, napi_value exports)
+{
+    const napi_property_descriptor props[] = {
+        {"deviceCount", nullptr, DeviceCount, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"createContext", nullptr, CreateContext, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"alloc", nullptr, Alloc, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"free", nullptr, Free, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"h2d", nullptr, H2D, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"d2h", nullptr, D2H, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"sync", nullptr, Sync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"setOption", nullptr, SetOption, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"timerBegin", nullptr, TimerBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"timerEnd", nullptr, TimerEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"matmulQ8", nullptr, MatmulQ8, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"matmulQ4", nullptr, MatmulQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"matmulQ3", nullptr, MatmulQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"moeMatmulQ4", nullptr, MoeMatmulQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"dequantQ8", nullptr, DequantQ8, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"dequantQ4", nullptr, DequantQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"dequantQ3", nullptr, DequantQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"gemvPlanRun", nullptr, GemvPlanRun, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"gemvPlanDestroy", nullptr, GemvPlanDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+    };
+    napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
+    return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

@@ -48,9 +48,9 @@ constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loo
 constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
 constexpr long kPlanMaxSets = 4;               // row sets per grouped-plan block, at most
 
-// LDS bytes of a staged activation row (xprep.h): three int8 limbs per element, then per group an
-// f32 sum and an int32 exponent, then a flag.
-size_t gemv_lds(int K) { return (size_t)3 * K + (size_t)(K / kGroup) * 8 + 16; }
+// LDS bytes of a staged activation row (xprep.h): per group (plus one zero group) 96 limb bytes, an
+// f32 sum and an int32 exponent; then a flag.
+size_t gemv_lds(int K) { return (size_t)104 * (K / kGroup + 1) + 16; }
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
 int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }

@@ -126,20 +126,16 @@ __device__ __forceinline__ float limb_dot(const uint32_t (&b)[8], const u32x4_t 
     return __builtin_fmaf((float)hm, 256.f, (float)a[2]);
 }
 
-// acc += s * sum(x q) + m * sum(x) for one (row, group); s and m zeroed for masked-out groups.
+// acc += s * sum(x q) + m * sum(x) for one (row, group). A group past the end of the row reads the
+// zero group of the staged x, so both terms vanish without a select.
 template <int FMT>
-__device__ __forceinline__ float use_grp(const Grp<FMT>& d, const u32x4_t (&xl)[3][2], float2 xse, bool valid,
-                                         float acc)
+__device__ __forceinline__ float use_grp(const Grp<FMT>& d, const u32x4_t (&xl)[3][2], float2 xse, float acc)
 {
     uint32_t b[8];
     unpack<FMT>(d, b);
-    const float p = limb_dot(b, xl);
-    const float s = valid ? f16_bits_to_f32(d.s) : 0.f;
-    acc += ldexpf(s * p, __builtin_bit_cast(int, xse.y));
-    if constexpr (FMT != FMT_Q8) {
-        const float m = valid ? f16_bits_to_f32(d.m) : 0.f;
-        acc = __builtin_fmaf(m, xse.x, acc);
-    }
+    const float p = ldexpf(limb_dot(b, xl), __builtin_bit_cast(int, xse.y));   // exact rescale
+    acc = __builtin_fmaf(f16_bits_to_f32(d.s), p, acc);
+    if constexpr (FMT != FMT_Q8) acc = __builtin_fmaf(f16_bits_to_f32(d.m), xse.x, acc);
     return acc;
 }
 
@@ -192,7 +188,11 @@ struct Work {
 
     __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
 
-    // Loads of step (p, b), branch-free, every address clamped in bounds.
+    // Loads of step (p, b), branch-free. Rows past r1 are clamped to r1 - 1 (their results are never
+    // written). EVEN (G a multiple of U * TEAM): every group of every step exists, so the step's group
+    // offset goes in the uniform soffset. Otherwise each lane's group index is clamped to G - 1 (the
+    // consumer reads the zero group for those).
+    template <bool EVEN>
     __device__ __forceinline__ void issue(Grp<FMT> (&d)[U][R], int p, int b) const
     {
         const int n = n0(p);
@@ -201,8 +201,12 @@ struct Work {
             const uint32_t row = (uint32_t)min(n + r, r1 - 1) * (uint32_t)G;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
-                load_grp<FMT>(d[u][r], rs, row + g, 0u, 0u);
+                if constexpr (EVEN) {
+                    load_grp<FMT>(d[u][r], rs, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
+                } else {
+                    const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
+                    load_grp<FMT>(d[u][r], rs, row + g, 0u, 0u);
+                }
             }
         }
     }
@@ -215,20 +219,19 @@ struct Work {
         for (int r = 0; r < R; ++r) acc[r] = b == 0 ? 0.f : acc[r];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int g = lane + TEAM * (U * b + u);
-            const int gl = min(g, G - 1);
-            const bool valid = g < G;
-            u32x4_t xl[3][2];
+            const int gl = min(lane + TEAM * (U * b + u), G);      // G: the zero group
             const int hs = brik::half_swap(gl);
+            const int8_t* b0 = S.limbs + 96 * gl + hs;              // half 0 of limb t at b0 + 32t
+            const int8_t* b1 = S.limbs + 96 * gl + (16 - hs);       // half 1 of limb t at b1 + 32t
+            u32x4_t xl[3][2];
 #pragma unroll
             for (int t = 0; t < 3; ++t) {
-                const int8_t* base = S.limbs + (size_t)t * 32 * G + 32 * gl;
-                xl[t][0] = *(const u32x4_t*)(base + hs);
-                xl[t][1] = *(const u32x4_t*)(base + (16 ^ hs));
+                xl[t][0] = *(const u32x4_t*)(b0 + 32 * t);
+                xl[t][1] = *(const u32x4_t*)(b1 + 32 * t);
             }
             const float2 xse = S.xse[gl];
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = use_grp<FMT>(d[u][r], xl, xse, valid, acc[r]);
+            for (int r = 0; r < R; ++r) acc[r] = use_grp<FMT>(d[u][r], xl, xse, acc[r]);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) part[(p * RPI + team * R + r) * TEAM + lane] = acc[r];
@@ -253,6 +256,56 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
     }
 }
 
+// The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
+// loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
+template <int FMT, int TEAM, int R, int U, int D, bool EVEN>
+__device__ __forceinline__ void pipeline(Work<FMT, TEAM, R, U>& w, const XStage& X, const float* __restrict__ x,
+                                         const Planes& P, float* __restrict__ yrow, int K, int S)
+{
+    Grp<FMT> d[D][U][R];
+    int ip = 0, bp = 0;                      // (p, b) of the next step to issue
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) {
+        w.template issue<EVEN>(d[k], ip, bp);
+        const bool wrap = bp + 1 == w.B;
+        bp = wrap ? 0 : bp + 1;
+        ip += wrap;
+    }
+    brik::xstage<FMT>(x, X, K);
+    if (*X.flag) {
+        gemv_rows_exact<FMT, TEAM, R>(x, P, yrow, K, w.r0, w.r1, w.rstep);
+        return;
+    }
+    float acc[R] = {};
+    int pc = 0, bc = 0;                      // (p, b) of the next step to consume
+    int i = 0;
+    for (; i + D <= S; i += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            w.template issue<EVEN>(d[(k + D - 1) % D], ip, bp);
+            {
+                const bool wrap = bp + 1 == w.B;
+                bp = wrap ? 0 : bp + 1;
+                ip += wrap;
+            }
+            w.consume(d[k], X, pc, bc, acc);
+            const bool wrap = bc + 1 == w.B;
+            bc = wrap ? 0 : bc + 1;
+            pc += wrap;
+        }
+    }
+    // the remaining S - i < D steps are already issued
+#pragma unroll
+    for (int k = 0; k < D - 1; ++k) {
+        if (i + k < S) {
+            w.consume(d[k], X, pc, bc, acc);
+            const bool wrap = bc + 1 == w.B;
+            bc = wrap ? 0 : bc + 1;
+            pc += wrap;
+        }
+    }
+}
+
 // Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
 // then the cross-lane sums of the LDS partials are written to y. The block owns row sets
 // p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
@@ -270,52 +323,11 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const P
     w.B = (w.G + U * TEAM - 1) / (U * TEAM);
     const int nsets = r0 < r1 ? (r1 - r0 + rstep - 1) / rstep : 0;     // block-uniform
     const int S = nsets * w.B;                                            // steps per team
-    Grp<FMT> d[D][U][R];
-    // prologue: steps 0 .. D-2 in flight before x is staged
-    int ip = 0, bp = 0;                      // (p, b) of the next step to issue
-#pragma unroll
-    for (int k = 0; k < D - 1; ++k) {
-        w.issue(d[k], ip, bp);
-        const bool wrap = bp + 1 == w.B;
-        bp = wrap ? 0 : bp + 1;
-        ip += wrap;
-    }
     const XStage X = brik::xstage_layout(lds, K);
     w.part = (float*)(lds + brik::xstage_bytes(K));
-    brik::xstage<FMT>(x, X, K);
-    if (*X.flag) {
-        gemv_rows_exact<FMT, TEAM, R>(x, P, yrow, K, r0, r1, rstep);
-        return;
-    }
-    float acc[R] = {};
-    int pc = 0, bc = 0;                      // (p, b) of the next step to consume
-    int i = 0;
-    // main loop, unrolled by D so every buffer index is static; straight-line body
-    for (; i + D <= S; i += D) {
-#pragma unroll
-        for (int k = 0; k < D; ++k) {
-            w.issue(d[(k + D - 1) % D], ip, bp);
-            {
-                const bool wrap = bp + 1 == w.B;
-                bp = wrap ? 0 : bp + 1;
-                ip += wrap;
-            }
-            w.consume(d[k], X, pc, bc, acc);
-            const bool wrap = bc + 1 == w.B;
-            bc = wrap ? 0 : bc + 1;
-            pc += wrap;
-        }
-    }
-    // remaining S - i < D steps are already issued
-#pragma unroll
-    for (int k = 0; k < D - 1; ++k) {
-        if (i + k < S) {
-            w.consume(d[k], X, pc, bc, acc);
-            const bool wrap = bc + 1 == w.B;
-            bc = wrap ? 0 : bc + 1;
-            pc += wrap;
-        }
-    }
+    if (w.G % (U * TEAM) == 0) pipeline<FMT, TEAM, R, U, D, true>(w, X, x, P, yrow, K, S);
+    else pipeline<FMT, TEAM, R, U, D, false>(w, X, x, P, yrow, K, S);
+    if (*X.flag) return;
     __syncthreads();
     // cross-lane sums: one thread per row, TEAM partials each (rows past r1 are skipped)
     for (int q = threadIdx.x; q < nsets * W::RPI; q += blockDim.x) {

@@ -7,12 +7,13 @@
 // per instruction, exact int32 sums), and the group's result is rescaled by 2^(e_g - 22) in f32.
 // Relative to the group's largest element this keeps 22 bits, about f32's 24-bit significand.
 //
-// LDS layout for K = 32 * G:
-//   limbs: limb t (0 = h, 1 = m, 2 = l) of group g occupies bytes [t*32G + 32g, +32), the 32 bytes in
-//          the byte order the format's code unpacking produces (code_pos), with the two 16-byte
-//          halves swapped when bit 3 of g is set (so the lanes reading groups g and g + 8 in the same
-//          instruction hit different banks);
-//   xse[g]: {f32 sum of the group's x, int32 e_g - 22};
+// LDS layout for K = 32 * G, group-major so a group's limbs are reached with immediate offsets:
+//   limbs: group g (0 <= g <= G) occupies bytes [96g, 96g + 96): limb t (0 = h, 1 = m, 2 = l) at
+//          96g + 32t, its 32 bytes in the byte order the format's code unpacking produces (code_pos),
+//          the two 16-byte halves swapped when bit 3 of g is set (so lanes reading groups g and g + 8
+//          in one instruction hit different banks). Group G is all zeros: consumers point groups past
+//          the end of a row at it, which zeroes their contribution without a select;
+//   xse[g]: {f32 sum of the group's x, int32 e_g - 22}, g <= G, xse[G] = {0, 0};
 //   flag:  int32, nonzero if the row holds a non-finite value (the exact f32 path then runs).
 #pragma once
 #include "common.h"
@@ -42,10 +43,10 @@ struct XStage {
     int G;
 };
 
-// Bytes of the staged row; the block's result buffer follows at this offset (16-byte aligned).
+// Bytes of the staged row; the block's partial-sum buffer follows at this offset (4-byte aligned).
 __host__ __device__ __forceinline__ size_t xstage_bytes(int K)
 {
-    return (size_t)3 * K + (size_t)(K / BRIK_GROUP) * 8 + 16;
+    return (size_t)104 * (K / BRIK_GROUP + 1) + 16;
 }
 
 __device__ __forceinline__ XStage xstage_layout(void* lds, int K)
@@ -53,8 +54,8 @@ __device__ __forceinline__ XStage xstage_layout(void* lds, int K)
     XStage s;
     s.G = K / BRIK_GROUP;
     s.limbs = (int8_t*)lds;
-    s.xse = (float2*)((char*)lds + 3 * (size_t)K);
-    s.flag = (int*)(s.xse + s.G);
+    s.xse = (float2*)((char*)lds + (size_t)96 * (s.G + 1));
+    s.flag = (int*)(s.xse + s.G + 1);
     return s;
 }
 
@@ -71,10 +72,14 @@ __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h
 template <int FMT>
 __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K)
 {
-    if (threadIdx.x == 0) *S.flag = 0;
+    const int G = S.G;
+    if (threadIdx.x == 0) {
+        *S.flag = 0;
+        S.xse[G] = float2{0.f, 0.f};
+    }
+    if (threadIdx.x < 24) ((uint32_t*)(S.limbs + 96 * G))[threadIdx.x] = 0u;   // the zero group
     __syncthreads();
     const int nq = K >> 2;
-    const int G = S.G;
     // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
     // every loop trip is entered by whole 8-lane groups, so the DPP group reductions see full groups
     for (int i = threadIdx.x; i < nq; i += blockDim.x) {
@@ -91,7 +96,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
         int hh[4], mm[4], ll[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) split_limbs(v[t], sh, finite, hh[t], mm[t], ll[t]);
-        int8_t* base = S.limbs + 32 * g;
+        int8_t* base = S.limbs + 96 * g;
         const int hs = half_swap(g);
         if constexpr (FMT == FMT_Q8) {
             // elements 4c..4c+3 are byte dword c of every limb
@@ -101,8 +106,8 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
                        ((uint32_t)(b[3] & 0xff) << 24);
             };
             *(uint32_t*)(base + pos) = pack(hh);
-            *(uint32_t*)(base + 32 * G + pos) = pack(mm);
-            *(uint32_t*)(base + 64 * G + pos) = pack(ll);
+            *(uint32_t*)(base + 32 + pos) = pack(mm);
+            *(uint32_t*)(base + 64 + pos) = pack(ll);
         } else if constexpr (FMT == FMT_Q4) {
             // elements 4c..4c+3 give bytes (c&1)*2 and +1 of byte dwords 2j (even elements) and
             // 2j+1 (odd elements), j = c/2: two 16-bit stores per limb
@@ -113,15 +118,15 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
                 *(uint16_t*)(lb + po) = (uint16_t)((b[1] & 0xff) | ((b[3] & 0xff) << 8));
             };
             st(base, hh);
-            st(base + 32 * G, mm);
-            st(base + 64 * G, ll);
+            st(base + 32, mm);
+            st(base + 64, ll);
         } else {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int pos = code_pos<FMT>(4 * c + t) ^ hs;
                 base[pos] = (int8_t)hh[t];
-                base[32 * G + pos] = (int8_t)mm[t];
-                base[64 * G + pos] = (int8_t)ll[t];
+                base[32 + pos] = (int8_t)mm[t];
+                base[64 + pos] = (int8_t)ll[t];
             }
         }
     }

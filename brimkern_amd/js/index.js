@@ -1,0 +1,192 @@
+'use strict';
+// JavaScript host of the MI355X quantized matmul library: a drop-in for the quantized-matmul surface
+// of the reference's WebGpuEngine (src/lib/webgpu/kernels.ts), over the N-API addon brik.node and
+// through it the C ABI of include/brik.h. Node 12 compatible CommonJS (no ?. / ??).
+//
+//   reference (kernels.ts)                          here
+//   uploadGpuRaw(bytes)                 :1032-1042  engine.uploadGpuRaw(bytes) -> DeviceBuffer
+//   matmulQ4(a, nib, sc, mn, m, k, n)   :1046-1053  engine.matmulQ4(...)  -> Promise<Float32Array>
+//   matmulQ4Tiled / matmulQ4Shared      :1055-1075  aliases of matmulQ4 (one entry picks the kernel by m)
+//   matmulQ3(a, lo, hi, sc, mn, m, k, n):1080-1087  engine.matmulQ3(...)
+//   matmulQ8(a, codes, sc, m, k, n)     :1140-1147  engine.matmulQ8(...), matmulQ8Tiled / Shared aliases
+//   recMM(enc, trash, a, w, m, k, n)    :1562-1567  engine.mm(a, w, m, k, n[, out]) (device resident,
+//                                                    dispatch on the handle's shape: q3 / nib / codes)
+//   dequantGpuQ4/Q3/Q8 Q4W/Q3W/Q8W path  model.ts:214-270  engine.weightFromBlob(fmt, blob, nElems)
+//   destroyWeight(b)                     model.ts:274-280  engine.destroyWeight(w)
+//
+// Plane arguments may be DeviceBuffers, plane views ({ptr: BigInt}) or BigInt addresses. Errors
+// (bad shapes, K % 32 != 0, misalignment, no device) throw an Error whose .code is "BRIK_E...";
+// the reference validated nothing and let WebGPU fail silently.
+
+const path = require('path');
+const planes = require('./planes');
+
+let native = null;
+function loadNative() {
+  if (native === null) native = require(path.join(__dirname, 'brik.node'));   // throws if not built
+  return native;
+}
+
+const FMT = { q8: 8, q4: 4, q3: 3 };
+const OPT_PATH = 1;
+const OPT_GEMV_VARIANT = 2;
+
+class DeviceBuffer {
+  constructor(engine, ptr, size) {
+    this.engine = engine;
+    this.ptr = ptr;       // BigInt device address
+    this.size = size;     // bytes
+  }
+  // A plane view `offset` bytes into the buffer.
+  view(offset) { return { ptr: this.ptr + BigInt(offset), buffer: this }; }
+  destroy() {
+    if (this.ptr !== null) {
+      this.engine.native.free(this.engine.ctx, this.ptr);
+      this.ptr = null;
+    }
+  }
+}
+
+function toBytes(data) {
+  if (data instanceof Uint8Array) return data;
+  if (ArrayBuffer.isView(data)) return new Uint8Array(data.buffer, data.byteOffset, data.byteLength);
+  if (data instanceof ArrayBuffer) return new Uint8Array(data);
+  throw new TypeError('expected bytes (TypedArray / ArrayBuffer)');
+}
+
+class Engine {
+  constructor(device) {
+    this.native = loadNative();
+    this.ctx = this.native.createContext(device === undefined ? 0 : device);
+  }
+
+  static deviceCount() { return loadNative().deviceCount(); }
+
+  // ---- memory ---------------------------------------------------------------------------------
+  alloc(bytes) { return new DeviceBuffer(this, this.native.alloc(this.ctx, Math.max(bytes, 1)), bytes); }
+
+  // Persistent device copy of raw bytes, padded to a 4-byte multiple (kernels.ts:1032-1042).
+  uploadGpuRaw(bytes) {
+    const b = toBytes(bytes);
+    const size = Math.ceil(b.byteLength / 4) * 4;
+    const buf = this.alloc(size);
+    if (b.byteLength) this.native.h2d(this.ctx, buf.ptr, b);
+    if (size !== b.byteLength) {
+      const tail = new Uint8Array(size - b.byteLength);
+      this.native.h2d(this.ctx, buf.ptr + BigInt(b.byteLength), tail);
+    }
+    return buf;
+  }
+
+  uploadGpu(f32) { return this.uploadGpuRaw(f32); }
+
+  readBack(buf, bytes) {
+    const ptr = typeof buf === 'bigint' ? buf : buf.ptr;
+    return new Float32Array(this.native.d2h(this.ctx, ptr, bytes));
+  }
+
+  // A quantized weight handle from one packed .brik blob: one upload, planes addressed in place.
+  // Shapes as model.ts:214-270 builds them: {nib, sc, mn} | {codes, sc} | {q3: true, lo, hi, sc, mn}.
+  weightFromBlob(fmt, blob, nElems) {
+    const offs = planes.planeOffsets(fmt, nElems);
+    const b = toBytes(blob);
+    const len = planes.byteLength(fmt, nElems);
+    if (b.byteLength < len) throw new Error(fmt + ' blob of ' + b.byteLength + ' bytes is shorter than ' + len);
+    const buf = this.uploadGpuRaw(b.subarray(0, len));
+    const h = { _buf: buf };
+    Object.keys(offs).forEach(function (k) { h[k] = buf.view(offs[k][0]); });
+    if (fmt === 'q3') h.q3 = true;
+    return h;
+  }
+
+  destroyWeight(w) {
+    if (!w) return;
+    if (w._buf) { w._buf.destroy(); return; }
+    ['nib', 'codes', 'lo', 'hi', 'sc', 'mn'].forEach(function (k) {
+      if (w[k] && typeof w[k].destroy === 'function') w[k].destroy();
+    });
+  }
+
+  // ---- readback ops (reference signatures) -----------------------------------------------------
+  _readback(fn, a, planeArgs, m, k, n) {
+    const x = a instanceof Float32Array ? a : Float32Array.from(a);
+    if (x.length !== m * k) {
+      const e = new Error('BRIK_EINVAL: activation has ' + x.length + ' floats, expected m*k = ' + m * k);
+      e.code = 'BRIK_EINVAL';
+      throw e;
+    }
+    const xb = this.alloc(x.byteLength);
+    const yb = this.alloc(m * n * 4);
+    try {
+      if (x.byteLength) this.native.h2d(this.ctx, xb.ptr, x);
+      fn.apply(this.native, [this.ctx, xb.ptr].concat(planeArgs, [yb.ptr, m, k, n]));
+      return this.readBack(yb, m * n * 4);
+    } finally {
+      xb.destroy();
+      yb.destroy();
+    }
+  }
+
+  matmulQ4(a, nib, sc, mn, m, k, n) {
+    return Promise.resolve(this._readback(this.native.matmulQ4, a, [nib, sc, mn], m, k, n));
+  }
+  matmulQ4Tiled(a, nib, sc, mn, m, k, n) { return this.matmulQ4(a, nib, sc, mn, m, k, n); }
+  matmulQ4Shared(a, nib, sc, mn, m, k, n) { return this.matmulQ4(a, nib, sc, mn, m, k, n); }
+
+  matmulQ8(a, codes, sc, m, k, n) {
+    return Promise.resolve(this._readback(this.native.matmulQ8, a, [codes, sc], m, k, n));
+  }
+  matmulQ8Tiled(a, codes, sc, m, k, n) { return this.matmulQ8(a, codes, sc, m, k, n); }
+  matmulQ8Shared(a, codes, sc, m, k, n) { return this.matmulQ8(a, codes, sc, m, k, n); }
+
+  matmulQ3(a, lo, hi, sc, mn, m, k, n) {
+    return Promise.resolve(this._readback(this.native.matmulQ3, a, [lo, hi, sc, mn], m, k, n));
+  }
+
+  // ---- recorded (device-resident) form: recMM ---------------------------------------------------
+  mm(a, w, m, k, n, out) {
+    const y = out || this.alloc(m * n * 4);
+    if (w && w.q3) this.native.matmulQ3(this.ctx, a, w.lo, w.hi, w.sc, w.mn, y, m, k, n);
+    else if (w && w.nib) this.native.matmulQ4(this.ctx, a, w.nib, w.sc, w.mn, y, m, k, n);
+    else if (w && w.codes) this.native.matmulQ8(this.ctx, a, w.codes, w.sc, y, m, k, n);
+    else {
+      const e = new Error('BRIK_EINVAL: mm: weight handle is not a q3/q4/q8 handle');
+      e.code = 'BRIK_EINVAL';
+      throw e;
+    }
+    return y;
+  }
+
+  // Expert-grouped q4 matmul over a stacked [E, N, K] q4 weight (no reference counterpart).
+  moeMatmulQ4(xSorted, rowOff, w, ySorted, E, R, K, N) {
+    this.native.moeMatmulQ4(this.ctx, xSorted, rowOff, w.nib, w.sc, w.mn, ySorted, E, R, K, N);
+    return ySorted;
+  }
+
+  // Grouped decode GEMV plan: jobs [{x, w, y, K, N}] (one format), executed by one launch per run().
+  gemvPlan(fmt, jobs) {
+    const nat = this.native;
+    const specs = jobs.map(function (j) {
+      const w = j.w;
+      return { x: j.x, p0: w.nib || w.codes || w.lo, p1: w.hi || null, scales: w.sc, mins: w.mn || null,
+        y: j.y, K: j.K, N: j.N };
+    });
+    const plan = nat.gemvPlanCreate(this.ctx, FMT[fmt], specs);
+    return { run: function () { nat.gemvPlanRun(plan); }, destroy: function () { nat.gemvPlanDestroy(plan); } };
+  }
+
+  dequant(fmt, w, out, nElems) {
+    if (fmt === 'q8') this.native.dequantQ8(this.ctx, w.codes, w.sc, out, nElems);
+    else if (fmt === 'q4') this.native.dequantQ4(this.ctx, w.nib, w.sc, w.mn, out, nElems);
+    else this.native.dequantQ3(this.ctx, w.lo, w.hi, w.sc, w.mn, out, nElems);
+    return out;
+  }
+
+  setOption(key, value) { this.native.setOption(this.ctx, key, value); }
+  sync() { this.native.sync(this.ctx); }
+  timerBegin() { this.native.timerBegin(this.ctx); }
+  timerEnd() { return this.native.timerEnd(this.ctx); }
+}
+
+module.exports = { Engine: Engine, DeviceBuffer: DeviceBuffer, planes: planes, FMT: FMT,
+  OPT_PATH: OPT_PATH, OPT_GEMV_VARIANT: OPT_GEMV_VARIANT, loadNative: loadNative };

@@ -1,0 +1,131 @@
+'use strict';
+// GPU parity of the JavaScript host (brimkern_amd/js over the N-API addon) against the golden fixtures
+// and against the JavaScript restatement of the reference CPU matmul (oracle/cpuref.js) on seeded
+// inputs. Prints one JSON line; exit code 0 iff every check passed. Run by tests/test_js_host.py.
+const fs = require('fs');
+const path = require('path');
+const root = path.join(__dirname, '..', '..');
+const brik = require(path.join(root, 'brimkern_amd', 'js'));
+const cpuref = require(path.join(root, 'oracle', 'cpuref.js'));
+
+const results = [];
+function check(name, ok, detail) {
+  results.push({ name: name, ok: !!ok, detail: detail });
+  if (!ok) console.error('FAIL ' + name + ' ' + JSON.stringify(detail));
+}
+
+function normwise(y, r) {
+  let num = 0, den = 0;
+  for (let i = 0; i < r.length; i++) {
+    num = Math.max(num, Math.abs(y[i] - r[i]));
+    den = Math.max(den, Math.abs(r[i]));
+  }
+  return den === 0 ? num : num / den;
+}
+
+// mulberry32: a small seeded generator for the JS-side inputs.
+function rng(seed) {
+  let a = seed >>> 0;
+  return function () {
+    a = (a + 0x6D2B79F5) >>> 0;
+    let t = a;
+    t = Math.imul(t ^ (t >>> 15), t | 1);
+    t ^= t + Math.imul(t ^ (t >>> 7), t | 61);
+    return ((t ^ (t >>> 14)) >>> 0) / 4294967296;
+  };
+}
+
+function f16bits(v) {   // f32 -> f16 for normal-range positive/negative scales (test data only)
+  const f = new Float32Array([v]);
+  const x = new Uint32Array(f.buffer)[0];
+  const sign = (x >>> 16) & 0x8000;
+  let exp = ((x >>> 23) & 0xff) - 127 + 15;
+  let mant = x & 0x7fffff;
+  let r = (mant >>> 13) + ((mant >>> 12) & 1);
+  if (r === 0x400) { r = 0; exp += 1; }
+  return sign | (exp << 10) | (r & 0x3ff);
+}
+
+async function main() {
+  const meta = JSON.parse(fs.readFileSync(path.join(root, 'tests', 'golden', 'golden.json')));
+  const raw = fs.readFileSync(path.join(root, 'tests', 'golden', 'golden.bin'));
+  const bytes = function (span) { return new Uint8Array(raw.buffer, raw.byteOffset + span[0], span[1]); };
+  const f32 = function (span) { return new Float32Array(bytes(span).slice().buffer); };
+  const engine = new brik.Engine(0);
+
+  // 1. golden fixtures through the reference-shaped readback ops + dequant bit-exactness
+  for (const c of meta.cases) {
+    const n = c.N * c.K;
+    const w = engine.weightFromBlob(c.fmt, bytes(c.blob), n);
+    const x = f32(c.x);
+    let y;
+    if (c.fmt === 'q4') y = await engine.matmulQ4(x, w.nib, w.sc, w.mn, c.M, c.K, c.N);
+    else if (c.fmt === 'q8') y = await engine.matmulQ8(x, w.codes, w.sc, c.M, c.K, c.N);
+    else y = await engine.matmulQ3(x, w.lo, w.hi, w.sc, w.mn, c.M, c.K, c.N);
+    const rel = normwise(y, f32(c.y));
+    check('golden ' + c.name, rel <= (c.M === 1 ? 1e-5 : 1e-3), { rel: rel });
+    const out = engine.alloc(n * 4);
+    engine.dequant(c.fmt, w, out.ptr, n);
+    const deq = new Uint32Array(engine.readBack(out, n * 4).buffer);
+    const ref = new Uint32Array(f32(c.deq).buffer);
+    let same = deq.length === ref.length;
+    for (let i = 0; same && i < ref.length; i++) same = deq[i] === ref[i];
+    check('dequant ' + c.name, same, {});
+    out.destroy();
+    engine.destroyWeight(w);
+  }
+
+  // 2. seeded q4 at a Qwen3-4B shape, GPU vs the JS CPU reference (oracle/cpuref.js)
+  {
+    const K = 2560, N = 1024, n = N * K;
+    const r = rng(12345);
+    const blob = new Uint8Array(brik.planes.byteLength('q4', n));
+    for (let i = 0; i < n / 2; i++) blob[i] = (r() * 256) | 0;
+    const dv = new DataView(blob.buffer);
+    for (let g = 0; g < n / 32; g++) {
+      const s = 0.005 + 0.015 * r();
+      dv.setUint16(n / 2 + 2 * g, f16bits(s), true);
+      dv.setUint16(n / 2 + n / 16 + 2 * g, f16bits(-7.5 * s), true);
+    }
+    const x = new Float32Array(K);
+    for (let i = 0; i < K; i++) x[i] = 2 * r() - 1;
+    const w = engine.weightFromBlob('q4', blob, n);
+    const y = await engine.matmulQ4(x, w.nib, w.sc, w.mn, 1, K, N);
+    const t0 = process.hrtime();
+    const ref = cpuref.cpuMatmul('q4', x, blob, 1, K, N);
+    const dt = process.hrtime(t0);
+    check('q4 K2560 N1024 vs JS CPU reference', normwise(y, ref) <= 1e-5, { rel: normwise(y, ref), cpu_ms: dt[0] * 1e3 + dt[1] / 1e6 });
+
+    // 3. recMM form: device-resident activation and output, dispatch on the handle shape
+    const xb = engine.uploadGpu(x);
+    const yb = engine.mm(xb.view(0), w, 1, K, N);
+    check('mm (recMM) q4', normwise(engine.readBack(yb, N * 4), ref) <= 1e-5, {});
+
+    // 4. grouped plan of two jobs sharing x
+    const y2 = engine.alloc(N * 4), y3 = engine.alloc(N * 4);
+    const plan = engine.gemvPlan('q4', [{ x: xb, w: w, y: y2, K: K, N: N }, { x: xb, w: w, y: y3, K: K, N: N }]);
+    plan.run();
+    check('gemv plan q4', normwise(engine.readBack(y2, N * 4), ref) <= 1e-5 &&
+      normwise(engine.readBack(y3, N * 4), ref) <= 1e-5, {});
+    plan.destroy();
+
+    // 5. errors surface as exceptions with BRIK_* codes
+    let code = null;
+    try { await engine.matmulQ4(x.subarray(0, 48), w.nib, w.sc, w.mn, 1, 48, N); } catch (e) { code = e.code; }
+    check('K % 32 != 0 throws BRIK_EINVAL', code === 'BRIK_EINVAL', { code: code });
+    code = null;
+    try { engine.mm(xb.view(4), w, 1, K, N, y2); } catch (e) { code = e.code; }
+    check('misaligned activation throws BRIK_EALIGN', code === 'BRIK_EALIGN', { code: code });
+    code = null;
+    try { engine.mm(xb, {}, 1, K, N, y2); } catch (e) { code = e.code; }
+    check('non-quantized handle throws BRIK_EINVAL', code === 'BRIK_EINVAL', { code: code });
+    [xb, yb, y2, y3].forEach(function (b) { b.destroy(); });
+    engine.destroyWeight(w);
+  }
+
+  const failed = results.filter(function (r) { return !r.ok; }).length;
+  process.stdout.write(JSON.stringify({ checks: results.length, failed: failed }) + '\n');
+  process.exit(failed === 0 ? 0 : 1);
+}
+
+main().catch(function (e) { console.error(e && e.stack ? e.stack : e); process.exit(2); });
