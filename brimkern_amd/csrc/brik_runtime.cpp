@@ -23,13 +23,13 @@ namespace {
 
 enum Kern {
     K_DEQ_Q8, K_DEQ_Q4, K_DEQ_Q3,
-    K_GEMM_Q4, K_GEMM_Q8, K_GEMM_Q3,
+    K_XPREP,
     K_COUNT
 };
 
 const char* const kKernelNames[K_COUNT] = {
     "brik_dequant_q8", "brik_dequant_q4", "brik_dequant_q3",
-    "brik_gemm_q4", "brik_gemm_q8", "brik_gemm_q3",
+    "brik_xprep_f16",
 };
 
 // GEMV variants (lanes per row team, rows per team, groups per pipeline step), in the order of
@@ -42,7 +42,14 @@ constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 
 constexpr int kGroup = 32;
-constexpr int kGemmTile = 64;                  // BM = BN of brik_gemm_*
+// GEMM block tiles (BM rows x 64 TN columns), in the order of BRIK_GEMM_FMT in gemm.hip:
+// brik_gemm_<fmt>_<BM>x<TN>.
+struct GemmTile { int bm, tn; };
+constexpr GemmTile kGemmTiles[] = {{128, 3}, {128, 2}, {128, 4}, {64, 3}, {64, 2}, {64, 4}, {32, 3}, {32, 2}, {32, 4}};
+constexpr int kNumGemmTiles = sizeof(kGemmTiles) / sizeof(kGemmTiles[0]);
+constexpr unsigned kCUs = 256;                 // MI355X compute units
+constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
+constexpr unsigned kGemmThreads = 256;         // threads per GEMM block (__launch_bounds__ of brik_gemm_*)
 constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
 constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loop over row sets
 constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
@@ -71,10 +78,14 @@ struct brik_ctx {
     hipFunction_t fn[K_COUNT] = {};
     hipFunction_t gemv[3][kNumGemvVariants] = {};
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
+    hipFunction_t gemm[3][kNumGemmTiles] = {};
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     int opt_path = 0;
     int opt_variant = 0;   // 0 auto, else 1 + index into kGemvVariants
+    int opt_tile = 0;      // 0 auto, else 1 + index into kGemmTiles
+    void* ws = nullptr;    // GEMM workspace: f16 activation rows, then per-row scales (grow-only)
+    size_t ws_bytes = 0;
     char err[512] = {0};
 };
 
@@ -97,6 +108,12 @@ int fail(brik_ctx* c, int code, const char* fmt, ...)
         if (e_ != hipSuccess)                                                                 \
             return fail((ctx), e_ == hipErrorOutOfMemory ? BRIK_ENOMEM : BRIK_EHIP, "%s: %s", \
                         #call, hipGetErrorString(e_));                                        \
+    } while (0)
+
+#define HIP_TRY_RC(call)          \
+    do {                          \
+        const int r_ = (call);    \
+        if (r_ != BRIK_OK) return r_; \
     } while (0)
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -139,6 +156,88 @@ int check_mm(brik_ctx* c, const char* who, const float* x, const void* p0, const
     return BRIK_OK;
 }
 
+unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
+
+// GEMM block tile (index into kGemmTiles). Dense (E == 0): the tile with the smallest modelled
+// makespan, rounds x tile area x a small-tile penalty, where rounds = ceil(blocks / CUs) (every block
+// of a round runs on its own compute unit). Expert-grouped: the row tile from the mean rows per
+// expert, 128 columns.
+int gemm_tile(brik_ctx* c, long M, long N, int E)
+{
+    if (c->opt_tile > 0) return c->opt_tile - 1;
+    if (E > 0) {
+        const long per = (M + E - 1) / E;
+        const int bm = per > 64 ? 128 : per > 32 ? 64 : 32;
+        for (int t = 0; t < kNumGemmTiles; ++t)
+            if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == 2) return t;
+    }
+    int best = 0;
+    double best_cost = 0;
+    for (int t = 0; t < kNumGemmTiles; ++t) {
+        const GemmTile& g = kGemmTiles[t];
+        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, 64 * g.tn);
+        const double rounds = std::ceil(blocks / kCUs);
+        const double penalty = g.bm == 128 ? 1.0 : g.bm == 64 ? 1.3 : 1.8;
+        const double cost = rounds * g.bm * 64.0 * g.tn * penalty;
+        if (t == 0 || cost < best_cost) {
+            best = t;
+            best_cost = cost;
+        }
+    }
+    return best;
+}
+
+// Grow the context workspace to at least `bytes`. Earlier launches on the context stream may still
+// read the old buffer, so the stream is drained before it is freed.
+int ensure_ws(brik_ctx* c, size_t bytes)
+{
+    if (c->ws_bytes >= bytes) return BRIK_OK;
+    if (c->ws) {
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        HIP_TRY(c, hipFree(c->ws));
+        c->ws = nullptr;
+        c->ws_bytes = 0;
+    }
+    bytes = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    HIP_TRY(c, hipMalloc(&c->ws, bytes));
+    c->ws_bytes = bytes;
+    return BRIK_OK;
+}
+
+// MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
+// tile kernel; dense when row_off is null, expert-grouped otherwise.
+int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
+         float* y, int rows, int K, int N, const int* row_off, int E)
+{
+    if (K == 0) {   // empty sums
+        HIP_TRY(c, hipSetDevice(c->device));
+        HIP_TRY(c, hipMemsetAsync(y, 0, (size_t)rows * N * sizeof(float), c->stream));
+        return BRIK_OK;
+    }
+    const long Kp = (K + kGemmKPad - 1) / kGemmKPad * kGemmKPad;
+    const size_t xbytes = (size_t)rows * Kp * 2;
+    if (xbytes >= (1ull << 31))
+        return fail(c, BRIK_EINVAL, "matmul: %d rows x K=%d exceed the 2 GiB staged-activation limit", rows, K);
+    HIP_TRY_RC(ensure_ws(c, xbytes + 4 * (size_t)rows));
+    uint16_t* xh = static_cast<uint16_t*>(c->ws);
+    float* rscale = reinterpret_cast<float*>(static_cast<char*>(c->ws) + xbytes);
+    int Mi = rows, Ki = K, Ni = N, Kpi = (int)Kp, Ei = E;
+    {
+        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
+        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
+    }
+    const int t = gemm_tile(c, rows, N, E);
+    const GemmTile& gt = kGemmTiles[t];
+    const int bn = 64 * gt.tn;
+    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
+    if (!row_off)
+        return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, kGemmThreads, 0,
+                         args);
+    // blockIdx.y enumerates (expert, row tile) pairs: at most ceil(rows / BM) + E of them
+    return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(N, bn), gemm_tiles(rows, gt.bm) + (unsigned)E,
+                     kGemmThreads, 0, args);
+}
+
 // GEMV variant for a given K (index into kGemvVariants).
 int gemv_variant(brik_ctx* c, int K)
 {
@@ -150,6 +249,11 @@ int gemv_variant(brik_ctx* c, int K)
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N)
 {
+    if (K == 0) {   // empty sums, whatever the path
+        HIP_TRY(c, hipSetDevice(c->device));
+        HIP_TRY(c, hipMemsetAsync(y, 0, (size_t)M * N * sizeof(float), c->stream));
+        return BRIK_OK;
+    }
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
     const int v = gemv_variant(c, K);
     const int rpi = (256 / kGemvVariants[v].team) * kGemvVariants[v].r;
@@ -157,24 +261,22 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
     const size_t lds = gemv_lds(K) + sizeof(float) * (size_t)rpi * kGemvVariants[v].team * ((sets + gx - 1) / gx);
     const bool gemv_fits = lds <= kGemvMaxLds;
-    bool use_gemv = (M == 1 && gemv_fits);
+    // the MFMA GEMM reads scales in 8-group windows, so a matrix of fewer than 8 groups (N * K < 256)
+    // always takes the GEMV path (which handles any M)
+    const bool tiny = (long)N * (K / kGroup) < 8;
+    bool use_gemv = ((M == 1 || tiny) && gemv_fits);
     if (c->opt_path == 1) {
         if (!gemv_fits) return fail(c, BRIK_EINVAL, "forced GEMV: K=%d exceeds the LDS staging limit", K);
         use_gemv = true;
-    } else if (c->opt_path == 2) {
+    } else if (c->opt_path == 2 && !tiny) {
         use_gemv = false;
     }
-    int Mi = M, Ki = K, Ni = N;
+    int Ki = K, Ni = N;
     if (use_gemv) {
         void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni};
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
-    const int* row_off = nullptr;
-    int E = 0;
-    const Kern k = f == F_Q4 ? K_GEMM_Q4 : f == F_Q8 ? K_GEMM_Q8 : K_GEMM_Q3;
-    void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &E};
-    return launch(c, k, (unsigned)((N + kGemmTile - 1) / kGemmTile), (unsigned)((M + kGemmTile - 1) / kGemmTile),
-                  256, 0, args);
+    return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0);
 }
 
 }  // namespace
@@ -232,6 +334,17 @@ int brik_create(int device, brik_ctx** out)
             snprintf(name, sizeof name, "brik_gemvg_%s_t%d_r%d_u%d_d%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d);
             if (hipModuleGetFunction(&c->gemvg[f][v], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
         }
+    for (int f = 0; f < 3; ++f)
+        for (int t = 0; t < kNumGemmTiles; ++t) {
+            char name[64];
+            snprintf(name, sizeof name, "brik_gemm_%s_%dx%d", kFmtNames[f], kGemmTiles[t].bm, kGemmTiles[t].tn);
+            if (hipModuleGetFunction(&c->gemm[f][t], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+            // the launch shape the runtime uses must fit the kernel's compiled bounds
+            int max_threads = 0;
+            if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->gemm[f][t]) != hipSuccess ||
+                max_threads < (int)kGemmThreads)
+                return bail(BRIK_EMODULE);
+        }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);
     if (hipEventCreate(&c->ev_begin) != hipSuccess || hipEventCreate(&c->ev_end) != hipSuccess)
         return bail(BRIK_EHIP);
@@ -248,6 +361,7 @@ void brik_destroy(brik_ctx* c)
     if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
     if (c->ev_end) (void)hipEventDestroy(c->ev_end);
     if (c->stream) (void)hipStreamDestroy(c->stream);
+    if (c->ws) (void)hipFree(c->ws);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
 }
@@ -327,11 +441,13 @@ int brik_moe_matmul_t_q4(brik_ctx* c, const float* x, const int32_t* row_off, co
     if (r != BRIK_OK || R == 0 || N == 0 || E == 0) return r;
     if (!row_off) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: row_off is null");
     if (!aligned(row_off, 4)) return fail(c, BRIK_EALIGN, "moe_matmul_t_q4: row_off must be 4-byte aligned");
-    const void* p1 = nullptr;
-    int Mi = R, Ki = K, Ni = N, Ei = E;
-    void* args[] = {&x, &nib, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
-    const unsigned gy = (unsigned)((R + kGemmTile - 1) / kGemmTile + E);
-    return launch(c, K_GEMM_Q4, (unsigned)((N + kGemmTile - 1) / kGemmTile), gy, 256, 0, args);
+    if (K == 0) return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
+    // the scale and min planes of all experts are addressed through one resource, in 8-group windows
+    const unsigned long long groups = (unsigned long long)E * N * (K / kGroup);
+    if (groups < 8 || groups * 2 >= (1ull << 32))
+        return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: E*N*K = %llu weight elements is outside [256, 2^35)",
+                    groups * kGroup);
+    return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
 }
 
 static int dequant(brik_ctx* c, Kern k, const char* who, void** args, size_t n, const void* p0,
@@ -484,6 +600,11 @@ int brik_set_option(brik_ctx* c, int key, int value)
         if (value < 0 || value > kNumGemvVariants)
             return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMV_VARIANT: %d not in 0..%d", value, kNumGemvVariants);
         c->opt_variant = value;
+        return BRIK_OK;
+    case BRIK_OPT_GEMM_TILE:
+        if (value < 0 || value > kNumGemmTiles)
+            return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMM_TILE: %d not in 0..%d", value, kNumGemmTiles);
+        c->opt_tile = value;
         return BRIK_OK;
     default:
         return fail(c, BRIK_EINVAL, "unknown option %d", key);

@@ -18,6 +18,10 @@
  *   M, K, N >= 0, non-null pointers when the operand is non-empty, plane alignment as listed.
  * M == 0 or N == 0 is a no-op. K == 0 writes y = 0.
  *
+ * Workspace: for M >= 2 the matmuls stage x as f16 rows in a device buffer owned by the context
+ * (grown with hipMalloc on demand, 2 * M * roundup(K, 256) + 4 * M bytes; growing it first waits
+ * for the context stream).
+ *
  * Alignment (what a 16-byte aligned packed .brik blob guarantees, BRIK_ALIGN = 16,
  * src/lib/brik/format.ts:8): x, y, out 16 B; q8 codes 16 B; q4 nibbles 16 B; q3 lo 16 B,
  * q3 hi 8 B; scales and mins 2 B.
@@ -85,8 +89,8 @@ int brik_matmul_t_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const ui
  * W is ONE stacked q4 tensor [E, N, K] in .brik layout (nElems = E*N*K; expert e's nibbles start at
  * e*N*K/2 bytes, its scales and mins at index e*N*K/32 of their planes).
  * row_off: DEVICE int32[E + 1], non-decreasing, row_off[0] == 0, row_off[E] == R, the number of
- * rows of x_sorted and y_sorted. The grid is sized from R and E alone (ceil(R/64) + E row tiles),
- * so routing can stay on the device. */
+ * rows of x_sorted and y_sorted. The grid is sized from R and E alone (ceil(R/BM) + E row tiles),
+ * so routing can stay on the device. Requires 256 <= E*N*K < 2^35 (BRIK_EINVAL otherwise). */
 int brik_moe_matmul_t_q4(brik_ctx *ctx, const float *x_sorted, const int32_t *row_off,
                          const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
                          float *y_sorted, int E, int R, int K, int N);
@@ -140,6 +144,10 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
 #define BRIK_OPT_PATH 1        /* 0 auto, 1 force GEMV (any M), 2 force MFMA GEMM (any M) */
 #define BRIK_OPT_GEMV_VARIANT 2  /* 0 auto, else 1 + index of a GEMV tiling variant (see brik_runtime.cpp) */
 #define BRIK_GEMV_VARIANTS 7
+#define BRIK_OPT_GEMM_TILE 3     /* 0 auto, else 1 + index of an MFMA GEMM block tile (rows x columns):
+                                    1 128x192, 2 128x128, 3 128x256, 4 64x192, 5 64x128, 6 64x256,
+                                    7 32x192, 8 32x128, 9 32x256 */
+#define BRIK_GEMM_TILES 9
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus

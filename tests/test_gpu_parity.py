@@ -10,7 +10,8 @@ import pytest
 
 import oracle as O
 from brimkern_amd import synth, layout
-from brimkern_amd.capi import BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT, BRIK_GEMV_VARIANTS
+from brimkern_amd.capi import (BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT,
+                               BRIK_GEMV_VARIANTS, BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES)
 from helpers import Gpu, load_golden, normwise_rel, componentwise_ok, PLANES, REL_TOL
 
 pytestmark = pytest.mark.gpu
@@ -24,6 +25,7 @@ def gpu(ctx):
     yield g
     ctx.set_option(BRIK_OPT_PATH, 0)
     ctx.set_option(BRIK_OPT_GEMV_VARIANT, 0)
+    ctx.set_option(BRIK_OPT_GEMM_TILE, 0)
     g.free()
 
 
@@ -161,6 +163,21 @@ def test_gemm_parity(gpu, fmt, M, K, N):
     check(y, r, den, REL_TOL)
 
 
+@pytest.mark.parametrize("tile", range(1, BRIK_GEMM_TILES + 1))
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_gemm_every_tile(gpu, fmt, tile):
+    # ragged in M and N (partial row and column tiles), 9 column tiles of 128: one full XCD-ordered
+    # group of 8 plus the row-major remainder
+    M, K, N = 130, 96, 1100
+    t = synth.tensor(fmt, 35, N, K)
+    x = synth.normal(36, M * K)
+    planes = gpu.planes(fmt, t)
+    gpu.ctx.set_option(BRIK_OPT_GEMM_TILE, tile)
+    y = gpu.matmul(fmt, x, planes, M, K, N)
+    r, den = oracle_mm(fmt, x, t, M, K, N)
+    check(y, r, den, REL_TOL)
+
+
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
 def test_forced_paths_agree(gpu, fmt):
     M, K, N = 6, 512, 200
@@ -197,7 +214,9 @@ def test_moe_cfg5(gpu, which):
     assert normwise_rel(y, r) <= REL_TOL
 
 
-def test_moe_empty_experts(gpu):
+@pytest.mark.parametrize("tile", range(0, BRIK_GEMM_TILES + 1))
+def test_moe_empty_experts(gpu, tile):
+    gpu.ctx.set_option(BRIK_OPT_GEMM_TILE, tile)
     E, K, N = 6, 64, 40
     row_off = np.array([0, 0, 5, 5, 5, 9, 9], np.int32)
     t = synth.q4_tensor(90, E * N, K)
