@@ -14,7 +14,12 @@ copies to exceed the Infinity Cache.
 
 ``cpu_baseline``: the reference's CPU matmul restated in JavaScript (oracle/cpuref.js: dequantize the
 tensor, f64-accumulated dot per output), run by node on this host on one Qwen3-4B layer set (M=1,
-the same six shapes), single-threaded.
+the same six shapes), single-threaded, repeated to a sample of about 15 s; value = mean rate.
+
+``roofline``: ``achieved`` = algorithmic bytes per launch / the launch's average duration (HIP events on
+the library's stream; one launch per step). ``traffic`` = HBM bytes per launch from two rocprofv3
+counter passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) run as child processes before this
+process opens the GPU, each scaled by the same counter's reading for a device copy of known size.
 
 Timing: HIP events on the library's stream bracket exactly ``--steps`` steps after ``--warmup``
 untimed ones, with a device synchronization on both sides.
@@ -88,7 +93,8 @@ def time_loop(ctx, fn, steps, warmup):
     return ms / steps
 
 
-def gemv_layer_set(ctx, steps, warmup, layers):
+def build_layer_plan(ctx, layers):
+    """One grouped GEMV plan over ``layers`` distinct copies of the Qwen3-4B q4 layer set."""
     from brimkern_amd import synth
     reps, jobs, nbytes = {}, [], 0
     xa = ctx.upload(synth.normal(101, 2560))
@@ -105,6 +111,12 @@ def gemv_layer_set(ctx, steps, warmup, layers):
             yo += N
             nbytes += q_bytes("q4", N, K) + 4 * K + 4 * N
     plan = ctx.gemv_plan("q4", jobs)
+    return plan, {"reps": reps, "xa": xa, "xd": xd, "ybuf": ybuf, "nbytes": nbytes}
+
+
+def gemv_layer_set(ctx, steps, warmup, layers):
+    plan, b = build_layer_plan(ctx, layers)
+    reps, xa, xd, ybuf, nbytes = b["reps"], b["xa"], b["xd"], b["ybuf"], b["nbytes"]
     ms = time_loop(ctx, lambda i: plan.run(), steps, warmup)
     # per-shape single launches, rotating over the layers' copies
     single = {}
@@ -156,7 +168,8 @@ def gemm_cfg4(ctx, steps, warmup):
     for bb in (r.buf, x, y):
         ctx.free(bb)
     tf = flops / (ms * 1e-3) / 1e12
-    return {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+    return {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1), "bound": "mfma", "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
+            "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "launches": "brik_xprep_f16 + brik_gemm_q4 per call"}
 
 
 def moe_cfg5(ctx, steps, warmup):
@@ -189,30 +202,115 @@ def moe_cfg5(ctx, steps, warmup):
             "max_rows_per_expert": int(np.diff(row_off).max()), "min_rows_per_expert": int(np.diff(row_off).min())}
 
 
-def cpu_baseline():
-    """JS restatement of the reference CPU matmul on one Qwen3-4B q4 layer set (M=1), 1 thread."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(target_s=15.0):
+    """JS restatement of the reference CPU matmul (oracle/cpuref.js) on one Qwen3-4B q4 layer set (M=1),
+    single-threaded under node. A first pass times the layer set once; the sample then repeats each
+    matrix so the whole sample takes about ``target_s`` seconds, and the value is the mean rate."""
     node = shutil.which("node")
     if node is None:
         return None
     from brimkern_amd import synth, layout
-    total_ms, nbytes = 0.0, 0
-    with tempfile.TemporaryDirectory() as d:
-        for si, (name, K, N) in enumerate(QWEN3_4B):
-            t = synth.q4_tensor(200 + si, N, K)
-            x = synth.normal(500 + si, K)
-            inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
-            with open(inp, "wb") as f:
-                f.write(x.tobytes())
-                f.write(layout.pack("q4", t).tobytes())
-            res = json.loads(subprocess.check_output([node, os.path.join(ROOT, "oracle", "cpuref.js"), "q4", "1",
-                                                      str(K), str(N), inp, out, "2"]))
-            total_ms += res["ms"]
-            nbytes += q_bytes("q4", N, K) + 4 * K + 4 * N
-    import platform
+
+    def run(reps):
+        total_ms, nbytes = 0.0, 0
+        with tempfile.TemporaryDirectory() as d:
+            for si, (name, K, N) in enumerate(QWEN3_4B):
+                t = synth.q4_tensor(200 + si, N, K)
+                x = synth.normal(500 + si, K)
+                inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
+                with open(inp, "wb") as f:
+                    f.write(x.tobytes())
+                    f.write(layout.pack("q4", t).tobytes())
+                res = json.loads(subprocess.check_output([node, os.path.join(ROOT, "oracle", "cpuref.js"), "q4", "1",
+                                                          str(K), str(N), inp, out, str(reps)]))
+                total_ms += res["total_ms"]
+                nbytes += reps * (q_bytes("q4", N, K) + 4 * K + 4 * N)
+        return total_ms, nbytes
+
+    t1, _ = run(1)
+    reps = max(1, min(200, int(round(target_s * 1e3 / max(t1, 1.0)))))
+    total_ms, nbytes = run(reps)
     return {"value": round(nbytes / (total_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"one Qwen3-4B q4 layer set (6 matrices, M=1, {nbytes / 1e6:.1f} MB), node "
-                      f"{subprocess.check_output([node, '--version']).decode().strip()}, best of 2 per matrix, "
-                      f"{total_ms / 1e3:.2f} s, cpu {platform.processor() or platform.machine()}"}
+            "sample": f"one Qwen3-4B q4 layer set (6 matrices, M=1, {nbytes / reps / 1e6:.1f} MB) x {reps} passes, "
+                      f"{total_ms / 1e3:.1f} s, node {subprocess.check_output([node, '--version']).decode().strip()} "
+                      f"single-threaded, {cpu_model()}"}
+
+
+# ---- HBM traffic of the dominant kernel (two rocprofv3 counter passes in child processes) ---------
+
+CAL_BYTES = 512 << 20      # device-to-device copy of known size: calibrates FETCH_SIZE / WRITE_SIZE
+
+
+def probe(layers, reps=6):
+    """Child-process body of the counter passes: a few plan launches and one calibration copy."""
+    from brimkern_amd import Context
+    ctx = Context(0)
+    plan, bufs = build_layer_plan(ctx, layers)
+    for _ in range(reps):
+        plan.run()
+    ctx.sync()
+    a, b = ctx.alloc(CAL_BYTES), ctx.alloc(CAL_BYTES)
+    ctx._check(ctx.lib.brik_d2d(ctx.handle, ctx_p(b.ptr), ctx_p(a.ptr), CAL_BYTES))
+    ctx.sync()
+    print("probe done", flush=True)
+
+
+def counter_pass(counter, layers, timeout=120):
+    """Run the probe under ``rocprofv3 --pmc <counter>``; returns {kernel: [values per dispatch]}."""
+    import csv
+    import glob
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "p", "--",
+               sys.executable, os.path.abspath(__file__), "--probe", "--layers", str(layers)]
+        env = dict(os.environ, TMPDIR="/tmp")
+        r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                           timeout=timeout)
+        if r.returncode != 0 or b"probe done" not in r.stdout:
+            return None
+        out = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for row in csv.DictReader(open(f)):
+                if row["Counter_Name"] == counter:
+                    out.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return out
+
+
+def hbm_traffic(layers):
+    """HBM bytes per launch of the grouped GEMV kernel: FETCH_SIZE + WRITE_SIZE (KiB per dispatch),
+    each scaled by what the same counter reads for a device copy of CAL_BYTES."""
+    try:
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            vals = counter_pass(counter, layers)
+            if not vals:
+                return None, None
+            gemv = [v for k, vs in vals.items() if k.startswith("brik_gemvg_") for v in vs]
+            copy = [v for k, vs in vals.items() if "copyBuffer" in k for v in vs]
+            if not gemv or not copy:
+                return None, None
+            kernel = [k for k in vals if k.startswith("brik_gemvg_")][0]
+            factor = CAL_BYTES / (max(copy) * 1024.0)
+            res[counter] = (float(np.median(gemv)) * 1024.0 * factor, factor)
+        return {"bytes": res["FETCH_SIZE"][0] + res["WRITE_SIZE"][0],
+                "fetch_bytes": round(res["FETCH_SIZE"][0]), "write_bytes": round(res["WRITE_SIZE"][0]),
+                "fetch_scale": round(res["FETCH_SIZE"][1], 4), "write_scale": round(res["WRITE_SIZE"][1], 4)}, kernel
+    except (subprocess.SubprocessError, OSError, ValueError, KeyError):
+        return None, None
 
 
 def main():
@@ -223,11 +321,21 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.probe:
+        probe(args.layers)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU form in this build "
               "(sharding along N is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    traffic, kernel = (None, None)
+    if not args.no_traffic:
+        # counter passes run in child processes before this process touches the GPU
+        log("bench: HBM traffic counter passes")
+        traffic, kernel = hbm_traffic(args.layers)
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
@@ -248,13 +356,15 @@ def main():
         "metric": "q4 GEMV HBM GB/s (% of peak) at Qwen3-4B shapes; prefill q4 GEMM TFLOP/s",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "q4 weights, f32 activations and accumulation", "data": "synthetic (seeded SplitMix64)",
+        "dtype": "f32", "data": "synthetic (seeded SplitMix64), random q4 weights of the Qwen3-4B shapes",
         "config": {"workload": f"matmul_t_q4 decode GEMV, Qwen3-4B layer set x {args.layers} layers "
                                f"(216 matrices, M=1), grouped plan, one launch per step",
                    "bytes_per_step": nbytes, "layers": args.layers},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "brik_gemv_grouped_q4_t16"},
+                     "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic["bytes"]),
+                     "traffic_detail": traffic, "algorithmic_bytes": nbytes,
+                     "kernel": kernel or "brik_gemvg_q4 (grouped plan)", "us_per_launch": round(ms * 1e3, 2)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

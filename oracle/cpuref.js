@@ -12,7 +12,8 @@
 // CLI (used by bench.py's cpu_baseline leg):
 //   node oracle/cpuref.js <fmt> <M> <K> <N> <input.bin> <output.bin> [reps]
 // input.bin = x (M*K f32) followed by the packed .brik blob of W [N, K]; output.bin receives y.
-// Prints one JSON line: {"ms": best wall time of one full matmul incl. dequant, "reps": ...}.
+// Prints one JSON line: {"ms": best wall time of one full matmul incl. dequant, "total_ms": wall time
+// of all reps, "reps": ...}.
 
 const GROUP = 32;
 
@@ -105,13 +106,15 @@ if (require.main === module) {
   const bytes = new Uint8Array(buf.buffer, buf.byteOffset, buf.byteLength);
   const a = new Float32Array(bytes.buffer.slice(bytes.byteOffset, bytes.byteOffset + M * K * 4));
   const blob = bytes.slice(M * K * 4);
-  let best = Infinity, y = null;
+  let best = Infinity, total = 0, y = null;
   for (let r = 0; r < reps; r++) {
     const t0 = process.hrtime();
     y = cpuMatmul(fmt, a, blob, M, K, N);
     const d = process.hrtime(t0);
-    best = Math.min(best, d[0] * 1e3 + d[1] / 1e6);
+    const ms = d[0] * 1e3 + d[1] / 1e6;
+    best = Math.min(best, ms);
+    total += ms;
   }
   fs.writeFileSync(argv[5], Buffer.from(y.buffer));
-  process.stdout.write(JSON.stringify({ ms: best, reps: reps, fmt: fmt, M: M, K: K, N: N }) + '\n');
+  process.stdout.write(JSON.stringify({ ms: best, total_ms: total, reps: reps, fmt: fmt, M: M, K: K, N: N }) + '\n');
 }
