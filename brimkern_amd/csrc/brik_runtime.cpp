@@ -32,10 +32,15 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_xprep_f16",
 };
 
-// GEMV variants (lanes per row team, rows per team, groups per pipeline step), in the order of
-// BRIK_GEMV_FMT in gemv.hip. Kernels: brik_gemv_<fmt>_t<T>_r<R>_u<U> (one matrix) and
-// brik_gemvg_<fmt>_t<T>_r<R>_u<U> (grouped job table).
-struct GemvVariant { int team, r, u, d; };
+// GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
+// R rows per team, U groups per pipeline step, pipeline depth D; kernels brik_gemv_<fmt>_t<T>_r<R>_u<U>_d<D>
+// (one matrix) and brik_gemvg_<fmt>_... (grouped job table).
+struct GemvVariant {
+    int team, r, u, d;
+    int rpi() const { return (256 / team) * r; }      // rows per block iteration
+    // LDS of a block past the staged x: TEAM partial sums for each of `rows` rows
+    size_t extra_lds(long rows) const { return sizeof(float) * (size_t)rows * team; }
+};
 constexpr GemvVariant kGemvVariants[] = {{16, 2, 1, 2}, {16, 2, 1, 3}, {16, 2, 1, 4}, {16, 4, 1, 2},
                                          {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}};
 constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]);
@@ -256,10 +261,10 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     }
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
     const int v = gemv_variant(c, K);
-    const int rpi = (256 / kGemvVariants[v].team) * kGemvVariants[v].r;
+    const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
-    const size_t lds = gemv_lds(K) + sizeof(float) * (size_t)rpi * kGemvVariants[v].team * ((sets + gx - 1) / gx);
+    const size_t lds = gemv_lds(K) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
     const bool gemv_fits = lds <= kGemvMaxLds;
     // the MFMA GEMM reads scales in 8-group windows, so a matrix of fewer than 8 groups (N * K < 256)
     // always takes the GEMV path (which handles any M)
@@ -511,7 +516,7 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
         kmin = b.K < kmin ? b.K : kmin;
     }
     const int v = gemv_variant(c, kmin);
-    const int rpi = (256 / kGemvVariants[v].team) * kGemvVariants[v].r;
+    const int rpi = kGemvVariants[v].rpi();
     // Blocks of about equal cost: rows per block ~ kPlanGroupRows / (K/32), in whole row sets of rpi
     // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). Jobs are laid out in order
     // of decreasing K, so the most expensive blocks are dispatched first and the tail of the launch
@@ -529,7 +534,7 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
         sets = sets < 1 ? 1 : sets > kPlanMaxSets ? kPlanMaxSets : sets;
         rpbs[k] = (uint32_t)(sets * rpi);
         start[k + 1] = start[k] + (uint32_t)((b.N + rpbs[k] - 1) / rpbs[k]);
-        const size_t need = gemv_lds(b.K) + sizeof(float) * (size_t)rpbs[k] * kGemvVariants[v].team;
+        const size_t need = gemv_lds(b.K) + kGemvVariants[v].extra_lds(rpbs[k]);
         lds = need > lds ? need : lds;
     }
     if (lds > kGemvMaxLds) return fail(c, BRIK_EINVAL, "gemv_plan: K=%d too large for LDS staging", kmax);

@@ -182,9 +182,20 @@ __device__ __forceinline__ float team_sum(float v)
 template <int FMT, int TEAM, int R, int U>
 struct Work {
     static constexpr int RPI = (256 / TEAM) * R;   // rows per block iteration
+    static constexpr int PARTS = TEAM;             // partial sums per row
+    static constexpr int NACC = R;                 // accumulators per lane
+    typedef Grp<FMT> Data[U][R];                   // loads of one step
     Rs rs;
     int G, r0, r1, rstep, B, lane, team;
     float* part;       // LDS [nsets][RPI][TEAM] lane partials (see gemv_matrix)
+
+    __device__ __forceinline__ void init()
+    {
+        lane = threadIdx.x % TEAM;
+        team = threadIdx.x / TEAM;
+        B = (G + U * TEAM - 1) / (U * TEAM);
+    }
+    __device__ __forceinline__ bool even() const { return G % (U * TEAM) == 0; }
 
     __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
 
@@ -258,11 +269,11 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
 
 // The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
-template <int FMT, int TEAM, int R, int U, int D, bool EVEN>
-__device__ __forceinline__ void pipeline(Work<FMT, TEAM, R, U>& w, const XStage& X, const float* __restrict__ x,
+template <int FMT, class W, int D, bool EVEN>
+__device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __restrict__ x,
                                          const Planes& P, float* __restrict__ yrow, int K, int S)
 {
-    Grp<FMT> d[D][U][R];
+    typename W::Data d[D];
     int ip = 0, bp = 0;                      // (p, b) of the next step to issue
 #pragma unroll
     for (int k = 0; k < D - 1; ++k) {
@@ -273,10 +284,11 @@ __device__ __forceinline__ void pipeline(Work<FMT, TEAM, R, U>& w, const XStage&
     }
     brik::xstage<FMT>(x, X, K);
     if (*X.flag) {
-        gemv_rows_exact<FMT, TEAM, R>(x, P, yrow, K, w.r0, w.r1, w.rstep);
+        // exact path: teams of 16 lanes over RPI rows per iteration
+        gemv_rows_exact<FMT, 16, W::RPI / 16>(x, P, yrow, K, w.r0, w.r1, w.rstep);
         return;
     }
-    float acc[R] = {};
+    float acc[W::NACC] = {};
     int pc = 0, bc = 0;                      // (p, b) of the next step to consume
     int i = 0;
     for (; i + D <= S; i += D) {
@@ -309,60 +321,58 @@ __device__ __forceinline__ void pipeline(Work<FMT, TEAM, R, U>& w, const XStage&
 // Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
 // then the cross-lane sums of the LDS partials are written to y. The block owns row sets
 // p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
-template <int FMT, int TEAM, int R, int U, int D>
+template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Planes& P, float* __restrict__ yrow,
                                             int N, int K, int r0, int r1, int rstep, unsigned char* lds)
 {
-    using W = Work<FMT, TEAM, R, U>;
     W w;
     w.G = K / BRIK_GROUP;
     w.rs = make_rs<FMT>(P, N, w.G);
     w.r0 = r0; w.r1 = r1; w.rstep = rstep;
-    w.lane = threadIdx.x % TEAM;
-    w.team = threadIdx.x / TEAM;
-    w.B = (w.G + U * TEAM - 1) / (U * TEAM);
+    w.init();
     const int nsets = r0 < r1 ? (r1 - r0 + rstep - 1) / rstep : 0;     // block-uniform
-    const int S = nsets * w.B;                                            // steps per team
+    const int S = nsets * w.B;                                            // steps per lane
     const XStage X = brik::xstage_layout(lds, K);
     w.part = (float*)(lds + brik::xstage_bytes(K));
-    if (w.G % (U * TEAM) == 0) pipeline<FMT, TEAM, R, U, D, true>(w, X, x, P, yrow, K, S);
-    else pipeline<FMT, TEAM, R, U, D, false>(w, X, x, P, yrow, K, S);
+    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, P, yrow, K, S);
+    else pipeline<FMT, W, D, false>(w, X, x, P, yrow, K, S);
     if (*X.flag) return;
     __syncthreads();
-    // cross-lane sums: one thread per row, TEAM partials each (rows past r1 are skipped)
+    // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped)
+    constexpr int PARTS = W::PARTS;
     for (int q = threadIdx.x; q < nsets * W::RPI; q += blockDim.x) {
         const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
         if (n < r1) {
-            const float* pp = w.part + (size_t)q * TEAM;
+            const float* pp = w.part + (size_t)q * PARTS;
             float v = 0.f;
 #pragma unroll
-            for (int l = 0; l < TEAM; ++l) v += pp[(l + q) % TEAM];
+            for (int l = 0; l < PARTS; ++l) v += pp[(l + q) % PARTS];
             yrow[n] = v;
         }
     }
 }
 
-template <int FMT, int TEAM, int R, int U, int D>
+template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uint8_t* __restrict__ p0,
                                           const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
                                           const uint16_t* __restrict__ mn, float* __restrict__ y, int K, int N)
 {
     extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int RPI = (256 / TEAM) * R;     // rows per block iteration
+    constexpr int RPI = W::RPI;     // rows per block iteration
     const Planes P{p0, p1, sc, mn};
-    gemv_matrix<FMT, TEAM, R, U, D>(x + (size_t)blockIdx.y * K, P, y + (size_t)blockIdx.y * N, N, K, blockIdx.x * RPI,
-                                    N, gridDim.x * RPI, lds);
+    gemv_matrix<FMT, W, D>(x + (size_t)blockIdx.y * K, P, y + (size_t)blockIdx.y * N, N, K, blockIdx.x * RPI, N,
+                           gridDim.x * RPI, lds);
 }
 
 // Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
 // block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts).
-template <int FMT, int TEAM, int R, int U, int D>
+template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restrict__ jobs,
                                                   const uint32_t* __restrict__ block_start,
                                                   const uint32_t* __restrict__ rows_per_block, int njobs)
 {
     extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int RPI = (256 / TEAM) * R;
+    constexpr int RPI = W::RPI;
     const uint32_t b = blockIdx.x;
     int lo = 0, hi = njobs - 1;          // last j with block_start[j] <= b
     while (lo < hi) {
@@ -374,7 +384,7 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restric
     const int rpb = (int)rows_per_block[lo];
     const int r0 = (int)(b - block_start[lo]) * rpb;
     const int r1 = min(job.N, r0 + rpb);
-    gemv_matrix<FMT, TEAM, R, U, D>(job.x, P, job.y, job.N, job.K, r0, r1, RPI, lds);
+    gemv_matrix<FMT, W, D>(job.x, P, job.y, job.N, job.K, r0, r1, RPI, lds);
 }
 
 }  // namespace
@@ -385,13 +395,13 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restric
         const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, float* __restrict__ y,    \
         int K, int N)                                                                               \
     {                                                                                               \
-        gemv_body<FMT, TEAM, RR, UU, DD>(x, p0, p1, sc, mn, y, K, N);                               \
+        gemv_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(x, p0, p1, sc, mn, y, K, N);                    \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
         const brik_gemv_job* __restrict__ jobs, const uint32_t* __restrict__ block_start,           \
         const uint32_t* __restrict__ rows_per_block, int njobs)                                      \
     {                                                                                               \
-        gemv_grouped_body<FMT, TEAM, RR, UU, DD>(jobs, block_start, rows_per_block, njobs);         \
+        gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(jobs, block_start, rows_per_block, njobs); \
     }
 
 // The variant table of the runtime (brik_runtime.cpp, kGemvVariants) lists these in this order.
