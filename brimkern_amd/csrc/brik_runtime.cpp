@@ -50,7 +50,9 @@ constexpr int kGroup = 32;
 // GEMM block tiles (BM rows x 64 TN columns), in the order of BRIK_GEMM_FMT in gemm.hip:
 // brik_gemm_<fmt>_<BM>x<TN>.
 struct GemmTile { int bm, tn; };
-constexpr GemmTile kGemmTiles[] = {{128, 3}, {128, 2}, {128, 4}, {64, 3}, {64, 2}, {64, 4}, {32, 3}, {32, 2}, {32, 4}};
+constexpr GemmTile kGemmTiles[] = {{128, 2}, {128, 1}, {128, 3}, {64, 2}, {64, 1}, {64, 3},
+                                   {32, 2},  {32, 1},  {32, 3},  {96, 2}, {96, 1}, {96, 3}};
+constexpr int kGemmColsPerTn = 128;            // block tile columns = 128 * tn
 constexpr int kNumGemmTiles = sizeof(kGemmTiles) / sizeof(kGemmTiles[0]);
 constexpr unsigned kCUs = 256;                 // MI355X compute units
 constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
@@ -166,13 +168,13 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 // GEMM block tile (index into kGemmTiles). Dense (E == 0): the tile with the smallest modelled
 // makespan, rounds x tile area x a small-tile penalty, where rounds = ceil(blocks / CUs) (every block
 // of a round runs on its own compute unit). Expert-grouped: the row tile from the mean rows per
-// expert, 128 columns.
+// expert, 256 columns.
 int gemm_tile(brik_ctx* c, long M, long N, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
     if (E > 0) {
         const long per = (M + E - 1) / E;
-        const int bm = per > 64 ? 128 : per > 32 ? 64 : 32;
+        const int bm = per > 96 ? 128 : per > 64 ? 96 : per > 32 ? 64 : 32;
         for (int t = 0; t < kNumGemmTiles; ++t)
             if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == 2) return t;
     }
@@ -180,10 +182,10 @@ int gemm_tile(brik_ctx* c, long M, long N, int E)
     double best_cost = 0;
     for (int t = 0; t < kNumGemmTiles; ++t) {
         const GemmTile& g = kGemmTiles[t];
-        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, 64 * g.tn);
+        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, kGemmColsPerTn * g.tn);
         const double rounds = std::ceil(blocks / kCUs);
-        const double penalty = g.bm == 128 ? 1.0 : g.bm == 64 ? 1.3 : 1.8;
-        const double cost = rounds * g.bm * 64.0 * g.tn * penalty;
+        const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
+        const double cost = rounds * g.bm * (double)kGemmColsPerTn * g.tn * penalty;
         if (t == 0 || cost < best_cost) {
             best = t;
             best_cost = cost;
@@ -233,7 +235,7 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     }
     const int t = gemm_tile(c, rows, N, E);
     const GemmTile& gt = kGemmTiles[t];
-    const int bn = 64 * gt.tn;
+    const int bn = kGemmColsPerTn * gt.tn;
     void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
     if (!row_off)
         return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, kGemmThreads, 0,
@@ -266,9 +268,9 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
     const size_t lds = gemv_lds(K) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
     const bool gemv_fits = lds <= kGemvMaxLds;
-    // the MFMA GEMM reads scales in 8-group windows, so a matrix of fewer than 8 groups (N * K < 256)
+    // the MFMA GEMM reads scales in 16-group chunks, so a matrix of fewer than 16 groups (N * K < 512)
     // always takes the GEMV path (which handles any M)
-    const bool tiny = (long)N * (K / kGroup) < 8;
+    const bool tiny = (long)N * (K / kGroup) < 16;
     bool use_gemv = ((M == 1 || tiny) && gemv_fits);
     if (c->opt_path == 1) {
         if (!gemv_fits) return fail(c, BRIK_EINVAL, "forced GEMV: K=%d exceeds the LDS staging limit", K);
@@ -447,10 +449,10 @@ int brik_moe_matmul_t_q4(brik_ctx* c, const float* x, const int32_t* row_off, co
     if (!row_off) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: row_off is null");
     if (!aligned(row_off, 4)) return fail(c, BRIK_EALIGN, "moe_matmul_t_q4: row_off must be 4-byte aligned");
     if (K == 0) return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
-    // the scale and min planes of all experts are addressed through one resource, in 8-group windows
+    // the scale and min planes of all experts are addressed through one resource, in 16-group chunks
     const unsigned long long groups = (unsigned long long)E * N * (K / kGroup);
-    if (groups < 8 || groups * 2 >= (1ull << 32))
-        return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: E*N*K = %llu weight elements is outside [256, 2^35)",
+    if (groups < 16 || groups * 2 >= (1ull << 32))
+        return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: E*N*K = %llu weight elements is outside [512, 2^35)",
                     groups * kGroup);
     return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
 }

@@ -15,6 +15,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
 
 // IEEE binary16 -> f32 (v_cvt_f32_f16). Exact for every finite half, including subnormals;
 // e == 31 decodes to +-Inf / NaN like the reference's CPU decoder (src/lib/brik/f16.ts:31).

@@ -6,18 +6,21 @@
 // Two launches:
 //   1. brik_xprep_f16: each row of x is scaled by a power of two 2^(15 - e) (e = the binary exponent
 //      of the row's largest |x|, so the scaled row fits binary16 whatever its magnitude), rounded to
-//      f16 and written to a workspace row of Kp = roundup(K, 128) halves (zero padded), with the 8
+//      f16 and written to a workspace row of Kp = roundup(K, 256) halves (zero padded), with the 8
 //      elements of every aligned 8-group in the order [0 4 1 5 2 6 3 7]; rscale[m] = 2^(e - 15).
-//   2. brik_gemm_<fmt>_<BM>x<TN>: 4 waves, block tile BM x 64 TN; each wave owns 16 TN columns over
-//      all BM rows and runs v_mfma_f32_16x16x32_f16 (f32 accumulation). A K step is 128 (four
-//      quantization groups). x goes through LDS (double buffered, shared by the 4 waves); W goes
-//      straight from global memory into the MFMA B operand: each lane loads one whole group of one
-//      column per fragment (16 bytes of q4), and dequantizes it in registers 8 codes at a time, just
-//      before the MFMA that consumes them. The dequant is packed f16: a code q placed in the mantissa
-//      of 1024.0h reads as 1024 + q (or 1024 + 16 q one nibble higher, which the scale s / 16
-//      undoes), and one packed subtract and one packed FMA give the dequantized pair (q s + m); the
-//      code pairs (j, j + 4) this produces from 8 packed codes fix the [0 4 1 5 2 6 3 7] order. The
-//      epilogue multiplies by rscale[m] (exact) and stores y.
+//   2. brik_gemm_<fmt>_<BM>x<TN>: 4 waves, block tile BM x 128 TN; each wave owns 32 TN columns over
+//      all BM rows and runs v_mfma_f32_32x32x16_f16 (f32 accumulation), which issues at full rate from
+//      one wave per SIMD and hides about six VALU instructions of the same wave beside each MFMA. A K
+//      step is 128 (four quantization groups, 8 MFMA slices of 16). x goes through LDS: three
+//      buffers filled two steps ahead by direct global->LDS loads, XOR-swizzled so that the A-fragment
+//      reads are free of bank conflicts. W goes straight from global memory into the MFMA B operand:
+//      each lane loads two whole groups of one column per step and dequantizes them in registers 8
+//      codes at a time, one slice ahead of the MFMAs that consume them. The dequant is packed f16: a
+//      code q placed in the mantissa of 1024.0h reads as 1024 + q (or 1024 + 16 q one nibble higher,
+//      which the scale s / 16 undoes), and one packed subtract and one packed FMA give the dequantized
+//      pair (q s + m); the code pairs (j, j + 4) this produces from 8 packed codes fix the
+//      [0 4 1 5 2 6 3 7] order. Scales and mins are staged in LDS per 4 steps by coalesced loads. The
+//      epilogue multiplies by rscale[m] (exact) and stores y through LDS with 16-byte stores.
 // f16 (not bf16) operands: 11-bit significands keep the normwise error near 3e-4, inside the 1e-3
 // bar; bf16's 8 bits would not. The row scaling removes f16's range limit on activations.
 //
@@ -124,102 +127,205 @@ extern "C" __global__ __launch_bounds__(256) void brik_xprep_f16(const float* __
 namespace {
 
 constexpr int GK = 128;              // K per pipeline step: four quantization groups
-constexpr int ALD = GK + 8;          // LDS row stride of the x tile in halves (272 bytes)
+constexpr int XROW = GK * 2;         // bytes of one x row per step in LDS (16 chunks of 16 bytes)
 
-// Block tile: BM rows x 64 TN columns, 4 waves; wave c owns columns [16 TN c, 16 TN (c + 1)) of every
-// BM row, so each W element of the block is loaded and dequantized by exactly one lane.
-template <int BM_, int TN_>
+// Block tile: BM rows x 128 TN columns, 4 waves (one per SIMD); wave w owns columns
+// [32 TN w, 32 TN (w + 1)) of all BM rows as TM = BM / 32 row blocks x TN column blocks of
+// v_mfma_f32_32x32x16_f16, so each W element of the block is loaded and dequantized by exactly one
+// lane, and the dequantization of one 16-k slice of a column block feeds TM MFMAs. The 32x32x16 MFMA
+// (32 cycles) issues at full rate from a single wave and leaves room for about six VALU instructions
+// of the same wave beside each one, which is what the dequantization needs at TM = 4.
+// x steps go through three LDS buffers of BM rows x 256 bytes, filled by direct global->LDS loads two
+// steps ahead. The 16-byte chunk c of row r sits at position c ^ (r & 15) of the row, so the 16 rows
+// that one 16-lane phase of an A-fragment read touches hit 16 different bank groups.
+// Scales and mins go through LDS too, a chunk of 4 steps (16 groups, 32 bytes of each column) at a
+// time, double buffered: the block loads them with 32-byte-per-column global->LDS loads (2 lanes per
+// column) instead of every lane fetching its own 2-byte values from a different cache line.
+template <int FMT, int BM_, int TN_>
 struct Tile {
-    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 16;
-    static constexpr int BN = 64 * TN_;
+    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 32;
+    static constexpr int BN = 128 * TN_;
     static constexpr int NT = 256;
-    static constexpr int XC = BM_ / 16;                   // 16-byte x chunks per thread per step
-    static constexpr int A_BYTES = 2 * BM_ * ALD * 2;     // double-buffered x tile
+    static constexpr int XI = BM_ / 16;                   // 16-byte x chunks per thread per step
+    static constexpr int XBUF = BM_ * XROW;               // one x buffer
+    static constexpr int A_BYTES = 3 * XBUF;
+    static constexpr int PLANES = FMT == FMT_Q8 ? 1 : 2;  // scales (and mins)
+    static constexpr int SPLANE = BN * 32;                // one plane of one scale chunk
+    static constexpr int SBUF = PLANES * SPLANE;          // one scale chunk
+    static constexpr int NSD = PLANES * BN / 128;         // scale-chunk load instructions per wave
+    static constexpr int S_OFF = A_BYTES;                 // scale chunks follow the x buffers
     static constexpr int CLD = BN + 4;                    // epilogue staging row stride (floats)
-    static constexpr int C_BYTES = 16 * CLD * 4;          // one 16-row fragment
-    static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 4 ? 4
-                            : (A_BYTES / C_BYTES) >= 2 ? 2 : 1;   // row fragments per epilogue round
-    static constexpr int SMEM = A_BYTES > RF * C_BYTES ? A_BYTES : RF * C_BYTES;
-    static_assert(BM_ % 16 == 0 && TN_ >= 1 && TM % RF == 0, "tile shape");
+    static constexpr int C_BYTES = 32 * CLD * 4;          // one 32-row block
+    static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 2 && TM % 2 == 0 ? 2 : 1;
+    static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
+    static constexpr int SMEM = MAIN > RF * C_BYTES ? MAIN : RF * C_BYTES;
+    static_assert(BM_ % 32 == 0 && TN_ >= 1 && TM % RF == 0 && SMEM <= 160 * 1024, "tile shape");
 };
 
-// Per lane and 16-column fragment: the codes of one group of one column.
-// Words: q4 4 nibble dwords; q8 8 code dwords; q3 2 dwords of 2-bit fields + 1 dword of high bits.
+// K mapping of a step (128 k = 8 slices of 16, one MFMA each): lane half h = lane >> 5, slice s and
+// element i hold the true K index 128 t + 64 h + 8 s + i. A lane half therefore owns groups 4 t + 2 h
+// and 4 t + 2 h + 1 of its column whole (slices 0-3 and 4-7), and one load brings each group's codes.
+// A (x from LDS) and B (W) use the same mapping, so the order of the contraction does not matter.
+
+// Per lane and 32-column block: the codes of two groups of one column, and their f16 scale and min
+// bits (one group per register, low half). Words: q4 2 x 4 nibble dwords; q8 2 x 8 code dwords; q3
+// 2 x 2 dwords of 2-bit fields, then 2 dwords of high bits (one byte per 8 codes).
 template <int FMT>
 struct WCodes {
-    uint32_t w[FMT == FMT_Q8 ? 8 : FMT == FMT_Q4 ? 4 : 3];
+    uint32_t w[FMT == FMT_Q8 ? 16 : FMT == FMT_Q4 ? 8 : 6];
+    uint32_t s[2], m[2];
 };
 
-// B-operand mapping (MFMA v_mfma_f32_16x16x32_f16, lane l: column l & 15, k slots 8 (l >> 4) + i):
-// in step t, k-slice kk (0..3) and lane quarter q = l >> 4 hold the true K index
-// 128 t + 32 q + 8 kk + i, so lane quarter q owns group 4 t + q whole: one load of its codes. The
-// A operand (x, from LDS) uses the same mapping.
-template <int FMT, int TN>
-__device__ __forceinline__ void w_load(WCodes<FMT> (&f)[TN], const brsrc_t& p0, const brsrc_t& p1,
-                                       const uint32_t (&colg)[TN], int step, int q, int G)
-{
-    // groups past the end are clamped in-bounds here and zeroed at the dequant
-    const uint32_t g = (uint32_t)min(4 * step + q, G - 1);
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// The loads of one step, split into ops that the multiply loop spreads over its slices: for each
+// column block the code loads of W step t + 1, in slices 0-1; then, after the barrier in slice 4, the
+// direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (4 i + w), +1024)
+// of the buffer, 16 bytes per lane: row 4 (4 i + w) + (lane >> 4), stored chunk lane & 15) over slices
+// 4-7. Every fourth step also loads the next scale chunk, in slice 4.
+template <int FMT, class T>
+struct Loader {
+    static constexpr int TN = T::TN, XI = T::XI, NSD = T::NSD;
+    static constexpr int CODE_OPS = FMT == FMT_Q4 ? 2 : 4;
+    static constexpr int W_OPS = CODE_OPS * TN;
+    static constexpr int OPS = W_OPS + XI;
+    static constexpr int WS = 2;                              // slices that issue the W loads
+    static constexpr int XS = 4;                              // first slice of the x loads (the barrier)
+    static constexpr int slice_of(int u) { return u < W_OPS ? u * WS / W_OPS : XS + (u - W_OPS) * (8 - XS) / XI; }
+
+    brsrc_t p0, p1, rsc, rmn, rx;
+    uint32_t colg[TN], sg[TN], xoff[XI];
+    int h, G, wave;
+    uint32_t slim;                 // last scale-chunk start that ends inside the plane (groups - 16)
+    unsigned char* lds;
+    // scale-chunk loads: flat group index of this lane's column for instruction k, and its LDS offset
+    // within a chunk buffer
+    uint32_t sdc[NSD], sdst[NSD];
+    // of the W step being loaded: clamped group indices
+    uint32_t ia[TN], ib[TN];
+
+    __device__ __forceinline__ void begin(int wstep)
+    {
+        const int g0 = 4 * wstep + 2 * h;
+        const uint32_t ga = (uint32_t)min(g0, G - 1), gb = (uint32_t)min(g0 + 1, G - 1);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const uint32_t gi = colg[j] + g;
-        if constexpr (FMT == FMT_Q4) {
-            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, gi * 16, 0, 0);
-            f[j].w[0] = v.x; f[j].w[1] = v.y; f[j].w[2] = v.z; f[j].w[3] = v.w;
-        } else if constexpr (FMT == FMT_Q8) {
-            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, gi * 32, 0, 0);
-            const u32x4_t u = __builtin_amdgcn_raw_buffer_load_b128(p0, gi * 32 + 16, 0, 0);
-            f[j].w[0] = v.x; f[j].w[1] = v.y; f[j].w[2] = v.z; f[j].w[3] = v.w;
-            f[j].w[4] = u.x; f[j].w[5] = u.y; f[j].w[6] = u.z; f[j].w[7] = u.w;
-        } else {
-            const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(p0, gi * 8, 0, 0);
-            f[j].w[0] = v.x; f[j].w[1] = v.y;
-            f[j].w[2] = __builtin_amdgcn_raw_buffer_load_b32(p1, gi * 4, 0, 0);
+        for (int j = 0; j < TN; ++j) {
+            ia[j] = colg[j] + ga;
+            ib[j] = colg[j] + gb;
         }
     }
-}
 
-// Scales (and mins) of two steps: the 8 groups 8 u .. 8 u + 7 of each of the lane's columns, one
-// 16-byte load per column shared by its four quarter lanes (one cache line per column every two
-// steps instead of one per step). The window starts at any even byte offset (unaligned buffer
-// loads are exact on this hardware) and is moved back to end inside the plane, `lim` being the
-// last valid window start (plane groups - 8); sm_pick re-indexes. Groups past the row end are
-// zeroed at the dequant.
-template <int TN>
-__device__ __forceinline__ void sm_load(u32x4_t (&v)[TN], const brsrc_t& r, const uint32_t (&colg)[TN], int u,
-                                        uint32_t lim)
-{
+    __device__ __forceinline__ void op(int u, WCodes<FMT> (&f)[TN], int xstep, uint32_t xbuf)
+    {
+        if (u >= W_OPS) {
+            const int i = u - W_OPS;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(lds + xbuf + (4 * i + wave) * 1024), 16,
+                                                     xoff[i], xstep * XROW, 0, 0);
+            return;
+        }
+        const int j = u / CODE_OPS, k = u % CODE_OPS;
+        WCodes<FMT>& w = f[j];
+        if constexpr (FMT == FMT_Q4) {
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, (k ? ib[j] : ia[j]) * 16, 0, 0);
+            w.w[4 * k + 0] = v.x; w.w[4 * k + 1] = v.y; w.w[4 * k + 2] = v.z; w.w[4 * k + 3] = v.w;
+        } else if constexpr (FMT == FMT_Q8) {
+            const uint32_t g = (k >> 1) ? ib[j] : ia[j];
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, g * 32 + 16 * (k & 1), 0, 0);
+            w.w[4 * k + 0] = v.x; w.w[4 * k + 1] = v.y; w.w[4 * k + 2] = v.z; w.w[4 * k + 3] = v.w;
+        } else {
+            if (k < 2) {
+                const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(p0, (k ? ib[j] : ia[j]) * 8, 0, 0);
+                w.w[2 * k] = v.x; w.w[2 * k + 1] = v.y;
+            } else {
+                w.w[4 + (k - 2)] = __builtin_amdgcn_raw_buffer_load_b32(p1, ((k - 2) ? ib[j] : ia[j]) * 4, 0, 0);
+            }
+        }
+    }
+
+    // all ops of slice sl
+    __device__ __forceinline__ void issue(int sl, WCodes<FMT> (&f)[TN], int xstep, uint32_t xbuf)
+    {
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-        v[j] = __builtin_amdgcn_raw_buffer_load_b128(r, min(colg[j] + 8 * u, lim) * 2, 0, 0);
-}
+        for (int u = 0; u < OPS; ++u)
+            if (slice_of(u) == sl) op(u, f, xstep, xbuf);
+    }
 
-// f16 bits of group 8 u + 4 e + q of column group base cg from the window of pair u (e = 0 / 1: which
-// step of the pair). For a live group the index into the window is 0..7.
-__device__ __forceinline__ uint32_t sm_pick(const u32x4_t& v, uint32_t cg, int u, int e, int q, uint32_t lim)
-{
-    const uint32_t g = cg + 8 * u;
-    const uint32_t k = g - min(g, lim) + 4 * e + q;
-    const uint32_t d = k < 2 ? v.x : k < 4 ? v.y : k < 6 ? v.z : v.w;
-    return (d >> (16 * (k & 1))) & 0xffffu;
-}
+    // Scale chunk v (groups 16 v .. 16 v + 15 of every column of the block) into the chunk buffer at
+    // byte offset `buf`: instruction k of wave w covers plane (4 k + w) / (BN / 32), columns 32 ((4 k + w)
+    // % (BN / 32)) + lane / 2, 16 bytes (8 groups) per lane. A chunk that would run past the end of the
+    // plane is moved back to end inside it; the reader shifts its index by the same amount.
+    __device__ __forceinline__ void scale_chunk(int v, uint32_t buf)
+    {
+#pragma unroll
+        for (int k = 0; k < NSD; ++k) {
+            const uint32_t plane = (uint32_t)(4 * k + wave) / (T::BN / 32);
+            const uint32_t off = (min(sdc[k] + 16 * v, slim) + 8 * (threadIdx.x & 1)) * 2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rmn : rsc, (lds_void_t*)(lds + buf + sdst[k]), 16,
+                                                     off, 0, 0, 0);
+        }
+    }
 
-// Dequantize 8 codes to 4 packed f16 pairs (codes j and j + 4 in pair j).
+    // Scales and mins of W step t (chunk buffer at `buf`) into f: groups 4 t + 2 h + e, e = 0, 1; groups
+    // past the row end get 0.
+    __device__ __forceinline__ void read_scales(WCodes<FMT> (&f)[TN], int t, uint32_t buf, int lane)
+    {
+        const int g0 = 4 * t + 2 * h;
+        const bool la = g0 < G, lb = g0 + 1 < G;
+        const uint32_t F0 = 16 * (uint32_t)(t >> 2);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const uint32_t F = sg[j] + F0;
+            // shift of a moved chunk; a live group's position is at most 15, and the clamp keeps reads of
+            // dead groups (masked below) within the chunk buffer and its 64-byte pad
+            const uint32_t pos = min((F - min(F, slim)) + 4 * (t & 3) + 2 * h, 15u);
+            const uint32_t col = (uint32_t)(wave * 32 * TN + 32 * j + (lane & 31));
+            const unsigned char* ps = lds + buf + col * 32 + pos * 2;
+            const uint32_t s0 = *(const uint16_t*)ps, s1 = *(const uint16_t*)(ps + 2);
+            f[j].s[0] = la ? s0 : 0u;
+            f[j].s[1] = lb ? s1 : 0u;
+            if constexpr (FMT != FMT_Q8) {
+                const uint32_t m0 = *(const uint16_t*)(ps + T::SPLANE), m1 = *(const uint16_t*)(ps + T::SPLANE + 2);
+                f[j].m[0] = la ? m0 : 0u;
+                f[j].m[1] = lb ? m1 : 0u;
+            } else {
+                f[j].m[0] = f[j].m[1] = 0u;
+            }
+        }
+    }
+};
+
+// Dequantize 8 codes to 4 packed f16 pairs (codes j and j + 4 in pair j). A code q placed in the
+// mantissa of 1024.0h reads as 1024 + q (or 1024 + 16 q one nibble higher, which the scale s / 16
+// undoes); one packed subtract and one packed FMA give the dequantized pair (q s + m). The pairs
+// (j, j + 4) match the [0 4 1 5 2 6 3 7] order of the staged x.
+// Mask and exponent constants of the dequantization, held in VGPRs so that a mask-and-insert is one
+// v_and_or_b32 (a VOP3 instruction here takes no literal operand, and with literals the compiler
+// emits a v_and_b32 / v_or_b32 pair instead).
+struct DeqConst {
+    uint32_t lo4, hi4, e1024, lo2;
+    __device__ __forceinline__ static DeqConst make()
+    {
+        DeqConst k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x00030003u};
+        asm volatile("" : "+v"(k.lo4), "+v"(k.hi4), "+v"(k.e1024), "+v"(k.lo2));
+        return k;
+    }
+};
+
 // q4: the low nibble of each byte lands on the mantissa units, the high nibble 16 units up.
-__device__ __forceinline__ u32x4_t deq8_q4(uint32_t w, half2_t s2, half2_t s2_16, half2_t m2)
+__device__ __forceinline__ u32x4_t deq8_q4(uint32_t w, half2_t s2, half2_t s2_16, half2_t m2, const DeqConst& k)
 {
     const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
     const uint32_t w8 = w >> 8;
     u32x4_t r;
-    r[0] = as_u32(__builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | 0x64006400u) - k1024, s2, m2));
-    r[1] = as_u32(__builtin_elementwise_fma(as_h2((w & 0x00F000F0u) | 0x64006400u) - k1024, s2_16, m2));
-    r[2] = as_u32(__builtin_elementwise_fma(as_h2((w8 & 0x000F000Fu) | 0x64006400u) - k1024, s2, m2));
-    r[3] = as_u32(__builtin_elementwise_fma(as_h2((w8 & 0x00F000F0u) | 0x64006400u) - k1024, s2_16, m2));
+    r[0] = as_u32(__builtin_elementwise_fma(as_h2((w & k.lo4) | k.e1024) - k1024, s2, m2));
+    r[1] = as_u32(__builtin_elementwise_fma(as_h2((w & k.hi4) | k.e1024) - k1024, s2_16, m2));
+    r[2] = as_u32(__builtin_elementwise_fma(as_h2((w8 & k.lo4) | k.e1024) - k1024, s2, m2));
+    r[3] = as_u32(__builtin_elementwise_fma(as_h2((w8 & k.hi4) | k.e1024) - k1024, s2_16, m2));
     return r;
 }
 
 // q3: `lo16` 8 two-bit fields, `hi8` their high bits.
-__device__ __forceinline__ u32x4_t deq8_q3(uint32_t lo16, uint32_t hi8, half2_t s2, half2_t m2)
+__device__ __forceinline__ u32x4_t deq8_q3(uint32_t lo16, uint32_t hi8, half2_t s2, half2_t m2, const DeqConst& k)
 {
     const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
     // code j sits at bits 2j of L and code j + 4 at bits 16 + 2j; high bits likewise at 2 + j, 18 + j of H
@@ -227,7 +333,7 @@ __device__ __forceinline__ u32x4_t deq8_q3(uint32_t lo16, uint32_t hi8, half2_t 
     u32x4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t c = ((L >> (2 * j)) & 0x00030003u) | ((H >> j) & 0x00040004u) | 0x64006400u;
+        const uint32_t c = ((L >> (2 * j)) & k.lo2) | ((H >> j) & 0x00040004u) | k.e1024;
         r[j] = as_u32(__builtin_elementwise_fma(as_h2(c) - k1024, s2, m2));
     }
     return r;
@@ -249,19 +355,42 @@ __device__ __forceinline__ u32x4_t deq8_q8(uint32_t w, uint32_t w2, half2_t s2)
     return r;
 }
 
-// B operand of k-slice kk from one lane's group: codes 8 kk .. 8 kk + 7, scale / min bits s, m.
+// Per-group scale operands of one column block for the current step: packed splats of the scale,
+// scale / 16 (q4 high nibbles) and min of groups e = 0, 1.
+struct GroupOps {
+    half2_t s2[2], s16[2], m2[2];
+    DeqConst k;
+};
+
 template <int FMT>
-__device__ __forceinline__ half8_t b_frag(const WCodes<FMT>& f, int kk, _Float16 s, _Float16 m)
+__device__ __forceinline__ GroupOps group_ops(const WCodes<FMT>& f, const DeqConst& k)
 {
-    const half2_t s2 = {s, s}, m2 = {m, m};
+    GroupOps o;
+    o.k = k;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)f.s[e]);
+        const _Float16 m = __builtin_bit_cast(_Float16, (uint16_t)f.m[e]);
+        const _Float16 s16 = s * (_Float16)0.0625f;     // exact for normal scales >= 2^-10
+        o.s2[e] = half2_t{s, s};
+        o.s16[e] = half2_t{s16, s16};
+        o.m2[e] = half2_t{m, m};
+    }
+    return o;
+}
+
+// B operand of slice sl (0..7): codes 8 (sl & 3) .. + 7 of group sl >> 2.
+template <int FMT>
+__device__ __forceinline__ half8_t b_frag(const WCodes<FMT>& f, const GroupOps& g, int sl)
+{
+    const int e = sl >> 2, c = sl & 3;
     u32x4_t o;
     if constexpr (FMT == FMT_Q4) {
-        const _Float16 s16 = s * (_Float16)0.0625f;     // exact for normal scales >= 2^-10
-        o = deq8_q4(f.w[kk], s2, half2_t{s16, s16}, m2);
+        o = deq8_q4(f.w[sl], g.s2[e], g.s16[e], g.m2[e], g.k);
     } else if constexpr (FMT == FMT_Q8) {
-        o = deq8_q8(f.w[2 * kk], f.w[2 * kk + 1], s2);
+        o = deq8_q8(f.w[2 * sl], f.w[2 * sl + 1], g.s2[e]);
     } else {
-        o = deq8_q3((f.w[kk >> 1] >> (16 * (kk & 1))) & 0xffffu, (f.w[2] >> (8 * kk)) & 0xffu, s2, m2);
+        o = deq8_q3((f.w[2 * e + (c >> 1)] >> (16 * (c & 1))) & 0xffffu, (f.w[4 + e] >> (8 * c)) & 0xffu, g.s2[e], g.m2[e], g.k);
     }
     return __builtin_bit_cast(half8_t, o);
 }
@@ -274,52 +403,80 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Wait until at most N vector-memory loads of this wave are in flight. The compiler does not track
+// direct global->LDS loads as writers of LDS, so their completion is waited for explicitly (they
+// complete in issue order with the other loads).
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Barrier between pipeline steps. A fence here would make the compiler wait for every direct
+// global->LDS load in flight (it counts them as LDS writes), including the ones issued for two steps
+// ahead; the LDS reads of this wave are waited for here, its direct loads by wait_vm before the call.
+// The memory clobber keeps LDS accesses on their side of the barrier.
+__device__ __forceinline__ void step_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// One step of the multiply loop, 8 slices. On entry a[0] and b[0] hold the operands of slice 0,
+// prepared by the previous step. Slice sl reads and dequantizes the operands of slice sl + 1 while its
+// MFMAs run; slices 6-7 prepare slice 0 of the next step (its scales, codes and x). Loads: W codes of
+// step t + 1 in slices 0-1; at slice 4 the wave waits for the loads of earlier steps (x step t + 1
+// among them) and meets the other waves at the barrier, after which x step t + 1 may be read and the
+// buffer of step t - 1 refilled: x step t + 2 goes there over slices 4-7, and at the first step of a
+// scale chunk the next chunk is loaded.
 template <int FMT, class T>
-__device__ __forceinline__ void mma_step(const _Float16* A, const WCodes<FMT> (&wc)[T::TN],
-                                         const u32x4_t (&sv)[T::TN], const u32x4_t (&mv)[T::TN],
-                                         const uint32_t (&sg)[T::TN], uint32_t lim, floatx4_t (&acc)[T::TM][T::TN],
-                                         int t, int lane, int q, int G)
+__device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_t (&aoff)[8], uint32_t abuf,
+                                         uint32_t anext, const WCodes<FMT> (&wc)[T::TN], const GroupOps (&go)[T::TN],
+                                         half8_t (&a)[2][T::TM], half8_t (&b)[2][T::TN],
+                                         floatx16_t (&acc)[T::TM][T::TN], Loader<FMT, T>& ld,
+                                         WCodes<FMT> (&wn)[T::TN], GroupOps (&gn)[T::TN], int t, int xstep,
+                                         uint32_t xbuf, bool schunk, int sv, uint32_t sdst, uint32_t snext, int lane)
 {
     constexpr int TM = T::TM, TN = T::TN;
-    const bool live = 4 * t + q < G;
-    _Float16 s[TN], m[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const uint32_t sb = sm_pick(sv[j], sg[j], t >> 1, t & 1, q, lim);
-        const uint32_t mb = FMT != FMT_Q8 ? sm_pick(mv[j], sg[j], t >> 1, t & 1, q, lim) : 0u;
-        s[j] = live ? __builtin_bit_cast(_Float16, (uint16_t)sb) : (_Float16)0.f;
-        m[j] = (FMT != FMT_Q8 && live) ? __builtin_bit_cast(_Float16, (uint16_t)mb) : (_Float16)0.f;
-    }
-    // k-slice kk + 1 is dequantized while the MFMAs of k-slice kk run: the scheduling groups below
-    // interleave one MFMA with two VALU instructions
-    half8_t b[TN];
+    for (int sl = 0; sl < 8; ++sl) {
+        const int cur = sl & 1, nxt = cur ^ 1;
+        if (sl == Loader<FMT, T>::XS) {
+            wait_vm<Loader<FMT, T>::W_OPS>();
+            step_barrier();
+            if (schunk) ld.scale_chunk(sv, sdst);
+        }
+        ld.issue(sl, wn, xstep, xbuf);
+        if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
+        if (sl < 7) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b[j] = b_frag<FMT>(wc[j], 0, s[j], m[j]);
+            for (int i = 0; i < TM; ++i) a[nxt][i] = *(const half8_t*)(lds + abuf + aoff[sl + 1] + i * 32 * XROW);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        half8_t a[TM], bn[TN];
+            for (int j = 0; j < TN; ++j) b[nxt][j] = b_frag<FMT>(wc[j], go[j], sl + 1);
+        } else {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-            a[i] = *(const half8_t*)(A + (i * 16 + (lane & 15)) * ALD + 32 * q + 8 * kk);
-        if (kk < 3) {
+            for (int i = 0; i < TM; ++i) a[nxt][i] = *(const half8_t*)(lds + anext + aoff[0] + i * 32 * XROW);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bn[j] = b_frag<FMT>(wc[j], kk + 1, s[j], m[j]);
+            for (int j = 0; j < TN; ++j) {
+                gn[j] = group_ops<FMT>(wn[j], go[j].k);
+                b[nxt][j] = b_frag<FMT>(wn[j], gn[j], 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);       // the A fragment reads first
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+        // the next slice's A reads first, then each MFMA with a share of the dequantization; the
+        // scheduling barrier keeps every slice's reads one slice ahead of their use
+        constexpr int VALU_PER = (FMT == FMT_Q8 ? 12 : 16) * TN / (TM * TN);
+        __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
 #pragma unroll
         for (int g = 0; g < TM * TN; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);    // two VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER > 0 ? VALU_PER : 1, 0);
         }
-        if (kk < 3) {
-#pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = bn[j];
-        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -330,10 +487,8 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
                                           float* __restrict__ y, int M, int K, int N,
                                           const int* __restrict__ row_off, int E)
 {
-    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, XC = T::XC, NT = T::NT;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[T::SMEM];
-    _Float16* const As0 = reinterpret_cast<_Float16*>(smem);
-    _Float16* const As1 = As0 + BM * ALD;
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, XI = T::XI, NT = T::NT;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
 
     const int G = K / BRIK_GROUP;
     const int Kp = (K + 2 * GK - 1) / (2 * GK) * (2 * GK);
@@ -371,7 +526,8 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         n0 = nt * BN;
     }
 
-    // buffer resources: the staged x rows of this launch; the W planes of this matrix (expert slice)
+    // buffer resources: the staged x rows of this launch; the W planes of this matrix (expert slice);
+    // the scales and mins of the whole (stacked) plane
     const size_t wel = (size_t)N * K;          // elements of one weight matrix
     const size_t gbase = (size_t)e * N * G;    // flat group offset of the expert slice
     const brsrc_t rx = make_rsrc(xh, (uint32_t)((size_t)M * Kp * 2));
@@ -384,105 +540,106 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         r0 = make_rsrc(p0 + (size_t)e * wel / 4, (uint32_t)(wel / 4));
         r1 = make_rsrc(p1 + (size_t)e * wel / 8, (uint32_t)(wel / 8));
     }
-    // scales and mins: one resource over the whole (stacked) plane, so scale windows of one expert
-    // may extend into the next; lim = last window start that ends inside the plane (the host routes
-    // planes of fewer than 8 groups elsewhere)
     const uint32_t sgroups = (uint32_t)((size_t)(row_off ? E : 1) * N * G);
-    const uint32_t lim = sgroups - 8;
     rsc = make_rsrc(sc, sgroups * 2);
     if constexpr (FMT != FMT_Q8) rmn = make_rsrc(mn, sgroups * 2);
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, q = lane >> 4;
-    // x staging: chunk c = tid + 256 i is row c / 16, 16-byte part c % 16 of the step's 256-byte row slice
-    uint32_t xoff[XC];
+    const int tid = threadIdx.x, lane = tid & 63;
+    Loader<FMT, T> ld;
+    ld.p0 = r0; ld.p1 = r1; ld.rsc = rsc; ld.rmn = rmn; ld.rx = rx;
+    ld.h = lane >> 5; ld.G = G; ld.lds = smem;
+    ld.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = ld.h, wave = ld.wave;
+    // x staging: this lane's chunk of each direct-load instruction (row 4 (4 i + wave) + (lane >> 4),
+    // stored chunk lane & 15, which holds logical chunk (lane & 15) ^ (row & 15))
 #pragma unroll
-    for (int i = 0; i < XC; ++i) {
-        const int c = tid + NT * i;
-        const int m = min(m0 + (c >> 4), m_end - 1);      // rows past the tile's end repeat a live row
-        xoff[i] = (uint32_t)(m * Kp + (c & 15) * 8) * 2;
+    for (int i = 0; i < XI; ++i) {
+        const int r = 4 * (4 * i + wave) + (lane >> 4);
+        const int m = min(m0 + r, m_end - 1);      // rows past the tile's end repeat a live row
+        ld.xoff[i] = (uint32_t)(m * Kp + (((lane & 15) ^ (r & 15)) * 8)) * 2;
     }
-    // W: flat group index of this lane's column in fragment j, at group 0
-    const int wn = wave * 16 * TN;
-    uint32_t colg[TN], sg[TN];
+    // A fragments of slice sl: row lane & 31 of a 32-row block, logical chunk 8 h + sl
+    uint32_t aoff[8];
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) aoff[sl] = (uint32_t)((lane & 31) * XROW + (((8 * h + sl) ^ (lane & 15)) * 16));
+    // W: flat group index of this lane's column in column block j, at group 0
+    const int wn = wave * 32 * TN;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        colg[j] = (uint32_t)(min(n0 + wn + 16 * j + (lane & 15), N - 1) * G);
-        sg[j] = (uint32_t)gbase + colg[j];         // the same group in the whole scale plane
+        ld.colg[j] = (uint32_t)(min(n0 + wn + 32 * j + (lane & 31), N - 1) * G);
+        ld.sg[j] = (uint32_t)gbase + ld.colg[j];   // the same group in the whole scale plane
+    }
+    // scale chunks (the host routes planes of fewer than 16 groups elsewhere)
+    ld.slim = sgroups - 16;
+#pragma unroll
+    for (int k = 0; k < T::NSD; ++k) {
+        const int gi = 4 * k + wave, cb = gi % (BN / 32), plane = gi / (BN / 32);
+        ld.sdc[k] = (uint32_t)gbase + (uint32_t)(min(n0 + 32 * cb + (lane >> 1), N - 1) * G);
+        ld.sdst[k] = (uint32_t)(plane * T::SPLANE + cb * 1024);
     }
 
-    floatx4_t acc[TM][TN];
+    floatx16_t acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // Prologue: step 0 of x into LDS buffer 0, step 0 of W and the scales of steps 0 and 1 into
-    // registers.
-    u32x4_t xs[XC];
+    // Prologue: W codes of step 0 into registers, scale chunk 0 and x steps 0 and 1 into LDS, then
+    // the operands of slice 0 of step 0.
     WCodes<FMT> wc[TN], wn_[TN];
-    u32x4_t sv[TN], mv[TN] = {};
+    GroupOps go[TN], gn[TN];
+    half8_t a[2][TM], b[2][TN];
+    ld.begin(0);
 #pragma unroll
-    for (int i = 0; i < XC; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[i], 0, 0);
-    w_load<FMT, TN>(wc, r0, r1, colg, 0, q, G);
-    sm_load<TN>(sv, rsc, sg, 0, lim);
-    if constexpr (FMT != FMT_Q8) sm_load<TN>(mv, rmn, sg, 0, lim);
+    for (int u = 0; u < ld.W_OPS; ++u) ld.op(u, wc, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    ld.scale_chunk(0, T::S_OFF);
 #pragma unroll
-    for (int i = 0; i < XC; ++i) {
-        const int c = tid + NT * i;
-        *(u32x4_t*)(As0 + (c >> 4) * ALD + (c & 15) * 8) = xs[i];
+    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wc, 0, 0);
+#pragma unroll
+    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wc, 1, T::XBUF);
+    wait_vm<XI>();
+    step_barrier();
+    ld.read_scales(wc, 0, T::S_OFF, lane);
+    const DeqConst dk = DeqConst::make();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[0][i] = *(const half8_t*)(smem + aoff[0] + i * 32 * XROW);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        go[j] = group_ops<FMT>(wc[j], dk);
+        b[0][j] = b_frag<FMT>(wc[j], go[j], 0);
     }
-    lds_barrier();
 
-    // Steps in pairs (t, t + 1). Step t: issue the loads of step t + 1 (x to registers, W to the next
-    // fragment set), multiply step t (x from LDS buffer t & 1, W dequantized from registers one
-    // k-slice at a time), then store x of step t + 1 to the other LDS buffer. The scales of a pair
-    // arrive with the first step's loads of the previous pair. The last step's extra loads are
-    // clamped.
-    u32x4_t svn[TN], mvn[TN] = {};
-    for (int t = 0; t < steps; t += 2) {
-        // -- step t
-#pragma unroll
-        for (int i = 0; i < XC; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[i], (t + 1) * (GK * 2), 0);
-        w_load<FMT, TN>(wn_, r0, r1, colg, t + 1, q, G);
-        const int un = min(t / 2 + 1, steps / 2 - 1);
-        sm_load<TN>(svn, rsc, sg, un, lim);
-        if constexpr (FMT != FMT_Q8) sm_load<TN>(mvn, rmn, sg, un, lim);
-        __builtin_amdgcn_sched_barrier(0);     // keep the loads ahead of the multiplies
-        mma_step<FMT, T>(As0, wc, sv, mv, sg, lim, acc, t, lane, q, G);
-#pragma unroll
-        for (int i = 0; i < XC; ++i) {
-            const int c = tid + NT * i;
-            *(u32x4_t*)(As1 + (c >> 4) * ALD + (c & 15) * 8) = xs[i];
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) wc[j] = wn_[j];
-        lds_barrier();
-
-        // -- step t + 1
-        const int tn = min(t + 2, steps - 1);
-#pragma unroll
-        for (int i = 0; i < XC; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff[i], tn * (GK * 2), 0);
-        w_load<FMT, TN>(wn_, r0, r1, colg, tn, q, G);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_step<FMT, T>(As1, wc, sv, mv, sg, lim, acc, t + 1, lane, q, G);
-#pragma unroll
-        for (int i = 0; i < XC; ++i) {
-            const int c = tid + NT * i;
-            *(u32x4_t*)(As0 + (c >> 4) * ALD + (c & 15) * 8) = xs[i];
-        }
+    // Step t multiplies x step t (LDS buffer b0) by W step t (wc); b1 holds x step t + 1, b2 the buffer
+    // of step t - 1, refilled with x step t + 2 once every wave is past the barrier of step t. Loads
+    // past the end are clamped, and the operands prepared for step `steps` are not used.
+    uint32_t b0 = 0, b1 = T::XBUF, b2 = 2 * T::XBUF;
+    const int nchunks = (steps + 3) / 4;
+    int t = 0;
+    do {     // steps >= 2: no loop guard for the prologue loads to sink past
+        ld.begin(min(t + 1, steps - 1));
+        const int v = t >> 2;
+        mma_step<FMT, T>(smem, aoff, b0, b1, wc, go, a, b, acc, ld, wn_, gn, t, min(t + 2, steps - 1), b2,
+                         (t & 3) == 0, min(v + 1, nchunks - 1), T::S_OFF + ((v + 1) & 1) * T::SBUF,
+                         T::S_OFF + (((t + 1) >> 2) & 1) * T::SBUF, lane);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             wc[j] = wn_[j];
-            sv[j] = svn[j];
-            mv[j] = mvn[j];
+            go[j] = gn[j];
         }
-        lds_barrier();
-    }
+        const uint32_t bt = b0; b0 = b1; b1 = b2; b2 = bt;
+        ++t;
+    } while (t < steps);
+    // the clamped loads of the last two steps may still be writing LDS, which the epilogue reuses
+    wait_vm<0>();
+    lds_barrier();
 
-    // Epilogue, RF row fragments per round: the accumulators are staged in LDS (D layout of a 16x16
-    // tile: lane holds column lane & 15, rows 4 q + r), then every thread scales 4 consecutive
-    // columns of one row by rscale and stores them with one 16-byte store (N % 4 == 0) or four
-    // 4-byte stores.
+    // Epilogue, RF row blocks per round: the accumulators are staged in LDS (D layout of a 32x32
+    // tile: lane holds column lane & 31, register r row 8 (r >> 2) + 4 h + (r & 3)), then every thread
+    // scales 4 consecutive columns of one row by rscale and stores them with one 16-byte store
+    // (N % 4 == 0) or four 4-byte stores.
     float* const Cs = reinterpret_cast<float*>(smem);
     constexpr int CH = BN / 4;                      // 4-column chunks per row
 #pragma unroll
@@ -493,12 +650,12 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 #pragma unroll
             for (int j = 0; j < TN; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    Cs[(ii * 16 + 4 * q + r) * T::CLD + wn + 16 * j + (lane & 15)] = acc[i0 + ii][j][r];
+                for (int r = 0; r < 16; ++r)
+                    Cs[(ii * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) * T::CLD + wn + 32 * j + (lane & 31)] = acc[i0 + ii][j][r];
         lds_barrier();
-        for (int c = tid; c < T::RF * 16 * CH; c += NT) {
+        for (int c = tid; c < T::RF * 32 * CH; c += NT) {
             const int row = c / CH, col = (c % CH) * 4;
-            const int m = m0 + i0 * 16 + row, n = n0 + col;
+            const int m = m0 + i0 * 32 + row, n = n0 + col;
             if (m >= m_end || n >= N) continue;
             const f32x4_t v = *(const f32x4_t*)(Cs + row * T::CLD + col) * rscale[m];
             float* dst = y + (size_t)m * N + n;
@@ -515,7 +672,7 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 
 }  // namespace
 
-// Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 64 TN), 256 threads (4 waves) each; the
+// Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN), 256 threads (4 waves) each; the
 // runtime picks the tile.
 #define BRIK_GEMM(FMTN, FMT, BM_, TN_)                                                                    \
     extern "C" __global__ __launch_bounds__(256) void brik_gemm_##FMTN##_##BM_##x##TN_(                   \
@@ -523,14 +680,15 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
         float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E)               \
     {                                                                                                     \
-        gemm_body<FMT, Tile<BM_, TN_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E);               \
+        gemm_body<FMT, Tile<FMT, BM_, TN_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E);               \
     }
 
 // Tiles in the order of the runtime's table: (BM, TN).
 #define BRIK_GEMM_FMT(FMTN, FMT)                                                       \
-    BRIK_GEMM(FMTN, FMT, 128, 3) BRIK_GEMM(FMTN, FMT, 128, 2) BRIK_GEMM(FMTN, FMT, 128, 4) \
-    BRIK_GEMM(FMTN, FMT, 64, 3) BRIK_GEMM(FMTN, FMT, 64, 2) BRIK_GEMM(FMTN, FMT, 64, 4)    \
-    BRIK_GEMM(FMTN, FMT, 32, 3) BRIK_GEMM(FMTN, FMT, 32, 2) BRIK_GEMM(FMTN, FMT, 32, 4)
+    BRIK_GEMM(FMTN, FMT, 128, 2) BRIK_GEMM(FMTN, FMT, 128, 1) BRIK_GEMM(FMTN, FMT, 128, 3) \
+    BRIK_GEMM(FMTN, FMT, 64, 2) BRIK_GEMM(FMTN, FMT, 64, 1) BRIK_GEMM(FMTN, FMT, 64, 3)    \
+    BRIK_GEMM(FMTN, FMT, 32, 2) BRIK_GEMM(FMTN, FMT, 32, 1) BRIK_GEMM(FMTN, FMT, 32, 3)    \
+    BRIK_GEMM(FMTN, FMT, 96, 2) BRIK_GEMM(FMTN, FMT, 96, 1) BRIK_GEMM(FMTN, FMT, 96, 3)
 
 BRIK_GEMM_FMT(q4, FMT_Q4)
 BRIK_GEMM_FMT(q8, FMT_Q8)

@@ -90,7 +90,7 @@ int brik_matmul_t_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const ui
  * e*N*K/2 bytes, its scales and mins at index e*N*K/32 of their planes).
  * row_off: DEVICE int32[E + 1], non-decreasing, row_off[0] == 0, row_off[E] == R, the number of
  * rows of x_sorted and y_sorted. The grid is sized from R and E alone (ceil(R/BM) + E row tiles),
- * so routing can stay on the device. Requires 256 <= E*N*K < 2^35 (BRIK_EINVAL otherwise). */
+ * so routing can stay on the device. Requires 512 <= E*N*K < 2^35 (BRIK_EINVAL otherwise). */
 int brik_moe_matmul_t_q4(brik_ctx *ctx, const float *x_sorted, const int32_t *row_off,
                          const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
                          float *y_sorted, int E, int R, int K, int N);
@@ -145,9 +145,9 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
 #define BRIK_OPT_GEMV_VARIANT 2  /* 0 auto, else 1 + index of a GEMV tiling variant (see brik_runtime.cpp) */
 #define BRIK_GEMV_VARIANTS 7
 #define BRIK_OPT_GEMM_TILE 3     /* 0 auto, else 1 + index of an MFMA GEMM block tile (rows x columns):
-                                    1 128x192, 2 128x128, 3 128x256, 4 64x192, 5 64x128, 6 64x256,
-                                    7 32x192, 8 32x128, 9 32x256 */
-#define BRIK_GEMM_TILES 9
+                                    1 128x256, 2 128x128, 3 128x384, 4 64x256, 5 64x128, 6 64x384,
+                                    7 32x256, 8 32x128, 9 32x384, 10 96x256, 11 96x128, 12 96x384 */
+#define BRIK_GEMM_TILES 12
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus
