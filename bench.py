@@ -156,6 +156,30 @@ def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
             "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
 
 
+def lm_head_topk_cfg3(ctx, steps, warmup, gemv_us, cache_bytes=768 << 20):
+    """The cfg 3 q3 LM head fused with the sampling pre-work (softcap 30, penalty 1.15 over 40 recent
+    ids, top 64), as decodeTopKQ8 records them; and the passes alone over 151936 logits."""
+    from brimkern_amd import synth
+    K, N, k = 2560, 151936, 64
+    t = synth.tensor("q3", 700, N, K)
+    copies = max(2, -(-cache_bytes // q_bytes("q3", N, K)))
+    r = Replicas(ctx, "q3", t, copies)
+    x = ctx.upload(synth.normal(701, K))
+    rec = ctx.upload(np.unique((synth.uniform(702, 40) * N).astype(np.int32)))
+    nrec = int(rec.nbytes // 4)
+    out = ctx.alloc(8 * k)
+    ms = time_loop(ctx, lambda i: ctx.lm_head_topk("q3", x, r.planes(i % copies), K, N, rec, nrec, 1.15, 30.0, k,
+                                                  out, out.offset(4 * k)), max(steps, copies), copies)
+    logits = ctx.upload(synth.normal(703, N) * 4)
+    ms_p = time_loop(ctx, lambda i: ctx.logits_topk(logits, N, rec, nrec, 1.15, 30.0, k, out, out.offset(4 * k)),
+                     steps, warmup)
+    for bb in (r.buf, x, rec, out, logits):
+        ctx.free(bb)
+    return {"us": round(ms * 1e3, 2), "passes_alone_us": round(ms_p * 1e3, 2),
+            "over_gemv_us": round(ms * 1e3 - gemv_us, 2), "readback_bytes": 8 * k,
+            "launches": "brik_gemv_q3 + brik_topk_prep + brik_topk_select"}
+
+
 def gemm_cfg4(ctx, steps, warmup):
     from brimkern_amd import synth
     M, K, N = 512, 2560, 9728
@@ -347,6 +371,9 @@ def main():
         extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)
         log("bench: cfg3 q3 LM head")
         extra["cfg3_q3_gemv_K2560_N151936"] = gemv_single_cfg(ctx, "q3", 2560, 151936, 700, args.steps, args.warmup)
+        log("bench: cfg3 LM head + sampling pre-work")
+        extra["f2_lm_head_topk_q3_K2560_N151936"] = lm_head_topk_cfg3(
+            ctx, args.steps, args.warmup, extra["cfg3_q3_gemv_K2560_N151936"]["us"])
         log("bench: cfg4 q4 GEMM")
         extra["cfg4_q4_gemm_M512_K2560_N9728"] = gemm_cfg4(ctx, args.steps, args.warmup)
         log("bench: cfg5 MoE")

@@ -47,7 +47,13 @@ SIGNATURES = {
     "brik_gemv_plan_create": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
     "brik_gemv_plan_run": (_I, [_P, _P]),
     "brik_gemv_plan_destroy": (None, [_P, _P]),
+    "brik_logits_topk": (_I, [_P, _P, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
+    "brik_lm_head_topk_q8": (_I, [_P, _P, _P, _P, _I, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
+    "brik_lm_head_topk_q4": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
+    "brik_lm_head_topk_q3": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P,
+                                  _P]),
 }
+BRIK_TOPK_MAX = 64
 
 FMT_CODES = {"q8": 8, "q4": 4, "q3": 3}
 
@@ -226,6 +232,18 @@ class Context:
         self._check(self.lib.brik_gemv_plan_create(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
                                                    ctypes.byref(h)))
         return GemvPlan(self, h)
+
+    # ---- sampling pre-work ----------------------------------------------------------------
+    def logits_topk(self, logits, n, recent, n_recent, penalty, softcap, k, ids, vals):
+        """Softcap, repetition penalty (in place on ``logits``) and the top ``k``, on the stream."""
+        self._check(self.lib.brik_logits_topk(self.handle, _addr(logits), n, _addr(recent), n_recent, penalty,
+                                              softcap, k, _addr(ids), _addr(vals)))
+
+    def lm_head_topk(self, fmt: str, x, planes, K, vocab, recent, n_recent, penalty, softcap, k, ids, vals):
+        """``x . deq(W)^T`` over the vocab, then :meth:`logits_topk` on the logits (a workspace)."""
+        tail = (K, vocab, _addr(recent), n_recent, penalty, softcap, k, _addr(ids), _addr(vals))
+        fn = getattr(self.lib, f"brik_lm_head_topk_{fmt}")
+        self._check(fn(self.handle, _addr(x), *[_addr(p) for p in planes], *tail))
 
     def dequant_q8(self, codes, sc, out, n):
         self._check(self.lib.brik_dequant_q8_f32(self.handle, _addr(codes), _addr(sc), _addr(out), n))

@@ -69,6 +69,17 @@ bool get_i32(napi_env env, napi_value v, int32_t* out)
     return true;
 }
 
+bool get_f32(napi_env env, napi_value v, float* out)
+{
+    double d;
+    if (napi_get_value_double(env, v, &d) != napi_ok) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a number");
+        return false;
+    }
+    *out = (float)d;
+    return true;
+}
+
 // A device pointer: BigInt address, null/undefined (-> nullptr), or an object with a BigInt `ptr`.
 bool get_ptr(napi_env env, napi_value v, void** out)
 {
@@ -355,6 +366,54 @@ napi_value DequantQ3(napi_env env, napi_callback_info info)   // (ctx, lo, hi, s
     return undefined(env);
 }
 
+// ---- sampling pre-work -------------------------------------------------------------------------
+
+// logitsTopK(ctx, logits, recent, ids, vals, n, nRecent, k, penalty, softcap)
+napi_value LogitsTopK(napi_env env, napi_callback_info info)
+{
+    brik_ctx* c; void* p[4]; int32_t i[3];
+    if (!parse(env, info, &c, p, 4, i, 3)) return nullptr;
+    Args a;
+    float pen, cap;
+    if (!get_args(env, info, a, 10) || !get_f32(env, a.v[8], &pen) || !get_f32(env, a.v[9], &cap)) return nullptr;
+    if (check(env, c, brik_logits_topk(c, (float*)p[0], i[0], (const int32_t*)p[1], i[1], pen, cap, i[2],
+                                       (int32_t*)p[2], (float*)p[3]))) return nullptr;
+    return undefined(env);
+}
+
+// lmHeadTopK(ctx, fmt, x, p0, p1, sc, mn, recent, ids, vals, K, vocab, nRecent, k, penalty, softcap)
+napi_value LmHeadTopK(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 16)) return nullptr;
+    brik_ctx* c;
+    int32_t fmt, iv[4];
+    void* p[8];
+    float pen, cap;
+    if (!get_ctx(env, a.v[0], &c) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    for (int k = 0; k < 8; ++k)
+        if (!get_ptr(env, a.v[2 + k], &p[k])) return nullptr;
+    for (int k = 0; k < 4; ++k)
+        if (!get_i32(env, a.v[10 + k], &iv[k])) return nullptr;
+    if (!get_f32(env, a.v[14], &pen) || !get_f32(env, a.v[15], &cap)) return nullptr;
+    const float* x = (const float*)p[0];
+    const int32_t* rec = (const int32_t*)p[5];
+    int32_t* ids = (int32_t*)p[6];
+    float* vals = (float*)p[7];
+    int rc;
+    if (fmt == BRIK_FMT_Q8)
+        rc = brik_lm_head_topk_q8(c, x, (const int8_t*)p[1], (const uint16_t*)p[3], iv[0], iv[1], rec, iv[2], pen, cap,
+                                  iv[3], ids, vals);
+    else if (fmt == BRIK_FMT_Q4)
+        rc = brik_lm_head_topk_q4(c, x, (const uint8_t*)p[1], (const uint16_t*)p[3], (const uint16_t*)p[4], iv[0], iv[1],
+                                  rec, iv[2], pen, cap, iv[3], ids, vals);
+    else
+        rc = brik_lm_head_topk_q3(c, x, (const uint32_t*)p[1], (const uint32_t*)p[2], (const uint16_t*)p[3],
+                                  (const uint16_t*)p[4], iv[0], iv[1], rec, iv[2], pen, cap, iv[3], ids, vals);
+    if (check(env, c, rc)) return nullptr;
+    return undefined(env);
+}
+
 // ---- grouped GEMV plans ----------------------------------------------------------------------
 
 struct PlanBox {
@@ -451,6 +510,8 @@ napi_value Init(napi_env env, napi_value exports)
         {"dequantQ8", nullptr, DequantQ8, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ4", nullptr, DequantQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ3", nullptr, DequantQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"logitsTopK", nullptr, LogitsTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"lmHeadTopK", nullptr, LmHeadTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanRun", nullptr, GemvPlanRun, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanDestroy", nullptr, GemvPlanDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

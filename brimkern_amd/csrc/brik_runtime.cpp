@@ -24,12 +24,14 @@ namespace {
 enum Kern {
     K_DEQ_Q8, K_DEQ_Q4, K_DEQ_Q3,
     K_XPREP,
+    K_TOPK_PREP, K_TOPK_SELECT,
     K_COUNT
 };
 
 const char* const kKernelNames[K_COUNT] = {
     "brik_dequant_q8", "brik_dequant_q4", "brik_dequant_q3",
     "brik_xprep_f16",
+    "brik_topk_prep", "brik_topk_select",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -47,7 +49,7 @@ constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 
 constexpr int kGroup = 32;
-// GEMM block tiles (BM rows x 64 TN columns), in the order of BRIK_GEMM_FMT in gemm.hip:
+// GEMM block tiles (BM rows x 128 TN columns), in the order of BRIK_GEMM_FMT in gemm.hip:
 // brik_gemm_<fmt>_<BM>x<TN>.
 struct GemmTile { int bm, tn; };
 constexpr GemmTile kGemmTiles[] = {{128, 2}, {128, 1}, {128, 3}, {64, 2}, {64, 1}, {64, 3},
@@ -93,6 +95,8 @@ struct brik_ctx {
     int opt_tile = 0;      // 0 auto, else 1 + index into kGemmTiles
     void* ws = nullptr;    // GEMM workspace: f16 activation rows, then per-row scales (grow-only)
     size_t ws_bytes = 0;
+    void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
+    size_t tws_bytes = 0;
     char err[512] = {0};
 };
 
@@ -194,22 +198,24 @@ int gemm_tile(brik_ctx* c, long M, long N, int E)
     return best;
 }
 
-// Grow the context workspace to at least `bytes`. Earlier launches on the context stream may still
+// Grow a context workspace to at least `bytes`. Earlier launches on the context stream may still
 // read the old buffer, so the stream is drained before it is freed.
-int ensure_ws(brik_ctx* c, size_t bytes)
+int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
 {
-    if (c->ws_bytes >= bytes) return BRIK_OK;
-    if (c->ws) {
+    if (have >= bytes) return BRIK_OK;
+    if (buf) {
         HIP_TRY(c, hipStreamSynchronize(c->stream));
-        HIP_TRY(c, hipFree(c->ws));
-        c->ws = nullptr;
-        c->ws_bytes = 0;
+        HIP_TRY(c, hipFree(buf));
+        buf = nullptr;
+        have = 0;
     }
     bytes = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-    HIP_TRY(c, hipMalloc(&c->ws, bytes));
-    c->ws_bytes = bytes;
+    HIP_TRY(c, hipMalloc(&buf, bytes));
+    have = bytes;
     return BRIK_OK;
 }
+
+int ensure_ws(brik_ctx* c, size_t bytes) { return ensure_buf(c, c->ws, c->ws_bytes, bytes); }
 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
 // tile kernel; dense when row_off is null, expert-grouped otherwise.
@@ -284,6 +290,63 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
     return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0);
+}
+
+// ---- sampling pre-work -------------------------------------------------------------------------
+
+constexpr int kTopkMax = 64;                      // BRIK_TOPK_MAX, TOPK_MAX in topk.hip
+size_t topk_blocks(int n) { return ((size_t)n + 4095) / 4096; }          // 4 waves x 1024 logits
+size_t topk_maxima(int n) { return 256 * topk_blocks(n); }                // one per lane (16 logits)
+// workspace: lane maxima, then the LM-head logits
+size_t topk_logits_off(int n) { return (4 * topk_maxima(n) + 255) / 256 * 256; }
+
+int check_topk(brik_ctx* c, const char* who, int n, const int32_t* recent, int n_recent, float penalty, int k,
+               const int32_t* ids, const float* vals, bool& pen)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n < 1) return fail(c, BRIK_EINVAL, "%s: n=%d must be >= 1", who, n);
+    if (k < 1 || k > kTopkMax || k > n) return fail(c, BRIK_EINVAL, "%s: k=%d not in [1, min(64, n=%d)]", who, k, n);
+    if (n_recent < 0) return fail(c, BRIK_EINVAL, "%s: n_recent=%d is negative", who, n_recent);
+    // applied when the reference's `penalty && penalty !== 1 && recent.length` holds (kernels.ts:1947)
+    pen = n_recent > 0 && penalty == penalty && penalty != 0.f && penalty != 1.f;
+    if (pen && !recent) return fail(c, BRIK_EINVAL, "%s: recent is null", who);
+    if (pen && !aligned(recent, 4)) return fail(c, BRIK_EALIGN, "%s: recent must be 4-byte aligned", who);
+    if (!ids || !vals) return fail(c, BRIK_EINVAL, "%s: null output pointer", who);
+    if (!aligned(ids, 4) || !aligned(vals, 4)) return fail(c, BRIK_EALIGN, "%s: outputs must be 4-byte aligned", who);
+    return BRIK_OK;
+}
+
+// The passes over a device logits vector (modified in place); the top-k workspace is ensured by the
+// caller. Two launches: brik_topk_prep (softcap, penalty, lane maxima), brik_topk_select (one block:
+// bound, candidates, sort, output).
+int topk_passes(brik_ctx* c, float* logits, int n, const int32_t* recent, int n_recent, float penalty,
+                float softcap, int k, int32_t* ids, float* vals, bool pen)
+{
+    uint32_t* maxima = static_cast<uint32_t*>(c->tws);
+    int peni = pen ? 1 : 0;
+    {
+        void* args[] = {&logits, &n, &softcap, &recent, &n_recent, &penalty, &peni, &maxima};
+        HIP_TRY_RC(launch(c, K_TOPK_PREP, (unsigned)topk_blocks(n), 1, 256, 0, args));
+    }
+    int m = (int)topk_maxima(n);
+    void* args[] = {&logits, &n, &k, &maxima, &m, &ids, &vals};
+    return launch(c, K_TOPK_SELECT, 1, 1, 1024, 0, args);
+}
+
+int ensure_topk_ws(brik_ctx* c, size_t bytes) { return ensure_buf(c, c->tws, c->tws_bytes, bytes); }
+
+int lm_head_topk(brik_ctx* c, const char* who, Fmt f, const float* x, const void* p0, const void* p1,
+                 const void* sc, const void* mn, int K, int vocab, const int32_t* recent, int n_recent,
+                 float penalty, float softcap, int k, int32_t* ids, float* vals)
+{
+    bool pen = false;
+    HIP_TRY_RC(check_topk(c, who, vocab, recent, n_recent, penalty, k, ids, vals, pen));
+    if (K < 1) return fail(c, BRIK_EINVAL, "%s: K=%d must be >= 32", who, K);
+    HIP_TRY_RC(ensure_topk_ws(c, topk_logits_off(vocab) + (size_t)vocab * 4));
+    float* logits = reinterpret_cast<float*>(static_cast<char*>(c->tws) + topk_logits_off(vocab));
+    HIP_TRY_RC(check_mm(c, who, x, p0, p1, sc, mn, logits, 1, K, vocab, f));
+    HIP_TRY_RC(matmul(c, f, x, p0, p1, sc, mn, logits, 1, K, vocab));
+    return topk_passes(c, logits, vocab, recent, n_recent, penalty, softcap, k, ids, vals, pen);
 }
 
 }  // namespace
@@ -369,6 +432,7 @@ void brik_destroy(brik_ctx* c)
     if (c->ev_end) (void)hipEventDestroy(c->ev_end);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->tws) (void)hipFree(c->tws);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
 }
@@ -575,6 +639,41 @@ void brik_gemv_plan_destroy(brik_ctx* c, brik_gemv_plan* p)
     if (!p) return;
     if (c) brik_free(c, p->dev);
     delete p;
+}
+
+int brik_logits_topk(brik_ctx* c, float* logits, int n, const int32_t* recent, int n_recent, float penalty,
+                     float softcap, int k, int32_t* out_ids, float* out_vals)
+{
+    bool pen = false;
+    HIP_TRY_RC(check_topk(c, "logits_topk", n, recent, n_recent, penalty, k, out_ids, out_vals, pen));
+    if (!logits) return fail(c, BRIK_EINVAL, "logits_topk: logits is null");
+    if (!aligned(logits, 4)) return fail(c, BRIK_EALIGN, "logits_topk: logits must be 4-byte aligned");
+    HIP_TRY_RC(ensure_topk_ws(c, topk_logits_off(n)));
+    return topk_passes(c, logits, n, recent, n_recent, penalty, softcap, k, out_ids, out_vals, pen);
+}
+
+int brik_lm_head_topk_q8(brik_ctx* c, const float* x, const int8_t* codes, const uint16_t* sc, int K, int vocab,
+                         const int32_t* recent, int n_recent, float penalty, float softcap, int k, int32_t* out_ids,
+                         float* out_vals)
+{
+    return lm_head_topk(c, "lm_head_topk_q8", F_Q8, x, codes, nullptr, sc, nullptr, K, vocab, recent, n_recent,
+                        penalty, softcap, k, out_ids, out_vals);
+}
+
+int brik_lm_head_topk_q4(brik_ctx* c, const float* x, const uint8_t* nib, const uint16_t* sc, const uint16_t* mn,
+                         int K, int vocab, const int32_t* recent, int n_recent, float penalty, float softcap, int k,
+                         int32_t* out_ids, float* out_vals)
+{
+    return lm_head_topk(c, "lm_head_topk_q4", F_Q4, x, nib, nullptr, sc, mn, K, vocab, recent, n_recent, penalty,
+                        softcap, k, out_ids, out_vals);
+}
+
+int brik_lm_head_topk_q3(brik_ctx* c, const float* x, const uint32_t* lo, const uint32_t* hi, const uint16_t* sc,
+                         const uint16_t* mn, int K, int vocab, const int32_t* recent, int n_recent, float penalty,
+                         float softcap, int k, int32_t* out_ids, float* out_vals)
+{
+    return lm_head_topk(c, "lm_head_topk_q3", F_Q3, x, lo, hi, sc, mn, K, vocab, recent, n_recent, penalty,
+                        softcap, k, out_ids, out_vals);
 }
 
 int brik_timer_begin(brik_ctx* c)

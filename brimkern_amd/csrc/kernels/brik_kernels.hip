@@ -2,3 +2,4 @@
 #include "dequant.hip"
 #include "gemv.hip"
 #include "gemm.hip"
+#include "topk.hip"

@@ -16,6 +16,9 @@ m,k,n)``
 ``dequantGpuQ4/Q3/Q8``     :meth:`Engine.weight` (one upload, planes in place)   model.ts:214-270
 ``recMM(enc,trash,a,w,     :meth:`Engine.mm` (dispatch on the handle's shape)    kernels.ts:1562-1567
 m,k,n)``
+``decodeTopKQ8`` head      :meth:`Engine.lm_head_top_k` (LM head + softcap +     kernels.ts:1934-1968
++ sampling passes          penalty + top-k, ``{ids, vals}`` sorted descending)
+softcap/penalize/top_k     :meth:`Engine.logits_top_k` (on device logits)        kernels.ts:1940-1958
 =========================  ===================================================  ==================
 
 The readback ops take host ``float32`` activations and return a host ``float32`` array of
@@ -114,3 +117,44 @@ class Engine:
             raise BrikError(BRIK_EINVAL, "mm: weight handle is not a q3/q4/q8 handle (f32/f16 weights are "
                                          "outside this library)")
         return out
+
+    # ---- sampling pre-work ---------------------------------------------------------------
+    def _top_k(self, run, recent, k):
+        ids = list(dict.fromkeys(int(i) for i in (recent or [])))      # each id once, as the callers pass them
+        rb = self.ctx.upload(np.asarray(ids, np.int32)) if ids else None
+        ob = self.ctx.alloc(8 * k)
+        try:
+            run(rb, len(ids), ob, ob.offset(4 * k))
+            out_ids = self.ctx.download(ob, np.int32, k).astype(np.uint32)
+            out_vals = self.ctx.download(ob, np.float32, k, src_offset=4 * k)
+        finally:
+            self.ctx.free(ob)
+            if rb is not None:
+                self.ctx.free(rb)
+        return out_ids, out_vals
+
+    def logits_top_k(self, logits: DeviceBuffer, vocab: int, recent=(), penalty: float = 1.0,
+                     softcap: float = 0.0, k: int = 64):
+        """The passes decodeTopKQ8 records after the head (kernels.ts:1940-1958) on a device logits
+        buffer, modified in place like the reference: softcap, repetition penalty, then the top ``k``.
+        Returns ``(ids uint32[k], vals float32[k])`` sorted descending."""
+        def run(rb, nr, ids, vals):
+            self.ctx.logits_topk(logits, vocab, rb, nr, penalty, softcap, k, ids, vals)
+        return self._top_k(run, recent, k)
+
+    def lm_head_top_k(self, x, w: QWeight, d: int, vocab: int, recent=(), penalty: float = 1.0,
+                      softcap: float = 0.0, k: int = 64):
+        """``decodeTopKQ8``'s projection and sampling pre-work (kernels.ts:1934-1968) for one
+        activation row ``x`` (host float32 [d] or a device buffer): logits = x . deq(W)^T over the
+        vocab in one launch, then the passes of :meth:`logits_top_k`. Returns ``(ids, vals)``."""
+        xa = x if isinstance(x, DeviceBuffer) else self.ctx.upload(np.ascontiguousarray(x, np.float32).ravel())
+        fmt = w.fmt
+        planes = {"q8": ("codes", "sc"), "q4": ("nib", "sc", "mn"), "q3": ("lo", "hi", "sc", "mn")}[fmt]
+
+        def run(rb, nr, ids, vals):
+            self.ctx.lm_head_topk(fmt, xa, [w[p] for p in planes], d, vocab, rb, nr, penalty, softcap, k, ids, vals)
+        try:
+            return self._top_k(run, recent, k)
+        finally:
+            if xa is not x:
+                self.ctx.free(xa)

@@ -13,6 +13,10 @@
 //                                                    dispatch on the handle's shape: q3 / nib / codes)
 //   dequantGpuQ4/Q3/Q8 Q4W/Q3W/Q8W path  model.ts:214-270  engine.weightFromBlob(fmt, blob, nElems)
 //   destroyWeight(b)                     model.ts:274-280  engine.destroyWeight(w)
+//   decodeTopKQ8 head + sampling passes :1934-1968  engine.lmHeadTopK(x, w, d, vocab, recent, penalty, softcap, K)
+//                                                    -> Promise<{ids: Uint32Array, vals: Float32Array}>
+//   softcap_logits / penalize_logits /  :1940-1958  engine.logitsTopK(logits, vocab, recent, penalty, softcap, K)
+//   top_k passes on a logits buffer                  (in place, like the reference's passes)
 //
 // Plane arguments may be DeviceBuffers, plane views ({ptr: BigInt}) or BigInt addresses. Errors
 // (bad shapes, K % 32 != 0, misalignment, no device) throw an Error whose .code is "BRIK_E...";
@@ -173,6 +177,48 @@ class Engine {
     });
     const plan = nat.gemvPlanCreate(this.ctx, FMT[fmt], specs);
     return { run: function () { nat.gemvPlanRun(plan); }, destroy: function () { nat.gemvPlanDestroy(plan); } };
+  }
+
+  // ---- sampling pre-work (decodeTopKQ8) --------------------------------------------------------
+  _topK(run, recent, K) {
+    const ids = Array.from(new Set(recent || []));              // each id once, as the reference's callers do
+    const rb = ids.length ? this.uploadGpuRaw(Int32Array.from(ids)) : null;
+    const ob = this.alloc(8 * K);
+    try {
+      run(rb ? rb.ptr : null, ids.length, ob.ptr, ob.ptr + BigInt(4 * K));
+      const raw = new Uint32Array(this.native.d2h(this.ctx, ob.ptr, 8 * K));
+      return { ids: raw.slice(0, K), vals: new Float32Array(raw.buffer.slice(4 * K, 8 * K)) };
+    } finally {
+      ob.destroy();
+      if (rb) rb.destroy();
+    }
+  }
+
+  // softcap -> repetition penalty -> top-K on a device logits buffer (modified in place), kernels.ts:1940-1958.
+  logitsTopK(logits, vocab, recent, penalty, softcap, K) {
+    const k = K === undefined ? 64 : K;
+    const nat = this.native, ctx = this.ctx;
+    return Promise.resolve(this._topK(function (rec, nrec, ids, vals) {
+      nat.logitsTopK(ctx, logits, rec, ids, vals, vocab, nrec, k, penalty || 0, softcap || 0);
+    }, recent, k));
+  }
+
+  // decodeTopKQ8's LM head and passes (kernels.ts:1934-1968) for one row x (Float32Array[d] or device
+  // buffer): one launch for the whole vocab (no tiling), then the passes; K ids + values come back.
+  lmHeadTopK(x, w, d, vocab, recent, penalty, softcap, K) {
+    const k = K === undefined ? 64 : K;
+    const nat = this.native, ctx = this.ctx;
+    const xb = (x instanceof Float32Array || Array.isArray(x)) ? this.uploadGpuRaw(Float32Array.from(x)) : null;
+    const xp = xb ? xb.ptr : x;
+    const fmt = w.q3 ? FMT.q3 : w.nib ? FMT.q4 : FMT.q8;
+    try {
+      return Promise.resolve(this._topK(function (rec, nrec, ids, vals) {
+        nat.lmHeadTopK(ctx, fmt, xp, w.nib || w.codes || w.lo, w.hi || null, w.sc, w.mn || null, rec, ids, vals,
+          d, vocab, nrec, k, penalty || 0, softcap || 0);
+      }, recent, k));
+    } finally {
+      if (xb) xb.destroy();
+    }
   }
 
   dequant(fmt, w, out, nElems) {

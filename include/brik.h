@@ -122,6 +122,37 @@ int brik_gemv_plan_create(brik_ctx *ctx, int fmt, const brik_gemv_job *jobs, int
 int brik_gemv_plan_run(brik_ctx *ctx, const brik_gemv_plan *plan);
 void brik_gemv_plan_destroy(brik_ctx *ctx, brik_gemv_plan *plan);
 
+/* ---- sampling pre-work on the logits (decodeTopKQ8) ---------------------------------------------
+ * The passes decodeTopKQ8 records after the LM head (src/lib/webgpu/kernels.ts:1940-1958; shaders
+ * softcap_logits, penalize_logits, top_k, src/lib/webgpu/shaders.ts:954-1020), in the same order and,
+ * like the reference, modifying the logits in place:
+ *   softcap when softcap > 0:            l = softcap * tanh(l / softcap)
+ *   penalty when penalty is not 0, 1 or NaN and n_recent > 0, for each recent id in [0, n):
+ *                                         l = l > 0 ? l / penalty : l * penalty
+ *   then the k largest logits (1 <= k <= BRIK_TOPK_MAX, k <= n): out_ids[k] (int32) and out_vals[k]
+ *   (f32), sorted descending, ties by smaller id; NaN ranks below every number.
+ * The reference's top_k is exact unless more than 8 of the true top k share an id mod 128; this one
+ * is exact for every input. recent: DEVICE int32 ids, deduplicated as the reference's callers do.
+ * All pointers are device pointers, 4-byte aligned. Uses a context workspace (grown with hipMalloc on
+ * demand: about n / 4 bytes, plus 4 * vocab bytes for the LM-head forms). */
+#define BRIK_TOPK_MAX 64
+int brik_logits_topk(brik_ctx *ctx, float *logits, int n, const int32_t *recent, int n_recent, float penalty,
+                     float softcap, int k, int32_t *out_ids, float *out_vals);
+
+/* Fused LM head + sampling pre-work: logits = x[K] . deq(W[vocab, K])^T (the M == 1 matmul, one
+ * launch: the reference tiles the head only for WebGPU's binding-size cap, model.ts:489-533) into the
+ * context workspace, then brik_logits_topk on them. Replaces decodeTopKQ8's projection and passes
+ * (kernels.ts:1934-1968); only k ids and values are left for the host to read. */
+int brik_lm_head_topk_q8(brik_ctx *ctx, const float *x, const int8_t *codes, const uint16_t *scales, int K,
+                         int vocab, const int32_t *recent, int n_recent, float penalty, float softcap, int k,
+                         int32_t *out_ids, float *out_vals);
+int brik_lm_head_topk_q4(brik_ctx *ctx, const float *x, const uint8_t *nibbles, const uint16_t *scales,
+                         const uint16_t *mins, int K, int vocab, const int32_t *recent, int n_recent, float penalty,
+                         float softcap, int k, int32_t *out_ids, float *out_vals);
+int brik_lm_head_topk_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const uint32_t *hi,
+                         const uint16_t *scales, const uint16_t *mins, int K, int vocab, const int32_t *recent,
+                         int n_recent, float penalty, float softcap, int k, int32_t *out_ids, float *out_vals);
+
 /* ---- dequantization (the bit-exactness check) ----------------------------------------------
  * out[i] = deq(W)[i] in f32 for n_elems elements (n_elems % 32 == 0), bit-identical to
  * dequantizeQ8 / dequantizeQ4 / dequantizeQ3 (q8web.ts:108-117, q4web.ts:199-213,

@@ -39,6 +39,7 @@ __all__ = [
     "quantize_q8", "quantize_q4", "quantize_q3",
     "pack_q8", "pack_q4", "pack_q3", "unpack_q8", "unpack_q4", "unpack_q3",
     "q8_byte_length", "q4_byte_length", "q3_byte_length", "js_round",
+    "softcap_logits", "penalize_logits", "top_k",
 ]
 
 
@@ -294,3 +295,34 @@ def unpack_q3(blob, n):
     sc = b[lb + hb:lb + hb + 2 * g].copy().view("<u2")
     mn = b[lb + hb + 2 * g:lb + hb + 4 * g].copy().view("<u2")
     return lo, hi, sc, mn
+
+
+# ---- sampling pre-work (decodeTopKQ8's passes) ---------------------------------------------------
+
+def softcap_logits(logits: np.ndarray, cap: float) -> np.ndarray:
+    """``cap * Math.tanh(l / cap)`` in double, stored to a Float32Array: the CPU reference of the
+    reference's own top-k validation (``kernels.ts:2833-2834``; GPU pass ``shaders.ts:954-964``)."""
+    v = np.asarray(logits, np.float32).astype(np.float64)
+    return (cap * np.tanh(v / cap)).astype(np.float32)
+
+
+def penalize_logits(logits: np.ndarray, recent, penalty: float) -> np.ndarray:
+    """Repetition penalty as ``sampleNextToken`` applies it (``sampling.ts:84-90``): each id once,
+    ids outside ``[0, n)`` skipped, ``l > 0 ? l / p : l * p`` in double, stored to float32."""
+    out = np.asarray(logits, np.float32).copy()
+    n = out.size
+    for i in dict.fromkeys(int(r) for r in recent):
+        if 0 <= i < n:
+            v = float(out[i])
+            out[i] = np.float32(v / penalty if v > 0 else v * penalty)
+    return out
+
+
+def top_k(logits: np.ndarray, k: int):
+    """The k largest values and their ids, sorted descending, ties by smaller id: the stable sort of
+    the reference's validation (``kernels.ts:2836``, ``Array.sort`` is stable). NaN ranks last."""
+    v = np.asarray(logits, np.float32)
+    key = np.where(np.isnan(v), -np.inf, v.astype(np.float64))
+    nan_last = np.isnan(v).astype(np.int8)
+    order = np.lexsort((np.arange(v.size), -key, nan_last))[:k]
+    return order.astype(np.uint32), v[order]

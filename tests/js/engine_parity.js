@@ -46,6 +46,17 @@ function f16bits(v) {   // f32 -> f16 for normal-range positive/negative scales 
   return sign | (exp << 10) | (r & 0x3ff);
 }
 
+// kernels.ts:2836 ranking (stable sort) and :2862-2866 acceptance rule
+function topkRule(got, ref, K) {
+  const order = Array.from(ref.keys()).sort(function (a, b) { return ref[b] - ref[a]; }).slice(0, K);
+  for (let r = 0; r < K; r++) {
+    const okV = Math.abs(got.vals[r] - ref[order[r]]) <= 1e-4 * (1 + Math.abs(ref[order[r]]));
+    const okI = Math.abs(ref[got.ids[r]] - got.vals[r]) <= 1e-4 * (1 + Math.abs(got.vals[r]));
+    if (!okV || !okI) return false;
+  }
+  return got.ids.length === K && got.vals.length === K;
+}
+
 async function main() {
   const meta = JSON.parse(fs.readFileSync(path.join(root, 'tests', 'golden', 'golden.json')));
   const raw = fs.readFileSync(path.join(root, 'tests', 'golden', 'golden.bin'));
@@ -119,8 +130,31 @@ async function main() {
     code = null;
     try { engine.mm(xb, {}, 1, K, N, y2); } catch (e) { code = e.code; }
     check('non-quantized handle throws BRIK_EINVAL', code === 'BRIK_EINVAL', { code: code });
+    // 6. LM head + sampling pre-work over this weight as a 1024-token head (decodeTopKQ8's passes)
+    const recent = [3, 500, 1023, 77];
+    const cap = 20, pen = 1.3, TK = 32;
+    const lref = Float32Array.from(ref, function (v) { return cap * Math.tanh(v / cap); });
+    recent.forEach(function (id) { lref[id] = lref[id] > 0 ? lref[id] / pen : lref[id] * pen; });
+    const got = await engine.lmHeadTopK(x, w, K, N, recent, pen, cap, TK);
+    check('lmHeadTopK q4', topkRule(got, lref, TK), {});
     [xb, yb, y2, y3].forEach(function (b) { b.destroy(); });
     engine.destroyWeight(w);
+  }
+
+  // 7. the reference's own top_k validation (kernels.ts:2828-2870): vocab 152064, K 64, penalty 1.15,
+  //    cap 30, logits U(-8, 8), 40 recent ids deduplicated, same CPU reference and acceptance rule
+  {
+    const vocab = 152064, TK = 64, penalty = 1.15, cap = 30;
+    const r = rng(777);
+    const logits = Float32Array.from({ length: vocab }, function () { return (r() * 2 - 1) * 8; });
+    const recent = Array.from(new Set(Array.from({ length: 40 }, function () { return Math.floor(r() * vocab); })));
+    const cpu = logits.slice();
+    for (let i = 0; i < vocab; i++) cpu[i] = cap * Math.tanh(cpu[i] / cap);
+    for (const id of recent) cpu[id] = cpu[id] > 0 ? cpu[id] / penalty : cpu[id] * penalty;
+    const lb = engine.uploadGpuRaw(logits);
+    const got = await engine.logitsTopK(lb, vocab, recent, penalty, cap, TK);
+    check('logitsTopK reference validation case', topkRule(got, cpu, TK), {});
+    lb.destroy();
   }
 
   const failed = results.filter(function (r) { return !r.ok; }).length;
