@@ -133,10 +133,59 @@ def gemv_layer_set(ctx, steps, warmup, layers):
         single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1)}
         ctx.free(yb)
     plan.destroy()
+    fused = decode_layers_fused(ctx, reps, layers, steps, warmup)
     for r in reps.values():
         ctx.free(r.buf)
     ctx.free(ybuf)
-    return ms, nbytes, single
+    return ms, nbytes, single, fused
+
+
+def decode_layers_fused(ctx, reps, layers, steps, warmup):
+    """The matmul side of ``layers`` Qwen3-4B decoder layers as recordLayerKV chains it
+    (kernels.ts:1701-1741), four fused plans per layer: q/k/v on rmsnorm(x), wo + residual, gate/up on
+    rmsnorm(h), down on swiglu(gate, up) + residual; layer l + 1 reads layer l's output. Attention is
+    outside this library: its output is a fixed seeded vector."""
+    from brimkern_amd import synth
+    d, qd, kvd, ffn = 2560, 4096, 1024, 9728
+    attn = ctx.upload(synth.normal(110, qd))
+    an, fn = ctx.upload(synth.normal(111, d) * 0.1 + 1), ctx.upload(synth.normal(112, d) * 0.1 + 1)
+    xs = [ctx.upload(synth.normal(113, d))] + [ctx.alloc(4 * d) for _ in range(layers)]
+    tmp = {n: ctx.alloc(4 * N) for n, N in (("q", qd), ("k", kvd), ("v", kvd), ("h", d), ("gate", ffn), ("up", ffn))}
+    shapes = {n: (K, N) for n, K, N in QWEN3_4B + [("o", qd, d)]}
+    reps = dict(reps, o=Replicas(ctx, "q4", synth.q4_tensor(114, d, qd), layers))   # wo, not in the GEMV layer set
+
+    def j(name, l, x, y, **f):
+        nib, sc, mn = reps[name].planes(l)
+        K, N = shapes[name]
+        return dict(x=x, p0=nib, sc=sc, mn=mn, y=y, K=K, N=N, **f)
+    plans, nbytes = [], 0
+    for l in range(layers):
+        x, y = xs[l], xs[l + 1]
+        plans += [ctx.gemv_plan("q4", [j(n, l, x, tmp[n], norm_w=an, eps=1e-6) for n in ("q", "k", "v")]),
+                  ctx.gemv_plan("q4", [j("o", l, attn, tmp["h"], res=x)]),
+                  ctx.gemv_plan("q4", [j(n, l, tmp["h"], tmp[n], norm_w=fn, eps=1e-6) for n in ("gate", "up")]),
+                  ctx.gemv_plan("q4", [j("down", l, tmp["up"], y, gate=tmp["gate"], res=tmp["h"])])]
+        nbytes += sum(q_bytes("q4", N, K) for K, N in shapes.values())
+
+    def step(i):
+        for p in plans:
+            p.run()
+    ms_eager = time_loop(ctx, step, max(2, steps // 4), max(1, warmup // 2))
+    # the same launches recorded once and replayed (brik_graph_*), as the reference records a layer
+    # into one command encoder
+    ctx.graph_begin()
+    step(0)
+    graph = ctx.graph_end()
+    ms = time_loop(ctx, lambda i: graph.launch(), steps, warmup)
+    graph.destroy()
+    for p in plans:
+        p.destroy()
+    for b in [attn, an, fn, reps["o"].buf] + xs + list(tmp.values()):
+        ctx.free(b)
+    return {"us_per_layer": round(ms * 1e3 / layers, 2), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "replay": "one recorded graph per step",
+            "eager_us_per_layer": round(ms_eager * 1e3 / layers, 2), "launches_per_layer": 4, "layers": layers,
+            "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up, swiglu -> down + residual"}
 
 
 def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
@@ -363,9 +412,9 @@ def main():
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
-    ms, nbytes, single = gemv_layer_set(ctx, args.steps, args.warmup, args.layers)
+    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers)
     value = nbytes / (ms * 1e-3) / 1e9
-    extra = {"per_matrix_single_launch": single}
+    extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused}
     if not args.no_extra:
         log("bench: cfg1 q8 GEMV")
         extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)

@@ -47,6 +47,11 @@ SIGNATURES = {
     "brik_gemv_plan_create": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
     "brik_gemv_plan_run": (_I, [_P, _P]),
     "brik_gemv_plan_destroy": (None, [_P, _P]),
+    "brik_gemv_plan_create_ex": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
+    "brik_graph_begin": (_I, [_P]),
+    "brik_graph_end": (_I, [_P, ctypes.POINTER(_P)]),
+    "brik_graph_launch": (_I, [_P, _P]),
+    "brik_graph_destroy": (None, [_P, _P]),
     "brik_logits_topk": (_I, [_P, _P, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
     "brik_lm_head_topk_q8": (_I, [_P, _P, _P, _P, _I, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
     "brik_lm_head_topk_q4": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I, ctypes.c_float, ctypes.c_float, _I, _P, _P]),
@@ -62,6 +67,15 @@ class GemvJob(ctypes.Structure):
     """``brik_gemv_job`` of include/brik.h."""
     _fields_ = [("x", _P), ("p0", _P), ("p1", _P), ("scales", _P), ("mins", _P), ("y", _P),
                 ("K", ctypes.c_int32), ("N", ctypes.c_int32)]
+
+
+class GemvJobEx(ctypes.Structure):
+    """``brik_gemv_job_ex`` of include/brik.h (fused input transform and residual)."""
+    _fields_ = [("job", GemvJob), ("gate", _P), ("norm_w", _P), ("res", _P), ("eps", ctypes.c_float),
+                ("flags", ctypes.c_int32)]
+
+
+BRIK_JOB_GAIN_ONE_PLUS, BRIK_JOB_ACT_GELU = 1, 2
 
 
 class BrikError(RuntimeError):
@@ -222,16 +236,40 @@ class Context:
                                                   _addr(sc), _addr(mn), _addr(y), E, R, K, N))
 
     def gemv_plan(self, fmt: str, jobs) -> "GemvPlan":
-        """jobs: iterable of dicts with x, p0, p1, sc, mn, y (device addresses), K, N."""
+        """jobs: iterable of dicts with x, p0, p1, sc, mn, y (device addresses), K, N, and optionally the
+        fusions of ``brik_gemv_job_ex``: gate, norm_w, eps, one_plus, gelu, res. Jobs without any
+        fusion key go through ``brik_gemv_plan_create``, the others through the ``_ex`` form."""
         jobs = list(jobs)
-        arr = (GemvJob * len(jobs))()
-        for i, j in enumerate(jobs):
-            arr[i] = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]),
-                             _addr(j.get("mn")), _addr(j["y"]), j["K"], j["N"])
+        fused = any(k in j for j in jobs for k in ("gate", "norm_w", "res"))
         h = _P()
-        self._check(self.lib.brik_gemv_plan_create(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
-                                                   ctypes.byref(h)))
+        if not fused:
+            arr = (GemvJob * len(jobs))()
+            for i, j in enumerate(jobs):
+                arr[i] = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]),
+                                 _addr(j.get("mn")), _addr(j["y"]), j["K"], j["N"])
+            self._check(self.lib.brik_gemv_plan_create(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
+                                                       ctypes.byref(h)))
+            return GemvPlan(self, h)
+        arr = (GemvJobEx * len(jobs))()
+        for i, j in enumerate(jobs):
+            base = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]), _addr(j.get("mn")),
+                           _addr(j["y"]), j["K"], j["N"])
+            flags = (BRIK_JOB_GAIN_ONE_PLUS if j.get("one_plus") else 0) | (BRIK_JOB_ACT_GELU if j.get("gelu") else 0)
+            arr[i] = GemvJobEx(base, _addr(j.get("gate")), _addr(j.get("norm_w")), _addr(j.get("res")),
+                               float(j.get("eps", 1e-6)), flags)
+        self._check(self.lib.brik_gemv_plan_create_ex(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
+                                                      ctypes.byref(h)))
         return GemvPlan(self, h)
+
+    # ---- recorded launches (HIP graphs) ---------------------------------------------------------
+    def graph_begin(self):
+        """Record (not run) every launch enqueued from now on until :meth:`graph_end`."""
+        self._check(self.lib.brik_graph_begin(self.handle))
+
+    def graph_end(self) -> "Graph":
+        h = _P()
+        self._check(self.lib.brik_graph_end(self.handle, ctypes.byref(h)))
+        return Graph(self, h)
 
     # ---- sampling pre-work ----------------------------------------------------------------
     def logits_topk(self, logits, n, recent, n_recent, penalty, softcap, k, ids, vals):
@@ -254,6 +292,21 @@ class Context:
     def dequant_q3(self, lo, hi, sc, mn, out, n):
         self._check(self.lib.brik_dequant_q3_f32(self.handle, _addr(lo), _addr(hi), _addr(sc), _addr(mn),
                                                  _addr(out), n))
+
+
+class Graph:
+    """A recorded launch sequence (``brik_graph``): :meth:`launch` replays it on the context stream."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx, self.handle = ctx, handle
+
+    def launch(self):
+        self.ctx._check(self.ctx.lib.brik_graph_launch(self.ctx.handle, self.handle))
+
+    def destroy(self):
+        if self.handle:
+            self.ctx.lib.brik_graph_destroy(self.ctx.handle, self.handle)
+            self.handle = None
 
 
 class GemvPlan:

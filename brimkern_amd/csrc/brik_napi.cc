@@ -428,7 +428,8 @@ void plan_finalize(napi_env, void* data, void*)
     delete b;
 }
 
-// gemvPlanCreate(ctx, fmt, [{x, p0, p1, scales, mins, y, K, N}, ...]) -> plan
+// gemvPlanCreate(ctx, fmt, [{x, p0, p1, scales, mins, y, K, N[, gate, normW, res, eps, flags]}, ...]) -> plan
+// (the optional fields are those of brik_gemv_job_ex; a job without them has no fusion)
 napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
 {
     Args a;
@@ -438,8 +439,9 @@ napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
     if (!get_ctx(env, a.v[0], &ctx) || !get_i32(env, a.v[1], &fmt)) return nullptr;
     uint32_t n = 0;
     NAPI_CALL(env, napi_get_array_length(env, a.v[2], &n));
-    std::vector<brik_gemv_job> jobs(n);
+    std::vector<brik_gemv_job_ex> jobs(n);
     static const char* const names[6] = {"x", "p0", "p1", "scales", "mins", "y"};
+    static const char* const fnames[3] = {"gate", "normW", "res"};
     for (uint32_t j = 0; j < n; ++j) {
         napi_value o, f;
         NAPI_CALL(env, napi_get_element(env, a.v[2], j, &o));
@@ -453,11 +455,33 @@ napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
         if (!get_i32(env, f, &K)) return nullptr;
         NAPI_CALL(env, napi_get_named_property(env, o, "N", &f));
         if (!get_i32(env, f, &N)) return nullptr;
-        jobs[j] = brik_gemv_job{(const float*)ptrs[0], ptrs[1], ptrs[2], (const uint16_t*)ptrs[3],
-                                (const uint16_t*)ptrs[4], (float*)ptrs[5], K, N};
+        void* fp[3] = {nullptr, nullptr, nullptr};
+        for (int k = 0; k < 3; ++k) {
+            bool has = false;
+            NAPI_CALL(env, napi_has_named_property(env, o, fnames[k], &has));
+            if (!has) continue;
+            NAPI_CALL(env, napi_get_named_property(env, o, fnames[k], &f));
+            if (!get_ptr(env, f, &fp[k])) return nullptr;
+        }
+        float eps = 1e-6f;
+        int32_t flags = 0;
+        bool has = false;
+        NAPI_CALL(env, napi_has_named_property(env, o, "eps", &has));
+        if (has) {
+            NAPI_CALL(env, napi_get_named_property(env, o, "eps", &f));
+            if (!get_f32(env, f, &eps)) return nullptr;
+        }
+        NAPI_CALL(env, napi_has_named_property(env, o, "flags", &has));
+        if (has) {
+            NAPI_CALL(env, napi_get_named_property(env, o, "flags", &f));
+            if (!get_i32(env, f, &flags)) return nullptr;
+        }
+        jobs[j] = brik_gemv_job_ex{brik_gemv_job{(const float*)ptrs[0], ptrs[1], ptrs[2], (const uint16_t*)ptrs[3],
+                                                 (const uint16_t*)ptrs[4], (float*)ptrs[5], K, N},
+                                   (const float*)fp[0], (const float*)fp[1], (const float*)fp[2], eps, flags};
     }
     brik_gemv_plan* plan = nullptr;
-    if (check(env, ctx, brik_gemv_plan_create(ctx, fmt, jobs.data(), (int)n, &plan))) return nullptr;
+    if (check(env, ctx, brik_gemv_plan_create_ex(ctx, fmt, jobs.data(), (int)n, &plan))) return nullptr;
     napi_value ext;
     NAPI_CALL(env, napi_create_external(env, new PlanBox{ctx, plan}, plan_finalize, nullptr, &ext));
     return ext;

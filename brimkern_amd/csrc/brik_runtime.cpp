@@ -25,6 +25,7 @@ enum Kern {
     K_DEQ_Q8, K_DEQ_Q4, K_DEQ_Q3,
     K_XPREP,
     K_TOPK_PREP, K_TOPK_SELECT,
+    K_FILL_ZERO,
     K_COUNT
 };
 
@@ -32,6 +33,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_dequant_q8", "brik_dequant_q4", "brik_dequant_q3",
     "brik_xprep_f16",
     "brik_topk_prep", "brik_topk_select",
+    "brik_fill_zero",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -63,10 +65,11 @@ constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV
 constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loop over row sets
 constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
 constexpr long kPlanMaxSets = 4;               // row sets per grouped-plan block, at most
+constexpr long kPlanMinBlocks = 1024;          // grouped-plan blocks, at least (while sets > 1)
 
 // LDS bytes of a staged activation row (xprep.h): per group (plus one zero group) 96 limb bytes, an
-// f32 sum and an int32 exponent; then a flag.
-size_t gemv_lds(int K) { return (size_t)104 * (K / kGroup + 1) + 16; }
+// f32 sum and an int32 exponent; then a flag, the RMSNorm factor and its reduction slots.
+size_t gemv_lds(int K) { return (size_t)104 * (K / kGroup + 1) + 32; }
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
 int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
@@ -75,10 +78,15 @@ int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 struct brik_gemv_plan {
     hipFunction_t kernel;
-    void* dev = nullptr;          // [jobs | block_start]
+    void* dev = nullptr;          // [jobs (brik_gemv_job_ex) | block_start | rows_per_block]
     int njobs = 0;
     unsigned blocks = 0;
     size_t lds = 0;
+};
+
+struct brik_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 struct brik_ctx {
@@ -97,6 +105,7 @@ struct brik_ctx {
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
     size_t tws_bytes = 0;
+    bool graph_capturing = false;
     char err[512] = {0};
 };
 
@@ -203,6 +212,9 @@ int gemm_tile(brik_ctx* c, long M, long N, int E)
 int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
 {
     if (have >= bytes) return BRIK_OK;
+    if (c->graph_capturing)
+        return fail(c, BRIK_EINVAL, "a workspace would grow during graph capture: run the same calls once "
+                                    "before brik_graph_begin");
     if (buf) {
         HIP_TRY(c, hipStreamSynchronize(c->stream));
         HIP_TRY(c, hipFree(buf));
@@ -217,16 +229,22 @@ int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
 
 int ensure_ws(brik_ctx* c, size_t bytes) { return ensure_buf(c, c->ws, c->ws_bytes, bytes); }
 
+// y[0, n) = 0 on the context stream (a kernel, so graph capture records no memset node).
+int fill_zero(brik_ctx* c, float* y, size_t n)
+{
+    if (n == 0) return BRIK_OK;
+    size_t blocks = (n + 255) / 256;
+    blocks = blocks < 4096 ? blocks : 4096;
+    void* args[] = {&y, &n};
+    return launch(c, K_FILL_ZERO, (unsigned)blocks, 1, 256, 0, args);
+}
+
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
 // tile kernel; dense when row_off is null, expert-grouped otherwise.
 int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
          float* y, int rows, int K, int N, const int* row_off, int E)
 {
-    if (K == 0) {   // empty sums
-        HIP_TRY(c, hipSetDevice(c->device));
-        HIP_TRY(c, hipMemsetAsync(y, 0, (size_t)rows * N * sizeof(float), c->stream));
-        return BRIK_OK;
-    }
+    if (K == 0) return fill_zero(c, y, (size_t)rows * N);   // empty sums
     const long Kp = (K + kGemmKPad - 1) / kGemmKPad * kGemmKPad;
     const size_t xbytes = (size_t)rows * Kp * 2;
     if (xbytes >= (1ull << 31))
@@ -252,23 +270,24 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 }
 
 // GEMV variant for a given K (index into kGemvVariants).
-int gemv_variant(brik_ctx* c, int K)
+// GEMV variant for a launch over `rows` rows in total (one matrix or a plan's jobs) with shortest row
+// K: the 32-row sets of variant 0 need enough blocks to keep every CU's loads in flight; below that
+// the 16-row sets of variant 5 (32 lanes per row, pipeline depth 3) give twice the blocks, when rows
+// are long enough (K >= 2048) for 32 lanes. Measured on the Qwen3-4B shapes: N = 9728 and the
+// 216-matrix layer set are faster with variant 0, N <= 4096 and the K = 9728 down projection with
+// variant 5; the K = 896 q8 FFN shape with variant 0.
+int gemv_variant(brik_ctx* c, long rows, int kmin)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
-    (void)K;
-    return 0;
+    return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
 
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N)
 {
-    if (K == 0) {   // empty sums, whatever the path
-        HIP_TRY(c, hipSetDevice(c->device));
-        HIP_TRY(c, hipMemsetAsync(y, 0, (size_t)M * N * sizeof(float), c->stream));
-        return BRIK_OK;
-    }
+    if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
-    const int v = gemv_variant(c, K);
+    const int v = gemv_variant(c, N, K);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
@@ -439,6 +458,7 @@ void brik_destroy(brik_ctx* c)
 
 int brik_alloc(brik_ctx* c, size_t bytes, void** dptr)
 {
+    if (c && c->graph_capturing) return fail(c, BRIK_EINVAL, "alloc / free: not allowed while a graph capture is open");
     if (!c || !dptr) return BRIK_EINVAL;
     *dptr = nullptr;
     HIP_TRY(c, hipSetDevice(c->device));
@@ -448,6 +468,7 @@ int brik_alloc(brik_ctx* c, size_t bytes, void** dptr)
 
 int brik_free(brik_ctx* c, void* dptr)
 {
+    if (c && c->graph_capturing) return fail(c, BRIK_EINVAL, "alloc / free: not allowed while a graph capture is open");
     if (!c) return BRIK_EINVAL;
     if (!dptr) return BRIK_OK;
     HIP_TRY(c, hipSetDevice(c->device));
@@ -461,6 +482,7 @@ static int copy(brik_ctx* c, void* dst, const void* src, size_t n, hipMemcpyKind
     if (!c) return BRIK_EINVAL;
     if (n == 0) return BRIK_OK;
     if (!dst || !src) return fail(c, BRIK_EINVAL, "copy: null pointer");
+    if (c->graph_capturing) return fail(c, BRIK_EINVAL, "copy: not allowed while a graph capture is open");
     HIP_TRY(c, hipSetDevice(c->device));
     HIP_TRY(c, hipMemcpyAsync(dst, src, n, kind, c->stream));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
@@ -473,6 +495,7 @@ int brik_d2d(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c,
 
 int brik_sync(brik_ctx* c)
 {
+    if (c && c->graph_capturing) return fail(c, BRIK_EINVAL, "sync: not allowed while a graph capture is open");
     if (!c) return BRIK_EINVAL;
     HIP_TRY(c, hipSetDevice(c->device));
     HIP_TRY(c, hipStreamSynchronize(c->stream));
@@ -561,7 +584,7 @@ int brik_dequant_q3_f32(brik_ctx* c, const uint32_t* lo, const uint32_t* hi, con
     return dequant(c, K_DEQ_Q3, "dequant_q3", args, n, lo, out, 4);
 }
 
-int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int njobs, brik_gemv_plan** out)
+int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out)
 {
     if (!c || !out) return BRIK_EINVAL;
     *out = nullptr;
@@ -571,7 +594,12 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
     const Fmt f = Fmt(fmt);
     int kmax = 0, kmin = 1 << 30;
     for (int j = 0; j < njobs; ++j) {
-        const brik_gemv_job& b = jobs[j];
+        const brik_gemv_job& b = jobs[j].job;
+        const brik_gemv_job_ex& e = jobs[j];
+        if (e.flags & ~(BRIK_JOB_GAIN_ONE_PLUS | BRIK_JOB_ACT_GELU))
+            return fail(c, BRIK_EINVAL, "gemv_plan: job %d has unknown flags 0x%x", j, (unsigned)e.flags);
+        if ((e.gate && !aligned(e.gate, 16)) || (e.norm_w && !aligned(e.norm_w, 16)) || (e.res && !aligned(e.res, 4)))
+            return fail(c, BRIK_EALIGN, "gemv_plan: job %d: gate / norm_w must be 16-byte, res 4-byte aligned", j);
         if (b.K < 32 || b.N < 1)
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d has K=%d N=%d (need K >= 32, N >= 1)", j, b.K, b.N);
         int r = check_mm(c, "gemv_plan", b.x, b.p0, b.p1, b.scales, b.mins, b.y, 1, b.K, b.N, f);
@@ -581,24 +609,41 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
         kmax = b.K > kmax ? b.K : kmax;
         kmin = b.K < kmin ? b.K : kmin;
     }
-    const int v = gemv_variant(c, kmin);
+    long rows = 0;
+    for (int j = 0; j < njobs; ++j) rows += jobs[j].job.N;
+    const int v = gemv_variant(c, rows, kmin);
     const int rpi = kGemvVariants[v].rpi();
     // Blocks of about equal cost: rows per block ~ kPlanGroupRows / (K/32), in whole row sets of rpi
-    // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). Jobs are laid out in order
-    // of decreasing K, so the most expensive blocks are dispatched first and the tail of the launch
-    // consists of the cheapest ones.
+    // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). A small plan (a decoder
+    // layer's q/k/v or gate/up) would then have too few blocks to reach every CU's memory bandwidth:
+    // the sets per block are halved until the launch has at least kPlanMinBlocks blocks (or one set
+    // per block). Jobs are laid out in order of decreasing K, so the most expensive blocks are
+    // dispatched first and the tail of the launch consists of the cheapest ones.
     std::vector<int> order(njobs);
     for (int j = 0; j < njobs; ++j) order[j] = j;
-    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return jobs[a].K > jobs[b].K; });
-    std::vector<brik_gemv_job> sorted(njobs);
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return jobs[a].job.K > jobs[b].job.K; });
+    std::vector<brik_gemv_job_ex> sorted(njobs);
     std::vector<uint32_t> start(njobs + 1, 0), rpbs(njobs);
+    std::vector<long> sets(njobs);
+    for (int k = 0; k < njobs; ++k) {
+        const brik_gemv_job& b = jobs[order[k]].job;
+        sorted[k] = jobs[order[k]];
+        long s0 = lround((double)kPlanGroupRows / ((double)(b.K / kGroup) * rpi));
+        sets[k] = s0 < 1 ? 1 : s0 > kPlanMaxSets ? kPlanMaxSets : s0;
+    }
+    for (;;) {
+        long blocks = 0, maxsets = 1;
+        for (int k = 0; k < njobs; ++k) {
+            blocks += (sorted[k].job.N + sets[k] * rpi - 1) / (sets[k] * rpi);
+            maxsets = sets[k] > maxsets ? sets[k] : maxsets;
+        }
+        if (blocks >= kPlanMinBlocks || maxsets == 1) break;
+        for (int k = 0; k < njobs; ++k) sets[k] = (sets[k] + 1) / 2;
+    }
     size_t lds = 0;
     for (int k = 0; k < njobs; ++k) {
-        const brik_gemv_job& b = jobs[order[k]];
-        sorted[k] = b;
-        long sets = lround((double)kPlanGroupRows / ((double)(b.K / kGroup) * rpi));
-        sets = sets < 1 ? 1 : sets > kPlanMaxSets ? kPlanMaxSets : sets;
-        rpbs[k] = (uint32_t)(sets * rpi);
+        const brik_gemv_job& b = sorted[k].job;
+        rpbs[k] = (uint32_t)(sets[k] * rpi);
         start[k + 1] = start[k] + (uint32_t)((b.N + rpbs[k] - 1) / rpbs[k]);
         const size_t need = gemv_lds(b.K) + kGemvVariants[v].extra_lds(rpbs[k]);
         lds = need > lds ? need : lds;
@@ -606,7 +651,7 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
     if (lds > kGemvMaxLds) return fail(c, BRIK_EINVAL, "gemv_plan: K=%d too large for LDS staging", kmax);
     brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();
     if (!p) return BRIK_ENOMEM;
-    const size_t jb = sizeof(brik_gemv_job) * (size_t)njobs;
+    const size_t jb = sizeof(brik_gemv_job_ex) * (size_t)njobs;
     const size_t bytes = jb + sizeof(uint32_t) * (start.size() + rpbs.size());
     std::vector<unsigned char> host(bytes);
     std::memcpy(host.data(), sorted.data(), jb);
@@ -623,11 +668,20 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
     return BRIK_OK;
 }
 
+int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int njobs, brik_gemv_plan** out)
+{
+    if (!c || !out) return BRIK_EINVAL;
+    if (njobs <= 0 || !jobs) return fail(c, BRIK_EINVAL, "gemv_plan: need at least one job");
+    std::vector<brik_gemv_job_ex> ex(njobs);
+    for (int j = 0; j < njobs; ++j) ex[j] = brik_gemv_job_ex{jobs[j], nullptr, nullptr, nullptr, 0.f, 0};
+    return brik_gemv_plan_create_ex(c, fmt, ex.data(), njobs, out);
+}
+
 int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
 {
     if (!c || !p) return BRIK_EINVAL;
-    const brik_gemv_job* jobs = (const brik_gemv_job*)p->dev;
-    const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job) * (size_t)p->njobs);
+    const brik_gemv_job_ex* jobs = (const brik_gemv_job_ex*)p->dev;
+    const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job_ex) * (size_t)p->njobs);
     const uint32_t* rpbs = start + p->njobs + 1;
     int nj = p->njobs;
     void* args[] = {&jobs, &start, &rpbs, &nj};
@@ -674,6 +728,52 @@ int brik_lm_head_topk_q3(brik_ctx* c, const float* x, const uint32_t* lo, const 
 {
     return lm_head_topk(c, "lm_head_topk_q3", F_Q3, x, lo, hi, sc, mn, K, vocab, recent, n_recent, penalty,
                         softcap, k, out_ids, out_vals);
+}
+
+int brik_graph_begin(brik_ctx* c)
+{
+    if (!c) return BRIK_EINVAL;
+    if (c->graph_capturing) return fail(c, BRIK_EINVAL, "graph_begin: a capture is already open");
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->graph_capturing = true;
+    return BRIK_OK;
+}
+
+int brik_graph_end(brik_ctx* c, brik_graph** out)
+{
+    if (!c || !out) return BRIK_EINVAL;
+    *out = nullptr;
+    if (!c->graph_capturing) return fail(c, BRIK_EINVAL, "graph_end: no capture is open");
+    c->graph_capturing = false;
+    brik_graph* g = new (std::nothrow) brik_graph();
+    if (!g) return BRIK_ENOMEM;
+    hipError_t e = hipStreamEndCapture(c->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (g->graph) (void)hipGraphDestroy(g->graph);
+        delete g;
+        return fail(c, BRIK_EHIP, "graph_end: %s", hipGetErrorString(e));
+    }
+    *out = g;
+    return BRIK_OK;
+}
+
+int brik_graph_launch(brik_ctx* c, const brik_graph* g)
+{
+    if (!c || !g) return BRIK_EINVAL;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipGraphLaunch(g->exec, c->stream));
+    return BRIK_OK;
+}
+
+void brik_graph_destroy(brik_ctx* c, brik_graph* g)
+{
+    (void)c;
+    if (!g) return;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
 }
 
 int brik_timer_begin(brik_ctx* c)

@@ -62,3 +62,10 @@ extern "C" __global__ __launch_bounds__(256) void brik_dequant_q3(
     *(f32x4_t*)(out + e0) = o0;
     *(f32x4_t*)(out + e0 + 4) = o1;
 }
+
+// y[0, n) = 0: the K == 0 matmul (empty sums). A kernel rather than a memset node, so a caller may
+// capture it in a graph.
+extern "C" __global__ __launch_bounds__(256) void brik_fill_zero(float* __restrict__ y, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) y[i] = 0.f;
+}

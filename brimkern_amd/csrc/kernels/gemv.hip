@@ -25,6 +25,7 @@
 namespace {
 
 using brik::XStage;
+using brik::Fuse;
 
 // Raw data of one (row, group) as loaded from the planes.
 template <int FMT> struct Grp;
@@ -251,8 +252,9 @@ struct Work {
 
 // Exact path for a row holding Inf/NaN.
 template <int FMT, int TEAM, int R>
-__device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Planes& P, float* __restrict__ yrow,
-                                                int K, int r0, int r1, int rstep)
+__device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Fuse& F, float inv,
+                                                const Planes& P, float* __restrict__ yrow,
+                                                const float* __restrict__ res, int K, int r0, int r1, int rstep)
 {
     const int lane = threadIdx.x % TEAM;
     const int team = threadIdx.x / TEAM;
@@ -260,9 +262,9 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
         for (int r = 0; r < R && n0 + r < r1; ++r) {
             float acc = 0.f;
             for (int k = lane; k < K; k += TEAM)
-                acc = __builtin_fmaf(x[k], deq_elem<FMT>(P, (size_t)(n0 + r) * K + k), acc);
+                acc = __builtin_fmaf(brik::fused_in(x, F, inv, k), deq_elem<FMT>(P, (size_t)(n0 + r) * K + k), acc);
             acc = team_sum<TEAM>(acc);
-            if (lane == 0) yrow[n0 + r] = acc;
+            if (lane == 0) yrow[n0 + r] = res ? res[n0 + r] + acc : acc;
         }
     }
 }
@@ -270,8 +272,9 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
 // The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
 template <int FMT, class W, int D, bool EVEN>
-__device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __restrict__ x,
-                                         const Planes& P, float* __restrict__ yrow, int K, int S)
+__device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __restrict__ x, const Fuse& F,
+                                         const Planes& P, float* __restrict__ yrow, const float* __restrict__ res,
+                                         int K, int S)
 {
     typename W::Data d[D];
     int ip = 0, bp = 0;                      // (p, b) of the next step to issue
@@ -282,10 +285,10 @@ __device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __r
         bp = wrap ? 0 : bp + 1;
         ip += wrap;
     }
-    brik::xstage<FMT>(x, X, K);
+    brik::xstage<FMT>(x, X, K, F);
     if (*X.flag) {
         // exact path: teams of 16 lanes over RPI rows per iteration
-        gemv_rows_exact<FMT, 16, W::RPI / 16>(x, P, yrow, K, w.r0, w.r1, w.rstep);
+        gemv_rows_exact<FMT, 16, W::RPI / 16>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
         return;
     }
     float acc[W::NACC] = {};
@@ -322,7 +325,8 @@ __device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __r
 // then the cross-lane sums of the LDS partials are written to y. The block owns row sets
 // p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
 template <int FMT, class W, int D>
-__device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Planes& P, float* __restrict__ yrow,
+__device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Fuse& F, const Planes& P,
+                                            float* __restrict__ yrow, const float* __restrict__ res,
                                             int N, int K, int r0, int r1, int rstep, unsigned char* lds)
 {
     W w;
@@ -334,8 +338,8 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const P
     const int S = nsets * w.B;                                            // steps per lane
     const XStage X = brik::xstage_layout(lds, K);
     w.part = (float*)(lds + brik::xstage_bytes(K));
-    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, P, yrow, K, S);
-    else pipeline<FMT, W, D, false>(w, X, x, P, yrow, K, S);
+    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, F, P, yrow, res, K, S);
+    else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S);
     if (*X.flag) return;
     __syncthreads();
     // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped)
@@ -347,7 +351,7 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const P
             float v = 0.f;
 #pragma unroll
             for (int l = 0; l < PARTS; ++l) v += pp[(l + q) % PARTS];
-            yrow[n] = v;
+            yrow[n] = res ? res[n] + v : v;
         }
     }
 }
@@ -360,14 +364,14 @@ __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uin
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int RPI = W::RPI;     // rows per block iteration
     const Planes P{p0, p1, sc, mn};
-    gemv_matrix<FMT, W, D>(x + (size_t)blockIdx.y * K, P, y + (size_t)blockIdx.y * N, N, K, blockIdx.x * RPI, N,
-                           gridDim.x * RPI, lds);
+    gemv_matrix<FMT, W, D>(x + (size_t)blockIdx.y * K, Fuse{nullptr, nullptr, 0.f, 0}, P, y + (size_t)blockIdx.y * N,
+                           nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds);
 }
 
 // Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
 // block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts).
 template <int FMT, class W, int D>
-__device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restrict__ jobs,
+__device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __restrict__ jobs,
                                                   const uint32_t* __restrict__ block_start,
                                                   const uint32_t* __restrict__ rows_per_block, int njobs)
 {
@@ -379,12 +383,14 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restric
         const int mid = (lo + hi + 1) >> 1;
         if (block_start[mid] <= b) lo = mid; else hi = mid - 1;
     }
-    const brik_gemv_job job = jobs[lo];
+    const brik_gemv_job_ex je = jobs[lo];
+    const brik_gemv_job& job = je.job;
     const Planes P{(const uint8_t*)job.p0, (const uint8_t*)job.p1, job.scales, job.mins};
     const int rpb = (int)rows_per_block[lo];
     const int r0 = (int)(b - block_start[lo]) * rpb;
     const int r1 = min(job.N, r0 + rpb);
-    gemv_matrix<FMT, W, D>(job.x, P, job.y, job.N, job.K, r0, r1, RPI, lds);
+    gemv_matrix<FMT, W, D>(job.x, Fuse{je.gate, je.norm_w, je.eps, je.flags}, P, job.y, je.res, job.N, job.K, r0, r1,
+                           RPI, lds);
 }
 
 }  // namespace
@@ -398,7 +404,7 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job* __restric
         gemv_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(x, p0, p1, sc, mn, y, K, N);                    \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
-        const brik_gemv_job* __restrict__ jobs, const uint32_t* __restrict__ block_start,           \
+        const brik_gemv_job_ex* __restrict__ jobs, const uint32_t* __restrict__ block_start,        \
         const uint32_t* __restrict__ rows_per_block, int njobs)                                      \
     {                                                                                               \
         gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(jobs, block_start, rows_per_block, njobs); \

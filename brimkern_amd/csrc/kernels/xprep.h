@@ -14,9 +14,18 @@
 //          in one instruction hit different banks). Group G is all zeros: consumers point groups past
 //          the end of a row at it, which zeroes their contribution without a select;
 //   xse[g]: {f32 sum of the group's x, int32 e_g - 22}, g <= G, xse[G] = {0, 0};
-//   flag:  int32, nonzero if the row holds a non-finite value (the exact f32 path then runs).
+//   flag:  int32, nonzero if the row holds a non-finite value (the exact f32 path then runs);
+//   inv:   f32, the RMSNorm factor of a fused input transform (1 without one), and 4 words of scratch
+//          for its block reduction.
+//
+// Fused input transform (grouped plans, brik_gemv_job_ex): the staged row may be
+//   act(gate[k]) * x[k]                  (SwiGLU act = SiLU, GeGLU act = tanh-GELU), then / or
+//   v[k] * inv * g[k],  inv = 1 / sqrt(sum v^2 / K + eps),  g = w or 1 + w   (RMSNorm)
+// as the reference computes n1 = rmsnorm(x) and g = swiglu(gate, up) before recMM
+// (src/lib/webgpu/shaders.ts:580-626; kernels.ts:1701, 1723, 1726).
 #pragma once
 #include "common.h"
+#include "../../../include/brik.h"   // BRIK_JOB_* flags
 
 namespace brik {
 
@@ -40,13 +49,14 @@ struct XStage {
     int8_t* limbs;
     float2* xse;      // {sum, bit-cast int exponent}
     int* flag;
+    float* inv;       // inv, then 4 reduction slots
     int G;
 };
 
 // Bytes of the staged row; the block's partial-sum buffer follows at this offset (4-byte aligned).
 __host__ __device__ __forceinline__ size_t xstage_bytes(int K)
 {
-    return (size_t)104 * (K / BRIK_GROUP + 1) + 16;
+    return (size_t)104 * (K / BRIK_GROUP + 1) + 32;
 }
 
 __device__ __forceinline__ XStage xstage_layout(void* lds, int K)
@@ -56,7 +66,48 @@ __device__ __forceinline__ XStage xstage_layout(void* lds, int K)
     s.limbs = (int8_t*)lds;
     s.xse = (float2*)((char*)lds + (size_t)96 * (s.G + 1));
     s.flag = (int*)(s.xse + s.G + 1);
+    s.inv = (float*)(s.flag + 1);
     return s;
+}
+
+// The fused input transform of a job; all null for a plain matmul.
+struct Fuse {
+    const float* gate;     // gated activation input, or null
+    const float* norm_w;   // RMSNorm gain, or null
+    float eps;
+    int flags;             // BRIK_JOB_GAIN_ONE_PLUS, BRIK_JOB_ACT_GELU
+};
+
+__device__ __forceinline__ float act(float v, int flags)
+{
+    if (flags & BRIK_JOB_ACT_GELU)          // tanh-approximated GELU, as the reference's geglu
+        return 0.5f * v * (1.f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
+    return v / (1.f + expf(-v));            // SiLU, as the reference's swiglu
+}
+
+// Element k of the transformed row given the RMSNorm factor inv (1 without a norm).
+__device__ __forceinline__ float fused_in(const float* __restrict__ x, const Fuse& F, float inv, int k)
+{
+    float v = x[k];
+    if (F.gate) v = act(F.gate[k], F.flags) * v;
+    if (F.norm_w) v = v * inv * ((F.flags & BRIK_JOB_GAIN_ONE_PLUS) ? 1.f + F.norm_w[k] : F.norm_w[k]);
+    return v;
+}
+
+__device__ __forceinline__ f32x4_t fused_in4(f32x4_t v, const Fuse& F, float inv, int k)
+{
+    if (F.gate) {
+        const f32x4_t g = *(const f32x4_t*)(F.gate + k);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = act(g[t], F.flags) * v[t];
+    }
+    if (F.norm_w) {
+        f32x4_t w = *(const f32x4_t*)(F.norm_w + k);
+        if (F.flags & BRIK_JOB_GAIN_ONE_PLUS) w = w + 1.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = v[t] * inv * w[t];
+    }
+    return v;
 }
 
 __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h, int& m, int& l)
@@ -70,7 +121,7 @@ __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h
 
 // Stage x[0..K) (16-byte aligned, K % 32 == 0). All threads of the block call it; ends with a barrier.
 template <int FMT>
-__device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K)
+__device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K, const Fuse& F)
 {
     const int G = S.G;
     if (threadIdx.x == 0) {
@@ -78,12 +129,28 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
         S.xse[G] = float2{0.f, 0.f};
     }
     if (threadIdx.x < 24) ((uint32_t*)(S.limbs + 96 * G))[threadIdx.x] = 0u;   // the zero group
-    __syncthreads();
     const int nq = K >> 2;
+    float inv = 1.f;
+    if (F.norm_w) {
+        // sum of squares of the (gated) row: per thread, per wave, then across the block's waves
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < nq; i += blockDim.x) {
+            const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), Fuse{F.gate, nullptr, 0.f, F.flags}, 1.f, 4 * i);
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
+        __syncthreads();
+        float t = 0.f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += S.inv[1 + w];
+        inv = 1.f / sqrtf(t / (float)K + F.eps);
+    }
+    if (threadIdx.x == 0) *S.inv = inv;
+    __syncthreads();
     // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
     // every loop trip is entered by whole 8-lane groups, so the DPP group reductions see full groups
     for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-        const f32x4_t v = *(const f32x4_t*)(x + 4 * i);
+        const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), F, inv, 4 * i);
         const int g = i >> 3, c = i & 7;
         const float p = sum8((v.x + v.y) + (v.z + v.w));
         const float a = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));

@@ -168,12 +168,21 @@ class Engine {
   }
 
   // Grouped decode GEMV plan: jobs [{x, w, y, K, N}] (one format), executed by one launch per run().
+  // Optional per job, the fusions of brik_gemv_job_ex (the ops recordLayerKV records around recMM,
+  // kernels.ts:1701-1741): norm (RMSNorm gain buffer), eps, onePlus (Gemma 1 + w gain), gate (the
+  // SwiGLU / GeGLU gate buffer, x being "up"), act ('gelu' for GeGLU), res (residual added to y).
   gemvPlan(fmt, jobs) {
     const nat = this.native;
     const specs = jobs.map(function (j) {
       const w = j.w;
-      return { x: j.x, p0: w.nib || w.codes || w.lo, p1: w.hi || null, scales: w.sc, mins: w.mn || null,
+      const s = { x: j.x, p0: w.nib || w.codes || w.lo, p1: w.hi || null, scales: w.sc, mins: w.mn || null,
         y: j.y, K: j.K, N: j.N };
+      if (j.gate) s.gate = j.gate;
+      if (j.norm) s.normW = j.norm;
+      if (j.res) s.res = j.res;
+      if (j.eps !== undefined) s.eps = j.eps;
+      s.flags = (j.onePlus ? 1 : 0) | (j.act === 'gelu' ? 2 : 0);
+      return s;
     });
     const plan = nat.gemvPlanCreate(this.ctx, FMT[fmt], specs);
     return { run: function () { nat.gemvPlanRun(plan); }, destroy: function () { nat.gemvPlanDestroy(plan); } };

@@ -16,7 +16,7 @@
  * leaves a message for brik_last_error(). Shapes are validated before any launch:
  *   K % 32 == 0 (the reference's documented precondition, src/lib/webgpu/kernels.ts:1045, 1139),
  *   M, K, N >= 0, non-null pointers when the operand is non-empty, plane alignment as listed.
- * M == 0 or N == 0 is a no-op. K == 0 writes y = 0.
+ * M == 0 or N == 0 is a no-op. K == 0 writes y = 0 (with a fill kernel).
  *
  * Workspace: for M >= 2 the matmuls stage x as f16 rows in a device buffer owned by the context
  * (grown with hipMalloc on demand, 2 * M * roundup(K, 256) + 4 * M bytes; growing it first waits
@@ -119,6 +119,31 @@ typedef struct brik_gemv_job {
 typedef struct brik_gemv_plan brik_gemv_plan;
 int brik_gemv_plan_create(brik_ctx *ctx, int fmt, const brik_gemv_job *jobs, int njobs,
                           brik_gemv_plan **out);
+
+/* A plan job with the operations the reference records around each recMM of a decoder layer
+ * (recordLayerKV, kernels.ts:1701-1741) folded in: the RMSNorm before q/k/v and gate/up (rmsnorm,
+ * shaders.ts:580-599; kernels.ts:1701, 1726), the SwiGLU / GeGLU gate before down (swiglu / geglu,
+ * shaders.ts:601-626; kernels.ts:1729) and the residual adds after wo and down (kernels.ts:1725,
+ * 1741). For an M == 1 layer that is 4 launches (q/k/v, wo, gate/up, down) instead of 7 matmuls and
+ * 5 elementwise passes. The input row of the job is, in this order:
+ *   in[k] = act(gate[k]) * x[k]                         when gate != NULL (x holds "up")
+ *   in[k] = in[k] * inv * g[k], inv = 1 / sqrt(sum(in^2) / K + eps), g = norm_w or 1 + norm_w
+ *                                                         when norm_w != NULL (rmsGainOnePlus flag)
+ * and the output y[n] = (res ? res[n] : 0) + (in . deq(W)^T)[n]; res may equal y. act is SiLU
+ * (v / (1 + exp(-v))) or, with BRIK_JOB_ACT_GELU, tanh-GELU. gate, norm_w: DEVICE float[K], 16 B
+ * aligned; res: DEVICE float[N]. No output of a plan may be an input of the same plan. */
+#define BRIK_JOB_GAIN_ONE_PLUS 1
+#define BRIK_JOB_ACT_GELU 2
+typedef struct brik_gemv_job_ex {
+    brik_gemv_job job;
+    const float *gate;
+    const float *norm_w;
+    const float *res;
+    float eps;
+    int32_t flags;
+} brik_gemv_job_ex;
+int brik_gemv_plan_create_ex(brik_ctx *ctx, int fmt, const brik_gemv_job_ex *jobs, int njobs,
+                             brik_gemv_plan **out);
 int brik_gemv_plan_run(brik_ctx *ctx, const brik_gemv_plan *plan);
 void brik_gemv_plan_destroy(brik_ctx *ctx, brik_gemv_plan *plan);
 
@@ -152,6 +177,22 @@ int brik_lm_head_topk_q4(brik_ctx *ctx, const float *x, const uint8_t *nibbles, 
 int brik_lm_head_topk_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const uint32_t *hi,
                          const uint16_t *scales, const uint16_t *mins, int K, int vocab, const int32_t *recent,
                          int n_recent, float penalty, float softcap, int k, int32_t *out_ids, float *out_vals);
+
+/* ---- recorded launches -----------------------------------------------------------------------
+ * The reference records a decoder layer's passes into one command encoder and submits it once
+ * (recordLayerKV, src/lib/webgpu/kernels.ts:1690-1744; decodeTopKQ8 :1908-1969). The MI355X form is
+ * a HIP graph: every launch the context enqueues between brik_graph_begin and brik_graph_end is
+ * recorded (not run), and brik_graph_launch replays them on the context stream in order, without a
+ * host-side launch per kernel. Pointers and shapes are those of the recorded calls; buffer contents
+ * may change between replays. While a capture is open, brik_alloc / brik_free, copies, brik_sync,
+ * plan creation and calls that would grow a context workspace fail with BRIK_EINVAL (make the same
+ * calls once before capturing); after such an error, close the capture with brik_graph_end and
+ * destroy what it returns. One capture per context at a time. */
+typedef struct brik_graph brik_graph;
+int brik_graph_begin(brik_ctx *ctx);
+int brik_graph_end(brik_ctx *ctx, brik_graph **out);
+int brik_graph_launch(brik_ctx *ctx, const brik_graph *graph);
+void brik_graph_destroy(brik_ctx *ctx, brik_graph *graph);
 
 /* ---- dequantization (the bit-exactness check) ----------------------------------------------
  * out[i] = deq(W)[i] in f32 for n_elems elements (n_elems % 32 == 0), bit-identical to

@@ -40,6 +40,7 @@ __all__ = [
     "pack_q8", "pack_q4", "pack_q3", "unpack_q8", "unpack_q4", "unpack_q3",
     "q8_byte_length", "q4_byte_length", "q3_byte_length", "js_round",
     "softcap_logits", "penalize_logits", "top_k",
+    "rmsnorm", "swiglu", "geglu",
 ]
 
 
@@ -326,3 +327,34 @@ def top_k(logits: np.ndarray, k: int):
     nan_last = np.isnan(v).astype(np.int8)
     order = np.lexsort((np.arange(v.size), -key, nan_last))[:k]
     return order.astype(np.uint32), v[order]
+
+
+# ---- the elementwise ops around recMM in a decoder layer (fused into GEMV plans) -------------------
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, rows: int, dim: int, eps: float = 1e-5, one_plus: bool = False):
+    """``rmsnormCpu`` (``kernels.ts:3395-3404``): sum of squares in double, ``1 / sqrt(ss / dim + eps)``,
+    ``x * inv * g`` with ``g = w`` or ``1 + w``, stored to float32."""
+    x = np.asarray(x, np.float32).astype(np.float64).reshape(rows, dim)
+    g = np.asarray(w, np.float32).astype(np.float64)
+    g = 1.0 + g if one_plus else g
+    out = np.empty_like(x)
+    for r in range(rows):
+        ss = 0.0
+        for v in x[r]:
+            ss += v * v
+        inv = 1.0 / np.sqrt(ss / dim + eps)
+        out[r] = x[r] * inv * g
+    return out.astype(np.float32).ravel()
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """``(g / (1 + Math.exp(-g))) * up`` in double, stored to float32 (``kernels.ts:3526-3528``)."""
+    g = np.asarray(gate, np.float32).astype(np.float64)
+    return ((g / (1.0 + np.exp(-g))) * np.asarray(up, np.float32)).astype(np.float32)
+
+
+def geglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """``geluTanh(g) * up`` (``kernels.ts:3498-3500, 3526``), double, stored to float32."""
+    g = np.asarray(gate, np.float32).astype(np.float64)
+    gelu = 0.5 * g * (1.0 + np.tanh(0.7978845608 * (g + 0.044715 * g * g * g)))
+    return (gelu * np.asarray(up, np.float32)).astype(np.float32)
