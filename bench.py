@@ -229,6 +229,31 @@ def lm_head_topk_cfg3(ctx, steps, warmup, gemv_us, cache_bytes=768 << 20):
             "launches": "brik_gemv_q3 + brik_topk_prep + brik_topk_select"}
 
 
+def quantize_f1(ctx, steps, warmup):
+    """The GPU encoders (quantizeQ* byte-exact) on a Qwen3-4B gate matrix, 9728 x 2560 f32 -> packed
+    planes: algorithmic bytes = 4 n read + the packed planes written. Two source copies alternate
+    (each 100 MB, so together beyond the 256 MB last-level cache)."""
+    from brimkern_amd import layout, synth
+    n = 9728 * 2560
+    src = [ctx.upload(synth.normal(900 + i, n)) for i in range(3)]
+    out = {}
+    planes_of = {"q8": ("codes", "sc"), "q4": ("nib", "sc", "mn"), "q3": ("lo", "hi", "sc", "mn")}
+    for fmt in ("q8", "q4", "q3"):
+        ob = ctx.alloc(layout.byte_length(fmt, n))
+        offs = layout.plane_offsets(fmt, n)
+        pl = [ob.offset(offs[p][0]) for p in planes_of[fmt]]
+        ms = time_loop(ctx, lambda i: ctx.quantize(fmt, src[i % 3], pl, n), steps, warmup)
+        b = 4 * n + layout.byte_length(fmt, n)
+        out[fmt] = {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "Gelem_per_s": round(n / (ms * 1e-3) / 1e9, 1)}
+        ctx.free(ob)
+    for bb in src:
+        ctx.free(bb)
+    out["elements"] = n
+    out["kernels"] = "brik_encode_q8 / brik_encode_q4 / brik_encode_q3"
+    return out
+
+
 def gemm_cfg4(ctx, steps, warmup):
     from brimkern_amd import synth
     M, K, N = 512, 2560, 9728
@@ -427,6 +452,8 @@ def main():
         extra["cfg4_q4_gemm_M512_K2560_N9728"] = gemm_cfg4(ctx, args.steps, args.warmup)
         log("bench: cfg5 MoE")
         extra["cfg5_moe_q4_gate_up_down"] = moe_cfg5(ctx, args.steps, args.warmup)
+        log("bench: F1 encoders")
+        extra["f1_quantize_f32_to_planes_N9728_K2560"] = quantize_f1(ctx, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) at Qwen3-4B shapes; prefill q4 GEMM TFLOP/s",

@@ -41,6 +41,10 @@ SIGNATURES = {
     "brik_dequant_q8_f32": (_I, [_P, _P, _P, _P, _Z]),
     "brik_dequant_q4_f32": (_I, [_P, _P, _P, _P, _P, _Z]),
     "brik_dequant_q3_f32": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
+    "brik_quantize_q8": (_I, [_P, _P, _P, _P, _Z]),
+    "brik_quantize_q4": (_I, [_P, _P, _P, _P, _P, _Z]),
+    "brik_quantize_q3": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
+    "brik_f16_to_f32": (_I, [_P, _P, _P, _Z]),
     "brik_timer_begin": (_I, [_P]),
     "brik_timer_end": (_I, [_P, _F]),
     "brik_set_option": (_I, [_P, _I, _I]),
@@ -292,6 +296,15 @@ class Context:
     def dequant_q3(self, lo, hi, sc, mn, out, n):
         self._check(self.lib.brik_dequant_q3_f32(self.handle, _addr(lo), _addr(hi), _addr(sc), _addr(mn),
                                                  _addr(out), n))
+
+    def quantize(self, fmt: str, src, planes, n):
+        """Encode ``n`` f32 values at ``src`` into the planes of ``fmt`` (the unpackQ* order:
+        q8 codes, sc; q4 nib, sc, mn; q3 lo, hi, sc, mn), byte-identical to quantizeQ*."""
+        fn = getattr(self.lib, f"brik_quantize_{fmt}")
+        self._check(fn(self.handle, _addr(src), *[_addr(p) for p in planes], n))
+
+    def f16_to_f32(self, src, out, n):
+        self._check(self.lib.brik_f16_to_f32(self.handle, _addr(src), _addr(out), n))
 
 
 class Graph:

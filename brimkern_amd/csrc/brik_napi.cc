@@ -80,6 +80,18 @@ bool get_f32(napi_env env, napi_value v, float* out)
     return true;
 }
 
+// An element count: a non-negative integral Number (exact below 2^53).
+bool get_size(napi_env env, napi_value v, size_t* out)
+{
+    double d;
+    if (napi_get_value_double(env, v, &d) != napi_ok || !(d >= 0) || d != (double)(uint64_t)d || d > 9007199254740992.0) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a non-negative integer count");
+        return false;
+    }
+    *out = (size_t)d;
+    return true;
+}
+
 // A device pointer: BigInt address, null/undefined (-> nullptr), or an object with a BigInt `ptr`.
 bool get_ptr(napi_env env, napi_value v, void** out)
 {
@@ -366,6 +378,41 @@ napi_value DequantQ3(napi_env env, napi_callback_info info)   // (ctx, lo, hi, s
     return undefined(env);
 }
 
+// (ctx, fmt, src, p0, p1, sc, mn, n): fmt 8 -> codes = p0; 4 -> nibbles = p0; 3 -> lo = p0, hi = p1
+napi_value Quantize(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 8)) return nullptr;
+    brik_ctx* c; int32_t fmt; void* p[5]; size_t n;
+    if (!get_ctx(env, a.v[0], &c) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    for (int k = 0; k < 5; ++k)
+        if (!get_ptr(env, a.v[2 + k], &p[k])) return nullptr;
+    if (!get_size(env, a.v[7], &n)) return nullptr;
+    const float* src = (const float*)p[0];
+    int rc;
+    if (fmt == BRIK_FMT_Q8) rc = brik_quantize_q8(c, src, (int8_t*)p[1], (uint16_t*)p[3], n);
+    else if (fmt == BRIK_FMT_Q4) rc = brik_quantize_q4(c, src, (uint8_t*)p[1], (uint16_t*)p[3], (uint16_t*)p[4], n);
+    else if (fmt == BRIK_FMT_Q3)
+        rc = brik_quantize_q3(c, src, (uint32_t*)p[1], (uint32_t*)p[2], (uint16_t*)p[3], (uint16_t*)p[4], n);
+    else {
+        napi_throw_error(env, "BRIK_EINVAL", "BRIK_EINVAL: quantize: unknown format");
+        return nullptr;
+    }
+    if (check(env, c, rc)) return nullptr;
+    return undefined(env);
+}
+
+napi_value F16ToF32(napi_env env, napi_callback_info info)   // (ctx, src, out, n)
+{
+    Args a;
+    if (!get_args(env, info, a, 4)) return nullptr;
+    brik_ctx* c; void* src; void* out; size_t n;
+    if (!get_ctx(env, a.v[0], &c) || !get_ptr(env, a.v[1], &src) || !get_ptr(env, a.v[2], &out) ||
+        !get_size(env, a.v[3], &n)) return nullptr;
+    if (check(env, c, brik_f16_to_f32(c, (const uint16_t*)src, (float*)out, n))) return nullptr;
+    return undefined(env);
+}
+
 // ---- sampling pre-work -------------------------------------------------------------------------
 
 // logitsTopK(ctx, logits, recent, ids, vals, n, nRecent, k, penalty, softcap)
@@ -534,6 +581,8 @@ napi_value Init(napi_env env, napi_value exports)
         {"dequantQ8", nullptr, DequantQ8, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ4", nullptr, DequantQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ3", nullptr, DequantQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"quantize", nullptr, Quantize, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"f16ToF32", nullptr, F16ToF32, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"logitsTopK", nullptr, LogitsTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"lmHeadTopK", nullptr, LmHeadTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

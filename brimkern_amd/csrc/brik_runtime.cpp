@@ -26,6 +26,7 @@ enum Kern {
     K_XPREP,
     K_TOPK_PREP, K_TOPK_SELECT,
     K_FILL_ZERO,
+    K_QUANT_Q8, K_QUANT_Q4, K_QUANT_Q3, K_F16_TO_F32,
     K_COUNT
 };
 
@@ -34,6 +35,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_xprep_f16",
     "brik_topk_prep", "brik_topk_select",
     "brik_fill_zero",
+    "brik_encode_q8", "brik_encode_q4", "brik_encode_q3", "brik_f16_decode",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -582,6 +584,59 @@ int brik_dequant_q3_f32(brik_ctx* c, const uint32_t* lo, const uint32_t* hi, con
     if (n && (!hi || !sc || !mn)) return fail(c, BRIK_EINVAL, "dequant_q3: null plane");
     void* args[] = {&lo, &hi, &sc, &mn, &out, &n8};
     return dequant(c, K_DEQ_Q3, "dequant_q3", args, n, lo, out, 4);
+}
+
+// Encoders: one thread per 32-element group, 256 groups per block iteration; at most 1024 blocks (four per
+// CU), so each wave loops over several iterations and prefetches the next one's data.
+static int quantize(brik_ctx* c, Kern k, const char* who, void** args, size_t n, const float* src,
+                    const void* codes, const void* hi, const uint16_t* sc, const uint16_t* mn, bool asym)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n % kGroup) return fail(c, BRIK_EINVAL, "%s: n=%zu is not a multiple of 32", who, n);
+    if (n == 0) return BRIK_OK;
+    if (!src || !codes || !sc || (asym && !mn) || (k == K_QUANT_Q3 && !hi))
+        return fail(c, BRIK_EINVAL, "%s: null pointer", who);
+    if (!aligned(src, 16)) return fail(c, BRIK_EALIGN, "%s: src must be 16-byte aligned", who);
+    if (!aligned(codes, 16) || (hi && !aligned(hi, 4)))
+        return fail(c, BRIK_EALIGN, "%s: the code plane (q8 codes, q4 nibbles, q3 lo) must be 16-byte aligned, "
+                    "the q3 hi plane 4-byte", who);
+    if (!aligned(sc, 2) || (mn && !aligned(mn, 2)))
+        return fail(c, BRIK_EALIGN, "%s: scales/mins must be 2-byte aligned", who);
+    const size_t blocks = (n / kGroup + 255) / 256;
+    return launch(c, k, (unsigned)(blocks < 1024 ? blocks : 1024), 1, 256, 0, args);
+}
+
+int brik_quantize_q8(brik_ctx* c, const float* src, int8_t* codes, uint16_t* sc, size_t n)
+{
+    size_t groups = n / kGroup;
+    void* args[] = {&src, &codes, &sc, &groups};
+    return quantize(c, K_QUANT_Q8, "quantize_q8", args, n, src, codes, nullptr, sc, nullptr, false);
+}
+
+int brik_quantize_q4(brik_ctx* c, const float* src, uint8_t* nib, uint16_t* sc, uint16_t* mn, size_t n)
+{
+    size_t groups = n / kGroup;
+    void* args[] = {&src, &nib, &sc, &mn, &groups};
+    return quantize(c, K_QUANT_Q4, "quantize_q4", args, n, src, nib, nullptr, sc, mn, true);
+}
+
+int brik_quantize_q3(brik_ctx* c, const float* src, uint32_t* lo, uint32_t* hi, uint16_t* sc, uint16_t* mn,
+                     size_t n)
+{
+    size_t groups = n / kGroup;
+    void* args[] = {&src, &lo, &hi, &sc, &mn, &groups};
+    return quantize(c, K_QUANT_Q3, "quantize_q3", args, n, src, lo, hi, sc, mn, true);
+}
+
+int brik_f16_to_f32(brik_ctx* c, const uint16_t* src, float* out, size_t n)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n == 0) return BRIK_OK;
+    if (!src || !out) return fail(c, BRIK_EINVAL, "f16_to_f32: null pointer");
+    if (!aligned(src, 16) || !aligned(out, 16)) return fail(c, BRIK_EALIGN, "f16_to_f32: src and out must be 16-byte aligned");
+    const size_t blocks = ((n + 7) / 8 + 255) / 256;
+    void* args[] = {&src, &out, &n};
+    return launch(c, K_F16_TO_F32, (unsigned)(blocks < 8192 ? blocks : 8192), 1, 256, 0, args);
 }
 
 int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out)

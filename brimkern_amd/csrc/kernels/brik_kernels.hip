@@ -3,3 +3,4 @@
 #include "gemv.hip"
 #include "gemm.hip"
 #include "topk.hip"
+#include "quantize.hip"

@@ -1,6 +1,6 @@
 // Standalone dequantization of .brik planes to f32: the bit-exactness check of the in-register
 // dequant the matmul kernels use. Reference semantics: dequantizeQ8/Q4/Q3
-// (src/lib/brik/q8web.ts:108-117, q4web.ts:199-213, q3web.ts:310-323).
+// (src/lib/brik/q8web.ts:74-83, q4web.ts:82-96, q3web.ts:97-110).
 //
 // Exactness argument: code*s is exact in f32 (<= 8-bit code times an 11-bit half mantissa),
 // so fmaf(code, s, m) rounds the exact q*s+m once, as the reference's double expression rounded
@@ -35,7 +35,7 @@ extern "C" __global__ __launch_bounds__(256) void brik_dequant_q4(
     float s = f16_bits_to_f32(sc[e0 / BRIK_GROUP]);
     float m = f16_bits_to_f32(mn[e0 / BRIK_GROUP]);
     f32x4_t o0, o1;
-    // nibble j of the word is element e0 + j (low nibble = even index, q4web.ts:165-166)
+    // nibble j of the word is element e0 + j (low nibble = even index, q4web.ts:48-49)
     for (int j = 0; j < 4; ++j) o0[j] = __builtin_fmaf((float)((w >> (4 * j)) & 15u), s, m);
     for (int j = 0; j < 4; ++j) o1[j] = __builtin_fmaf((float)((w >> (4 * (j + 4))) & 15u), s, m);
     *(f32x4_t*)(out + e0) = o0;
@@ -49,7 +49,7 @@ extern "C" __global__ __launch_bounds__(256) void brik_dequant_q3(
     uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n8) return;
     uint64_t e0 = t * 8;
-    // code i: 2 low bits at lo[i>>4] bit (i&15)*2, high bit at hi[i>>5] bit (i&31) (q3web.ts:268-269)
+    // code i: 2 low bits at lo[i>>4] bit (i&15)*2, high bit at hi[i>>5] bit (i&31) (q3web.ts:55-56)
     uint32_t l = lo[e0 >> 4] >> ((e0 & 15) * 2);
     uint32_t h = hi[e0 >> 5] >> (e0 & 31);
     float s = f16_bits_to_f32(sc[e0 / BRIK_GROUP]);

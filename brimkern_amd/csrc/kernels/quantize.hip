@@ -1,0 +1,390 @@
+// f32 -> packed .brik planes on the GPU, byte-identical to the reference's CPU encoders quantizeQ8 /
+// quantizeQ4 / quantizeQ3 + packQ* (src/lib/brik/q8web.ts:28-50, q4web.ts:28-53, q3web.ts:34-60),
+// which the loader and the GGUF->BRIK converter produce and the matmuls consume. The reference's own
+// GPU quantizers (quantize_q8 / quantize_q4, src/lib/webgpu/shaders.ts:1285-1356) round ties to even
+// and compute in f32; these follow the CPU encoders instead, whose arithmetic is JavaScript doubles:
+//   q8: s = f16(amax / 127 || 1e-8);                 q = clamp(round_half_up(x / s), -127, 127)
+//   q4: s = f16((max - min) / 15 || 1e-8), m = f16(min); q = clamp(round_half_up((x - m) / s), 0, 15)
+//   q3: as q4 with 7 levels
+// with f16() = f32ToF16Bits (src/lib/brik/f16.ts:8-22) and the decoded value of the f16 bits used for
+// the codes (|| 1e-8 again when it decodes to 0). The arithmetic that has to round as JavaScript's does
+// (differences, quotients, the f16 round trip) runs in f64 on the GPU, where each of these operations is
+// correctly rounded, and none of it has a product feeding a sum, so fused multiply-add contraction
+// cannot change it; code_fast below decides the rounding of each code in f32 with a proven margin and
+// hands the rare close cases to the f64 path.
+//
+// Layout: one thread per 32-element group. A wave takes 64 consecutive groups (8 KiB of f32): its
+// lanes load them with consecutive 16-byte loads (1 KiB per instruction), stage them in the wave's own
+// LDS rows with a 16-byte pad per group (36 floats; the per-lane reads of 16 bytes at a 144-byte stride
+// hit every bank once per 16 lanes), and each lane then encodes its own group from LDS, so the scan
+// order, the min / max ties and the stores follow the reference's loop.
+#include "common.h"
+
+namespace {
+
+// f32ToF16Bits: the value rounded to f32, then sign | exponent | 10-bit mantissa rounded half up on
+// the first dropped bit; exponents below the normal range give +-0, above it +-65504 (0x7bff), and a
+// mantissa carry out of exponent 30 gives the infinity bits, as the reference's conversion does.
+__device__ __forceinline__ uint32_t f16_encode(double v)
+{
+    const uint32_t x = __builtin_bit_cast(uint32_t, (float)v);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    int exp = (int)((x >> 23) & 0xffu) - 127 + 15;
+    const uint32_t mant = x & 0x7fffffu;
+    if (exp <= 0) return sign;
+    if (exp >= 31) return sign | 0x7bffu;
+    uint32_t r = (mant >> 13) + ((mant >> 12) & 1u);
+    if (r == 0x400u) {
+        r = 0u;
+        exp += 1;
+    }
+    return sign | ((uint32_t)exp << 10) | (r & 0x3ffu);
+}
+
+// f16BitsToF32 for the bits f16_encode produces (no subnormals): the exact value as a double.
+__device__ __forceinline__ double f16_decode(uint32_t h)
+{
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    double v;
+    if (e == 0u) v = 0.0;
+    else if (e == 31u) v = m ? __builtin_nan("") : __builtin_inf();
+    else v = ldexp(1.0 + m / 1024.0, (int)e - 15);
+    return (h >> 15) ? -v : v;
+}
+
+// JavaScript's `v || 1e-8` for a number: 0 and NaN are falsy.
+__device__ __forceinline__ double or_tiny(double v) { return (v == 0.0 || v != v) ? 1e-8 : v; }
+
+// Math.round: the nearest integer, ties toward +infinity (exact for every double: v - floor(v) is
+// exact below 2^52 and v is integral above). NaN stays NaN.
+__device__ __forceinline__ double js_round(double v)
+{
+    const double f = floor(v);
+    return v - f >= 0.5 ? f + 1.0 : f;
+}
+
+// The integer a clamped code becomes when stored into a typed array (NaN -> 0).
+__device__ __forceinline__ int code_of(double q, double lo, double hi)
+{
+    if (q != q) return 0;
+    q = q < lo ? lo : q > hi ? hi : q;
+    return (int)q;
+}
+
+// The code of one value exactly as the reference computes it: Math.round(d / s) with the f64
+// division, clamped to [lo, hi].
+__device__ __forceinline__ int code_exact(double d, double s, double lo, double hi)
+{
+    return code_of(js_round(d / s), lo, hi);
+}
+
+// v_cvt_i32_f32: the integer part, saturating, with NaN -> 0 (the hardware conversion; a C cast of
+// NaN would be undefined).
+__device__ __forceinline__ int cvt_i32(float v)
+{
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// The same code in f32, without a division: d = x - m and t = d * r (r = 1 / s rounded to f32) are
+// each rounded once in f32, so t is within 3 * 2^-24 (|x| + |m|) / s of the exact (x - m) / s, and
+// JavaScript's f64 quotient is closer still (and rounds half up exactly as the exact quotient does).
+// With the margin e = (|x| + |m|) * r * 2^-20, five times that bound, plus the rounding of t + 1/2
+// (which the compiler may fuse with the product, removing one rounding): when t + 1/2 is farther than
+// e from every integer, floor(t + 1/2) is JavaScript's Math.round.
+// Otherwise `unsure` is set and the caller redoes the group with code_exact (rare for weights: exact
+// ties, values within about 2^-20 of one, or groups far from zero relative to their spread). NaN
+// gives 0 and infinities saturate before the clamp, as the reference's stores and clamp do.
+// `er` is r * 2^-20 and `am` is |m|, both per group.
+__device__ __forceinline__ int code_fast(float x, float m, float r, float er, float am, int lo, int hi, bool& unsure)
+{
+    const float t = (x - m) * r;
+    const float e = (fabsf(x) + am) * er;
+    const float u = t + 0.5f, fu = floorf(u);
+    unsure |= fabsf((u - fu) - 0.5f) >= 0.5f - e;
+    const int q = cvt_i32(fu);
+    return q < lo ? lo : q > hi ? hi : q;
+}
+
+constexpr int ENC_GROUPS = 64;           // groups per wave iteration (one per lane)
+constexpr int ENC_ROW = 36;              // floats per staged group: 32 + a 16-byte pad
+
+// The wave's groups [g0, g0 + 64) of src, as lane-interleaved float4s: t[i] of lane l is float4
+// 64 i + l of the range, so each load of the wave reads 1 KiB of consecutive f32. Past the end of
+// src the last float4 is read again (in bounds; those rows are never encoded).
+__device__ __forceinline__ void load_rows(const f32x4_t* __restrict__ src, size_t g0, size_t groups, f32x4_t (&t)[8])
+{
+    const int lane = threadIdx.x & 63;
+    const size_t limit = (groups - g0) * 8;           // float4s of this wave iteration that exist
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const size_t f = (size_t)i * 64 + lane;
+        t[i] = src[g0 * 8 + (f < limit ? f : limit - 1)];
+    }
+}
+
+// Write loaded rows into the wave's own LDS rows (row j = group g0 + j, 16-byte pad per row). Only
+// the wave itself touches its rows, so waiting for its own LDS writes orders them before its reads
+// (no block barrier).
+__device__ __forceinline__ void store_rows(const f32x4_t (&t)[8], float* __restrict__ rows)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int f = i * 64 + lane;
+        *reinterpret_cast<f32x4_t*>(rows + (f >> 3) * ENC_ROW + (f & 7) * 4) = t[i];
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ f32x4_t row4(const float* row, int i) { return *reinterpret_cast<const f32x4_t*>(row + 4 * i); }
+
+// min and max as the reference's loop finds them: NaN never replaces a value, and of equal values
+// (+0 and -0) the first stays.
+__device__ __forceinline__ void min_max(const float* row, float& mn, float& mx)
+{
+    mn = __builtin_inff();
+    mx = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const f32x4_t w = row4(row, i);
+        const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (e[j] < mn) mn = e[j];
+            if (e[j] > mx) mx = e[j];
+        }
+    }
+}
+
+// The asymmetric (q4 / q3) group header: f16 scale (max - min) / L || 1e-8 and min, their decoded
+// values s (|| 1e-8) and m, and 1 / s.
+template <int L>
+__device__ __forceinline__ void asym_header(const float* row, uint32_t& sh, uint32_t& mh, double& s, double& m,
+                                            double& r)
+{
+    float mn, mx;
+    min_max(row, mn, mx);
+    sh = f16_encode(or_tiny(((double)mx - (double)mn) / (double)L));
+    mh = f16_encode((double)mn);
+    s = or_tiny(f16_decode(sh));
+    m = f16_decode(mh);
+    r = 1.0 / s;
+}
+
+}  // namespace
+
+// In every encoder a wave iteration stages 64 groups and each lane encodes its own group from its row:
+// the codes with code_fast, word by word, and, in the rare case that a value was unsure, the whole group
+// again with code_exact (the later stores overwrite the earlier words). The loads of the wave's next
+// 64 groups are issued before the encoding, so they overlap it.
+extern "C" __global__ __launch_bounds__(256) void brik_encode_q8(const f32x4_t* __restrict__ src,
+                                                                 uint32_t* __restrict__ codes,
+                                                                 uint16_t* __restrict__ scales, size_t groups)
+{
+    __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
+    const float* row = rows + lane * ENC_ROW;
+    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
+    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
+    f32x4_t t[8];
+    if (g0 < groups) load_rows(src, g0, groups, t);
+    for (; g0 < groups; g0 += stride) {
+        store_rows(t, rows);
+        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
+        const size_t g = g0 + lane;
+        if (g < groups) {
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const f32x4_t w = row4(row, i);
+                const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float a = fabsf(e[j]);
+                    if (a > amax) amax = a;
+                }
+            }
+            const uint32_t sh = f16_encode(or_tiny((double)amax / 127.0));
+            scales[g] = (uint16_t)sh;
+            const double s = or_tiny(f16_decode(sh));
+            const float r = (float)(1.0 / s), er = r * 0x1p-20f;
+            bool unsure = false;
+#pragma unroll 1
+            for (int k = 0; k < 8; ++k) {
+                const f32x4_t w = row4(row, k);
+                const float e[4] = {w.x, w.y, w.z, w.w};
+                uint32_t word = 0u;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    word |= ((uint32_t)code_fast(e[b], 0.f, r, er, 0.f, -127, 127, unsure) & 0xffu) << (8 * b);
+                codes[g * 8 + k] = word;
+            }
+            if (unsure) {
+#pragma unroll 1
+                for (int k = 0; k < 8; ++k) {
+                    uint32_t word = 0u;
+                    for (int b = 0; b < 4; ++b)
+                        word |= ((uint32_t)code_exact((double)row[4 * k + b], s, -127.0, 127.0) & 0xffu) << (8 * b);
+                    codes[g * 8 + k] = word;
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // this lane's row reads are done
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void brik_encode_q4(const f32x4_t* __restrict__ src,
+                                                                 uint32_t* __restrict__ nibbles,
+                                                                 uint16_t* __restrict__ scales,
+                                                                 uint16_t* __restrict__ mins, size_t groups)
+{
+    __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
+    const float* row = rows + lane * ENC_ROW;
+    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
+    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
+    f32x4_t t[8];
+    if (g0 < groups) load_rows(src, g0, groups, t);
+    for (; g0 < groups; g0 += stride) {
+        store_rows(t, rows);
+        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
+        const size_t g = g0 + lane;
+        if (g < groups) {
+            uint32_t sh, mh;
+            double s, m, r;
+            asym_header<15>(row, sh, mh, s, m, r);
+            scales[g] = (uint16_t)sh;
+            mins[g] = (uint16_t)mh;
+            const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
+            bool unsure = false;
+#pragma unroll 1
+            for (int k = 0; k < 4; ++k) {         // element 8 k + b is nibble b of word k (low nibble = even)
+                const f32x4_t a = row4(row, 2 * k), c = row4(row, 2 * k + 1);
+                const float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+                uint32_t word = 0u;
+#pragma unroll
+                for (int b = 0; b < 8; ++b) word |= (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 15, unsure) << (4 * b);
+                nibbles[g * 4 + k] = word;
+            }
+            if (unsure) {
+#pragma unroll 1
+                for (int k = 0; k < 4; ++k) {
+                    uint32_t word = 0u;
+                    for (int b = 0; b < 8; ++b)
+                        word |= (uint32_t)code_exact((double)row[8 * k + b] - m, s, 0.0, 15.0) << (4 * b);
+                    nibbles[g * 4 + k] = word;
+                }
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void brik_encode_q3(const f32x4_t* __restrict__ src,
+                                                                 uint32_t* __restrict__ lo, uint32_t* __restrict__ hi,
+                                                                 uint16_t* __restrict__ scales,
+                                                                 uint16_t* __restrict__ mins, size_t groups)
+{
+    __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
+    const float* row = rows + lane * ENC_ROW;
+    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
+    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
+    f32x4_t t[8];
+    if (g0 < groups) load_rows(src, g0, groups, t);
+    for (; g0 < groups; g0 += stride) {
+        store_rows(t, rows);
+        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
+        const size_t g = g0 + lane;
+        if (g < groups) {
+            uint32_t sh, mh;
+            double s, m, r;
+            asym_header<7>(row, sh, mh, s, m, r);
+            scales[g] = (uint16_t)sh;
+            mins[g] = (uint16_t)mh;
+            const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
+            bool unsure = false;
+            uint32_t h = 0u;
+            // half k: elements [16 k, 16 k + 16) -> lo word k (2 low bits each) and hi bits [16 k, 16 k + 16)
+#pragma unroll 1
+            for (int k = 0; k < 2; ++k) {
+                uint32_t l = 0u, hb = 0u;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const f32x4_t w = row4(row, 4 * k + c);
+                    const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) {
+                        const uint32_t q = (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 7, unsure);
+                        l |= (q & 3u) << (2 * (4 * c + b));
+                        hb |= (q >> 2) << (4 * c + b);
+                    }
+                }
+                lo[g * 2 + k] = l;
+                h |= hb << (16 * k);
+            }
+            if (unsure) {
+                h = 0u;
+#pragma unroll 1
+                for (int k = 0; k < 2; ++k) {
+                    uint32_t l = 0u;
+                    for (int i = 0; i < 16; ++i) {
+                        const uint32_t q = (uint32_t)code_exact((double)row[16 * k + i] - m, s, 0.0, 7.0);
+                        l |= (q & 3u) << (2 * i);
+                        h |= (q >> 2) << (16 * k + i);
+                    }
+                    lo[g * 2 + k] = l;
+                }
+            }
+            hi[g] = h;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
+// f16 bits -> f32 as the reference's conversion path decodes an F16 tensor before quantizing it
+// (f16ToF32, src/lib/webgpu/kernels.ts:3213-3222, applied by dequantizeToGpu at kernels.ts:798-803):
+// the IEEE half value, subnormals included, except that exponent 31 (infinity and NaN) decodes to
+// +-65504. Thread t converts elements [8 t, 8 t + 8); src and out are 16-byte aligned.
+extern "C" __global__ __launch_bounds__(256) void brik_f16_decode(const uint16_t* __restrict__ src,
+                                                                  float* __restrict__ out, size_t n)
+{
+    const size_t n8 = (n + 7) / 8;
+    for (size_t t = (size_t)blockIdx.x * 256 + threadIdx.x; t < n8; t += (size_t)gridDim.x * 256) {
+        const size_t i0 = t * 8;
+        uint32_t h[8];
+        if (i0 + 8 <= n) {
+            const u32x4_t w = *reinterpret_cast<const u32x4_t*>(src + i0);
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h[2 * j] = ws[j] & 0xffffu;
+                h[2 * j + 1] = ws[j] >> 16;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = i0 + j < n ? src[i0 + j] : 0u;
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool top = ((h[j] >> 10) & 0x1fu) == 0x1fu;
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)h[j]);
+            v[j] = top ? ((h[j] & 0x8000u) ? -65504.f : 65504.f) : d;
+        }
+        if (i0 + 8 <= n) {
+            f32x4_t* o = reinterpret_cast<f32x4_t*>(out + i0);
+            o[0] = f32x4_t{v[0], v[1], v[2], v[3]};
+            o[1] = f32x4_t{v[4], v[5], v[6], v[7]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (i0 + j < n) out[i0 + j] = v[j];
+        }
+    }
+}

@@ -19,6 +19,11 @@ m,k,n)``
 ``decodeTopKQ8`` head      :meth:`Engine.lm_head_top_k` (LM head + softcap +     kernels.ts:1934-1968
 + sampling passes          penalty + top-k, ``{ids, vals}`` sorted descending)
 softcap/penalize/top_k     :meth:`Engine.logits_top_k` (on device logits)        kernels.ts:1940-1958
+``quantizeToBytes(type,    :meth:`Engine.quantize_to_bytes` (GPU encode, bytes   kernels.ts:281-331
+data,n,dtype)``            equal to the CPU ``encodeTensor``)
+``f32ToQ8Gpu/f32ToQ4Gpu``  :meth:`Engine.quantize` (device f32 -> handle)        kernels.ts:986-1010
+.brik container            :mod:`brimkern_amd.container`,                        container.ts:30-87
+                           :meth:`Engine.weight_from_container`
 =========================  ===================================================  ==================
 
 The readback ops take host ``float32`` activations and return a host ``float32`` array of
@@ -31,7 +36,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import layout
+from . import container, layout
 from .capi import BrikError, Context, DeviceBuffer, BRIK_EINVAL
 
 
@@ -45,11 +50,15 @@ class QWeight(dict):
 
 
 class Engine:
-    def __init__(self, device: int = 0):
-        self.ctx = Context(device)
+    def __init__(self, device: int = 0, ctx: Context | None = None):
+        """An engine on HIP device ``device``, or over an existing context ``ctx`` (not closed by
+        :meth:`close`)."""
+        self._own = ctx is None
+        self.ctx = Context(device) if ctx is None else ctx
 
     def close(self):
-        self.ctx.close()
+        if self._own:
+            self.ctx.close()
 
     # ---- uploads ---------------------------------------------------------------------
     def upload_gpu_raw(self, data) -> DeviceBuffer:
@@ -69,6 +78,95 @@ class Engine:
             h["q3"] = True
         h["_buf"] = buf
         return h
+
+    # ---- encoding -------------------------------------------------------------------------
+    _PLANES = {"q8": ("codes", "sc"), "q4": ("nib", "sc", "mn"), "q3": ("lo", "hi", "sc", "mn")}
+    # bytes of each plane per element
+    _PER_ELEM = {"codes": 1.0, "nib": 0.5, "lo": 0.25, "hi": 0.125, "sc": 1 / 16, "mn": 1 / 16}
+
+    def quantize(self, dtype: str, src, n_elems: int) -> QWeight:
+        """``f32ToQ8Gpu`` / ``f32ToQ4Gpu`` (kernels.ts:986-1010) and the q3 analogue: ``n_elems`` f32
+        values at device address ``src`` -> a weight handle (one buffer in packQ* layout), with the
+        bytes of the CPU encoder quantizeQ*."""
+        if dtype not in self._PLANES:
+            raise BrikError(BRIK_EINVAL, f"quantize: unknown dtype {dtype!r}")
+        offs = layout.plane_offsets(dtype, n_elems)
+        buf = self.ctx.alloc(max(layout.byte_length(dtype, n_elems), 1))
+        h = QWeight({k: buf.offset(o) for k, (o, _) in offs.items()})
+        try:
+            self.ctx.quantize(dtype, src, [h[p] for p in self._PLANES[dtype]], n_elems)
+        except BrikError:
+            self.ctx.free(buf)
+            raise
+        if dtype == "q3":
+            h["q3"] = True
+        h["_buf"] = buf
+        return h
+
+    def quantize_to_bytes(self, type_: str, data, n_elems: int, dtype: str, chunk: int | None = None) -> np.ndarray:
+        """``quantizeToBytes`` (kernels.ts:281-331): tensor bytes -> packed .brik bytes (uint8), encoded
+        on the GPU chunk by chunk and read back; equal to the CPU ``encodeTensor`` bytes (codec.ts:17-29).
+        ``type_``: 'F32', 'F16' (decoded as kernels.ts:3213-3222 does) or 'Q8W' / 'Q4W' / 'Q3W' (a packed
+        .brik quant, dequantized on the GPU). ``chunk`` elements per pass (default 2^26), rounded to
+        whole groups (512 elements for quant sources); every chunking gives the same bytes."""
+        if dtype not in self._PLANES:
+            raise BrikError(BRIK_EINVAL, f"quantize_to_bytes: unknown dtype {dtype!r}")
+        if n_elems < 0 or n_elems % 32:
+            raise BrikError(BRIK_EINVAL, f"quantize_to_bytes: nElems {n_elems} is not a multiple of 32")
+        src = np.frombuffer(memoryview(np.ascontiguousarray(data)).cast("B"), np.uint8)
+        qsrc = {"Q8W": "q8", "Q4W": "q4", "Q3W": "q3"}.get(type_)
+        need = {"F32": 4 * n_elems, "F16": 2 * n_elems}.get(type_)
+        if need is None and qsrc:
+            need = layout.byte_length(qsrc, n_elems)
+        if need is None:
+            raise BrikError(BRIK_EINVAL, f"quantize_to_bytes: unsupported source type {type_!r}")
+        if src.size < need:
+            raise BrikError(BRIK_EINVAL, f"quantize_to_bytes: {type_} data has {src.size} bytes, need {need}")
+        out = np.zeros(layout.byte_length(dtype, n_elems), np.uint8)
+        if n_elems == 0:
+            return out
+        unit = 512 if qsrc else 32
+        ch = (1 << 26) if chunk is None else int(chunk)
+        ch = min(max(unit, ch // unit * unit), n_elems)
+        out_offs = layout.plane_offsets(dtype, n_elems)
+        cap = -(-ch // 32) * 32
+        ch_offs = layout.plane_offsets(dtype, cap)
+        f32 = self.ctx.alloc(4 * ch)
+        qbuf = self.ctx.alloc(layout.byte_length(dtype, cap))
+        stage = self.ctx.alloc(2 * ch) if type_ == "F16" else None
+        w = self.weight(qsrc, src, n_elems) if qsrc else None
+        pe = self._PER_ELEM
+        try:
+            for e0 in range(0, n_elems, ch):
+                ce = min(ch, n_elems - e0)
+                if type_ == "F32":
+                    self.ctx.h2d(f32, src[4 * e0:4 * (e0 + ce)])
+                elif type_ == "F16":
+                    self.ctx.h2d(stage, src[2 * e0:2 * (e0 + ce)])
+                    self.ctx.f16_to_f32(stage, f32, ce)
+                else:
+                    at = {p: w[p] + int(e0 * pe[p]) for p in self._PLANES[qsrc]}
+                    getattr(self.ctx, f"dequant_{qsrc}")(*[at[p] for p in self._PLANES[qsrc]], f32, ce)
+                dst = {p: qbuf.offset(ch_offs[p][0]) for p in self._PLANES[dtype]}
+                self.ctx.quantize(dtype, f32, [dst[p] for p in self._PLANES[dtype]], ce)
+                for p in self._PLANES[dtype]:
+                    ln, o = int(ce * pe[p]), out_offs[p][0] + int(e0 * pe[p])
+                    out[o:o + ln] = self.ctx.download(dst[p], np.uint8, ln)
+        finally:
+            self.ctx.free(f32)
+            self.ctx.free(qbuf)
+            if stage is not None:
+                self.ctx.free(stage)
+            if w is not None:
+                self.ctx.free(w["_buf"])
+        return out
+
+    def weight_from_container(self, parsed: dict, name: str) -> QWeight:
+        """A weight handle for tensor ``name`` of a parsed .brik file (:func:`container.parse_brik`)."""
+        entry, b = container.tensor_bytes(parsed, name)
+        if entry["dtype"] not in self._PLANES:
+            raise BrikError(BRIK_EINVAL, f"weight_from_container: {name} has dtype {entry['dtype']}, not q8/q4/q3")
+        return self.weight(entry["dtype"], np.frombuffer(b, np.uint8), entry["nElems"])
 
     # ---- readback ops ------------------------------------------------------------------
     def _run(self, fn, a, planes, m, k, n):

@@ -17,6 +17,10 @@
 //                                                    -> Promise<{ids: Uint32Array, vals: Float32Array}>
 //   softcap_logits / penalize_logits /  :1940-1958  engine.logitsTopK(logits, vocab, recent, penalty, softcap, K)
 //   top_k passes on a logits buffer                  (in place, like the reference's passes)
+//   quantizeToBytes(type, data, n, dt)  :281-331    engine.quantizeToBytes(type, data, n, dtype[, chunk]) -> Promise<Uint8Array>
+//   f32ToQ8Gpu / f32ToQ4Gpu             :986-1010   engine.quantize(dtype, src, n) -> device weight handle
+//   .brik container (container.ts)                   require('./container'): parseBrik, serializeBrik, ...;
+//                                                    engine.weightFromContainer(parsed, name)
 //
 // Plane arguments may be DeviceBuffers, plane views ({ptr: BigInt}) or BigInt addresses. Errors
 // (bad shapes, K % 32 != 0, misalignment, no device) throw an Error whose .code is "BRIK_E...";
@@ -24,6 +28,7 @@
 
 const path = require('path');
 const planes = require('./planes');
+const container = require('./container');
 
 let native = null;
 function loadNative() {
@@ -49,6 +54,12 @@ class DeviceBuffer {
       this.ptr = null;
     }
   }
+}
+
+function einval(msg) {
+  const e = new Error('BRIK_EINVAL: ' + msg);
+  e.code = 'BRIK_EINVAL';
+  return e;
 }
 
 function toBytes(data) {
@@ -237,11 +248,101 @@ class Engine {
     return out;
   }
 
+  // ---- encoding (the conversion pipeline's GPU quantizer) ------------------------------------------
+  // Tensor bytes -> packed .brik bytes (packQ8 / packQ4 / packQ3 layout), quantized on the GPU and
+  // read back, like quantizeToBytes (kernels.ts:281-331). The bytes equal the CPU encoders'
+  // (encodeTensor -> packQ*, codec.ts:17-29) for every input. `type` is the source encoding: 'F32',
+  // 'F16' (decoded as kernels.ts:3213-3222 does), or a .brik quant 'Q8W' / 'Q4W' / 'Q3W' (dequantized
+  // on the GPU first). `dtype`: 'q8' | 'q4' | 'q3'. The work runs in chunks of `chunkOverride`
+  // elements (default 2^26), rounded to whole groups (whole 512-element blocks for quant sources),
+  // so the device holds one chunk at a time; any chunking gives the same bytes.
+  quantizeToBytes(type, data, nElems, dtype, chunkOverride) {
+    const src = toBytes(data);
+    if (!FMT[dtype]) throw einval('quantizeToBytes: unknown dtype ' + dtype);
+    if (!(nElems >= 0) || nElems % 32 !== 0) throw einval('quantizeToBytes: nElems ' + nElems + ' is not a multiple of 32');
+    const quantSrc = { Q8W: 'q8', Q4W: 'q4', Q3W: 'q3' }[type];
+    const need = type === 'F32' ? 4 * nElems : type === 'F16' ? 2 * nElems : quantSrc ? planes.byteLength(quantSrc, nElems) : -1;
+    if (need < 0) throw einval('quantizeToBytes: unsupported source type ' + type);
+    if (src.byteLength < need) throw einval('quantizeToBytes: ' + type + ' data has ' + src.byteLength + ' bytes, need ' + need);
+    const out = new Uint8Array(planes.byteLength(dtype, nElems));
+    if (nElems === 0) return Promise.resolve(out);
+    const unit = quantSrc ? 512 : 32;
+    let chunk = chunkOverride === undefined ? (1 << 26) : chunkOverride;
+    chunk = Math.max(unit, Math.floor(chunk / unit) * unit);
+    chunk = Math.min(chunk, nElems);
+    const outOffs = planes.planeOffsets(dtype, nElems);
+    const chunkOffs = planes.planeOffsets(dtype, Math.ceil(chunk / 32) * 32);
+    const nat = this.native, ctx = this.ctx;
+    const f32 = this.alloc(4 * chunk);
+    const qbuf = this.alloc(planes.byteLength(dtype, Math.ceil(chunk / 32) * 32));
+    const stage = type === 'F16' ? this.alloc(2 * chunk) : null;
+    const w = quantSrc ? this.weightFromBlob(quantSrc, src, nElems) : null;
+    // bytes per element of each plane (codes 1, nibbles 1/2, lo 1/4, hi 1/8, scales and mins 2/32)
+    const perElem = { codes: 1, nib: 0.5, lo: 0.25, hi: 0.125, sc: 1 / 16, mn: 1 / 16 };
+    try {
+      for (let e0 = 0; e0 < nElems; e0 += chunk) {
+        const ce = Math.min(chunk, nElems - e0);
+        if (type === 'F32') {
+          nat.h2d(ctx, f32.ptr, src.subarray(4 * e0, 4 * (e0 + ce)));
+        } else if (type === 'F16') {
+          nat.h2d(ctx, stage.ptr, src.subarray(2 * e0, 2 * (e0 + ce)));
+          nat.f16ToF32(ctx, stage.ptr, f32.ptr, ce);
+        } else {
+          const at = function (p) { return w[p].ptr + BigInt(e0 * perElem[p]); };
+          if (quantSrc === 'q8') nat.dequantQ8(ctx, at('codes'), at('sc'), f32.ptr, ce);
+          else if (quantSrc === 'q4') nat.dequantQ4(ctx, at('nib'), at('sc'), at('mn'), f32.ptr, ce);
+          else nat.dequantQ3(ctx, at('lo'), at('hi'), at('sc'), at('mn'), f32.ptr, ce);
+        }
+        const dst = function (p) { return qbuf.ptr + BigInt(chunkOffs[p][0]); };
+        const names = Object.keys(outOffs);
+        nat.quantize(ctx, FMT[dtype], f32.ptr, dst(names[0]), dtype === 'q3' ? dst('hi') : null, dst('sc'),
+          dtype === 'q8' ? null : dst('mn'), ce);
+        names.forEach(function (p) {
+          const len = ce * perElem[p];
+          out.set(new Uint8Array(nat.d2h(ctx, dst(p), len)), outOffs[p][0] + e0 * perElem[p]);
+        });
+      }
+    } finally {
+      f32.destroy();
+      qbuf.destroy();
+      if (stage) stage.destroy();
+      if (w) this.destroyWeight(w);
+    }
+    return Promise.resolve(out);
+  }
+
+  // f32ToQ8Gpu / f32ToQ4Gpu (kernels.ts:986-1010) and the q3 analogue: a device f32 buffer of nElems
+  // values -> a device weight handle (one buffer in packQ* layout, planes addressed in place) that
+  // mm / matmul* consume directly; the bytes are the CPU encoder's.
+  quantize(dtype, src, nElems) {
+    if (!FMT[dtype]) throw einval('quantize: unknown dtype ' + dtype);
+    const offs = planes.planeOffsets(dtype, nElems);
+    const buf = this.alloc(planes.byteLength(dtype, nElems));
+    const h = { _buf: buf };
+    Object.keys(offs).forEach(function (k) { h[k] = buf.view(offs[k][0]); });
+    try {
+      this.native.quantize(this.ctx, FMT[dtype], src, h.codes || h.nib || h.lo, h.hi || null, h.sc, h.mn || null, nElems);
+    } catch (e) {
+      buf.destroy();
+      throw e;
+    }
+    if (dtype === 'q3') h.q3 = true;
+    return h;
+  }
+
+  // A weight handle for tensor `name` of a parsed .brik file (container.parseBrik): its packed bytes
+  // uploaded once, planes addressed in place (weightFromBlob). Quantized dtypes only.
+  weightFromContainer(parsed, name) {
+    const t = container.tensorBytes(parsed, name);
+    if (!FMT[t.entry.dtype]) throw einval('weightFromContainer: ' + name + ' has dtype ' + t.entry.dtype + ', not q8/q4/q3');
+    return this.weightFromBlob(t.entry.dtype, t.bytes, t.entry.nElems);
+  }
+
   setOption(key, value) { this.native.setOption(this.ctx, key, value); }
   sync() { this.native.sync(this.ctx); }
   timerBegin() { this.native.timerBegin(this.ctx); }
   timerEnd() { return this.native.timerEnd(this.ctx); }
 }
 
-module.exports = { Engine: Engine, DeviceBuffer: DeviceBuffer, planes: planes, FMT: FMT,
+module.exports = { Engine: Engine, DeviceBuffer: DeviceBuffer, planes: planes, container: container, FMT: FMT,
   OPT_PATH: OPT_PATH, OPT_GEMV_VARIANT: OPT_GEMV_VARIANT, loadNative: loadNative };

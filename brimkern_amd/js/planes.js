@@ -1,9 +1,9 @@
 'use strict';
 // .brik quantized tensor layouts: byte lengths and plane offsets inside one packed blob.
 //
-// Same offsets as the reference's unpackQ8 / unpackQ4 / unpackQ3 (src/lib/brik/q8web.ts:99-106,
-// q4web.ts:187-197, q3web.ts:293-308) and lengths as q8ByteLength / q4ByteLength / q3ByteLength
-// (q8web.ts:57-60, q4web.ts:140-143, q3web.ts:242-245). Node 12 compatible CommonJS.
+// Same offsets as the reference's unpackQ8 / unpackQ4 / unpackQ3 (src/lib/brik/q8web.ts:65-72,
+// q4web.ts:70-80, q3web.ts:80-95) and lengths as q8ByteLength / q4ByteLength / q3ByteLength
+// (q8web.ts:23-26, q4web.ts:23-26, q3web.ts:29-32). Node 12 compatible CommonJS.
 
 const GROUP = 32;
 

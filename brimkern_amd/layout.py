@@ -1,9 +1,9 @@
 """.brik quantized tensor layouts: plane offsets inside one packed blob.
 
 Same offsets as the reference's ``unpackQ8`` / ``unpackQ4`` / ``unpackQ3``
-(``src/lib/brik/q8web.ts:99-106``, ``q4web.ts:187-197``, ``q3web.ts:293-308``) and byte lengths as
-``q8ByteLength`` / ``q4ByteLength`` / ``q3ByteLength`` (``q8web.ts:57-60``, ``q4web.ts:140-143``,
-``q3web.ts:242-245``). The reference copies each plane into its own GPU buffer
+(``src/lib/brik/q8web.ts:65-72``, ``q4web.ts:70-80``, ``q3web.ts:80-95``) and byte lengths as
+``q8ByteLength`` / ``q4ByteLength`` / ``q3ByteLength`` (``q8web.ts:23-26``, ``q4web.ts:23-26``,
+``q3web.ts:29-32``). The reference copies each plane into its own GPU buffer
 (``model.ts:214-270``); here a blob is uploaded once and the planes are addressed in place, which the
 alignment contract of ``include/brik.h`` allows for any 16-byte aligned blob.
 """

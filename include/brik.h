@@ -71,7 +71,7 @@ int brik_sync(brik_ctx *ctx);
  * matmulQ4Tiled / matmulQ4Shared (kernels.ts:1046-1075), matmulQ3 (kernels.ts:1080-1087) and the
  * recorded forms recMatmulQ8/Q4/Q3 behind recMM (kernels.ts:1521-1567). The kernel is chosen by
  * M as recMatmulQ4 does (kernels.ts:1524-1531): M == 1 -> streaming GEMV; M >= 2 -> f16 MFMA GEMM.
- * Planes are the unpackQ8/Q4/Q3 sub-arrays (q8web.ts:99-106, q4web.ts:187-197, q3web.ts:293-308),
+ * Planes are the unpackQ8/Q4/Q3 sub-arrays (q8web.ts:65-72, q4web.ts:70-80, q3web.ts:80-95),
  * i.e. the packed blob split at the offsets those functions use. */
 
 int brik_matmul_t_q8(brik_ctx *ctx, const float *x, const int8_t *codes, const uint16_t *scales,
@@ -196,14 +196,42 @@ void brik_graph_destroy(brik_ctx *ctx, brik_graph *graph);
 
 /* ---- dequantization (the bit-exactness check) ----------------------------------------------
  * out[i] = deq(W)[i] in f32 for n_elems elements (n_elems % 32 == 0), bit-identical to
- * dequantizeQ8 / dequantizeQ4 / dequantizeQ3 (q8web.ts:108-117, q4web.ts:199-213,
- * q3web.ts:310-323) for every normal (non-subnormal, finite) scale and min. */
+ * dequantizeQ8 / dequantizeQ4 / dequantizeQ3 (q8web.ts:74-83, q4web.ts:82-96,
+ * q3web.ts:97-110) for every normal (non-subnormal, finite) scale and min. */
 int brik_dequant_q8_f32(brik_ctx *ctx, const int8_t *codes, const uint16_t *scales, float *out,
                         size_t n_elems);
 int brik_dequant_q4_f32(brik_ctx *ctx, const uint8_t *nibbles, const uint16_t *scales,
                         const uint16_t *mins, float *out, size_t n_elems);
 int brik_dequant_q3_f32(brik_ctx *ctx, const uint32_t *lo, const uint32_t *hi, const uint16_t *scales,
                         const uint16_t *mins, float *out, size_t n_elems);
+
+/* ---- quantization (f32 -> .brik planes) ----------------------------------------------------
+ * Encode n_elems f32 values (n_elems % 32 == 0) into the planes the matmuls read, byte-identical to
+ * the reference's CPU encoders quantizeQ8 / quantizeQ4 / quantizeQ3 (q8web.ts:28-50, q4web.ts:28-53,
+ * q3web.ts:34-60) for every input, NaN and infinities included: per 32-element group
+ *   q8:    scale = f16(amax / 127 || 1e-8),                  code = clamp(round(x / s), -127, 127)
+ *   q4/q3: scale = f16((max - min) / L || 1e-8), min = f16(min), code = clamp(round((x - m) / s), 0, L)
+ * with L = 15 / 7, f16() = f32ToF16Bits (f16.ts:8-22), s and m the decoded f16 values (s || 1e-8),
+ * round() = Math.round (ties toward +infinity) and NaN codes stored as 0. These replace the GPU
+ * encoders quantize_q8 / quantize_q4 (shaders.ts:1285-1356, f32ToQ8Gpu / f32ToQ4Gpu at
+ * kernels.ts:986-1010), which compute in f32 and round ties to even, so their codes can differ from
+ * the CPU encoder's by one (the reference accepts that through a matmul tolerance,
+ * kernels.ts:2341-2348, 2418-2424); these agree with the CPU bytes on every input. Outputs are the unpacked planes (codes int8[n],
+ * nibbles u8[n/2], lo u32[n/16] + hi u32[n/32], scales and mins u16[n/32]); packQ* concatenates them
+ * (q8web.ts:55-62, q4web.ts:58-66, q3web.ts:65-76). src 16-byte, code planes 4-byte, scales/mins
+ * 2-byte aligned. */
+int brik_quantize_q8(brik_ctx *ctx, const float *src, int8_t *codes, uint16_t *scales, size_t n_elems);
+int brik_quantize_q4(brik_ctx *ctx, const float *src, uint8_t *nibbles, uint16_t *scales, uint16_t *mins,
+                     size_t n_elems);
+int brik_quantize_q3(brik_ctx *ctx, const float *src, uint32_t *lo, uint32_t *hi, uint16_t *scales,
+                     uint16_t *mins, size_t n_elems);
+
+/* out[i] = f16ToF32(src[i]) for n_elems half values (any count; src and out 16-byte aligned): the
+ * decode the reference's conversion path applies to an F16 tensor before quantizing it
+ * (kernels.ts:3213-3222 via dequantizeToGpu, kernels.ts:798-803) — the IEEE half value, subnormals
+ * included, with exponent 31 (infinity, NaN) decoded as +-65504. The reference's GPU f16_to_f32
+ * shader (shaders.ts:932-943) decodes those two as infinity / NaN; every other input agrees. */
+int brik_f16_to_f32(brik_ctx *ctx, const uint16_t *src, float *out, size_t n_elems);
 
 /* ---- timing and tuning -------------------------------------------------------------------
  * The reference has no kernel timing (it times whole tokens with performance.now(),

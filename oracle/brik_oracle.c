@@ -7,9 +7,9 @@
  *
  * It restates, in plain C, the reference's own CPU-side arithmetic for this path:
  *   - f16 decode / encode ........ src/lib/brik/f16.ts:8-22, 25-34
- *   - q8 dequant ................. src/lib/brik/q8web.ts:108-117   (w = code * s)
- *   - q4 dequant ................. src/lib/brik/q4web.ts:199-213   (w = q * s + m, low nibble = even index)
- *   - q3 dequant ................. src/lib/brik/q3web.ts:310-323   (q = lo2 | hi1 << 2, w = q * s + m)
+ *   - q8 dequant ................. src/lib/brik/q8web.ts:74-83   (w = code * s)
+ *   - q4 dequant ................. src/lib/brik/q4web.ts:82-96   (w = q * s + m, low nibble = even index)
+ *   - q3 dequant ................. src/lib/brik/q3web.ts:97-110   (q = lo2 | hi1 << 2, w = q * s + m)
  *   - reference matmul ........... src/lib/webgpu/kernels.ts:2335-2337 (and its q3/q8/tiled/shared
  *                                  siblings at 2364-2365, 2381-2382, 2397-2398, 2412-2414,
  *                                  2438-2439, 2455-2456): Wd = dequantize(q) as Float32Array,
@@ -91,7 +91,7 @@ void oracle_f32_to_f16_n(const float *v, size_t n, uint16_t *out)
 
 /* ---- dequantization of a contiguous range of elements [e0, e0 + cnt) ---------------------- */
 
-/* q8web.ts:108-117: out[i] = codes[i] * s (double), stored to f32. */
+/* q8web.ts:74-83: out[i] = codes[i] * s (double), stored to f32. */
 static void deq_q8_range(const int8_t *codes, const uint16_t *sc, size_t e0, size_t cnt, float *out)
 {
     for (size_t j = 0; j < cnt; j++) {
@@ -101,7 +101,7 @@ static void deq_q8_range(const int8_t *codes, const uint16_t *sc, size_t e0, siz
     }
 }
 
-/* q4web.ts:199-213: byte = nibbles[i >> 1]; q = even i ? low nibble : high nibble; q*s + m. */
+/* q4web.ts:82-96: byte = nibbles[i >> 1]; q = even i ? low nibble : high nibble; q*s + m. */
 static void deq_q4_range(const uint8_t *nib, const uint16_t *sc, const uint16_t *mn,
                          size_t e0, size_t cnt, float *out)
 {
@@ -115,7 +115,7 @@ static void deq_q4_range(const uint8_t *nib, const uint16_t *sc, const uint16_t 
     }
 }
 
-/* q3web.ts:310-323: q = ((lo[i>>4] >> ((i&15)*2)) & 3) | (((hi[i>>5] >> (i&31)) & 1) << 2). */
+/* q3web.ts:97-110: q = ((lo[i>>4] >> ((i&15)*2)) & 3) | (((hi[i>>5] >> (i&31)) & 1) << 2). */
 static void deq_q3_range(const uint32_t *lo, const uint32_t *hi, const uint16_t *sc,
                          const uint16_t *mn, size_t e0, size_t cnt, float *out)
 {

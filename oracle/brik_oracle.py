@@ -7,14 +7,14 @@ Two parts:
 
 * ctypes wrappers over ``brik_oracle.c`` — the C restatement of the reference's CPU arithmetic:
   f16 decode/encode (``src/lib/brik/f16.ts:8-34``), ``dequantizeQ8/Q4/Q3``
-  (``src/lib/brik/q8web.ts:108-117``, ``q4web.ts:199-213``, ``q3web.ts:310-323``) and the
+  (``src/lib/brik/q8web.ts:74-83``, ``q4web.ts:82-96``, ``q3web.ts:97-110``) and the
   self-validation reference matmul (``src/lib/webgpu/kernels.ts:2335-2337``: dequantize to
   Float32Array, sum ``a*w`` left to right in a JS double, round once to f32).
 * numpy restatements of the reference's encoder side, used only to re-derive the reference's own
-  codec unit tests as pins of the layout: ``quantizeQ8/Q4/Q3`` (``q8web.ts:62-84``,
-  ``q4web.ts:145-170``, ``q3web.ts:247-273``), ``packQ*`` / ``unpackQ*`` offsets
-  (``q8web.ts:89-106``, ``q4web.ts:175-197``, ``q3web.ts:278-308``) and the byte-length formulas
-  (``q8web.ts:57-60``, ``q4web.ts:140-143``, ``q3web.ts:242-245``).
+  codec unit tests as pins of the layout: ``quantizeQ8/Q4/Q3`` (``q8web.ts:28-50``,
+  ``q4web.ts:28-53``, ``q3web.ts:34-60``), ``packQ*`` / ``unpackQ*`` offsets
+  (``q8web.ts:55-72``, ``q4web.ts:58-80``, ``q3web.ts:65-95``) and the byte-length formulas
+  (``q8web.ts:23-26``, ``q4web.ts:23-26``, ``q3web.ts:29-32``).
 
 Pinning status (which independent check fixes each function) is listed in the test files
 ``tests/test_oracle_*.py``.
@@ -186,16 +186,16 @@ def js_round(v: np.ndarray) -> np.ndarray:
     return f + ((v - f) >= 0.5)
 
 
-def q8_byte_length(n: int) -> int:   # q8web.ts:57-60
+def q8_byte_length(n: int) -> int:   # q8web.ts:23-26
     return n + (n // GROUP) * 2
 
 
-def q4_byte_length(n: int) -> int:   # q4web.ts:140-143
+def q4_byte_length(n: int) -> int:   # q4web.ts:23-26
     g = n // GROUP
     return n // 2 + g * 2 + g * 2
 
 
-def q3_byte_length(n: int) -> int:   # q3web.ts:242-245
+def q3_byte_length(n: int) -> int:   # q3web.ts:29-32
     g = n // GROUP
     return (n // 16) * 4 + (n // 32) * 4 + g * 2 + g * 2
 
@@ -213,38 +213,56 @@ def _or_tiny(v):
     return np.where((v == 0) | np.isnan(v), 1e-8, v)
 
 
+def _first_equal(d, v):
+    """Per row, the first element of ``d`` equal to ``v`` (keeps the sign of a zero), else ``v``."""
+    hit = d == v[:, None]
+    first = d[np.arange(d.shape[0]), hit.argmax(axis=1)]
+    return np.where(hit.any(axis=1), first, v)
+
+
+def _store_code(q):
+    """A clamped code as a typed-array store keeps it: NaN (from a NaN input) becomes 0."""
+    return np.where(np.isnan(q), 0.0, q)
+
+
 def quantize_q8(data):
-    """``quantizeQ8`` (q8web.ts:62-84). Returns (codes int8[n], scales u16[n/32])."""
+    """``quantizeQ8`` (q8web.ts:28-50). Returns (codes int8[n], scales u16[n/32])."""
     d = _groups(data)
-    amax = np.abs(d).max(axis=1)
-    scale = _or_tiny(amax / 127)
-    sH = f32_to_f16(scale.astype(np.float32))
-    s = _or_tiny(f16_to_f64(sH))
-    q = np.clip(js_round(d / s[:, None]), -127, 127)
+    # the reference's loop: `if (a > amax) amax = a` from 0, so NaN never wins
+    amax = np.fmax.reduce(np.abs(d), axis=1, initial=0.0)
+    with np.errstate(over="ignore", invalid="ignore"):
+        scale = _or_tiny(amax / 127)
+        sH = f32_to_f16(scale.astype(np.float32))
+        s = _or_tiny(f16_to_f64(sH))
+        q = _store_code(np.clip(js_round(d / s[:, None]), -127, 127))
     return q.astype(np.int8).ravel(), sH
 
 
 def _quant_asym(data, levels):
     d = _groups(data)
-    mn, mx = d.min(axis=1), d.max(axis=1)
-    scale = _or_tiny((mx - mn) / levels)
-    sH = f32_to_f16(scale.astype(np.float32))
-    mH = f32_to_f16(mn.astype(np.float32))
-    s = _or_tiny(f16_to_f64(sH))
-    m = f16_to_f64(mH)
-    q = np.clip(js_round((d - m[:, None]) / s[:, None]), 0, levels).astype(np.uint32).ravel()
+    # `if (v < mn) mn = v; if (v > mx) mx = v` from +-Infinity: NaN is skipped, an all-NaN group
+    # keeps mn = Infinity, mx = -Infinity, and among equal values (+0 and -0) the first one stays
+    mn = _first_equal(d, np.fmin.reduce(d, axis=1, initial=np.inf))
+    mx = _first_equal(d, np.fmax.reduce(d, axis=1, initial=-np.inf))
+    with np.errstate(over="ignore", invalid="ignore"):
+        scale = _or_tiny((mx - mn) / levels)
+        sH = f32_to_f16(scale.astype(np.float32))
+        mH = f32_to_f16(mn.astype(np.float32))
+        s = _or_tiny(f16_to_f64(sH))
+        m = f16_to_f64(mH)
+        q = _store_code(np.clip(js_round((d - m[:, None]) / s[:, None]), 0, levels)).astype(np.uint32).ravel()
     return q, sH, mH
 
 
 def quantize_q4(data):
-    """``quantizeQ4`` (q4web.ts:145-170). Returns (nibbles u8[n/2], scales, mins)."""
+    """``quantizeQ4`` (q4web.ts:28-53). Returns (nibbles u8[n/2], scales, mins)."""
     q, sH, mH = _quant_asym(data, 15)
     nib = (q[0::2] | (q[1::2] << 4)).astype(np.uint8)   # low nibble = even index
     return nib, sH, mH
 
 
 def quantize_q3(data):
-    """``quantizeQ3`` (q3web.ts:247-273). Returns (lo u32[n/16], hi u32[n/32], scales, mins)."""
+    """``quantizeQ3`` (q3web.ts:34-60). Returns (lo u32[n/16], hi u32[n/32], scales, mins)."""
     q, sH, mH = _quant_asym(data, 7)
     n = q.size
     idx = np.arange(n, dtype=np.uint64)
@@ -256,30 +274,30 @@ def quantize_q3(data):
 
 
 def pack_q8(codes, sc) -> np.ndarray:
-    """``packQ8`` (q8web.ts:89-96): [codes | scales LE]."""
+    """``packQ8`` (q8web.ts:55-62): [codes | scales LE]."""
     return np.concatenate([_c(codes, np.int8).view(np.uint8), _c(sc, "<u2").view(np.uint8)])
 
 
 def pack_q4(nib, sc, mn) -> np.ndarray:
-    """``packQ4`` (q4web.ts:175-183): [nibbles | scales | mins]."""
+    """``packQ4`` (q4web.ts:58-66): [nibbles | scales | mins]."""
     return np.concatenate([_c(nib, np.uint8), _c(sc, "<u2").view(np.uint8), _c(mn, "<u2").view(np.uint8)])
 
 
 def pack_q3(lo, hi, sc, mn) -> np.ndarray:
-    """``packQ3`` (q3web.ts:278-289): [lo | hi | scales | mins]."""
+    """``packQ3`` (q3web.ts:65-76): [lo | hi | scales | mins]."""
     return np.concatenate([_c(lo, "<u4").view(np.uint8), _c(hi, "<u4").view(np.uint8),
                            _c(sc, "<u2").view(np.uint8), _c(mn, "<u2").view(np.uint8)])
 
 
 def unpack_q8(blob, n):
-    """``unpackQ8`` (q8web.ts:99-106)."""
+    """``unpackQ8`` (q8web.ts:65-72)."""
     b = _c(blob, np.uint8)
     g = n // GROUP
     return b[:n].view(np.int8).copy(), b[n:n + 2 * g].view("<u2").copy()
 
 
 def unpack_q4(blob, n):
-    """``unpackQ4`` (q4web.ts:187-197): scales at n/2, mins at n/2 + 2*groups."""
+    """``unpackQ4`` (q4web.ts:70-80): scales at n/2, mins at n/2 + 2*groups."""
     b = _c(blob, np.uint8)
     g = n // GROUP
     nl = n // 2
@@ -287,7 +305,7 @@ def unpack_q4(blob, n):
 
 
 def unpack_q3(blob, n):
-    """``unpackQ3`` (q3web.ts:293-308): lo words, hi words, scales, mins."""
+    """``unpackQ3`` (q3web.ts:80-95): lo words, hi words, scales, mins."""
     b = _c(blob, np.uint8)
     g = n // GROUP
     lb, hb = (n // 16) * 4, (n // 32) * 4

@@ -4,13 +4,17 @@
 //
 // Follows, in the reference's own language and numeric model:
 //   f16BitsToF32 ........ src/lib/brik/f16.ts:25-34
-//   dequantizeQ8/Q4/Q3 .. src/lib/brik/q8web.ts:108-117, q4web.ts:199-213, q3web.ts:310-323
+//   dequantizeQ8/Q4/Q3 .. src/lib/brik/q8web.ts:74-83, q4web.ts:82-96, q3web.ts:97-110
 //   reference matmul .... src/lib/webgpu/kernels.ts:2335-2337 (Wd = dequantize(q) into a
 //                         Float32Array; ref[c] = sum over i of a[i] * Wd[c*k + i] in a JS double)
+//   f32ToF16Bits ........ src/lib/brik/f16.ts:8-22
+//   quantizeQ8/Q4/Q3 .... src/lib/brik/q8web.ts:28-50, q4web.ts:28-53, q3web.ts:34-60, packed as
+//                         packQ8/Q4/Q3 (q8web.ts:55-62, q4web.ts:58-66, q3web.ts:65-76)
 // Node 12 compatible (CommonJS, no optional chaining / nullish coalescing).
 //
-// CLI (used by bench.py's cpu_baseline leg):
+// CLI (used by bench.py's cpu_baseline leg and the encoder tests):
 //   node oracle/cpuref.js <fmt> <M> <K> <N> <input.bin> <output.bin> [reps]
+//   node oracle/cpuref.js quantize <dtype> <input.f32> <output.bin> [reps]   (packed bytes of the f32 input)
 // input.bin = x (M*K f32) followed by the packed .brik blob of W [N, K]; output.bin receives y.
 // Prints one JSON line: {"ms": best wall time of one full matmul incl. dequant, "total_ms": wall time
 // of all reps, "reps": ...}.
@@ -94,10 +98,100 @@ function cpuMatmul(fmt, a, blob, m, k, n) {
   return matmulRef(a, Wd, m, k, n);
 }
 
-module.exports = { f16BitsToF32: f16BitsToF32, planes: planes, dequantize: dequantize,
-  matmulRef: matmulRef, cpuMatmul: cpuMatmul };
+function f32ToF16Bits(val) {
+  const f = new Float32Array(1);
+  const i = new Uint32Array(f.buffer);
+  f[0] = val;
+  const x = i[0];
+  const sign = (x >> 16) & 0x8000;
+  let exp = ((x >> 23) & 0xff) - 127 + 15;
+  let mant = x & 0x7fffff;
+  if (exp <= 0) return sign;
+  if (exp >= 31) return sign | 0x7bff;
+  mant = (mant >> 13) + ((mant >> 12) & 1);
+  if (mant === 0x400) { mant = 0; exp += 1; }
+  return sign | (exp << 10) | (mant & 0x3ff);
+}
 
-if (require.main === module) {
+// The encoders, in the reference's numeric model (JS doubles, Math.round, typed-array stores), each
+// returning the packed bytes. levels = 127 (q8, symmetric) / 15 (q4) / 7 (q3).
+function quantize(dtype, data) {
+  const n = data.length;
+  if (n % GROUP !== 0) throw new Error(dtype + ': length ' + n + ' not a multiple of ' + GROUP);
+  const groups = n / GROUP;
+  const scales = new Uint16Array(groups), mins = new Uint16Array(groups);
+  const codes = new Int8Array(dtype === 'q8' ? n : 0);
+  const nibbles = new Uint8Array(dtype === 'q4' ? n / 2 : 0);
+  const lo = new Uint32Array(dtype === 'q3' ? n / 16 : 0), hi = new Uint32Array(dtype === 'q3' ? n / 32 : 0);
+  for (let g = 0; g < groups; g++) {
+    const base = g * GROUP;
+    if (dtype === 'q8') {
+      let amax = 0;
+      for (let i = 0; i < GROUP; i++) { const a = Math.abs(data[base + i]); if (a > amax) amax = a; }
+      const sH = f32ToF16Bits(amax / 127 || 1e-8);
+      scales[g] = sH;
+      const s = f16BitsToF32(sH) || 1e-8;
+      for (let i = 0; i < GROUP; i++) {
+        let q = Math.round(data[base + i] / s);
+        q = q < -127 ? -127 : q > 127 ? 127 : q;
+        codes[base + i] = q;
+      }
+      continue;
+    }
+    const L = dtype === 'q4' ? 15 : 7;
+    let mn = Infinity, mx = -Infinity;
+    for (let i = 0; i < GROUP; i++) { const v = data[base + i]; if (v < mn) mn = v; if (v > mx) mx = v; }
+    const sH = f32ToF16Bits((mx - mn) / L || 1e-8), mH = f32ToF16Bits(mn);
+    scales[g] = sH; mins[g] = mH;
+    const s = f16BitsToF32(sH) || 1e-8, m = f16BitsToF32(mH);
+    for (let i = 0; i < GROUP; i++) {
+      let q = Math.round((data[base + i] - m) / s);
+      q = q < 0 ? 0 : q > L ? L : q;
+      const idx = base + i;
+      if (dtype === 'q4') {
+        if ((i & 1) === 0) nibbles[idx >> 1] = q;
+        else nibbles[idx >> 1] |= q << 4;
+      } else {
+        lo[idx >> 4] |= (q & 3) << ((idx & 15) * 2);
+        hi[idx >> 5] |= (q >> 2) << (idx & 31);
+      }
+    }
+  }
+  const parts = dtype === 'q8' ? [codes, scales] : dtype === 'q4' ? [nibbles, scales, mins] : [lo, hi, scales, mins];
+  const len = parts.reduce(function (a, p) { return a + p.byteLength; }, 0);
+  const out = new Uint8Array(len);
+  let off = 0;
+  parts.forEach(function (p) {
+    out.set(new Uint8Array(p.buffer, p.byteOffset, p.byteLength), off);
+    off += p.byteLength;
+  });
+  return out;
+}
+
+module.exports = { f16BitsToF32: f16BitsToF32, f32ToF16Bits: f32ToF16Bits, planes: planes, dequantize: dequantize,
+  matmulRef: matmulRef, cpuMatmul: cpuMatmul, quantize: quantize };
+
+function quantizeCli(argv) {
+  const fs = require('fs');
+  const buf = fs.readFileSync(argv[2]);
+  const data = new Float32Array(buf.buffer.slice(buf.byteOffset, buf.byteOffset + (buf.byteLength & ~3)));
+  const reps = argv.length > 4 ? +argv[4] : 1;
+  let best = Infinity, total = 0, out = null;
+  for (let r = 0; r < reps; r++) {
+    const t0 = process.hrtime();
+    out = quantize(argv[1], data);
+    const d = process.hrtime(t0);
+    const ms = d[0] * 1e3 + d[1] / 1e6;
+    best = Math.min(best, ms);
+    total += ms;
+  }
+  fs.writeFileSync(argv[3], Buffer.from(out.buffer, out.byteOffset, out.byteLength));
+  process.stdout.write(JSON.stringify({ ms: best, total_ms: total, reps: reps, dtype: argv[1], n: data.length }) + '\n');
+}
+
+if (require.main === module && process.argv[2] === 'quantize') {
+  quantizeCli(process.argv.slice(2));
+} else if (require.main === module) {
   const fs = require('fs');
   const argv = process.argv.slice(2);
   const fmt = argv[0], M = +argv[1], K = +argv[2], N = +argv[3];

@@ -157,6 +157,51 @@ async function main() {
     lb.destroy();
   }
 
+  // 8. the GPU encoder against the reference's CPU encoder (encodeTensor -> packQ*, restated in
+  //    oracle/cpuref.js): quantizeToBytes in one pass and in chunks of 256 (kernels.ts:2461-2472),
+  //    then a .brik file of the encoded tensors read back into a weight handle for the matmul
+  {
+    const r = rng(4242);
+    const n = 32 * 51;
+    const w = Float32Array.from({ length: n }, function () { return (r() * 2 - 1) * 3; });
+    w[7] = NaN; w[40] = Infinity;
+    for (let i = 64; i < 96; i++) w[i] = 0;
+    for (let i = 96; i < 128; i++) w[i] = (i - 111.5) / 16;      // exact ties
+    const bytes = new Uint8Array(w.buffer);
+    for (const dt of ['q8', 'q4', 'q3']) {
+      const cpu = cpuref.quantize(dt, w);
+      const one = await engine.quantizeToBytes('F32', bytes, n, dt);
+      const many = await engine.quantizeToBytes('F32', bytes, n, dt, 256);
+      const same = function (a, b) { return a.length === b.length && a.every(function (v, i) { return v === b[i]; }); };
+      check('quantizeToBytes ' + dt + ' equals the CPU encoder', same(one, cpu), {});
+      check('quantizeToBytes ' + dt + ' chunked equals one pass', same(one, many), {});
+    }
+    const K = 256, N = 96;
+    const wm = Float32Array.from({ length: N * K }, function () { return r() * 2 - 1; });
+    const q4 = await engine.quantizeToBytes('F32', new Uint8Array(wm.buffer), N * K, 'q4');
+    const c = brik.container;
+    const built = c.assembleBrik({ model: { name: 't' }, arch: { d: K }, chat: { template: '', stopTokenIds: [] },
+      tokenizer: { kind: 'hf-hub', id: 'x' },
+      tensors: [{ name: 'blk.0.ffn_up.weight', dtype: 'q4', shape: [N, K], bytes: q4, nElems: N * K }] });
+    const parsed = c.parseBrik(c.serializeBrik(built.manifest, built.shards));
+    const hw = engine.weightFromContainer(parsed, 'blk.0.ffn_up.weight');
+    const xv = Float32Array.from({ length: K }, function () { return r() * 2 - 1; });
+    const y = await engine.matmulQ4(xv, hw.nib, hw.sc, hw.mn, 1, K, N);
+    const ref = cpuref.cpuMatmul('q4', xv, q4, 1, K, N);
+    check('weightFromContainer q4 -> matmulQ4', normwise(y, ref) <= 1e-5, { rel: normwise(y, ref) });
+    engine.destroyWeight(hw);
+    // device-resident encode (f32ToQ4Gpu analogue) feeding recMM
+    const wb = engine.uploadGpu(wm);
+    const hq = engine.quantize('q4', wb, N * K);
+    const raw = new Uint8Array(engine.native.d2h(engine.ctx, hq._buf.ptr, q4.length));
+    check('quantize (device handle) bytes', raw.every(function (v, i) { return v === q4[i]; }), {});
+    const xb = engine.uploadGpu(xv);
+    const yb = engine.mm(xb, hq, 1, K, N);
+    check('quantize handle -> mm', normwise(engine.readBack(yb, N * 4), ref) <= 1e-5, {});
+    [wb, xb, yb].forEach(function (b) { b.destroy(); });
+    engine.destroyWeight(hq);
+  }
+
   const failed = results.filter(function (r) { return !r.ok; }).length;
   process.stdout.write(JSON.stringify({ checks: results.length, failed: failed }) + '\n');
   process.exit(failed === 0 ? 0 : 1);
