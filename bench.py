@@ -254,6 +254,36 @@ def quantize_f1(ctx, steps, warmup):
     return out
 
 
+def conv_f4(ctx, steps, warmup):
+    """A UNet-sized 3x3 convolution with a q4 weight (Cin = Cout = 320 on a 64 x 64 latent, stride 1,
+    pad 1): the implicit MFMA GEMM path and, for comparison, the direct kernel (the reference's
+    conv2d_direct_q4 scheme: one output per thread)."""
+    from brimkern_amd import layout, synth
+    from brimkern_amd.capi import BRIK_OPT_PATH
+    Cin, H, W, Cout, k = 320, 64, 64, 320, 3
+    nw = Cout * Cin * k * k
+    t = synth.q4_tensor(950, Cout, Cin * k * k)
+    wb = ctx.upload(layout.pack("q4", t))
+    offs = layout.plane_offsets("q4", nw)
+    planes = [wb.offset(offs[p][0]) for p in ("nib", "sc", "mn")]
+    x = ctx.upload(synth.normal(951, Cin * H * W))
+    b = ctx.upload(synth.normal(952, Cout))
+    y = ctx.alloc(4 * Cout * H * W)
+    flops = 2.0 * Cout * H * W * Cin * k * k
+    out = {}
+    for name, path, st in (("implicit_gemm", 0, steps), ("direct", 1, max(2, steps // 10))):
+        ctx.set_option(BRIK_OPT_PATH, path)
+        ms = time_loop(ctx, lambda i: ctx.conv2d("q4", x, planes, b, y, Cin, H, W, Cout, k, k, 1, 1), st, 2)
+        out[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1)}
+    ctx.set_option(BRIK_OPT_PATH, 0)
+    for bb in (wb, x, b, y):
+        ctx.free(bb)
+    out["shape"] = "Cin 320, 64x64, Cout 320, 3x3, stride 1, pad 1, q4 weight"
+    out["frac_of_mfma_peak"] = round(out["implicit_gemm"]["TFLOPs"] / MFMA_F16_PEAK_TFLOPS, 4)
+    out["launches"] = "brik_xprep_im2col_f16 + brik_gemm_q4 + brik_conv_out"
+    return out
+
+
 def gemm_cfg4(ctx, steps, warmup):
     from brimkern_amd import synth
     M, K, N = 512, 2560, 9728
@@ -452,6 +482,8 @@ def main():
         extra["cfg4_q4_gemm_M512_K2560_N9728"] = gemm_cfg4(ctx, args.steps, args.warmup)
         log("bench: cfg5 MoE")
         extra["cfg5_moe_q4_gate_up_down"] = moe_cfg5(ctx, args.steps, args.warmup)
+        log("bench: F4 q4 convolution")
+        extra["f4_conv2d_q4_320x64x64_k3"] = conv_f4(ctx, args.steps, args.warmup)
         log("bench: F1 encoders")
         extra["f1_quantize_f32_to_planes_N9728_K2560"] = quantize_f1(ctx, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline()

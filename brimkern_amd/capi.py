@@ -45,6 +45,8 @@ SIGNATURES = {
     "brik_quantize_q4": (_I, [_P, _P, _P, _P, _P, _Z]),
     "brik_quantize_q3": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
     "brik_f16_to_f32": (_I, [_P, _P, _P, _Z]),
+    "brik_conv2d_q8": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 8),
+    "brik_conv2d_q4": (_I, [_P, _P, _P, _P, _P, _P, _P] + [_I] * 8),
     "brik_timer_begin": (_I, [_P]),
     "brik_timer_end": (_I, [_P, _F]),
     "brik_set_option": (_I, [_P, _I, _I]),
@@ -302,6 +304,13 @@ class Context:
         q8 codes, sc; q4 nib, sc, mn; q3 lo, hi, sc, mn), byte-identical to quantizeQ*."""
         fn = getattr(self.lib, f"brik_quantize_{fmt}")
         self._check(fn(self.handle, _addr(src), *[_addr(p) for p in planes], n))
+
+    def conv2d(self, fmt: str, inp, planes, bias, out, Cin, H, W, Cout, kh, kw, stride=1, pad=0):
+        """conv2d_direct_q8 / _q4: ``out[Cout, OH, OW]`` from ``inp[Cin, H, W]`` and a q8 (codes, sc) or
+        q4 (nib, sc, mn) OIHW weight; ``bias`` may be None."""
+        fn = getattr(self.lib, f"brik_conv2d_{fmt}")
+        self._check(fn(self.handle, _addr(inp), *[_addr(p) for p in planes], _addr(bias), _addr(out),
+                       Cin, H, W, Cout, kh, kw, stride, pad))
 
     def f16_to_f32(self, src, out, n):
         self._check(self.lib.brik_f16_to_f32(self.handle, _addr(src), _addr(out), n))

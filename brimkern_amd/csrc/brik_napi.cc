@@ -402,6 +402,32 @@ napi_value Quantize(napi_env env, napi_callback_info info)
     return undefined(env);
 }
 
+// (ctx, fmt, inp, p0, sc, mn, bias, out, Cin, H, W, Cout, kh, kw, stride, pad); fmt 8: codes = p0, 4: nibbles
+napi_value Conv2d(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 16)) return nullptr;
+    brik_ctx* c; int32_t fmt; void* p[6]; int32_t i[8];
+    if (!get_ctx(env, a.v[0], &c) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    for (int k = 0; k < 6; ++k)
+        if (!get_ptr(env, a.v[2 + k], &p[k])) return nullptr;
+    for (int k = 0; k < 8; ++k)
+        if (!get_i32(env, a.v[8 + k], &i[k])) return nullptr;
+    int rc;
+    if (fmt == BRIK_FMT_Q8)
+        rc = brik_conv2d_q8(c, (const float*)p[0], (const int8_t*)p[1], (const uint16_t*)p[2], (const float*)p[4],
+                            (float*)p[5], i[0], i[1], i[2], i[3], i[4], i[5], i[6], i[7]);
+    else if (fmt == BRIK_FMT_Q4)
+        rc = brik_conv2d_q4(c, (const float*)p[0], (const uint8_t*)p[1], (const uint16_t*)p[2], (const uint16_t*)p[3],
+                            (const float*)p[4], (float*)p[5], i[0], i[1], i[2], i[3], i[4], i[5], i[6], i[7]);
+    else {
+        napi_throw_error(env, "BRIK_EINVAL", "BRIK_EINVAL: conv2d: the weight must be q8 or q4");
+        return nullptr;
+    }
+    if (check(env, c, rc)) return nullptr;
+    return undefined(env);
+}
+
 napi_value F16ToF32(napi_env env, napi_callback_info info)   // (ctx, src, out, n)
 {
     Args a;
@@ -583,6 +609,7 @@ napi_value Init(napi_env env, napi_value exports)
         {"dequantQ3", nullptr, DequantQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"quantize", nullptr, Quantize, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"f16ToF32", nullptr, F16ToF32, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"conv2d", nullptr, Conv2d, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"logitsTopK", nullptr, LogitsTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"lmHeadTopK", nullptr, LmHeadTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

@@ -27,6 +27,7 @@ enum Kern {
     K_TOPK_PREP, K_TOPK_SELECT,
     K_FILL_ZERO,
     K_QUANT_Q8, K_QUANT_Q4, K_QUANT_Q3, K_F16_TO_F32,
+    K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT,
     K_COUNT
 };
 
@@ -36,6 +37,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_topk_prep", "brik_topk_select",
     "brik_fill_zero",
     "brik_encode_q8", "brik_encode_q4", "brik_encode_q3", "brik_f16_decode",
+    "brik_conv2d_direct_q8", "brik_conv2d_direct_q4", "brik_xprep_im2col_f16", "brik_conv_out",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -107,6 +109,8 @@ struct brik_ctx {
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
     size_t tws_bytes = 0;
+    void* cws = nullptr;   // convolution workspace: the [pixels, Cout] GEMM output (grow-only)
+    size_t cws_bytes = 0;
     bool graph_capturing = false;
     char err[512] = {0};
 };
@@ -241,24 +245,24 @@ int fill_zero(brik_ctx* c, float* y, size_t n)
     return launch(c, K_FILL_ZERO, (unsigned)blocks, 1, 256, 0, args);
 }
 
-// MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
-// tile kernel; dense when row_off is null, expert-grouped otherwise.
-int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
-         float* y, int rows, int K, int N, const int* row_off, int E)
+// Workspace for `rows` staged f16 activation rows of K (padded to Kp) and their row scales.
+int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*& rscale)
 {
-    if (K == 0) return fill_zero(c, y, (size_t)rows * N);   // empty sums
-    const long Kp = (K + kGemmKPad - 1) / kGemmKPad * kGemmKPad;
+    Kp = (K + kGemmKPad - 1) / kGemmKPad * kGemmKPad;
     const size_t xbytes = (size_t)rows * Kp * 2;
     if (xbytes >= (1ull << 31))
         return fail(c, BRIK_EINVAL, "matmul: %d rows x K=%d exceed the 2 GiB staged-activation limit", rows, K);
     HIP_TRY_RC(ensure_ws(c, xbytes + 4 * (size_t)rows));
-    uint16_t* xh = static_cast<uint16_t*>(c->ws);
-    float* rscale = reinterpret_cast<float*>(static_cast<char*>(c->ws) + xbytes);
-    int Mi = rows, Ki = K, Ni = N, Kpi = (int)Kp, Ei = E;
-    {
-        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
-        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
-    }
+    xh = static_cast<uint16_t*>(c->ws);
+    rscale = reinterpret_cast<float*>(static_cast<char*>(c->ws) + xbytes);
+    return BRIK_OK;
+}
+
+// The tile kernel over staged rows: dense when row_off is null, expert-grouped otherwise.
+int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
+             const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E)
+{
+    int Mi = rows, Ki = K, Ni = N, Ei = E;
     const int t = gemm_tile(c, rows, N, E);
     const GemmTile& gt = kGemmTiles[t];
     const int bn = kGemmColsPerTn * gt.tn;
@@ -269,6 +273,24 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     // blockIdx.y enumerates (expert, row tile) pairs: at most ceil(rows / BM) + E of them
     return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(N, bn), gemm_tiles(rows, gt.bm) + (unsigned)E,
                      kGemmThreads, 0, args);
+}
+
+// MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
+// tile kernel.
+int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
+         float* y, int rows, int K, int N, const int* row_off, int E)
+{
+    if (K == 0) return fill_zero(c, y, (size_t)rows * N);   // empty sums
+    long Kp;
+    uint16_t* xh;
+    float* rscale;
+    HIP_TRY_RC(gemm_stage_ws(c, rows, K, Kp, xh, rscale));
+    int Mi = rows, Ki = K, Kpi = (int)Kp;
+    {
+        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
+        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
+    }
+    return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E);
 }
 
 // GEMV variant for a given K (index into kGemvVariants).
@@ -454,6 +476,7 @@ void brik_destroy(brik_ctx* c)
     if (c->stream) (void)hipStreamDestroy(c->stream);
     if (c->ws) (void)hipFree(c->ws);
     if (c->tws) (void)hipFree(c->tws);
+    if (c->cws) (void)hipFree(c->cws);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
 }
@@ -626,6 +649,75 @@ int brik_quantize_q3(brik_ctx* c, const float* src, uint32_t* lo, uint32_t* hi, 
     size_t groups = n / kGroup;
     void* args[] = {&src, &lo, &hi, &sc, &mn, &groups};
     return quantize(c, K_QUANT_Q3, "quantize_q3", args, n, src, lo, hi, sc, mn, true);
+}
+
+// Convolution with a quantized weight: implicit MFMA GEMM when the weight rows are whole groups
+// (K = Cin kh kw a multiple of 32) and the shape is large enough for the GEMM tiles, else the direct
+// kernel. Option BRIK_OPT_PATH 1 forces the direct kernel, 2 the GEMM (when K % 32 == 0).
+static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const void* p0, const uint16_t* sc,
+                  const uint16_t* mn, const float* bias, float* out, int Cin, int H, int W, int Cout, int kh, int kw,
+                  int stride, int pad)
+{
+    if (!c) return BRIK_EINVAL;
+    if (Cin < 1 || H < 1 || W < 1 || Cout < 1 || kh < 1 || kw < 1 || stride < 1 || pad < 0)
+        return fail(c, BRIK_EINVAL, "%s: bad shape Cin=%d H=%d W=%d Cout=%d kernel %dx%d stride %d pad %d", who, Cin,
+                    H, W, Cout, kh, kw, stride, pad);
+    if (H + 2 * pad < kh || W + 2 * pad < kw)
+        return fail(c, BRIK_EINVAL, "%s: the %dx%d kernel does not fit the padded %dx%d input", who, kh, kw, H, W);
+    const int OH = (H + 2 * pad - kh) / stride + 1, OW = (W + 2 * pad - kw) / stride + 1;
+    const long long K = (long long)Cin * kh * kw, M = (long long)OH * OW;
+    const long long nw = K * Cout;
+    if (nw % kGroup) return fail(c, BRIK_EINVAL, "%s: the weight has %lld elements, not a multiple of 32", who, nw);
+    if (nw >= (1ll << 32) || M * Cout >= (1ll << 31) || (long long)Cin * H * W >= (1ll << 31))
+        return fail(c, BRIK_EINVAL, "%s: tensor sizes exceed the 2^31-element limit", who);
+    if (!inp || !p0 || !sc || (f == F_Q4 && !mn) || !out) return fail(c, BRIK_EINVAL, "%s: null pointer", who);
+    if (!aligned(inp, 4) || !aligned(out, 16) || (bias && !aligned(bias, 4)) || !aligned(sc, 2) ||
+        (mn && !aligned(mn, 2)) || !aligned(p0, 16))
+        return fail(c, BRIK_EALIGN, "%s: inp / bias 4-byte, out and the code plane 16-byte, scales / mins 2-byte "
+                    "aligned", who);
+    const bool gemm_ok = K % kGroup == 0 && Cout * (K / kGroup) >= 16 && K <= (1 << 30);
+    bool use_gemm = gemm_ok && M >= 64;
+    if (c->opt_path == 1) use_gemm = false;
+    else if (c->opt_path == 2 && gemm_ok) use_gemm = true;
+    int Ci = Cin, Hi = H, Wi = W, Co = Cout, khi = kh, kwi = kw, si = stride, pi = pad, OHi = OH, OWi = OW;
+    if (!use_gemm) {
+        const long long n = M * Cout, blocks = (n + 255) / 256;
+        const unsigned gx = (unsigned)(blocks < 65536 ? blocks : 65536);
+        if (f == F_Q8) {
+            void* args[] = {&inp, &p0, &sc, &bias, &out, &Ci, &Hi, &Wi, &Co, &khi, &kwi, &si, &pi, &OHi, &OWi};
+            return launch(c, K_CONV_Q8, gx, 1, 256, 0, args);
+        }
+        void* args[] = {&inp, &p0, &sc, &mn, &bias, &out, &Ci, &Hi, &Wi, &Co, &khi, &kwi, &si, &pi, &OHi, &OWi};
+        return launch(c, K_CONV_Q4, gx, 1, 256, 0, args);
+    }
+    const int rows = (int)M, Kint = (int)K;
+    long Kp;
+    uint16_t* xh;
+    float* rscale;
+    HIP_TRY_RC(gemm_stage_ws(c, rows, Kint, Kp, xh, rscale));
+    HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, (size_t)M * Cout * 4));
+    float* yt = static_cast<float*>(c->cws);
+    int Kpi = (int)Kp;
+    {
+        void* args[] = {&inp, &xh, &rscale, (void*)&rows, (void*)&Kint, &Kpi, &Hi, &Wi, &khi, &kwi, &si, &pi, &OWi};
+        HIP_TRY_RC(launch(c, K_XPREP_IM2COL, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
+    }
+    HIP_TRY_RC(gemm_run(c, f, xh, rscale, p0, nullptr, sc, mn, yt, rows, Kint, Cout, nullptr, 0));
+    int P = rows;
+    void* args[] = {&yt, &bias, &out, &P, &Co};
+    return launch(c, K_CONV_OUT, (unsigned)((P + 31) / 32), (unsigned)((Cout + 31) / 32), 256, 0, args);
+}
+
+int brik_conv2d_q8(brik_ctx* c, const float* inp, const int8_t* codes, const uint16_t* sc, const float* bias,
+                   float* out, int Cin, int H, int W, int Cout, int kh, int kw, int stride, int pad)
+{
+    return conv2d(c, F_Q8, "conv2d_q8", inp, codes, sc, nullptr, bias, out, Cin, H, W, Cout, kh, kw, stride, pad);
+}
+
+int brik_conv2d_q4(brik_ctx* c, const float* inp, const uint8_t* nib, const uint16_t* sc, const uint16_t* mn,
+                   const float* bias, float* out, int Cin, int H, int W, int Cout, int kh, int kw, int stride, int pad)
+{
+    return conv2d(c, F_Q4, "conv2d_q4", inp, nib, sc, mn, bias, out, Cin, H, W, Cout, kh, kw, stride, pad);
 }
 
 int brik_f16_to_f32(brik_ctx* c, const uint16_t* src, float* out, size_t n)

@@ -4,3 +4,4 @@
 #include "gemm.hip"
 #include "topk.hip"
 #include "quantize.hip"
+#include "conv.hip"

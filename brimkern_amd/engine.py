@@ -22,6 +22,8 @@ softcap/penalize/top_k     :meth:`Engine.logits_top_k` (on device logits)       
 ``quantizeToBytes(type,    :meth:`Engine.quantize_to_bytes` (GPU encode, bytes   kernels.ts:281-331
 data,n,dtype)``            equal to the CPU ``encodeTensor``)
 ``f32ToQ8Gpu/f32ToQ4Gpu``  :meth:`Engine.quantize` (device f32 -> handle)        kernels.ts:986-1010
+session ``conv2d`` with a  :meth:`Engine.conv2d` (q8 / q4 handle)              kernels.ts:1233-1256,
+q8 / q4 weight                                                                  1369-1374
 .brik container            :mod:`brimkern_amd.container`,                        container.ts:30-87
                            :meth:`Engine.weight_from_container`
 =========================  ===================================================  ==================
@@ -160,6 +162,36 @@ class Engine:
             if w is not None:
                 self.ctx.free(w["_buf"])
         return out
+
+    def conv2d(self, inp, w: QWeight, bias, Cin: int, H: int, W: int, Cout: int, kh: int, kw: int,
+               stride: int = 1, pad: int = 0, out=None) -> DeviceBuffer:
+        """The recording session's conv2d for a q8 / q4 weight handle (kernels.ts:1369-1374, fused-dequant
+        conv2d_direct_q8 / q4): ``inp`` [Cin, H, W] and ``bias`` [Cout] (or None) are device buffers or
+        host float32 arrays; returns the device buffer ``out`` [Cout, OH, OW]."""
+        fmt = w.fmt
+        if fmt == "q3":
+            raise BrikError(BRIK_EINVAL, "conv2d: the weight must be a q8 or q4 handle")
+        OH, OW = (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+        tmp = []
+
+        def dev(v):
+            if v is None or isinstance(v, (DeviceBuffer, int)):
+                return v
+            b = self.ctx.upload(np.ascontiguousarray(v, np.float32).ravel())
+            tmp.append(b)
+            return b
+        y = out if out is not None else self.ctx.alloc(max(Cout * OH * OW, 1) * 4)
+        planes = (w["codes"], w["sc"]) if fmt == "q8" else (w["nib"], w["sc"], w["mn"])
+        try:
+            self.ctx.conv2d(fmt, dev(inp), planes, dev(bias), y, Cin, H, W, Cout, kh, kw, stride, pad)
+        except BrikError:
+            if out is None:
+                self.ctx.free(y)
+            raise
+        finally:
+            for b in tmp:
+                self.ctx.free(b)
+        return y
 
     def weight_from_container(self, parsed: dict, name: str) -> QWeight:
         """A weight handle for tensor ``name`` of a parsed .brik file (:func:`container.parse_brik`)."""

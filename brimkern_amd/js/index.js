@@ -19,6 +19,8 @@
 //   top_k passes on a logits buffer                  (in place, like the reference's passes)
 //   quantizeToBytes(type, data, n, dt)  :281-331    engine.quantizeToBytes(type, data, n, dtype[, chunk]) -> Promise<Uint8Array>
 //   f32ToQ8Gpu / f32ToQ4Gpu             :986-1010   engine.quantize(dtype, src, n) -> device weight handle
+//   session conv2d with a q8 / q4 weight :1369-1374  engine.conv2d(inp, w, bias, Cin, H, W, Cout, kh, kw, st, pd[, out])
+//   (recConv2dDirectQ8 / Q4)            :1233-1256  (device resident; inputs may be Float32Arrays)
 //   .brik container (container.ts)                   require('./container'): parseBrik, serializeBrik, ...;
 //                                                    engine.weightFromContainer(parsed, name)
 //
@@ -328,6 +330,33 @@ class Engine {
     }
     if (dtype === 'q3') h.q3 = true;
     return h;
+  }
+
+  // The recording session's conv2d for a quantized weight (kernels.ts:1369-1374, recConv2dDirectQ8 / Q4
+  // at :1233-1256): w is a {codes, sc} or {nib, sc, mn} handle (f32 weights are outside this library);
+  // inp and bias are device buffers or Float32Arrays (uploaded for the call). Returns the device
+  // buffer out [Cout, OH, OW] (allocated when not given).
+  conv2d(inp, w, bias, Cin, H, W, Cout, kh, kw, stride, pad, out) {
+    const st = stride === undefined ? 1 : stride, pd = pad === undefined ? 0 : pad;
+    const fmt = w && w.nib ? FMT.q4 : w && w.codes && !w.q3 ? FMT.q8 : 0;
+    if (!fmt) throw einval('conv2d: the weight must be a q8 {codes, sc} or q4 {nib, sc, mn} handle');
+    const OH = Math.floor((H + 2 * pd - kh) / st) + 1, OW = Math.floor((W + 2 * pd - kw) / st) + 1;
+    const tmp = [];
+    const dev = function (self, v) {
+      if (v instanceof Float32Array) { const b = self.uploadGpu(v); tmp.push(b); return b.ptr; }
+      return v;
+    };
+    const y = out || this.alloc(Math.max(Cout * OH * OW, 1) * 4);
+    try {
+      this.native.conv2d(this.ctx, fmt, dev(this, inp), w.nib || w.codes, w.sc, w.mn || null, dev(this, bias) || null,
+        y, Cin, H, W, Cout, kh, kw, st, pd);
+    } catch (e) {
+      if (!out) y.destroy();
+      throw e;
+    } finally {
+      tmp.forEach(function (b) { b.destroy(); });
+    }
+    return y;
   }
 
   // A weight handle for tensor `name` of a parsed .brik file (container.parseBrik): its packed bytes

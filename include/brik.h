@@ -226,6 +226,25 @@ int brik_quantize_q4(brik_ctx *ctx, const float *src, uint8_t *nibbles, uint16_t
 int brik_quantize_q3(brik_ctx *ctx, const float *src, uint32_t *lo, uint32_t *hi, uint16_t *scales,
                      uint16_t *mins, size_t n_elems);
 
+/* ---- other fused-dequant consumers ---------------------------------------------------------
+ * 2-D convolution with a q8 / q4 weight dequantized on the fly: replaces conv2d_direct_q8 /
+ * conv2d_direct_q4 (shaders.ts:1026-1123) behind recConv2dDirectQ8 / Q4 (kernels.ts:1233-1256):
+ *   out[co, oy, ox] = bias[co] + sum over ci, ky, kx inside the image of
+ *                     inp[ci, oy*stride + ky - pad, ox*stride + kx - pad] * deq(W)[co, ci, ky, kx]
+ * inp [Cin, H, W] f32, W the flat OIHW weight quantized in 32-element groups of its flat index
+ * (Cout*Cin*kh*kw % 32 == 0), bias [Cout] f32 or NULL (zeros), out [Cout, OH, OW] f32 with
+ * OH = (H + 2*pad - kh) / stride + 1, OW likewise. When Cin*kh*kw % 32 == 0 and there are at least 64
+ * output pixels, the convolution runs as an implicit GEMM on the MFMA matmul (im2col rows staged as
+ * scaled f16, the matmul's 1e-3 bar; workspaces as for matmuls, plus 4*OH*OW*Cout bytes); otherwise
+ * a direct kernel accumulates in f32 in the reference's (ci, ky, kx) order. inp and bias 4-byte,
+ * out and the code plane 16-byte, scales / mins 2-byte aligned. */
+int brik_conv2d_q8(brik_ctx *ctx, const float *inp, const int8_t *codes, const uint16_t *scales,
+                   const float *bias, float *out, int Cin, int H, int W, int Cout, int kh, int kw,
+                   int stride, int pad);
+int brik_conv2d_q4(brik_ctx *ctx, const float *inp, const uint8_t *nibbles, const uint16_t *scales,
+                   const uint16_t *mins, const float *bias, float *out, int Cin, int H, int W, int Cout,
+                   int kh, int kw, int stride, int pad);
+
 /* out[i] = f16ToF32(src[i]) for n_elems half values (any count; src and out 16-byte aligned): the
  * decode the reference's conversion path applies to an F16 tensor before quantizing it
  * (kernels.ts:3213-3222 via dequantizeToGpu, kernels.ts:798-803) — the IEEE half value, subnormals

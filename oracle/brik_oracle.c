@@ -222,3 +222,36 @@ void oracle_moe_matmul_t_q4(const float *x_sorted, const int32_t *row_off, const
                     mn + e * per_g, NULL, r1 - r0, K, N, y_sorted + (size_t)r0 * N, NULL, threads);
     }
 }
+
+/* ---- 2-D convolution on dequantized weights (fused-dequant consumers conv2d_direct_q8 / q4) -----
+ * src/lib/webgpu/kernels.ts:3049-3061 (the self-validation reference conv, used for the q8 / q4
+ * conv checks at 3085-3120 on dequantizeQ8 / dequantizeQ4 weights): acc starts at bias[co] and adds
+ * inp * w over ci, ky, kx (taps inside the image) in a JS double; the result is stored to f32.
+ * absden (optional) receives sum |inp * w| + |bias| per output, the scale of its rounding error. */
+void oracle_conv2d(const float *inp, const float *w, const float *bias, int Cin, int H, int W, int Cout,
+                   int kh, int kw, int stride, int pad, float *out, double *absden)
+{
+    int OH = (H + 2 * pad - kh) / stride + 1, OW = (W + 2 * pad - kw) / stride + 1;
+#pragma omp parallel for schedule(static)
+    for (int co = 0; co < Cout; co++)
+        for (int oy = 0; oy < OH; oy++)
+            for (int ox = 0; ox < OW; ox++) {
+                double acc = bias ? bias[co] : 0.0, den = bias ? fabs((double)bias[co]) : 0.0;
+                for (int ci = 0; ci < Cin; ci++)
+                    for (int ky = 0; ky < kh; ky++) {
+                        int iy = oy * stride + ky - pad;
+                        if (iy < 0 || iy >= H) continue;
+                        for (int kx = 0; kx < kw; kx++) {
+                            int ix = ox * stride + kx - pad;
+                            if (ix < 0 || ix >= W) continue;
+                            double p = (double)inp[((size_t)ci * H + iy) * W + ix] *
+                                       (double)w[(((size_t)co * Cin + ci) * kh + ky) * kw + kx];
+                            acc += p;
+                            den += fabs(p);
+                        }
+                    }
+                size_t o = ((size_t)co * OH + oy) * OW + ox;
+                out[o] = (float)acc;
+                if (absden) absden[o] = den;
+            }
+}

@@ -40,7 +40,7 @@ __all__ = [
     "pack_q8", "pack_q4", "pack_q3", "unpack_q8", "unpack_q4", "unpack_q3",
     "q8_byte_length", "q4_byte_length", "q3_byte_length", "js_round",
     "softcap_logits", "penalize_logits", "top_k",
-    "rmsnorm", "swiglu", "geglu",
+    "rmsnorm", "swiglu", "geglu", "conv2d",
 ]
 
 
@@ -73,6 +73,7 @@ def _L():
         lib.oracle_matmul_t_q4.argtypes = [P, P, P, P, I, I, I, P, P, I]
         lib.oracle_matmul_t_q3.argtypes = [P, P, P, P, P, I, I, I, P, P, I]
         lib.oracle_moe_matmul_t_q4.argtypes = [P, P, P, P, P, I, I, I, P, I]
+        lib.oracle_conv2d.argtypes = [P, P, P, I, I, I, I, I, I, I, I, P, P]
         _lib = lib
     return _lib
 
@@ -376,3 +377,21 @@ def geglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     g = np.asarray(gate, np.float32).astype(np.float64)
     gelu = 0.5 * g * (1.0 + np.tanh(0.7978845608 * (g + 0.044715 * g * g * g)))
     return (gelu * np.asarray(up, np.float32)).astype(np.float32)
+
+
+# ---- convolution (fused-dequant consumers) ------------------------------------------------------
+
+def conv2d(inp, w, bias, Cin, H, W, Cout, kh, kw, stride=1, pad=0, return_absden=False):
+    """The reference conv of the self-validation (kernels.ts:3049-3061): ``out[Cout, OH, OW]`` with
+    the f64 sum over (ci, ky, kx) starting from ``bias[co]``, stored to f32; ``w`` is the
+    dequantized flat OIHW weight (float32). With ``return_absden``, also sum |inp * w| + |bias|."""
+    OH, OW = (H + 2 * pad - kh) // stride + 1, (W + 2 * pad - kw) // stride + 1
+    inp = _c(inp, np.float32).ravel()
+    w = _c(w, np.float32).ravel()
+    assert inp.size == Cin * H * W and w.size == Cout * Cin * kh * kw
+    b = None if bias is None else _c(bias, np.float32).ravel()
+    out = np.empty(Cout * OH * OW, np.float32)
+    den = np.empty(Cout * OH * OW, np.float64) if return_absden else None
+    _L().oracle_conv2d(_p(inp), _p(w), _p(b), Cin, H, W, Cout, kh, kw, stride, pad, _p(out), _p(den))
+    out = out.reshape(Cout, OH, OW)
+    return (out, den.reshape(Cout, OH, OW)) if return_absden else out

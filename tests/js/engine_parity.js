@@ -202,6 +202,40 @@ async function main() {
     engine.destroyWeight(hq);
   }
 
+  // 9. the session conv2d with quantized weights on the reference's validation shape (kernels.ts:3085-3120):
+  //    Cin 8, 4x4, Cout 4, 3x3, stride 1, pad 1, against the reference loop (kernels.ts:3049-3061) on the
+  //    dequantized weights
+  {
+    const r = rng(99);
+    const Cin = 8, Hh = 4, Ww = 4, Cout = 4, kk = 3;
+    const cx = Float32Array.from({ length: Cin * Hh * Ww }, function () { return r() * 2 - 1; });
+    const cw = Float32Array.from({ length: Cout * Cin * kk * kk }, function () { return r() * 2 - 1; });
+    const cb = Float32Array.from({ length: Cout }, function () { return r() * 2 - 1; });
+    for (const dt of ['q8', 'q4']) {
+      const blob = cpuref.quantize(dt, cw);
+      const wd = cpuref.dequantize(dt, cpuref.planes(dt, blob, cw.length), cw.length);
+      const ref = new Float32Array(Cout * Hh * Ww);
+      for (let co = 0; co < Cout; co++)
+        for (let oy = 0; oy < Hh; oy++)
+          for (let ox = 0; ox < Ww; ox++) {
+            let acc = cb[co];
+            for (let ci = 0; ci < Cin; ci++)
+              for (let ky = 0; ky < kk; ky++)
+                for (let kx = 0; kx < kk; kx++) {
+                  const iy = oy + ky - 1, ix = ox + kx - 1;
+                  if (iy >= 0 && iy < Hh && ix >= 0 && ix < Ww)
+                    acc += cx[ci * Hh * Ww + iy * Ww + ix] * wd[((co * Cin + ci) * kk + ky) * kk + kx];
+                }
+            ref[(co * Hh + oy) * Ww + ox] = acc;
+          }
+      const hw = engine.weightFromBlob(dt, blob, cw.length);
+      const yb = engine.conv2d(cx, hw, cb, Cin, Hh, Ww, Cout, kk, kk, 1, 1);
+      check('conv2d ' + dt + ' (session form)', normwise(engine.readBack(yb, ref.length * 4), ref) <= 1e-5, {});
+      yb.destroy();
+      engine.destroyWeight(hw);
+    }
+  }
+
   const failed = results.filter(function (r) { return !r.ok; }).length;
   process.stdout.write(JSON.stringify({ checks: results.length, failed: failed }) + '\n');
   process.exit(failed === 0 ? 0 : 1);
