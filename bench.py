@@ -284,6 +284,31 @@ def conv_f4(ctx, steps, warmup):
     return out
 
 
+def f16w_f4(ctx, steps, warmup, cache_bytes=768 << 20):
+    """The f16-weight matmul (MATMUL_T_F16W) on the Qwen3-4B gate shape (N 9728, K 2560, W 49.8 MB):
+    decode GEMV (M = 1, rotating weight copies beyond the last-level cache; HBM bytes = 2 N K + x + y)
+    and prefill (M = 512, MFMA)."""
+    from brimkern_amd import synth
+    M, K, N = 512, 2560, 9728
+    wbytes = 2 * N * K
+    copies = max(2, -(-cache_bytes // wbytes))
+    w = (synth.normal(960, N * K) * 0.05).astype(np.float16).view(np.uint16)
+    ws = [ctx.upload(w) for _ in range(copies)]
+    x = ctx.upload(synth.normal(961, M * K))
+    y = ctx.alloc(4 * M * N)
+    ms1 = time_loop(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, 1, K, N), max(steps, copies), copies)
+    b1 = wbytes + 4 * K + 4 * N
+    msm = time_loop(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, M, K, N), steps, warmup)
+    tf = 2.0 * M * N * K / (msm * 1e-3) / 1e12
+    for bb in ws + [x, y]:
+        ctx.free(bb)
+    return {"gemv_M1": {"us": round(ms1 * 1e3, 2), "GBps": round(b1 / (ms1 * 1e-3) / 1e9, 1),
+                        "frac": round(b1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies},
+            "gemm_M512": {"us": round(msm * 1e3, 2), "TFLOPs": round(tf, 1),
+                          "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)},
+            "kernels": "brik_gemv_f16w_v8 (M = 1); brik_xprep_f16 + brik_gemm_f16w (M = 512)"}
+
+
 def gemm_cfg4(ctx, steps, warmup):
     from brimkern_amd import synth
     M, K, N = 512, 2560, 9728
@@ -484,6 +509,8 @@ def main():
         extra["cfg5_moe_q4_gate_up_down"] = moe_cfg5(ctx, args.steps, args.warmup)
         log("bench: F4 q4 convolution")
         extra["f4_conv2d_q4_320x64x64_k3"] = conv_f4(ctx, args.steps, args.warmup)
+        log("bench: F4 f16-weight matmul")
+        extra["f4_matmul_t_f16w_K2560_N9728"] = f16w_f4(ctx, args.steps, args.warmup)
         log("bench: F1 encoders")
         extra["f1_quantize_f32_to_planes_N9728_K2560"] = quantize_f1(ctx, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline()

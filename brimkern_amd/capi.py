@@ -45,6 +45,7 @@ SIGNATURES = {
     "brik_quantize_q4": (_I, [_P, _P, _P, _P, _P, _Z]),
     "brik_quantize_q3": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
     "brik_f16_to_f32": (_I, [_P, _P, _P, _Z]),
+    "brik_matmul_t_f16w": (_I, [_P, _P, _P, _P, _I, _I, _I]),
     "brik_conv2d_q8": (_I, [_P, _P, _P, _P, _P, _P] + [_I] * 8),
     "brik_conv2d_q4": (_I, [_P, _P, _P, _P, _P, _P, _P] + [_I] * 8),
     "brik_timer_begin": (_I, [_P]),
@@ -311,6 +312,10 @@ class Context:
         fn = getattr(self.lib, f"brik_conv2d_{fmt}")
         self._check(fn(self.handle, _addr(inp), *[_addr(p) for p in planes], _addr(bias), _addr(out),
                        Cin, H, W, Cout, kh, kw, stride, pad))
+
+    def matmul_t_f16w(self, x, w, y, M, K, N):
+        """y = x . W^T with W [N, K] IEEE f16 bits (MATMUL_T_F16W)."""
+        self._check(self.lib.brik_matmul_t_f16w(self.handle, _addr(x), _addr(w), _addr(y), M, K, N))
 
     def f16_to_f32(self, src, out, n):
         self._check(self.lib.brik_f16_to_f32(self.handle, _addr(src), _addr(out), n))

@@ -428,6 +428,15 @@ napi_value Conv2d(napi_env env, napi_callback_info info)
     return undefined(env);
 }
 
+napi_value MatmulF16W(napi_env env, napi_callback_info info)   // (ctx, x, w, y, M, K, N)
+{
+    brik_ctx* c; void* p[3]; int32_t i[3];
+    if (!parse(env, info, &c, p, 3, i, 3)) return nullptr;
+    if (check(env, c, brik_matmul_t_f16w(c, (const float*)p[0], (const uint16_t*)p[1], (float*)p[2], i[0], i[1], i[2])))
+        return nullptr;
+    return undefined(env);
+}
+
 napi_value F16ToF32(napi_env env, napi_callback_info info)   // (ctx, src, out, n)
 {
     Args a;
@@ -610,6 +619,7 @@ napi_value Init(napi_env env, napi_value exports)
         {"quantize", nullptr, Quantize, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"f16ToF32", nullptr, F16ToF32, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"conv2d", nullptr, Conv2d, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"matmulF16W", nullptr, MatmulF16W, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"logitsTopK", nullptr, LogitsTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"lmHeadTopK", nullptr, LmHeadTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

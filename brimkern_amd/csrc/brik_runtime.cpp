@@ -28,6 +28,7 @@ enum Kern {
     K_FILL_ZERO,
     K_QUANT_Q8, K_QUANT_Q4, K_QUANT_Q3, K_F16_TO_F32,
     K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT,
+    K_GEMV_F16W_V8, K_GEMV_F16W_V4, K_GEMM_F16W,
     K_COUNT
 };
 
@@ -38,6 +39,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_fill_zero",
     "brik_encode_q8", "brik_encode_q4", "brik_encode_q3", "brik_f16_decode",
     "brik_conv2d_direct_q8", "brik_conv2d_direct_q4", "brik_xprep_im2col_f16", "brik_conv_out",
+    "brik_gemv_f16w_v8", "brik_gemv_f16w_v4", "brik_gemm_f16w",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -718,6 +720,48 @@ int brik_conv2d_q4(brik_ctx* c, const float* inp, const uint8_t* nib, const uint
                    const float* bias, float* out, int Cin, int H, int W, int Cout, int kh, int kw, int stride, int pad)
 {
     return conv2d(c, F_Q4, "conv2d_q4", inp, nib, sc, mn, bias, out, Cin, H, W, Cout, kh, kw, stride, pad);
+}
+
+// f16-weight matmul: the GEMV kernel for one activation row (x staged in LDS, K <= 16384) or for
+// K % 8 != 0; otherwise staged f16 rows and the MFMA kernel. BRIK_OPT_PATH 1 / 2 force GEMV / MFMA.
+int brik_matmul_t_f16w(brik_ctx* c, const float* x, const uint16_t* w, float* y, int M, int K, int N)
+{
+    if (!c) return BRIK_EINVAL;
+    if (M < 0 || K < 0 || N < 0) return fail(c, BRIK_EINVAL, "matmul_t_f16w: negative shape M=%d K=%d N=%d", M, K, N);
+    if (K % 4) return fail(c, BRIK_EINVAL, "matmul_t_f16w: K=%d is not a multiple of 4", K);
+    if (M == 0 || N == 0) return BRIK_OK;
+    if (!y) return fail(c, BRIK_EINVAL, "matmul_t_f16w: y is null");
+    if (!aligned(y, 4)) return fail(c, BRIK_EALIGN, "matmul_t_f16w: y must be 4-byte aligned");
+    if (K == 0) return fill_zero(c, y, (size_t)M * N);
+    if (!x || !w) return fail(c, BRIK_EINVAL, "matmul_t_f16w: null operand pointer");
+    if (!aligned(x, 16) || !aligned(w, 16))
+        return fail(c, BRIK_EALIGN, "matmul_t_f16w: x and w must be 16-byte aligned");
+    if ((long long)N * K >= (1ll << 31) || (long long)M * N >= (1ll << 31))
+        return fail(c, BRIK_EINVAL, "matmul_t_f16w: tensors exceed 2^31 elements");
+    const bool gemv_ok = K <= 16384, mfma_ok = K % 8 == 0;
+    bool use_gemv = gemv_ok && (M == 1 || !mfma_ok);
+    if (c->opt_path == 1 && gemv_ok) use_gemv = true;
+    else if (c->opt_path == 2 && mfma_ok) use_gemv = false;
+    if (!use_gemv && !mfma_ok)
+        return fail(c, BRIK_EINVAL, "matmul_t_f16w: K=%d needs K %% 8 == 0 or K <= 16384", K);
+    int Mi = M, Ki = K, Ni = N;
+    if (use_gemv) {
+        const long sets = ((long)N + 7) / 8;
+        const unsigned gx = (unsigned)(sets < 16384 ? sets : 16384);
+        void* args[] = {&x, &w, &y, &Ki, &Ni};
+        return launch(c, K % 8 ? K_GEMV_F16W_V4 : K_GEMV_F16W_V8, gx, (unsigned)M, 256, (size_t)K * 4, args);
+    }
+    long Kp;
+    uint16_t* xh;
+    float* rscale;
+    HIP_TRY_RC(gemm_stage_ws(c, M, K, Kp, xh, rscale));
+    int Kpi = (int)Kp;
+    {
+        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};
+        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((M + 3) / 4), 1, 256, 0, args));
+    }
+    void* args[] = {&xh, &rscale, &w, &y, &Mi, &Ki, &Ni, &Kpi};
+    return launch(c, K_GEMM_F16W, (unsigned)((N + 127) / 128), (unsigned)((M + 63) / 64), 256, 0, args);
 }
 
 int brik_f16_to_f32(brik_ctx* c, const uint16_t* src, float* out, size_t n)

@@ -5,3 +5,4 @@
 #include "topk.hip"
 #include "quantize.hip"
 #include "conv.hip"
+#include "f16w.hip"

@@ -22,6 +22,8 @@ softcap/penalize/top_k     :meth:`Engine.logits_top_k` (on device logits)       
 ``quantizeToBytes(type,    :meth:`Engine.quantize_to_bytes` (GPU encode, bytes   kernels.ts:281-331
 data,n,dtype)``            equal to the CPU ``encodeTensor``)
 ``f32ToQ8Gpu/f32ToQ4Gpu``  :meth:`Engine.quantize` (device f32 -> handle)        kernels.ts:986-1010
+``matmulT(a,w,m,k,n,      :meth:`Engine.matmul_t_f16w` (f16 weight bits)       kernels.ts:410-426,
+wF16)``                    (MATMUL_T_F16W)                                      shaders.ts:2240-2259
 session ``conv2d`` with a  :meth:`Engine.conv2d` (q8 / q4 handle)              kernels.ts:1233-1256,
 q8 / q4 weight                                                                  1369-1374
 .brik container            :mod:`brimkern_amd.container`,                        container.ts:30-87
@@ -227,6 +229,11 @@ class Engine:
 
     matmul_q8_tiled = matmul_q8
     matmul_q8_shared = matmul_q8
+
+    def matmul_t_f16w(self, a, w, m, k, n) -> np.ndarray:
+        """``matmulT(a, w, m, k, n, wF16=true)`` (kernels.ts:410-426 -> MATMUL_T_F16W): ``w`` is a device
+        buffer / address of N x K IEEE f16 bits; returns host float32 [m*n]."""
+        return self._run(lambda xa, wb, out, M, K, N: self.ctx.matmul_t_f16w(xa, wb, out, M, K, N), a, (w,), m, k, n)
 
     def matmul_q3(self, a, lo, hi, sc, mn, m, k, n) -> np.ndarray:
         return self._run(self.ctx.matmul_t_q3, a, (lo, hi, sc, mn), m, k, n)

@@ -19,6 +19,8 @@
 //   top_k passes on a logits buffer                  (in place, like the reference's passes)
 //   quantizeToBytes(type, data, n, dt)  :281-331    engine.quantizeToBytes(type, data, n, dtype[, chunk]) -> Promise<Uint8Array>
 //   f32ToQ8Gpu / f32ToQ4Gpu             :986-1010   engine.quantize(dtype, src, n) -> device weight handle
+//   matmulT(a, w, m, k, n, wF16=true)   :410-426    engine.matmulT(a, w, m, k, n, true) -> Promise<Float32Array>
+//   (MATMUL_T_F16W, shaders.ts:2240)                 (w: f16 bits on the device); engine.mmF16(a, w, m, k, n[, out])
 //   session conv2d with a q8 / q4 weight :1369-1374  engine.conv2d(inp, w, bias, Cin, H, W, Cout, kh, kw, st, pd[, out])
 //   (recConv2dDirectQ8 / Q4)            :1233-1256  (device resident; inputs may be Float32Arrays)
 //   .brik container (container.ts)                   require('./container'): parseBrik, serializeBrik, ...;
@@ -330,6 +332,21 @@ class Engine {
     }
     if (dtype === 'q3') h.q3 = true;
     return h;
+  }
+
+  // matmulT with an f16 weight (kernels.ts:410-426 -> MATMUL_T_F16W): w is a device buffer / address of
+  // N x K IEEE f16 values (uploadGpuRaw of the raw bytes). f32 weights (wF16 false) are outside this
+  // library and throw BRIK_EINVAL.
+  matmulT(a, w, m, k, n, wF16) {
+    if (!wF16) throw einval('matmulT: only f16 weights (wF16 = true) are handled here');
+    return Promise.resolve(this._readback(this.native.matmulF16W, a, [w], m, k, n));
+  }
+
+  // Device-resident form of matmulT with an f16 weight.
+  mmF16(a, w, m, k, n, out) {
+    const y = out || this.alloc(m * n * 4);
+    this.native.matmulF16W(this.ctx, a, w, y, m, k, n);
+    return y;
   }
 
   // The recording session's conv2d for a quantized weight (kernels.ts:1369-1374, recConv2dDirectQ8 / Q4

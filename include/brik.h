@@ -245,6 +245,13 @@ int brik_conv2d_q4(brik_ctx *ctx, const float *inp, const uint8_t *nibbles, cons
                    const uint16_t *mins, const float *bias, float *out, int Cin, int H, int W, int Cout,
                    int kh, int kw, int stride, int pad);
 
+/* y[M, N] = x[M, K] . W[N, K]^T with W stored as IEEE f16 bits: replaces MATMUL_T_F16W
+ * (shaders.ts:2240-2259), which matmulT picks for an f16 weight (kernels.ts:410-426). K % 4 == 0
+ * (the reference's contract); x, w 16-byte aligned, y 4-byte. M == 1 (or K % 8 != 0) streams W with
+ * f32 accumulation (K <= 16384); otherwise x is staged as scaled f16 rows (workspace as for the
+ * quantized matmuls) and an MFMA kernel accumulates in f32 (the matmuls' 1e-3 bar). */
+int brik_matmul_t_f16w(brik_ctx *ctx, const float *x, const uint16_t *w, float *y, int M, int K, int N);
+
 /* out[i] = f16ToF32(src[i]) for n_elems half values (any count; src and out 16-byte aligned): the
  * decode the reference's conversion path applies to an F16 tensor before quantizing it
  * (kernels.ts:3213-3222 via dequantizeToGpu, kernels.ts:798-803) — the IEEE half value, subnormals

@@ -40,7 +40,7 @@ __all__ = [
     "pack_q8", "pack_q4", "pack_q3", "unpack_q8", "unpack_q4", "unpack_q3",
     "q8_byte_length", "q4_byte_length", "q3_byte_length", "js_round",
     "softcap_logits", "penalize_logits", "top_k",
-    "rmsnorm", "swiglu", "geglu", "conv2d",
+    "rmsnorm", "swiglu", "geglu", "conv2d", "matmul_t_f16w",
 ]
 
 
@@ -395,3 +395,11 @@ def conv2d(inp, w, bias, Cin, H, W, Cout, kh, kw, stride=1, pad=0, return_absden
     _L().oracle_conv2d(_p(inp), _p(w), _p(b), Cin, H, W, Cout, kh, kw, stride, pad, _p(out), _p(den))
     out = out.reshape(Cout, OH, OW)
     return (out, den.reshape(Cout, OH, OW)) if return_absden else out
+
+
+def matmul_t_f16w(x, w_bits, M, K, N):
+    """MATMUL_T_F16W (shaders.ts:2240-2259): y = x . W^T with W [N, K] IEEE f16 bits widened to f32
+    (exact), the sum in f64 here. Returns (y float64 [M, N], sum |x w| [M, N])."""
+    x = np.asarray(x, np.float32).reshape(M, K).astype(np.float64)
+    w = np.asarray(w_bits, np.uint16).reshape(N, K).view(np.float16).astype(np.float64)
+    return x @ w.T, np.abs(x) @ np.abs(w).T

@@ -236,6 +236,27 @@ async function main() {
     }
   }
 
+  // 10. matmulT with an f16 weight (MATMUL_T_F16W): decode row and a small prefill, against the JS sum
+  {
+    const r = rng(1234);
+    const K = 512, N = 96;
+    const wf = Float32Array.from({ length: N * K }, function () { return (r() * 2 - 1) * 0.1; });
+    const bits = new Uint16Array(N * K);
+    for (let i = 0; i < bits.length; i++) bits[i] = cpuref.f32ToF16Bits(wf[i]);
+    const wd = Float32Array.from(bits, function (h) { return cpuref.f16BitsToF32(h); });
+    const wb = engine.uploadGpuRaw(bits);
+    for (const m of [1, 4]) {
+      const xv = Float32Array.from({ length: m * K }, function () { return r() * 2 - 1; });
+      const y = await engine.matmulT(xv, wb, m, K, N, true);
+      const ref = cpuref.matmulRef(xv, wd, m, K, N);
+      check('matmulT f16 weight m=' + m, normwise(y, ref) <= (m === 1 ? 1e-5 : 1e-3), { rel: normwise(y, ref) });
+    }
+    let code = null;
+    try { await engine.matmulT(new Float32Array(K), wb, 1, K, N, false); } catch (e) { code = e.code; }
+    check('matmulT with f32 weights throws BRIK_EINVAL', code === 'BRIK_EINVAL', { code: code });
+    wb.destroy();
+  }
+
   const failed = results.filter(function (r) { return !r.ok; }).length;
   process.stdout.write(JSON.stringify({ checks: results.length, failed: failed }) + '\n');
   process.exit(failed === 0 ? 0 : 1);
