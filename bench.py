@@ -22,7 +22,10 @@ counter passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) run as child proc
 process opens the GPU, each scaled by the same counter's reading for a device copy of known size.
 
 Timing: HIP events on the library's stream bracket exactly ``--steps`` steps after ``--warmup``
-untimed ones, with a device synchronization on both sides.
+untimed ones, with a device synchronization on both sides. Before the headline's warmup steps the
+same step runs untimed for ``--settle`` seconds: a freshly started process meets the GPU's clocks in
+a transient (on the box, the first ~10 ms of back-to-back launches vary by +-15 % before holding
+steady), and the headline is the steady-state rate a decode loop sees.
 """
 import argparse
 import json
@@ -93,6 +96,19 @@ def time_loop(ctx, fn, steps, warmup):
     return ms / steps
 
 
+def settle(ctx, fn, seconds):
+    """Run ``fn`` untimed until ``seconds`` of wall time have passed (GPU clocks reach steady state)."""
+    if seconds <= 0:
+        return
+    t0 = time.time()
+    i = 0
+    while time.time() - t0 < seconds:
+        for _ in range(16):
+            fn(i)
+            i += 1
+        ctx.sync()
+
+
 def build_layer_plan(ctx, layers):
     """One grouped GEMV plan over ``layers`` distinct copies of the Qwen3-4B q4 layer set."""
     from brimkern_amd import synth
@@ -114,9 +130,10 @@ def build_layer_plan(ctx, layers):
     return plan, {"reps": reps, "xa": xa, "xd": xd, "ybuf": ybuf, "nbytes": nbytes}
 
 
-def gemv_layer_set(ctx, steps, warmup, layers):
+def gemv_layer_set(ctx, steps, warmup, layers, settle_s):
     plan, b = build_layer_plan(ctx, layers)
     reps, xa, xd, ybuf, nbytes = b["reps"], b["xa"], b["xd"], b["ybuf"], b["nbytes"]
+    settle(ctx, lambda i: plan.run(), settle_s)
     ms = time_loop(ctx, lambda i: plan.run(), steps, warmup)
     # per-shape single launches, rotating over the layers' copies
     single = {}
@@ -469,9 +486,11 @@ def hbm_traffic(layers):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--settle", type=float, default=0.3,
+                    help="seconds of untimed headline steps before the warmup (GPU clock steady state)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
@@ -492,7 +511,7 @@ def main():
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
-    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers)
+    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle)
     value = nbytes / (ms * 1e-3) / 1e9
     extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused}
     if not args.no_extra:
@@ -517,7 +536,8 @@ def main():
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) at Qwen3-4B shapes; prefill q4 GEMM TFLOP/s",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "ms_per_step": round(ms, 4), "settle_s": args.settle, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded SplitMix64), random q4 weights of the Qwen3-4B shapes",
         "config": {"workload": f"matmul_t_q4 decode GEMV, Qwen3-4B layer set x {args.layers} layers "
                                f"(216 matrices, M=1), grouped plan, one launch per step",

@@ -52,7 +52,8 @@ struct GemvVariant {
     size_t extra_lds(long rows) const { return sizeof(float) * (size_t)rows * team; }
 };
 constexpr GemvVariant kGemvVariants[] = {{16, 2, 1, 2}, {16, 2, 1, 3}, {16, 2, 1, 4}, {16, 4, 1, 2},
-                                         {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}};
+                                         {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}, {16, 2, 5, 2},
+                                         {16, 1, 5, 2}};
 constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]);
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 
@@ -73,11 +74,12 @@ constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per gro
 constexpr long kPlanMaxSets = 4;               // row sets per grouped-plan block, at most
 constexpr long kPlanMinBlocks = 1024;          // grouped-plan blocks, at least (while sets > 1)
 
-// LDS bytes of a staged activation row (xprep.h): per group (plus one zero group) 96 limb bytes, an
-// f32 sum and an int32 exponent; then a flag, the RMSNorm factor and its reduction slots.
-size_t gemv_lds(int K) { return (size_t)104 * (K / kGroup + 1) + 32; }
-
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
+
+// LDS bytes of a staged activation row (xprep.h), per group plus one zero group: q8 / q3 96 limb
+// bytes, an f32 sum and an int32 exponent; q4 96 bytes of digit planes and 16 bytes of sums and
+// exponent. Then a flag, the RMSNorm factor and its reduction slots.
+size_t gemv_lds(int K, Fmt f) { return (size_t)(f == F_Q4 ? 112 : 104) * (K / kGroup + 1) + 32; }
 int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 }  // namespace
@@ -295,16 +297,25 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E);
 }
 
-// GEMV variant for a given K (index into kGemvVariants).
 // GEMV variant for a launch over `rows` rows in total (one matrix or a plan's jobs) with shortest row
-// K: the 32-row sets of variant 0 need enough blocks to keep every CU's loads in flight; below that
-// the 16-row sets of variant 5 (32 lanes per row, pipeline depth 3) give twice the blocks, when rows
-// are long enough (K >= 2048) for 32 lanes. Measured on the Qwen3-4B shapes: N = 9728 and the
+// K (index into kGemvVariants).
+// q8 / q3: the 32-row sets of variant 0 need enough blocks to keep every CU's loads in flight; below
+// that the 16-row sets of variant 5 (32 lanes per row, pipeline depth 3) give twice the blocks, when
+// rows are long enough (K >= 2048) for 32 lanes. Measured on the Qwen3-4B shapes: N = 9728 and the
 // 216-matrix layer set are faster with variant 0, N <= 4096 and the K = 9728 down projection with
 // variant 5; the K = 896 q8 FFN shape with variant 0.
-int gemv_variant(brik_ctx* c, long rows, int kmin)
+// q4: large launches (the 36-layer set: 98k rows) stream whole rows per step with variant 7 (16
+// lanes x 5 groups = a K = 2560 row, 2 rows per team); rows of K >= 4096 alone take variant 5;
+// launches of a layer's gate/up size (8k-24k rows) variant 0; small ones the one-row-per-team form
+// of variant 8, which gives twice the blocks of variant 7.
+int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
+    if (f == F_Q4) {
+        if (rows >= 96L * 256) return 7;
+        if (kmin >= 4096) return 5;
+        return rows >= 32L * 256 ? 0 : 8;
+    }
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
 
@@ -313,11 +324,11 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
 {
     if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
-    const int v = gemv_variant(c, N, K);
+    const int v = gemv_variant(c, f, N, K);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
-    const size_t lds = gemv_lds(K) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
+    const size_t lds = gemv_lds(K, f) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
     const bool gemv_fits = lds <= kGemvMaxLds;
     // the MFMA GEMM reads scales in 16-group chunks, so a matrix of fewer than 16 groups (N * K < 512)
     // always takes the GEMV path (which handles any M)
@@ -795,14 +806,14 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d has K=%d N=%d (need K >= 32, N >= 1)", j, b.K, b.N);
         int r = check_mm(c, "gemv_plan", b.x, b.p0, b.p1, b.scales, b.mins, b.y, 1, b.K, b.N, f);
         if (r != BRIK_OK) return r;
-        if (gemv_lds(b.K) + 16384 > kGemvMaxLds)
+        if (gemv_lds(b.K, f) + 16384 > kGemvMaxLds)
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d K=%d exceeds the LDS staging limit", j, b.K);
         kmax = b.K > kmax ? b.K : kmax;
         kmin = b.K < kmin ? b.K : kmin;
     }
     long rows = 0;
     for (int j = 0; j < njobs; ++j) rows += jobs[j].job.N;
-    const int v = gemv_variant(c, rows, kmin);
+    const int v = gemv_variant(c, f, rows, kmin);
     const int rpi = kGemvVariants[v].rpi();
     // Blocks of about equal cost: rows per block ~ kPlanGroupRows / (K/32), in whole row sets of rpi
     // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). A small plan (a decoder
@@ -836,7 +847,7 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
         const brik_gemv_job& b = sorted[k].job;
         rpbs[k] = (uint32_t)(sets[k] * rpi);
         start[k + 1] = start[k] + (uint32_t)((b.N + rpbs[k] - 1) / rpbs[k]);
-        const size_t need = gemv_lds(b.K) + kGemvVariants[v].extra_lds(rpbs[k]);
+        const size_t need = gemv_lds(b.K, f) + kGemvVariants[v].extra_lds(rpbs[k]);
         lds = need > lds ? need : lds;
     }
     if (lds > kGemvMaxLds) return fail(c, BRIK_EINVAL, "gemv_plan: K=%d too large for LDS staging", kmax);

@@ -6,14 +6,18 @@
 // Arithmetic. The group scale factors out of the dot product:
 //   y_n = sum_g [ s_ng * sum_{k in g} x_k q_nk + m_ng * sum_{k in g} x_k ].
 // x is staged once per block as 24-bit block floating point (xprep.h), so sum x_k q_nk is an exact
-// int32 dot product of int8 limbs with the integer codes (v_dot4_i32_i8), rescaled once per group.
+// int32 dot product, rescaled once per group: for q8 and q3 of int8 limbs with the codes unpacked to
+// bytes (v_dot4_i32_i8); for q4 of signed 4-bit digits with the packed nibbles as loaded
+// (v_dot8_i32_i4), which leaves no unpacking at all.
 // A one-hot x reproduces deq(W) bit-exactly: the single product s*q*2^21 and its rescale are exact
 // and the final fmaf(m, 1, s*q) rounds q*s + m once, as the reference's dequantize does.
 //
 // Mapping (wave64, 256-thread blocks):
 //   * a team of TEAM lanes (16, 32 or 64) owns R adjacent weight rows; lane l handles groups
-//     g = l, l + TEAM, ... so one step of a team loads TEAM consecutive groups per row: for q4,
-//     TEAM x 16 contiguous bytes, one 128-bit load per lane per group;
+//     g = l, l + TEAM, ... so one step of a team loads U * TEAM consecutive groups per row: for q4,
+//     U x TEAM x 16 contiguous bytes, one 128-bit load per lane per group. With U * TEAM = K / 32 a
+//     step is whole rows, and the block streams one contiguous stretch of the code plane per step,
+//     the pattern HBM serves fastest;
 //   * each lane reads a group's x limbs from LDS once and applies them to its R rows;
 //   * software pipeline: a lane's work is a sequence of steps of U groups x R rows; the loads of
 //     step i + 1 are issued before step i is consumed, and the first step's loads before x is staged;
@@ -190,6 +194,15 @@ struct Work {
     int G, r0, r1, rstep, B, lane, team;
     float* part;       // LDS [nsets][RPI][TEAM] lane partials (see gemv_matrix)
 
+    // activation staging: int8 limbs (xprep.h)
+    using XS = XStage;
+    static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_layout(lds, K); }
+    static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_bytes(K); }
+    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
+    {
+        brik::xstage<FMT>(x, S, K, F);
+    }
+
     __device__ __forceinline__ void init()
     {
         lane = threadIdx.x % TEAM;
@@ -224,6 +237,7 @@ struct Work {
     }
 
     // Consume step (p, b) into acc (reset first when b == 0) and store the lane partials.
+    template <bool EVEN>
     __device__ __forceinline__ void consume(const Grp<FMT> (&d)[U][R], const XStage& S, int p, int b,
                                             float (&acc)[R]) const
     {
@@ -244,6 +258,98 @@ struct Work {
             const float2 xse = S.xse[gl];
 #pragma unroll
             for (int r = 0; r < R; ++r) acc[r] = use_grp<FMT>(d[u][r], xl, xse, acc[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[(p * RPI + team * R + r) * TEAM + lane] = acc[r];
+    }
+};
+
+// q4 on v_dot8_i32_i4: x as signed 4-bit digit planes (xprep.h, xstage_d), codes as loaded. Per
+// (row, group): 4 XORs make the codes signed nibbles q - 8, 24 dot8 run the Horner chain over the six
+// digit planes (most significant first, shifting by 4 between planes; the last shift also adds the
+// staged 8 * sum X that undoes the -8), then one conversion, one exact rescale and two FMAs.
+// The dot products use the clamping form: no partial sum can overflow, so the value is the same,
+// and the compiler keeps the chain as written instead of splitting it into six sums.
+template <int TEAM, int R, int U>
+struct Work<FMT_Q4, TEAM, R, U> {
+    static constexpr int RPI = (256 / TEAM) * R;
+    static constexpr int PARTS = TEAM;
+    static constexpr int NACC = R;
+    typedef Grp<FMT_Q4> Data[U][R];
+    Rs rs;
+    int G, r0, r1, rstep, B, lane, team;
+    float* part;
+
+    using XS = brik::XStageD;
+    static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_d_layout(lds, K); }
+    static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_d_bytes(K); }
+    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
+    {
+        brik::xstage_d(x, S, K, F);
+    }
+
+    __device__ __forceinline__ void init()
+    {
+        lane = threadIdx.x % TEAM;
+        team = threadIdx.x / TEAM;
+        B = (G + U * TEAM - 1) / (U * TEAM);
+    }
+    __device__ __forceinline__ bool even() const { return G % (U * TEAM) == 0; }
+    __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
+
+    template <bool EVEN>
+    __device__ __forceinline__ void issue(Grp<FMT_Q4> (&d)[U][R], int p, int b) const
+    {
+        const int n = n0(p);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = (uint32_t)min(n + r, r1 - 1) * (uint32_t)G;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if constexpr (EVEN) {
+                    load_grp<FMT_Q4>(d[u][r], rs, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
+                } else {
+                    const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
+                    load_grp<FMT_Q4>(d[u][r], rs, row + g, 0u, 0u);
+                }
+            }
+        }
+    }
+
+    template <bool EVEN>
+    __device__ __forceinline__ void consume(const Grp<FMT_Q4> (&d)[U][R], const XS& S, int p, int b,
+                                            float (&acc)[R]) const
+    {
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = b == 0 ? 0.f : acc[r];
+        // EVEN: group lane + TEAM (U b + u) sits at 112 (lane + TEAM U b) + 112 TEAM u (an immediate)
+        const unsigned char* a0 = S.base + 112 * (lane + TEAM * U * b);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const unsigned char* a;
+            if constexpr (EVEN) a = a0 + 112 * TEAM * u;
+            else a = S.base + 112 * min(lane + TEAM * (U * b + u), G);    // G: the zero group
+            u32x4_t L[6];
+#pragma unroll
+            for (int n = 0; n < 6; ++n) L[n] = *(const u32x4_t*)(a + 16 * n);
+            const i32x4_t xs = *(const i32x4_t*)(a + 96);                   // {sum x, e - 22, 8 sum X, 0}
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t c[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[j] = d[u][r].w[j] ^ 0x88888888u;
+                int v = 0;
+#pragma unroll
+                for (int n = 5; n >= 0; --n) {
+                    if (n == 0) v = (v << 4) + xs.z;
+                    else if (n != 5) v <<= 4;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v = __builtin_amdgcn_sdot8((int)c[j], (int)L[n][j], v, true);
+                }
+                const float pr = ldexpf((float)v, xs.y);                       // exact rescale
+                acc[r] = __builtin_fmaf(f16_bits_to_f32(d[u][r].s), pr, acc[r]);
+                acc[r] = __builtin_fmaf(f16_bits_to_f32(d[u][r].m), __builtin_bit_cast(float, xs.x), acc[r]);
+            }
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) part[(p * RPI + team * R + r) * TEAM + lane] = acc[r];
@@ -272,7 +378,7 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
 // The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
 template <int FMT, class W, int D, bool EVEN>
-__device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __restrict__ x, const Fuse& F,
+__device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
                                          const Planes& P, float* __restrict__ yrow, const float* __restrict__ res,
                                          int K, int S)
 {
@@ -285,7 +391,7 @@ __device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __r
         bp = wrap ? 0 : bp + 1;
         ip += wrap;
     }
-    brik::xstage<FMT>(x, X, K, F);
+    W::stage(x, X, K, F);
     if (*X.flag) {
         // exact path: teams of 16 lanes over RPI rows per iteration
         gemv_rows_exact<FMT, 16, W::RPI / 16>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
@@ -303,7 +409,7 @@ __device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __r
                 bp = wrap ? 0 : bp + 1;
                 ip += wrap;
             }
-            w.consume(d[k], X, pc, bc, acc);
+            w.template consume<EVEN>(d[k], X, pc, bc, acc);
             const bool wrap = bc + 1 == w.B;
             bc = wrap ? 0 : bc + 1;
             pc += wrap;
@@ -313,7 +419,7 @@ __device__ __forceinline__ void pipeline(W& w, const XStage& X, const float* __r
 #pragma unroll
     for (int k = 0; k < D - 1; ++k) {
         if (i + k < S) {
-            w.consume(d[k], X, pc, bc, acc);
+            w.template consume<EVEN>(d[k], X, pc, bc, acc);
             const bool wrap = bc + 1 == w.B;
             bc = wrap ? 0 : bc + 1;
             pc += wrap;
@@ -336,8 +442,8 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     w.init();
     const int nsets = r0 < r1 ? (r1 - r0 + rstep - 1) / rstep : 0;     // block-uniform
     const int S = nsets * w.B;                                            // steps per lane
-    const XStage X = brik::xstage_layout(lds, K);
-    w.part = (float*)(lds + brik::xstage_bytes(K));
+    const typename W::XS X = W::xs_layout(lds, K);
+    w.part = (float*)(lds + W::xs_bytes(K));
     if (w.even()) pipeline<FMT, W, D, true>(w, X, x, F, P, yrow, res, K, S);
     else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S);
     if (*X.flag) return;
@@ -418,7 +524,9 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
     BRIK_GEMV(FMTN, FMT, 16, 4, 1, 2) \
     BRIK_GEMV(FMTN, FMT, 16, 2, 2, 2) \
     BRIK_GEMV(FMTN, FMT, 32, 2, 1, 3) \
-    BRIK_GEMV(FMTN, FMT, 64, 1, 1, 3)
+    BRIK_GEMV(FMTN, FMT, 64, 1, 1, 3) \
+    BRIK_GEMV(FMTN, FMT, 16, 2, 5, 2) \
+    BRIK_GEMV(FMTN, FMT, 16, 1, 5, 2)
 
 BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)

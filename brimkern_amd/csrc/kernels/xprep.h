@@ -200,4 +200,141 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
     __syncthreads();
 }
 
+// ---- q4: x as six signed 4-bit digit planes ---------------------------------------------------
+// The q4 GEMV multiplies x with the nibble codes directly on v_dot8_i32_i4 (eight 4-bit MACs per
+// instruction), so no code is ever unpacked. x is staged with the same per-group scaling as above,
+// X = rint(x * 2^(22 - e_g)), |X| < 2^22, written as six balanced base-16 digits
+//   X = sum_n d_n 16^n, d_n in [-8, 7].
+// (X + 0x888888) holds the digits offset by 8 in its six nibbles, so XOR 0x888888 of it leaves each
+// d_n as a signed nibble: two instructions per element. Digit plane n of a group is 16 bytes, eight
+// nibbles per dword in element order (nibble i of dword j is element 8j + i), the order of the q4
+// codes themselves (element 2i is the low nibble of byte i).
+// The codes enter the dot products as signed nibbles q - 8 (XOR 0x8 per nibble); the group term is
+// sum X q = sum_n 16^n (d_n . (q - 8)) + 8 sum X, every step an exact int32 (|sum X q| < 15 * 2^27).
+//
+// LDS layout, group-major so every read uses an immediate offset: group g (0 <= g <= G) occupies
+// bytes [112g, 112g + 112): digit plane n at 112g + 16n (n < 6), then {f32 sum of the group's x,
+// int32 e_g - 22, int32 8 * sum X, 0} at 112g + 96. Group G is all zeros (the zero group). A team's
+// lanes read consecutive groups 112 bytes apart, which spreads any 8 of them over distinct banks.
+// Then the flag, the RMSNorm factor and its 4 reduction slots as in the byte-limb layout.
+struct XStageD {
+    unsigned char* base;
+    int* flag;
+    float* inv;
+    int G;
+};
+
+__host__ __device__ __forceinline__ size_t xstage_d_bytes(int K)
+{
+    return (size_t)112 * (K / BRIK_GROUP + 1) + 32;
+}
+
+__device__ __forceinline__ XStageD xstage_d_layout(void* lds, int K)
+{
+    XStageD s;
+    s.G = K / BRIK_GROUP;
+    s.base = (unsigned char*)lds;
+    s.flag = (int*)(s.base + (size_t)112 * (s.G + 1));
+    s.inv = (float*)(s.flag + 1);
+    return s;
+}
+
+// max / sum over aligned groups of 4 lanes (one quantization group: 4 lanes x 8 elements)
+__device__ __forceinline__ float max4(float v)
+{
+    v = BRIK_DPP_MAX(v, DPP_QUAD_1032);
+    return BRIK_DPP_MAX(v, DPP_QUAD_2301);
+}
+__device__ __forceinline__ float sum4(float v)
+{
+    v = BRIK_DPP_ADD(v, DPP_QUAD_1032);
+    return BRIK_DPP_ADD(v, DPP_QUAD_2301);
+}
+__device__ __forceinline__ int sum4i(int v)
+{
+    v += __builtin_amdgcn_mov_dpp(v, DPP_QUAD_1032, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_mov_dpp(v, DPP_QUAD_2301, 0xF, 0xF, false);
+}
+
+// Transpose 8 x 8 nibbles: out[n] nibble i = in[i] nibble n (three stages: 16-bit halves between
+// words 4 apart, bytes between words 2 apart, nibbles between neighbours).
+__device__ __forceinline__ void nibble_transpose8(const uint32_t (&a)[8], uint32_t (&w)[8])
+{
+    uint32_t t[8], u[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        t[i] = __builtin_amdgcn_perm(a[i + 4], a[i], 0x05040100u);       // a_i.h0  a_{i+4}.h0
+        t[i + 4] = __builtin_amdgcn_perm(a[i + 4], a[i], 0x07060302u);   // a_i.h1  a_{i+4}.h1
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int i = q < 2 ? q : q + 2;
+        u[i] = __builtin_amdgcn_perm(t[i + 2], t[i], 0x06020400u);       // t_i.b0 t_{i+2}.b0 t_i.b2 t_{i+2}.b2
+        u[i + 2] = __builtin_amdgcn_perm(t[i + 2], t[i], 0x07030501u);   // t_i.b1 t_{i+2}.b1 t_i.b3 t_{i+2}.b3
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+        w[i] = (u[i] & 0x0F0F0F0Fu) | ((u[i + 1] << 4) & 0xF0F0F0F0u);
+        w[i + 1] = ((u[i] >> 4) & 0x0F0F0F0Fu) | (u[i + 1] & 0xF0F0F0F0u);
+    }
+}
+
+// Stage x[0..K) (16-byte aligned, K % 32 == 0) as digit planes: one thread per 8 consecutive elements,
+// a quad of lanes per group. All threads of the block call it; ends with a barrier.
+__device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XStageD& S, int K, const Fuse& F)
+{
+    const int G = S.G;
+    if (threadIdx.x == 0) *S.flag = 0;
+    if (threadIdx.x < 7) *(u32x4_t*)(S.base + 112 * G + 16 * threadIdx.x) = u32x4_t{0u, 0u, 0u, 0u};
+    const int nq = K >> 2;
+    float inv = 1.f;
+    if (F.norm_w) {
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < nq; i += blockDim.x) {
+            const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), Fuse{F.gate, nullptr, 0.f, F.flags}, 1.f, 4 * i);
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
+        __syncthreads();
+        float t = 0.f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += S.inv[1 + w];
+        inv = 1.f / sqrtf(t / (float)K + F.eps);
+    }
+    if (threadIdx.x == 0) *S.inv = inv;
+    __syncthreads();
+    // every loop trip is entered by whole quads (blockDim % 4 == 0, K/8 % 4 == 0), so the DPP group
+    // reductions see full groups
+    const int n8 = K >> 3;
+    for (int i = threadIdx.x; i < n8; i += blockDim.x) {
+        const f32x4_t v0 = fused_in4(*(const f32x4_t*)(x + 8 * i), F, inv, 8 * i);
+        const f32x4_t v1 = fused_in4(*(const f32x4_t*)(x + 8 * i + 4), F, inv, 8 * i + 4);
+        const int g = i >> 2, j = i & 3;
+        const float p = sum4(((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)));
+        const float a = max4(fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                                   fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w)))));
+        const bool finite = __builtin_isfinite(p) && __builtin_isfinite(a);
+        int e = 0;
+        (void)frexpf(a, &e);                 // a < 2^e, so |x * 2^(22-e)| < 2^22
+        const int sh = 22 - e;
+        uint32_t dg[8];
+        int sx = 0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int X = finite ? (int)__builtin_rintf(ldexpf(t < 4 ? v0[t] : v1[t - 4], sh)) : 0;
+            sx += X;
+            dg[t] = (uint32_t)(X + 0x888888) ^ 0x888888u;   // digit n of X in nibble n, as a signed nibble
+        }
+        sx = sum4i(sx);
+        uint32_t w[8];
+        nibble_transpose8(dg, w);
+        unsigned char* gb = S.base + 112 * g;
+#pragma unroll
+        for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
+        if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, 0};
+        if (!finite) *S.flag = 1;
+    }
+    __syncthreads();
+}
+
 }  // namespace brik
