@@ -130,7 +130,7 @@ def build_layer_plan(ctx, layers):
     return plan, {"reps": reps, "xa": xa, "xd": xd, "ybuf": ybuf, "nbytes": nbytes}
 
 
-def gemv_layer_set(ctx, steps, warmup, layers, settle_s):
+def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
     plan, b = build_layer_plan(ctx, layers)
     reps, xa, xd, ybuf, nbytes = b["reps"], b["xa"], b["xd"], b["ybuf"], b["nbytes"]
     settle(ctx, lambda i: plan.run(), settle_s)
@@ -150,14 +150,14 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s):
         single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1)}
         ctx.free(yb)
     plan.destroy()
-    fused = decode_layers_fused(ctx, reps, layers, steps, warmup)
+    fused = decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay)
     for r in reps.values():
         ctx.free(r.buf)
     ctx.free(ybuf)
     return ms, nbytes, single, fused
 
 
-def decode_layers_fused(ctx, reps, layers, steps, warmup):
+def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
     """The matmul side of ``layers`` Qwen3-4B decoder layers as recordLayerKV chains it
     (kernels.ts:1701-1741), four fused plans per layer: q/k/v on rmsnorm(x), wo + residual, gate/up on
     rmsnorm(h), down on swiglu(gate, up) + residual; layer l + 1 reads layer l's output. Attention is
@@ -188,19 +188,24 @@ def decode_layers_fused(ctx, reps, layers, steps, warmup):
         for p in plans:
             p.run()
     ms_eager = time_loop(ctx, step, max(2, steps // 4), max(1, warmup // 2))
-    # the same launches recorded once and replayed (brik_graph_*), as the reference records a layer
-    # into one command encoder
-    ctx.graph_begin()
-    step(0)
-    graph = ctx.graph_end()
-    ms = time_loop(ctx, lambda i: graph.launch(), steps, warmup)
-    graph.destroy()
+    ms = None
+    if graph_replay:
+        # the same launches recorded once and replayed (brik_graph_*), as the reference records a
+        # layer into one command encoder
+        ctx.graph_begin()
+        step(0)
+        graph = ctx.graph_end()
+        ms = time_loop(ctx, lambda i: graph.launch(), steps, warmup)
+        graph.destroy()
     for p in plans:
         p.destroy()
     for b in [attn, an, fn, reps["o"].buf] + xs + list(tmp.values()):
         ctx.free(b)
+    replay = "one recorded graph per step"
+    if ms is None:
+        ms, replay = ms_eager, "eager (graph replay skipped: --no-graph)"
     return {"us_per_layer": round(ms * 1e3 / layers, 2), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "replay": "one recorded graph per step",
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "replay": replay,
             "eager_us_per_layer": round(ms_eager * 1e3 / layers, 2), "launches_per_layer": 4, "layers": layers,
             "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up, swiglu -> down + residual"}
 
@@ -494,6 +499,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time the fused decoder layers eagerly only (rocprofv3's kernel trace has crashed in "
+                         "hipGraphLaunch on the box)")
     ap.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.probe:
@@ -511,7 +519,8 @@ def main():
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
-    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle)
+    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle,
+                                               not args.no_graph)
     value = nbytes / (ms * 1e-3) / 1e9
     extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused}
     if not args.no_extra:
