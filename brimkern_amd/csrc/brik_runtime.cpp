@@ -58,16 +58,19 @@ constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 
 constexpr int kGroup = 32;
-// GEMM block tiles (BM rows x 128 TN columns), in the order of BRIK_GEMM_FMT in gemm.hip:
-// brik_gemm_<fmt>_<BM>x<TN>.
-struct GemmTile { int bm, tn; };
-constexpr GemmTile kGemmTiles[] = {{128, 2}, {128, 1}, {128, 3}, {64, 2}, {64, 1}, {64, 3},
-                                   {32, 2},  {32, 1},  {32, 3},  {96, 2}, {96, 1}, {96, 3}};
-constexpr int kGemmColsPerTn = 128;            // block tile columns = 128 * tn
+// GEMM block tiles (BM rows x 32 TN NW columns, NW waves), in the order of BRIK_GEMM_FMT in gemm.hip:
+// brik_gemm_<fmt>_<BM>x<TN> (NW = 4) and brik_gemm_<fmt>_<BM>x<TN>w8 (NW = 8).
+struct GemmTile {
+    int bm, tn, nw;
+    int bn() const { return 32 * tn * nw; }
+    unsigned threads() const { return 64u * (unsigned)nw; }
+};
+constexpr GemmTile kGemmTiles[] = {{128, 2, 4}, {128, 1, 4}, {128, 3, 4}, {64, 2, 4}, {64, 1, 4}, {64, 3, 4},
+                                   {32, 2, 4},  {32, 1, 4},  {32, 3, 4},  {96, 2, 4}, {96, 1, 4}, {96, 3, 4},
+                                   {128, 1, 8}, {96, 1, 8},  {64, 1, 8},  {32, 1, 8}, {64, 2, 8}};
 constexpr int kNumGemmTiles = sizeof(kGemmTiles) / sizeof(kGemmTiles[0]);
 constexpr unsigned kCUs = 256;                 // MI355X compute units
 constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
-constexpr unsigned kGemmThreads = 256;         // threads per GEMM block (__launch_bounds__ of brik_gemm_*)
 constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
 constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loop over row sets
 constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
@@ -188,33 +191,42 @@ int check_mm(brik_ctx* c, const char* who, const float* x, const void* p0, const
 
 unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 
-// GEMM block tile (index into kGemmTiles). Dense (E == 0): the tile with the smallest modelled
-// makespan, rounds x tile area x a small-tile penalty, where rounds = ceil(blocks / CUs) (every block
-// of a round runs on its own compute unit). Expert-grouped: the row tile from the mean rows per
-// expert, 256 columns.
-int gemm_tile(brik_ctx* c, long M, long N, int E)
+// GEMM block tile (index into kGemmTiles).
+// Dense (E == 0): the tile with the smallest modelled makespan, rounds x tile area x a small-tile
+// penalty, where rounds = ceil(blocks / CUs) (every block of a round runs on its own compute unit).
+// A 256-column tile runs as its 8-wave form (two waves per SIMD): measured on the cfg 4 shape
+// (M = 512, K = 2560, N = 9728) with cold weights 44.9 us against 47.5 us for 96 x 256 with 4 waves,
+// and 5-10 % faster at every other row count.
+// Expert-grouped (MoE): 256 columns, 8 waves; 64-row tiles when rows are long (K >= 1024: each block
+// then streams enough weight per launch to amortize its latency-bound steps), else 32-row tiles.
+// Measured on cfg 5 (64 experts, 22-47 rows each): gate/up (K = 2048, N = 768) 35 us with 64-row
+// tiles against 43-45 us with 32-row tiles; down (K = 768, N = 2048) 36 us with 32-row tiles
+// against 45 us with 64-row tiles.
+int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
-    if (E > 0) {
-        const long per = (M + E - 1) / E;
-        const int bm = per > 96 ? 128 : per > 64 ? 96 : per > 32 ? 64 : 32;
+    auto find = [](int bm, int tn, int nw) {
         for (int t = 0; t < kNumGemmTiles; ++t)
-            if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == 2) return t;
-    }
+            if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == tn && kGemmTiles[t].nw == nw) return t;
+        return 0;
+    };
+    if (E > 0) return find(K >= 1024 ? 64 : 32, 1, 8);
     int best = 0;
     double best_cost = 0;
     for (int t = 0; t < kNumGemmTiles; ++t) {
-        const GemmTile& g = kGemmTiles[t];
-        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, kGemmColsPerTn * g.tn);
+        GemmTile g = kGemmTiles[t];
+        if (g.nw != 4) continue;
+        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn());
         const double rounds = std::ceil(blocks / kCUs);
         const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
-        const double cost = rounds * g.bm * (double)kGemmColsPerTn * g.tn * penalty;
-        if (t == 0 || cost < best_cost) {
+        const double cost = rounds * g.bm * (double)g.bn() * penalty;
+        if (best_cost == 0 || cost < best_cost) {
             best = t;
             best_cost = cost;
         }
     }
-    return best;
+    const GemmTile& g = kGemmTiles[best];
+    return g.tn == 2 ? find(g.bm, 1, 8) : best;     // the 8-wave form of a 256-column tile
 }
 
 // Grow a context workspace to at least `bytes`. Earlier launches on the context stream may still
@@ -267,16 +279,16 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
              const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E)
 {
     int Mi = rows, Ki = K, Ni = N, Ei = E;
-    const int t = gemm_tile(c, rows, N, E);
+    const int t = gemm_tile(c, rows, N, K, E);
     const GemmTile& gt = kGemmTiles[t];
-    const int bn = kGemmColsPerTn * gt.tn;
+    const int bn = gt.bn();
     void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
     if (!row_off)
-        return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, kGemmThreads, 0,
+        return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, gt.threads(), 0,
                          args);
     // blockIdx.y enumerates (expert, row tile) pairs: at most ceil(rows / BM) + E of them
     return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(N, bn), gemm_tiles(rows, gt.bm) + (unsigned)E,
-                     kGemmThreads, 0, args);
+                     gt.threads(), 0, args);
 }
 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
@@ -308,6 +320,9 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 // lanes x 5 groups = a K = 2560 row, 2 rows per team); rows of K >= 4096 alone take variant 5;
 // launches of a layer's gate/up size (8k-24k rows) variant 0; small ones the one-row-per-team form
 // of variant 8, which gives twice the blocks of variant 7.
+// q3 is bound by its unpacking (2-bit and 1-bit planes merged to bytes, ~35 VALU per row and group):
+// large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (cfg 3)
+// measured 45 us against 47-51 us with variant 0 and 52-58 us with the whole-row variants.
 int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
@@ -316,6 +331,7 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin)
         if (kmin >= 4096) return 5;
         return rows >= 32L * 256 ? 0 : 8;
     }
+    if (f == F_Q3 && rows >= 96L * 256) return 3;
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
 
@@ -463,12 +479,13 @@ int brik_create(int device, brik_ctx** out)
     for (int f = 0; f < 3; ++f)
         for (int t = 0; t < kNumGemmTiles; ++t) {
             char name[64];
-            snprintf(name, sizeof name, "brik_gemm_%s_%dx%d", kFmtNames[f], kGemmTiles[t].bm, kGemmTiles[t].tn);
+            snprintf(name, sizeof name, "brik_gemm_%s_%dx%d%s", kFmtNames[f], kGemmTiles[t].bm, kGemmTiles[t].tn,
+                     kGemmTiles[t].nw == 8 ? "w8" : "");
             if (hipModuleGetFunction(&c->gemm[f][t], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
             // the launch shape the runtime uses must fit the kernel's compiled bounds
             int max_threads = 0;
             if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->gemm[f][t]) != hipSuccess ||
-                max_threads < (int)kGemmThreads)
+                max_threads < (int)kGemmTiles[t].threads())
                 return bail(BRIK_EMODULE);
         }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);

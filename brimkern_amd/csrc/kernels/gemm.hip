@@ -8,9 +8,10 @@
 //      of the row's largest |x|, so the scaled row fits binary16 whatever its magnitude), rounded to
 //      f16 and written to a workspace row of Kp = roundup(K, 256) halves (zero padded), with the 8
 //      elements of every aligned 8-group in the order [0 4 1 5 2 6 3 7]; rscale[m] = 2^(e - 15).
-//   2. brik_gemm_<fmt>_<BM>x<TN>: 4 waves, block tile BM x 128 TN; each wave owns 32 TN columns over
-//      all BM rows and runs v_mfma_f32_32x32x16_f16 (f32 accumulation), which issues at full rate from
-//      one wave per SIMD and hides about six VALU instructions of the same wave beside each MFMA. A K
+//   2. brik_gemm_<fmt>_<BM>x<TN>[w8]: 4 (or 8) waves, block tile BM x 32 TN NW; each wave owns 32 TN
+//      columns over all BM rows and runs v_mfma_f32_32x32x16_f16 (f32 accumulation), which issues at
+//      full rate from one wave per SIMD and hides about six VALU instructions of the same wave beside
+//      each MFMA; with 8 waves two share each SIMD. A K
 //      step is 128 (four quantization groups, 8 MFMA slices of 16). x goes through LDS: three
 //      buffers filled two steps ahead by direct global->LDS loads, XOR-swizzled so that the A-fragment
 //      reads are free of bank conflicts. W goes straight from global memory into the MFMA B operand:
@@ -129,8 +130,8 @@ namespace {
 constexpr int GK = 128;              // K per pipeline step: four quantization groups
 constexpr int XROW = GK * 2;         // bytes of one x row per step in LDS (16 chunks of 16 bytes)
 
-// Block tile: BM rows x 128 TN columns, 4 waves (one per SIMD); wave w owns columns
-// [32 TN w, 32 TN (w + 1)) of all BM rows as TM = BM / 32 row blocks x TN column blocks of
+// Block tile: BM rows x 32 TN NW columns, NW waves (4: one per SIMD, 8: two per SIMD); wave w owns
+// columns [32 TN w, 32 TN (w + 1)) of all BM rows as TM = BM / 32 row blocks x TN column blocks of
 // v_mfma_f32_32x32x16_f16, so each W element of the block is loaded and dequantized by exactly one
 // lane, and the dequantization of one 16-k slice of a column block feeds TM MFMAs. The 32x32x16 MFMA
 // (32 cycles) issues at full rate from a single wave and leaves room for about six VALU instructions
@@ -141,25 +142,26 @@ constexpr int XROW = GK * 2;         // bytes of one x row per step in LDS (16 c
 // Scales and mins go through LDS too, a chunk of 4 steps (16 groups, 32 bytes of each column) at a
 // time, double buffered: the block loads them with 32-byte-per-column global->LDS loads (2 lanes per
 // column) instead of every lane fetching its own 2-byte values from a different cache line.
-template <int FMT, int BM_, int TN_>
+template <int FMT, int BM_, int TN_, int NW_ = 4>
 struct Tile {
-    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 32;
-    static constexpr int BN = 128 * TN_;
-    static constexpr int NT = 256;
-    static constexpr int XI = BM_ / 16;                   // 16-byte x chunks per thread per step
+    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 32, NW = NW_;
+    static constexpr int BN = 32 * TN_ * NW_;
+    static constexpr int NT = 64 * NW_;
+    static constexpr int XI = BM_ / (4 * NW_);           // 16-byte x chunks per thread per step
     static constexpr int XBUF = BM_ * XROW;               // one x buffer
     static constexpr int A_BYTES = 3 * XBUF;
     static constexpr int PLANES = FMT == FMT_Q8 ? 1 : 2;  // scales (and mins)
     static constexpr int SPLANE = BN * 32;                // one plane of one scale chunk
     static constexpr int SBUF = PLANES * SPLANE;          // one scale chunk
-    static constexpr int NSD = PLANES * BN / 128;         // scale-chunk load instructions per wave
+    static constexpr int NSD = PLANES * TN_;              // scale-chunk load instructions per wave
     static constexpr int S_OFF = A_BYTES;                 // scale chunks follow the x buffers
     static constexpr int CLD = BN + 4;                    // epilogue staging row stride (floats)
     static constexpr int C_BYTES = 32 * CLD * 4;          // one 32-row block
     static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 2 && TM % 2 == 0 ? 2 : 1;
     static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
     static constexpr int SMEM = MAIN > RF * C_BYTES ? MAIN : RF * C_BYTES;
-    static_assert(BM_ % 32 == 0 && TN_ >= 1 && TM % RF == 0 && SMEM <= 160 * 1024, "tile shape");
+    static_assert(BM_ % 32 == 0 && TN_ >= 1 && (NW_ == 4 || NW_ == 8) && BM_ % (4 * NW_) == 0 && TM % RF == 0 &&
+                  SMEM <= 160 * 1024, "tile shape");
 };
 
 // K mapping of a step (128 k = 8 slices of 16, one MFMA each): lane half h = lane >> 5, slice s and
@@ -180,8 +182,8 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 
 // The loads of one step, split into ops that the multiply loop spreads over its slices: for each
 // column block the code loads of W step t + 1, in slices 0-1; then, after the barrier in slice 4, the
-// direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (4 i + w), +1024)
-// of the buffer, 16 bytes per lane: row 4 (4 i + w) + (lane >> 4), stored chunk lane & 15) over slices
+// direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (NW i + w), +1024)
+// of the buffer, 16 bytes per lane: row 4 (NW i + w) + (lane >> 4), stored chunk lane & 15) over slices
 // 4-7. Every fourth step also loads the next scale chunk, in slice 4.
 template <int FMT, class T>
 struct Loader {
@@ -219,7 +221,7 @@ struct Loader {
     {
         if (u >= W_OPS) {
             const int i = u - W_OPS;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(lds + xbuf + (4 * i + wave) * 1024), 16,
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(lds + xbuf + (T::NW * i + wave) * 1024), 16,
                                                      xoff[i], xstep * XROW, 0, 0);
             return;
         }
@@ -251,14 +253,14 @@ struct Loader {
     }
 
     // Scale chunk v (groups 16 v .. 16 v + 15 of every column of the block) into the chunk buffer at
-    // byte offset `buf`: instruction k of wave w covers plane (4 k + w) / (BN / 32), columns 32 ((4 k + w)
-    // % (BN / 32)) + lane / 2, 16 bytes (8 groups) per lane. A chunk that would run past the end of the
+    // byte offset `buf`: instruction k of wave w covers plane (NW k + w) / (BN / 32), columns
+    // 32 ((NW k + w) % (BN / 32)) + lane / 2, 16 bytes (8 groups) per lane. A chunk that would run past the end of the
     // plane is moved back to end inside it; the reader shifts its index by the same amount.
     __device__ __forceinline__ void scale_chunk(int v, uint32_t buf)
     {
 #pragma unroll
         for (int k = 0; k < NSD; ++k) {
-            const uint32_t plane = (uint32_t)(4 * k + wave) / (T::BN / 32);
+            const uint32_t plane = (uint32_t)(T::NW * k + wave) / (T::BN / 32);
             const uint32_t off = (min(sdc[k] + 16 * v, slim) + 8 * (threadIdx.x & 1)) * 2;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rmn : rsc, (lds_void_t*)(lds + buf + sdst[k]), 16,
                                                      off, 0, 0, 0);
@@ -550,11 +552,11 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     ld.h = lane >> 5; ld.G = G; ld.lds = smem;
     ld.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = ld.h, wave = ld.wave;
-    // x staging: this lane's chunk of each direct-load instruction (row 4 (4 i + wave) + (lane >> 4),
+    // x staging: this lane's chunk of each direct-load instruction (row 4 (NW i + wave) + (lane >> 4),
     // stored chunk lane & 15, which holds logical chunk (lane & 15) ^ (row & 15))
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
-        const int r = 4 * (4 * i + wave) + (lane >> 4);
+        const int r = 4 * (T::NW * i + wave) + (lane >> 4);
         const int m = min(m0 + r, m_end - 1);      // rows past the tile's end repeat a live row
         ld.xoff[i] = (uint32_t)(m * Kp + (((lane & 15) ^ (r & 15)) * 8)) * 2;
     }
@@ -573,7 +575,7 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     ld.slim = sgroups - 16;
 #pragma unroll
     for (int k = 0; k < T::NSD; ++k) {
-        const int gi = 4 * k + wave, cb = gi % (BN / 32), plane = gi / (BN / 32);
+        const int gi = T::NW * k + wave, cb = gi % (BN / 32), plane = gi / (BN / 32);
         ld.sdc[k] = (uint32_t)gbase + (uint32_t)(min(n0 + 32 * cb + (lane >> 1), N - 1) * G);
         ld.sdst[k] = (uint32_t)(plane * T::SPLANE + cb * 1024);
     }
@@ -672,23 +674,27 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 
 }  // namespace
 
-// Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN), 256 threads (4 waves) each; the
-// runtime picks the tile.
-#define BRIK_GEMM(FMTN, FMT, BM_, TN_)                                                                    \
-    extern "C" __global__ __launch_bounds__(256) void brik_gemm_##FMTN##_##BM_##x##TN_(                   \
+// Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN, 256 threads = 4 waves) and
+// brik_gemm_<fmt>_<BM>x<TN>w8 (BM x 256 TN, 512 threads = 8 waves); the runtime picks the tile.
+#define BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, NW_, SUFFIX)                                                    \
+    extern "C" __global__ __launch_bounds__(64 * NW_) void brik_gemm_##FMTN##_##BM_##x##TN_##SUFFIX(      \
         const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
         float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E)               \
     {                                                                                                     \
-        gemm_body<FMT, Tile<FMT, BM_, TN_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E);               \
+        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E);      \
     }
+#define BRIK_GEMM(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, )
+#define BRIK_GEMM8(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, w8)
 
-// Tiles in the order of the runtime's table: (BM, TN).
+// Tiles in the order of the runtime's table: (BM, TN[, 8 waves]).
 #define BRIK_GEMM_FMT(FMTN, FMT)                                                       \
     BRIK_GEMM(FMTN, FMT, 128, 2) BRIK_GEMM(FMTN, FMT, 128, 1) BRIK_GEMM(FMTN, FMT, 128, 3) \
     BRIK_GEMM(FMTN, FMT, 64, 2) BRIK_GEMM(FMTN, FMT, 64, 1) BRIK_GEMM(FMTN, FMT, 64, 3)    \
     BRIK_GEMM(FMTN, FMT, 32, 2) BRIK_GEMM(FMTN, FMT, 32, 1) BRIK_GEMM(FMTN, FMT, 32, 3)    \
-    BRIK_GEMM(FMTN, FMT, 96, 2) BRIK_GEMM(FMTN, FMT, 96, 1) BRIK_GEMM(FMTN, FMT, 96, 3)
+    BRIK_GEMM(FMTN, FMT, 96, 2) BRIK_GEMM(FMTN, FMT, 96, 1) BRIK_GEMM(FMTN, FMT, 96, 3)    \
+    BRIK_GEMM8(FMTN, FMT, 128, 1) BRIK_GEMM8(FMTN, FMT, 96, 1) BRIK_GEMM8(FMTN, FMT, 64, 1) \
+    BRIK_GEMM8(FMTN, FMT, 32, 1) BRIK_GEMM8(FMTN, FMT, 64, 2)
 
 BRIK_GEMM_FMT(q4, FMT_Q4)
 BRIK_GEMM_FMT(q8, FMT_Q8)

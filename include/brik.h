@@ -272,8 +272,10 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
 #define BRIK_GEMV_VARIANTS 9
 #define BRIK_OPT_GEMM_TILE 3     /* 0 auto, else 1 + index of an MFMA GEMM block tile (rows x columns):
                                     1 128x256, 2 128x128, 3 128x384, 4 64x256, 5 64x128, 6 64x384,
-                                    7 32x256, 8 32x128, 9 32x384, 10 96x256, 11 96x128, 12 96x384 */
-#define BRIK_GEMM_TILES 12
+                                    7 32x256, 8 32x128, 9 32x384, 10 96x256, 11 96x128, 12 96x384
+                                    (4 waves); 13 128x256, 14 96x256, 15 64x256, 16 32x256,
+                                    17 64x512 (8 waves) */
+#define BRIK_GEMM_TILES 17
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus
