@@ -356,21 +356,24 @@ struct Work<FMT_Q4, TEAM, R, U> {
     }
 };
 
-// Exact path for a row holding Inf/NaN.
-template <int FMT, int TEAM, int R>
+// Exact path for a row holding Inf/NaN: 16 teams of 16 lanes; in every row set (rows
+// base + [0, RPI), base = r0, r0 + rstep, ...) team t takes rows t, t + 16, ... (any RPI, also below 16).
+template <int FMT, int RPI>
 __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Fuse& F, float inv,
                                                 const Planes& P, float* __restrict__ yrow,
                                                 const float* __restrict__ res, int K, int r0, int r1, int rstep)
 {
-    const int lane = threadIdx.x % TEAM;
-    const int team = threadIdx.x / TEAM;
-    for (int n0 = r0 + team * R; n0 < r1; n0 += rstep) {
-        for (int r = 0; r < R && n0 + r < r1; ++r) {
+    const int lane = threadIdx.x % 16;
+    const int team = threadIdx.x / 16;
+    for (int base = r0; base < r1; base += rstep) {
+        for (int i = team; i < RPI; i += 16) {
+            const int n = base + i;         // uniform across the team's 16 lanes
+            if (n >= r1) break;
             float acc = 0.f;
-            for (int k = lane; k < K; k += TEAM)
-                acc = __builtin_fmaf(brik::fused_in(x, F, inv, k), deq_elem<FMT>(P, (size_t)(n0 + r) * K + k), acc);
-            acc = team_sum<TEAM>(acc);
-            if (lane == 0) yrow[n0 + r] = res ? res[n0 + r] + acc : acc;
+            for (int k = lane; k < K; k += 16)
+                acc = __builtin_fmaf(brik::fused_in(x, F, inv, k), deq_elem<FMT>(P, (size_t)n * K + k), acc);
+            acc = team_sum<16>(acc);
+            if (lane == 0) yrow[n] = res ? res[n] + acc : acc;
         }
     }
 }
@@ -394,7 +397,7 @@ __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const fl
     W::stage(x, X, K, F);
     if (*X.flag) {
         // exact path: teams of 16 lanes over RPI rows per iteration
-        gemv_rows_exact<FMT, 16, W::RPI / 16>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
+        gemv_rows_exact<FMT, W::RPI>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
         return;
     }
     float acc[W::NACC] = {};

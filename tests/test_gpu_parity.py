@@ -329,10 +329,12 @@ def test_grouped_plan_rejects_bad_jobs(gpu):
             gpu.ctx.gemv_plan("q4", [good, bad])
 
 
+@pytest.mark.parametrize("variant", range(0, BRIK_GEMV_VARIANTS + 1))
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
-def test_non_finite_activation_follows_f32_semantics(gpu, fmt):
+def test_non_finite_activation_follows_f32_semantics(gpu, fmt, variant):
     """Inf/NaN in x cannot be held in the integer limbs; such a row takes the exact f32 path and
-    yields the same Inf/NaN pattern as the f64 reference sum."""
+    yields the same Inf/NaN pattern as the f64 reference sum, under every tiling variant (including
+    those with fewer than 16 rows per block iteration); N = 40 is not a multiple of any row set."""
     K, N = 256, 40
     t = synth.tensor(fmt, 330, N, K)
     planes = gpu.planes(fmt, t)
@@ -340,6 +342,7 @@ def test_non_finite_activation_follows_f32_semantics(gpu, fmt):
     x[0, 17] = np.inf
     x[1, 200] = np.nan
     gpu.ctx.set_option(BRIK_OPT_PATH, 1)        # GEMV for every row
+    gpu.ctx.set_option(BRIK_OPT_GEMV_VARIANT, variant)
     y = gpu.matmul(fmt, x, planes, 3, K, N)
     r, den = oracle_mm(fmt, x, t, 3, K, N)
     for row in (0, 1):
