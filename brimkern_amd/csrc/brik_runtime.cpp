@@ -73,8 +73,12 @@ constexpr unsigned kCUs = 256;                 // MI355X compute units
 constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
 constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
 constexpr unsigned kGemvMaxBlocks = 16384;     // GEMV grid cap; blocks then loop over row sets
-constexpr double kPlanGroupRows = 16384;       // target (rows x groups) per grouped-plan block
-constexpr long kPlanMaxSets = 4;               // row sets per grouped-plan block, at most
+// target (rows x groups) per grouped-plan block and its row sets, at most: each block stages x once,
+// so fewer, larger blocks spend less on staging (36-layer q4 set: 311 us at 32768 x 8 sets, 313.5 us
+// at 16384 x 4, 321 us at 8192 x 4, 342 us at 4096 x 4)
+constexpr double kPlanGroupRows = 32768;
+constexpr long kPlanMaxSets = 8;
+constexpr size_t kPlanPartialLds = 16384;      // LDS reserved for a plan block's lane partials
 constexpr long kPlanMinBlocks = 1024;          // grouped-plan blocks, at least (while sets > 1)
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
@@ -823,7 +827,7 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d has K=%d N=%d (need K >= 32, N >= 1)", j, b.K, b.N);
         int r = check_mm(c, "gemv_plan", b.x, b.p0, b.p1, b.scales, b.mins, b.y, 1, b.K, b.N, f);
         if (r != BRIK_OK) return r;
-        if (gemv_lds(b.K, f) + 16384 > kGemvMaxLds)
+        if (gemv_lds(b.K, f) + kPlanPartialLds > kGemvMaxLds)
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d K=%d exceeds the LDS staging limit", j, b.K);
         kmax = b.K > kmax ? b.K : kmax;
         kmin = b.K < kmin ? b.K : kmin;
@@ -844,11 +848,14 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
     std::vector<brik_gemv_job_ex> sorted(njobs);
     std::vector<uint32_t> start(njobs + 1, 0), rpbs(njobs);
     std::vector<long> sets(njobs);
+    // the lane partials of a block's row sets stay within the 16 KiB the per-job LDS check reserves
+    long maxsets = (long)(kPlanPartialLds / kGemvVariants[v].extra_lds(rpi));
+    maxsets = maxsets < 1 ? 1 : maxsets > kPlanMaxSets ? kPlanMaxSets : maxsets;
     for (int k = 0; k < njobs; ++k) {
         const brik_gemv_job& b = jobs[order[k]].job;
         sorted[k] = jobs[order[k]];
         long s0 = lround((double)kPlanGroupRows / ((double)(b.K / kGroup) * rpi));
-        sets[k] = s0 < 1 ? 1 : s0 > kPlanMaxSets ? kPlanMaxSets : s0;
+        sets[k] = s0 < 1 ? 1 : s0 > maxsets ? maxsets : s0;
     }
     for (;;) {
         long blocks = 0, maxsets = 1;
