@@ -508,8 +508,9 @@ def main():
         probe(args.layers)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this path has no multi-GPU form in this build "
-              "(sharding along N is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this path has no multi-GPU form in this build (it would shard "
+              "the weight rows along N, one slice per GPU, and all-gather y); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     traffic, kernel = (None, None)
     if not args.no_traffic:

@@ -82,3 +82,15 @@ __device__ __forceinline__ float sum16(float v)
     v = BRIK_DPP_ADD(v, DPP_ROW_ROR4);
     return BRIK_DPP_ADD(v, DPP_ROW_ROR8);
 }
+
+// Wait until at most N vector-memory loads of this wave are in flight (direct global->LDS loads count;
+// the compiler does not track those as writers of LDS, so their completion is waited for explicitly).
+namespace brik {
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+typedef __attribute__((address_space(3))) void lds_void_t;
+}  // namespace brik

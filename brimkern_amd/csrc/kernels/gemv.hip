@@ -24,6 +24,7 @@
 //   * team partial sums are reduced with cross-lane shuffles; lane 0 writes y.
 #include "common.h"
 #include "xprep.h"
+#include "stage_abi.h"
 #include "../../../include/brik.h"   // brik_gemv_job
 
 namespace {
@@ -38,6 +39,9 @@ template <int FMT> struct Grp;
 template <> struct Grp<FMT_Q4> { u32x4_t w; uint16_t s, m; };
 template <> struct Grp<FMT_Q8> { u32x4_t w0, w1; uint16_t s; };
 template <> struct Grp<FMT_Q3> { u32x2_t l; uint32_t h; uint16_t s, m; };
+
+// Vector-memory load instructions load_grp issues per (row, group).
+template <int FMT> struct LoadsPerGroup { static constexpr int v = FMT == FMT_Q3 ? 4 : 3; };
 
 // Bytes per group in the code plane (p0).
 template <int FMT> struct CodeBytes { static constexpr int v = FMT == FMT_Q4 ? 16 : FMT == FMT_Q8 ? 32 : 8; };
@@ -189,6 +193,7 @@ struct Work {
     static constexpr int RPI = (256 / TEAM) * R;   // rows per block iteration
     static constexpr int PARTS = TEAM;             // partial sums per row
     static constexpr int NACC = R;                 // accumulators per lane
+    static constexpr int UG = U;                   // groups per lane per step
     typedef Grp<FMT> Data[U][R];                   // loads of one step
     Rs rs;
     int G, r0, r1, rstep, B, lane, team;
@@ -275,6 +280,7 @@ struct Work<FMT_Q4, TEAM, R, U> {
     static constexpr int RPI = (256 / TEAM) * R;
     static constexpr int PARTS = TEAM;
     static constexpr int NACC = R;
+    static constexpr int UG = U;
     typedef Grp<FMT_Q4> Data[U][R];
     Rs rs;
     int G, r0, r1, rstep, B, lane, team;
@@ -378,15 +384,32 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
     }
 }
 
+// Copy a staged x image of `bytes` bytes (a multiple of 8) from global memory into LDS at `lds`:
+// direct global->LDS loads, 1 KiB per wave instruction, 16 bytes per lane.
+__device__ __forceinline__ void stage_copy(const unsigned char* __restrict__ src, unsigned char* lds, uint32_t bytes)
+{
+    const brsrc_t r = make_rsrc(src, bytes);
+    const uint32_t lane = threadIdx.x & 63;
+    for (uint32_t c0 = (threadIdx.x >> 6) * 1024u; c0 < bytes; c0 += blockDim.x * 16u)
+        if (c0 + 16u * lane < bytes)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (brik::lds_void_t*)(lds + c0), 16, c0 + 16u * lane, 0, 0, 0);
+}
+
 // The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
+// With a pre-staged image (`staged`, written by brik_gemv_stage_<fmt>) the block copies it into LDS,
+// issued ahead of the first weight loads so that waiting for it does not wait for them.
 template <int FMT, class W, int D, bool EVEN>
 __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
                                          const Planes& P, float* __restrict__ yrow, const float* __restrict__ res,
-                                         int K, int S)
+                                         int K, int S, const unsigned char* __restrict__ staged, unsigned char* lds)
 {
     typename W::Data d[D];
     int ip = 0, bp = 0;                      // (p, b) of the next step to issue
+    if (staged) {
+        stage_copy(staged, lds, (uint32_t)((W::xs_bytes(K) + 15) & ~(size_t)15));
+        __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int k = 0; k < D - 1; ++k) {
         w.template issue<EVEN>(d[k], ip, bp);
@@ -394,7 +417,13 @@ __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const fl
         bp = wrap ? 0 : bp + 1;
         ip += wrap;
     }
-    W::stage(x, X, K, F);
+    if (staged) {
+        // every load issued after the copy is one of the D - 1 weight steps above
+        brik::wait_vmcnt<(D - 1) * W::NACC * W::UG * LoadsPerGroup<FMT>::v>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        W::stage(x, X, K, F);
+    }
     if (*X.flag) {
         // exact path: teams of 16 lanes over RPI rows per iteration
         gemv_rows_exact<FMT, W::RPI>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
@@ -436,7 +465,8 @@ __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const fl
 template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Fuse& F, const Planes& P,
                                             float* __restrict__ yrow, const float* __restrict__ res,
-                                            int N, int K, int r0, int r1, int rstep, unsigned char* lds)
+                                            int N, int K, int r0, int r1, int rstep, unsigned char* lds,
+                                            const unsigned char* __restrict__ staged)
 {
     W w;
     w.G = K / BRIK_GROUP;
@@ -447,8 +477,8 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     const int S = nsets * w.B;                                            // steps per lane
     const typename W::XS X = W::xs_layout(lds, K);
     w.part = (float*)(lds + W::xs_bytes(K));
-    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, F, P, yrow, res, K, S);
-    else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S);
+    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, F, P, yrow, res, K, S, staged, lds);
+    else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S, staged, lds);
     if (*X.flag) return;
     __syncthreads();
     // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped)
@@ -474,15 +504,18 @@ __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uin
     constexpr int RPI = W::RPI;     // rows per block iteration
     const Planes P{p0, p1, sc, mn};
     gemv_matrix<FMT, W, D>(x + (size_t)blockIdx.y * K, Fuse{nullptr, nullptr, 0.f, 0}, P, y + (size_t)blockIdx.y * N,
-                           nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds);
+                           nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds, nullptr);
 }
 
 // Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
-// block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts).
+// block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts). With a stage buffer
+// (non-null stage_base) job j's x image is at stage_base + stage_off[j].
 template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __restrict__ jobs,
                                                   const uint32_t* __restrict__ block_start,
-                                                  const uint32_t* __restrict__ rows_per_block, int njobs)
+                                                  const uint32_t* __restrict__ rows_per_block, int njobs,
+                                                  const unsigned char* __restrict__ stage_base,
+                                                  const uint32_t* __restrict__ stage_off)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int RPI = W::RPI;
@@ -499,7 +532,7 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
     const int r0 = (int)(b - block_start[lo]) * rpb;
     const int r1 = min(job.N, r0 + rpb);
     gemv_matrix<FMT, W, D>(job.x, Fuse{je.gate, je.norm_w, je.eps, je.flags}, P, job.y, je.res, job.N, job.K, r0, r1,
-                           RPI, lds);
+                           RPI, lds, stage_base ? stage_base + stage_off[lo] : nullptr);
 }
 
 }  // namespace
@@ -514,9 +547,11 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
         const brik_gemv_job_ex* __restrict__ jobs, const uint32_t* __restrict__ block_start,        \
-        const uint32_t* __restrict__ rows_per_block, int njobs)                                      \
+        const uint32_t* __restrict__ rows_per_block, int njobs,                                      \
+        const unsigned char* __restrict__ stage_base, const uint32_t* __restrict__ stage_off)        \
     {                                                                                               \
-        gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(jobs, block_start, rows_per_block, njobs); \
+        gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(jobs, block_start, rows_per_block, njobs,   \
+                                                           stage_base, stage_off);                   \
     }
 
 // The variant table of the runtime (brik_runtime.cpp, kGemvVariants) lists these in this order.
@@ -534,3 +569,34 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
 BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)
 BRIK_GEMV_FMT(q3, FMT_Q3)
+
+// Staging pass of a large grouped plan: block i (1024 threads) writes the LDS image of input i (x, or
+// its fused transform) to out + in[i].off in the layout a plan block stages (it depends only on the
+// format). An RMSNorm factor's f32 sum of squares runs over 16 waves here, so it may round
+// differently from a 4-wave block's.
+namespace {
+template <int FMT>
+__device__ __forceinline__ void stage_input(const brik_stage_input* __restrict__ in, unsigned char* __restrict__ out)
+{
+    using W = Work<FMT, 16, 2, 1>;
+    const brik_stage_input e = in[blockIdx.x];
+    const typename W::XS S = W::xs_layout(out + e.off, e.K);
+    W::stage(e.x, S, e.K, Fuse{e.gate, e.norm_w, e.eps, e.flags});
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage_q8(const brik_stage_input* __restrict__ in,
+                                                                     unsigned char* __restrict__ out)
+{
+    stage_input<FMT_Q8>(in, out);
+}
+extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage_q4(const brik_stage_input* __restrict__ in,
+                                                                     unsigned char* __restrict__ out)
+{
+    stage_input<FMT_Q4>(in, out);
+}
+extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage_q3(const brik_stage_input* __restrict__ in,
+                                                                     unsigned char* __restrict__ out)
+{
+    stage_input<FMT_Q3>(in, out);
+}

@@ -15,8 +15,8 @@
 //          the end of a row at it, which zeroes their contribution without a select;
 //   xse[g]: {f32 sum of the group's x, int32 e_g - 22}, g <= G, xse[G] = {0, 0};
 //   flag:  int32, nonzero if the row holds a non-finite value (the exact f32 path then runs);
-//   inv:   f32, the RMSNorm factor of a fused input transform (1 without one), and 4 words of scratch
-//          for its block reduction.
+//   inv:   f32, the RMSNorm factor of a fused input transform (1 without one), and 16 words of
+//          scratch for its block reduction (one per wave; a plan's staging pass runs 16 waves).
 //
 // Fused input transform (grouped plans, brik_gemv_job_ex): the staged row may be
 //   act(gate[k]) * x[k]                  (SwiGLU act = SiLU, GeGLU act = tanh-GELU), then / or
@@ -49,14 +49,17 @@ struct XStage {
     int8_t* limbs;
     float2* xse;      // {sum, bit-cast int exponent}
     int* flag;
-    float* inv;       // inv, then 4 reduction slots
+    float* inv;       // inv, then 16 reduction slots
     int G;
 };
+
+// Bytes after the groups: flag, RMSNorm factor, 16 reduction slots, padded to 16 bytes.
+#define BRIK_XSTAGE_TAIL 80
 
 // Bytes of the staged row; the block's partial-sum buffer follows at this offset (4-byte aligned).
 __host__ __device__ __forceinline__ size_t xstage_bytes(int K)
 {
-    return (size_t)104 * (K / BRIK_GROUP + 1) + 32;
+    return (size_t)104 * (K / BRIK_GROUP + 1) + BRIK_XSTAGE_TAIL;
 }
 
 __device__ __forceinline__ XStage xstage_layout(void* lds, int K)
@@ -216,7 +219,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
 // bytes [112g, 112g + 112): digit plane n at 112g + 16n (n < 6), then {f32 sum of the group's x,
 // int32 e_g - 22, int32 8 * sum X, 0} at 112g + 96. Group G is all zeros (the zero group). A team's
 // lanes read consecutive groups 112 bytes apart, which spreads any 8 of them over distinct banks.
-// Then the flag, the RMSNorm factor and its 4 reduction slots as in the byte-limb layout.
+// Then the flag, the RMSNorm factor and its reduction slots as in the byte-limb layout.
 struct XStageD {
     unsigned char* base;
     int* flag;
@@ -226,7 +229,7 @@ struct XStageD {
 
 __host__ __device__ __forceinline__ size_t xstage_d_bytes(int K)
 {
-    return (size_t)112 * (K / BRIK_GROUP + 1) + 32;
+    return (size_t)112 * (K / BRIK_GROUP + 1) + BRIK_XSTAGE_TAIL;
 }
 
 __device__ __forceinline__ XStageD xstage_d_layout(void* lds, int K)

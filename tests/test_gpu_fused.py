@@ -136,3 +136,49 @@ def test_decode_layer_chain_qwen3_4b(gpu):
     g = O.swiglu(got["gate"], got["up"])
     y = (got["h"] + oracle_mm("q4", g, W["down"], ffn, d)).astype(np.float32)
     assert normwise_rel(got["y"], y) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_prestaged_large_plan(gpu, fmt):
+    """A plan of at least 24576 rows stages every distinct input row once per run (a staging launch)
+    and its blocks copy the staged image instead of staging it themselves. Jobs here share one input
+    (same x, same RMSNorm: staged once), use another with SwiGLU + residual, and a third input holds
+    Inf, so its job must take the exact path through the staged flag."""
+    cases = [  # (K, N, input id, fuse)
+        (1024, 12000, "a", "norm"), (1024, 8000, "a", "norm"), (512, 6000, "b", "swiglu_res"), (256, 1000, "c", "plain"),
+    ]
+    xs = {"a": synth.normal(71, 1024) * 2, "b": synth.normal(72, 512), "c": synth.normal(73, 256)}
+    xs["c"][37] = np.inf
+    gate = synth.normal(74, 512)
+    w = synth.normal(75, 1024) * 0.3 + 1
+    xb = {k: gpu.up(v) for k, v in xs.items()}
+    gb, wb = gpu.up(gate), gpu.up(w)
+    jobs, expect, outs = [], [], []
+    for i, (K, N, xi, fuse) in enumerate(cases):
+        t = synth.tensor(fmt, 80 + i, N, K)
+        yb = gpu.up(np.zeros(N, np.float32))
+        f, xin, radd = {}, xs[xi], np.zeros(N, np.float32)
+        if fuse == "norm":
+            f.update(norm_w=wb, eps=1e-6)
+            xin = O.rmsnorm(xin, w, 1, K, 1e-6, False)
+        elif fuse == "swiglu_res":
+            res = synth.normal(76, N)
+            f.update(gate=gb, res=gpu.up(res))
+            xin, radd = O.swiglu(gate, xin), res
+        jobs.append(job(gpu, fmt, t, xb[xi], yb, K, N, **f))
+        expect.append(oracle_mm(fmt, xin, t, K, N) + radd)
+        outs.append((yb, N))
+    assert sum(N for _, N, _, _ in cases) >= 24576
+    plan = gpu.ctx.gemv_plan(fmt, jobs)
+    for rep in range(2):
+        plan.run()
+        for (yb, N), r, (_, _, xi, _) in zip(outs, expect, cases):
+            y = gpu.ctx.download(yb, np.float32, N)
+            if xi == "c":
+                assert np.array_equal(np.isnan(y), np.isnan(r))
+                assert np.array_equal(np.isposinf(y), np.isposinf(r)) and np.array_equal(np.isneginf(y), np.isneginf(r))
+                fin = np.isfinite(r)
+                assert np.array_equal(y[fin], y[fin]) and np.allclose(y[fin], r[fin], rtol=1e-5, atol=0)
+            else:
+                assert normwise_rel(y, r) <= TOL
+    plan.destroy()
