@@ -30,7 +30,7 @@ enum Kern {
     K_QUANT_Q8, K_QUANT_Q4, K_QUANT_Q3, K_F16_TO_F32,
     K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT,
     K_GEMV_F16W_V8, K_GEMV_F16W_V4, K_GEMM_F16W,
-    K_GEMV_STAGE_Q8, K_GEMV_STAGE_Q4, K_GEMV_STAGE_Q3,
+    K_GEMV_STAGE_Q8, K_GEMV_STAGE_Q4, K_GEMV_STAGE_Q3, K_GEMV_STAGE1_Q4, K_GEMV_STAGE1_Q3,
     K_COUNT
 };
 
@@ -42,7 +42,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_encode_q8", "brik_encode_q4", "brik_encode_q3", "brik_f16_decode",
     "brik_conv2d_direct_q8", "brik_conv2d_direct_q4", "brik_xprep_im2col_f16", "brik_conv_out",
     "brik_gemv_f16w_v8", "brik_gemv_f16w_v4", "brik_gemm_f16w",
-    "brik_gemv_stage_q8", "brik_gemv_stage_q4", "brik_gemv_stage_q3",
+    "brik_gemv_stage_q8", "brik_gemv_stage_q4", "brik_gemv_stage_q3", "brik_gemv_stage1_q4", "brik_gemv_stage1_q3",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -137,6 +137,8 @@ struct brik_ctx {
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
     size_t tws_bytes = 0;
+    void* sws = nullptr;   // staged activation row of a large single-matrix GEMV (grow-only)
+    size_t sws_bytes = 0;
     void* cws = nullptr;   // convolution workspace: the [pixels, Cout] GEMM output (grow-only)
     size_t cws_bytes = 0;
     bool graph_capturing = false;
@@ -344,9 +346,11 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 // q3 is bound by its unpacking (2-bit and 1-bit planes merged to bytes, ~35 VALU per row and group):
 // large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (cfg 3)
 // measured 45 us against 47-51 us with variant 0 and 52-58 us with the whole-row variants.
-int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin)
+int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
+    // with x staged once per call, q3 streams whole rows too (cfg 3: 42.8 us against 45 us)
+    if (staged && f == F_Q3) return 7;
     if (f == F_Q4) {
         if (rows >= 96L * 256) return 7;
         if (kmin >= 4096) return 5;
@@ -360,8 +364,11 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
            const void* mn, float* y, int M, int K, int N)
 {
     if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
+    // A large q4 / q3 matrix at M = 1 (an LM head) stages x once per call (brik_gemv_stage1_<fmt>, one
+    // block) and its blocks copy the image instead of each staging x themselves. q8 measured no gain.
+    const bool stage1 = M == 1 && N >= kPrestageRows && f != F_Q8 && c->opt_path != 2;
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
-    const int v = gemv_variant(c, f, N, K);
+    const int v = gemv_variant(c, f, N, K, stage1);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
     const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
@@ -379,7 +386,14 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     }
     int Ki = K, Ni = N;
     if (use_gemv) {
-        void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni};
+        const unsigned char* staged = nullptr;
+        if (stage1) {
+            HIP_TRY_RC(ensure_buf(c, c->sws, c->sws_bytes, (gemv_lds(K, f) + 15) & ~(size_t)15));
+            staged = static_cast<const unsigned char*>(c->sws);
+            void* sargs[] = {&x, &Ki, &c->sws};
+            HIP_TRY_RC(launch(c, f == F_Q4 ? K_GEMV_STAGE1_Q4 : K_GEMV_STAGE1_Q3, 1, 1, kStageThreads, 0, sargs));
+        }
+        void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged};
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
     return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0);
@@ -527,6 +541,7 @@ void brik_destroy(brik_ctx* c)
     if (c->stream) (void)hipStreamDestroy(c->stream);
     if (c->ws) (void)hipFree(c->ws);
     if (c->tws) (void)hipFree(c->tws);
+    if (c->sws) (void)hipFree(c->sws);
     if (c->cws) (void)hipFree(c->cws);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;

@@ -495,16 +495,19 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     }
 }
 
+// One matrix, one activation row per grid.y. `staged` (M = 1 only): the row's LDS image, written by
+// brik_gemv_stage1_<fmt>, which every block copies instead of staging x itself.
 template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uint8_t* __restrict__ p0,
                                           const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
-                                          const uint16_t* __restrict__ mn, float* __restrict__ y, int K, int N)
+                                          const uint16_t* __restrict__ mn, float* __restrict__ y, int K, int N,
+                                          const unsigned char* __restrict__ staged)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int RPI = W::RPI;     // rows per block iteration
     const Planes P{p0, p1, sc, mn};
     gemv_matrix<FMT, W, D>(x + (size_t)blockIdx.y * K, Fuse{nullptr, nullptr, 0.f, 0}, P, y + (size_t)blockIdx.y * N,
-                           nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds, nullptr);
+                           nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds, staged);
 }
 
 // Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
@@ -541,9 +544,9 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
     extern "C" __global__ __launch_bounds__(256) void brik_gemv_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
         const float* __restrict__ x, const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1, \
         const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, float* __restrict__ y,    \
-        int K, int N)                                                                               \
+        int K, int N, const unsigned char* __restrict__ staged)                                     \
     {                                                                                               \
-        gemv_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(x, p0, p1, sc, mn, y, K, N);                    \
+        gemv_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(x, p0, p1, sc, mn, y, K, N, staged);            \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
         const brik_gemv_job_ex* __restrict__ jobs, const uint32_t* __restrict__ block_start,        \
@@ -584,6 +587,27 @@ __device__ __forceinline__ void stage_input(const brik_stage_input* __restrict__
     W::stage(e.x, S, e.K, Fuse{e.gate, e.norm_w, e.eps, e.flags});
 }
 }  // namespace
+
+// Staging of one plain activation row for a single-matrix M = 1 call (brik_matmul_t_<fmt>): one block.
+namespace {
+template <int FMT>
+__device__ __forceinline__ void stage_row(const float* __restrict__ x, int K, unsigned char* __restrict__ out)
+{
+    using W = Work<FMT, 16, 2, 1>;
+    W::stage(x, W::xs_layout(out, K), K, Fuse{nullptr, nullptr, 0.f, 0});
+}
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage1_q4(const float* __restrict__ x, int K,
+                                                                      unsigned char* __restrict__ out)
+{
+    stage_row<FMT_Q4>(x, K, out);
+}
+extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage1_q3(const float* __restrict__ x, int K,
+                                                                      unsigned char* __restrict__ out)
+{
+    stage_row<FMT_Q3>(x, K, out);
+}
 
 extern "C" __global__ __launch_bounds__(1024) void brik_gemv_stage_q8(const brik_stage_input* __restrict__ in,
                                                                      unsigned char* __restrict__ out)

@@ -329,6 +329,29 @@ def test_grouped_plan_rejects_bad_jobs(gpu):
             gpu.ctx.gemv_plan("q4", [good, bad])
 
 
+@pytest.mark.parametrize("fmt", ["q4", "q3"])
+def test_staged_single_row(gpu, fmt):
+    """A single M = 1 matrix of at least 24576 rows stages x once per call (one staging block) and its
+    blocks copy the image: a finite row matches the oracle, and a row holding Inf takes the exact path
+    through the staged flag."""
+    K, N = 256, 24583
+    t = synth.tensor(fmt, 340, N, K)
+    planes = gpu.planes(fmt, t)
+    for bad in (False, True):
+        x = synth.normal(341, K)
+        if bad:
+            x[100] = -np.inf
+        y2 = gpu.matmul(fmt, x, planes, 1, K, N)
+        r, den = oracle_mm(fmt, x, t, 1, K, N)
+        if bad:
+            y, r0 = y2[0], r.reshape(-1)
+            inf = np.isinf(y)
+            assert np.array_equal(np.isnan(y), np.isnan(r0)) and np.array_equal(inf, np.isinf(r0))
+            assert np.array_equal(np.sign(y[inf]), np.sign(r0[inf]))
+        else:
+            check(y2, r, den, GEMV_TOL)
+
+
 @pytest.mark.parametrize("variant", range(0, BRIK_GEMV_VARIANTS + 1))
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
 def test_non_finite_activation_follows_f32_semantics(gpu, fmt, variant):
