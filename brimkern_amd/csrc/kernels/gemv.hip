@@ -188,6 +188,12 @@ __device__ __forceinline__ float team_sum(float v)
 // accumulation, and each lane stores its running partial sums to LDS every step (the value after a
 // row set's last step is the lane's final partial). The cross-lane sums and the y writes happen
 // once, after the loop.
+// Loop trips of the in-block x staging whose loads a thread issues together (xprep.h batched_in).
+// The whole-row two-row variant keeps one: its blocks hold the most weight registers, and the launches
+// it serves (large plans, large single matrices) copy a pre-staged image instead; for the others the
+// extra registers cost no occupancy that their launches (at most a few blocks per CU) use.
+constexpr int stage_trips(int R, int U) { return U >= 5 && R >= 2 ? 1 : 4; }
+
 template <int FMT, int TEAM, int R, int U>
 struct Work {
     static constexpr int RPI = (256 / TEAM) * R;   // rows per block iteration
@@ -200,12 +206,13 @@ struct Work {
     float* part;       // LDS [nsets][RPI][TEAM] lane partials (see gemv_matrix)
 
     // activation staging: int8 limbs (xprep.h)
+    static constexpr int STAGE_TRIPS = stage_trips(R, U);
     using XS = XStage;
     static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_layout(lds, K); }
     static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_bytes(K); }
     static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
     {
-        brik::xstage<FMT>(x, S, K, F);
+        brik::xstage<FMT, STAGE_TRIPS>(x, S, K, F);
     }
 
     __device__ __forceinline__ void init()
@@ -286,12 +293,13 @@ struct Work<FMT_Q4, TEAM, R, U> {
     int G, r0, r1, rstep, B, lane, team;
     float* part;
 
+    static constexpr int STAGE_TRIPS = stage_trips(R, U);
     using XS = brik::XStageD;
     static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_d_layout(lds, K); }
     static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_d_bytes(K); }
     static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
     {
-        brik::xstage_d(x, S, K, F);
+        brik::xstage_d<STAGE_TRIPS>(x, S, K, F);
     }
 
     __device__ __forceinline__ void init()

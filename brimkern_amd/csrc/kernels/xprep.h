@@ -81,11 +81,18 @@ struct Fuse {
     int flags;             // BRIK_JOB_GAIN_ONE_PLUS, BRIK_JOB_ACT_GELU
 };
 
+// SiLU v / (1 + e^-v), as the reference's swiglu; with BRIK_JOB_ACT_GELU its tanh-GELU
+// 0.5 v (1 + tanh u), u = 0.7978845608 (v + 0.044715 v^3), written as v / (1 + e^(-2u)) (the same
+// function: 0.5 (1 + tanh u) = 1 / (1 + e^(-2u))). The exponential is v_exp_f32 of the argument times
+// log2(e) and the quotient one v_rcp_f32 (about 1 ulp each; for |v| <= 10 the result is within ~1e-6
+// relative) instead of libm's expf / tanhf and an IEEE divide: a handful of instructions per element
+// instead of ~30 matters because every block of a fused launch transforms the whole row, on one wave
+// per SIMD. Limits match the reference's: v -> -inf gives -0, v -> +inf gives v, NaN stays NaN, and
+// v = -inf gives NaN (-inf / inf).
 __device__ __forceinline__ float act(float v, int flags)
 {
-    if (flags & BRIK_JOB_ACT_GELU)          // tanh-approximated GELU, as the reference's geglu
-        return 0.5f * v * (1.f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
-    return v / (1.f + expf(-v));            // SiLU, as the reference's swiglu
+    const float t = (flags & BRIK_JOB_ACT_GELU) ? -1.5957691216f * (v + 0.044715f * v * v * v) : -v;
+    return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(t * 1.4426950409f));
 }
 
 // Element k of the transformed row given the RMSNorm factor inv (1 without a norm).
@@ -97,20 +104,83 @@ __device__ __forceinline__ float fused_in(const float* __restrict__ x, const Fus
     return v;
 }
 
-__device__ __forceinline__ f32x4_t fused_in4(f32x4_t v, const Fuse& F, float inv, int k)
+// The loads behind C consecutive float4 chunks of the transformed row: x, and the gate and RMSNorm
+// gain where the fusion uses them (the others stay unset).
+template <int C>
+struct RawIn {
+    f32x4_t x[C], g[C], w[C];
+};
+
+template <int C>
+__device__ __forceinline__ void load_in(RawIn<C>& r, const float* __restrict__ x, const Fuse& F, int k)
 {
-    if (F.gate) {
-        const f32x4_t g = *(const f32x4_t*)(F.gate + k);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = act(g[t], F.flags) * v[t];
+    for (int c = 0; c < C; ++c) r.x[c] = *(const f32x4_t*)(x + k + 4 * c);
+    if (F.gate) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) r.g[c] = *(const f32x4_t*)(F.gate + k + 4 * c);
     }
     if (F.norm_w) {
-        f32x4_t w = *(const f32x4_t*)(F.norm_w + k);
+#pragma unroll
+        for (int c = 0; c < C; ++c) r.w[c] = *(const f32x4_t*)(F.norm_w + k + 4 * c);
+    }
+}
+
+// Chunk c of the transformed row from its loads, given the RMSNorm factor inv (1 without a norm).
+template <int C>
+__device__ __forceinline__ f32x4_t apply_in(const RawIn<C>& r, int c, const Fuse& F, float inv)
+{
+    f32x4_t v = r.x[c];
+    if (F.gate) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = act(r.g[c][t], F.flags) * v[t];
+    }
+    if (F.norm_w) {
+        f32x4_t w = r.w[c];
         if (F.flags & BRIK_JOB_GAIN_ONE_PLUS) w = w + 1.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] = v[t] * inv * w[t];
     }
     return v;
+}
+
+// body(i, loads) for i = threadIdx.x, + blockDim.x, ... < n over chunks of 4C floats, in that order.
+// The loads of SB consecutive trips are issued together before any is used, so a thread pays one
+// memory round trip per SB trips instead of one per trip (a K = 9728 row takes five trips of a
+// 256-thread block). Indices past n are clamped for the loads, which then stay in range, and their
+// trips run no body. Whole aligned lane groups enter each body together when n and blockDim are
+// multiples of the group size, as the DPP group reductions need.
+template <int SB, int C, class Body>
+__device__ __forceinline__ void batched_in(const float* __restrict__ x, const Fuse& F, int n, Body body)
+{
+    const int bd = (int)blockDim.x, tid = (int)threadIdx.x;
+    for (int b = 0; b < n; b += SB * bd) {
+        RawIn<C> r[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            const int i = min(b + u * bd + tid, n - 1);
+            load_in<C>(r[u], x, F, 4 * C * i);
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+            if (b + u * bd >= n) break;           // the same for every thread of the block
+            const int i = b + u * bd + tid;
+            if (i < n) body(i, r[u]);
+        }
+    }
+}
+
+// Sum of squares of this thread's share of the (gated) row, accumulated in ascending chunk order.
+template <int SB>
+__device__ __forceinline__ float row_ss(const float* __restrict__ x, const Fuse& F, int K)
+{
+    const Fuse G{F.gate, nullptr, 0.f, F.flags};
+    float ss = 0.f;
+    batched_in<SB, 1>(x, G, K >> 2, [&](int, const RawIn<1>& r) {
+        const f32x4_t v = apply_in<1>(r, 0, G, 1.f);
+        ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    });
+    return ss;
 }
 
 __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h, int& m, int& l)
@@ -123,7 +193,8 @@ __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h
 }
 
 // Stage x[0..K) (16-byte aligned, K % 32 == 0). All threads of the block call it; ends with a barrier.
-template <int FMT>
+// SB: loop trips whose loads a thread issues together (batched_in); more trips hold more registers.
+template <int FMT, int SB>
 __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K, const Fuse& F)
 {
     const int G = S.G;
@@ -136,11 +207,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
     float inv = 1.f;
     if (F.norm_w) {
         // sum of squares of the (gated) row: per thread, per wave, then across the block's waves
-        float ss = 0.f;
-        for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-            const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), Fuse{F.gate, nullptr, 0.f, F.flags}, 1.f, 4 * i);
-            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-        }
+        float ss = row_ss<SB>(x, F, K);
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
         __syncthreads();
@@ -151,9 +218,9 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
     if (threadIdx.x == 0) *S.inv = inv;
     __syncthreads();
     // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
-    // every loop trip is entered by whole 8-lane groups, so the DPP group reductions see full groups
-    for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-        const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), F, inv, 4 * i);
+    // every body is entered by whole 8-lane groups, so the DPP group reductions see full groups
+    batched_in<SB, 1>(x, F, nq, [&](int i, const RawIn<1>& r) {
+        const f32x4_t v = apply_in<1>(r, 0, F, inv);
         const int g = i >> 3, c = i & 7;
         const float p = sum8((v.x + v.y) + (v.z + v.w));
         const float a = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -199,7 +266,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
                 base[64 + pos] = (int8_t)ll[t];
             }
         }
-    }
+    });
     __syncthreads();
 }
 
@@ -284,19 +351,15 @@ __device__ __forceinline__ void nibble_transpose8(const uint32_t (&a)[8], uint32
 
 // Stage x[0..K) (16-byte aligned, K % 32 == 0) as digit planes: one thread per 8 consecutive elements,
 // a quad of lanes per group. All threads of the block call it; ends with a barrier.
+template <int SB>
 __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XStageD& S, int K, const Fuse& F)
 {
     const int G = S.G;
     if (threadIdx.x == 0) *S.flag = 0;
     if (threadIdx.x < 7) *(u32x4_t*)(S.base + 112 * G + 16 * threadIdx.x) = u32x4_t{0u, 0u, 0u, 0u};
-    const int nq = K >> 2;
     float inv = 1.f;
     if (F.norm_w) {
-        float ss = 0.f;
-        for (int i = threadIdx.x; i < nq; i += blockDim.x) {
-            const f32x4_t v = fused_in4(*(const f32x4_t*)(x + 4 * i), Fuse{F.gate, nullptr, 0.f, F.flags}, 1.f, 4 * i);
-            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-        }
+        float ss = row_ss<SB>(x, F, K);
         for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
         if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
         __syncthreads();
@@ -306,12 +369,12 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
     }
     if (threadIdx.x == 0) *S.inv = inv;
     __syncthreads();
-    // every loop trip is entered by whole quads (blockDim % 4 == 0, K/8 % 4 == 0), so the DPP group
+    // every body is entered by whole quads (blockDim % 4 == 0, K/8 % 4 == 0), so the DPP group
     // reductions see full groups
     const int n8 = K >> 3;
-    for (int i = threadIdx.x; i < n8; i += blockDim.x) {
-        const f32x4_t v0 = fused_in4(*(const f32x4_t*)(x + 8 * i), F, inv, 8 * i);
-        const f32x4_t v1 = fused_in4(*(const f32x4_t*)(x + 8 * i + 4), F, inv, 8 * i + 4);
+    batched_in<(SB > 1 ? SB - 1 : 1), 2>(x, F, n8, [&](int i, const RawIn<2>& r) {
+        const f32x4_t v0 = apply_in<2>(r, 0, F, inv);
+        const f32x4_t v1 = apply_in<2>(r, 1, F, inv);
         const int g = i >> 2, j = i & 3;
         const float p = sum4(((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)));
         const float a = max4(fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
@@ -336,7 +399,7 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
         for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
         if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, 0};
         if (!finite) *S.flag = 1;
-    }
+    });
     __syncthreads();
 }
 
