@@ -489,8 +489,10 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S, staged, lds);
     if (*X.flag) return;
     __syncthreads();
-    // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped)
+    // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped), times the
+    // RMSNorm factor of a fused input (1 otherwise: exact), which the staged image leaves out
     constexpr int PARTS = W::PARTS;
+    const float inv = *X.inv;
     for (int q = threadIdx.x; q < nsets * W::RPI; q += blockDim.x) {
         const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
         if (n < r1) {
@@ -498,6 +500,7 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
             float v = 0.f;
 #pragma unroll
             for (int l = 0; l < PARTS; ++l) v += pp[(l + q) % PARTS];
+            v *= inv;
             yrow[n] = res ? res[n] + v : v;
         }
     }

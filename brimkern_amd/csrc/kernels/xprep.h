@@ -22,7 +22,8 @@
 //   act(gate[k]) * x[k]                  (SwiGLU act = SiLU, GeGLU act = tanh-GELU), then / or
 //   v[k] * inv * g[k],  inv = 1 / sqrt(sum v^2 / K + eps),  g = w or 1 + w   (RMSNorm)
 // as the reference computes n1 = rmsnorm(x) and g = swiglu(gate, up) before recMM
-// (src/lib/webgpu/shaders.ts:580-626; kernels.ts:1701, 1723, 1726).
+// (src/lib/webgpu/shaders.ts:580-626; kernels.ts:1701, 1723, 1726). The image holds v[k] * g[k]; the
+// scalar inv multiplies each row's result instead (stage_finish).
 #pragma once
 #include "common.h"
 #include "../../../include/brik.h"   // BRIK_JOB_* flags
@@ -126,23 +127,28 @@ __device__ __forceinline__ void load_in(RawIn<C>& r, const float* __restrict__ x
     }
 }
 
-// Chunk c of the transformed row from its loads, given the RMSNorm factor inv (1 without a norm).
+// Chunk c of the gated row act(gate) * x from its loads (x itself without a gate).
 template <int C>
-__device__ __forceinline__ f32x4_t apply_in(const RawIn<C>& r, int c, const Fuse& F, float inv)
+__device__ __forceinline__ f32x4_t apply_in(const RawIn<C>& r, int c, const Fuse& F)
 {
     f32x4_t v = r.x[c];
     if (F.gate) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] = act(r.g[c][t], F.flags) * v[t];
     }
-    if (F.norm_w) {
-        f32x4_t w = r.w[c];
-        if (F.flags & BRIK_JOB_GAIN_ONE_PLUS) w = w + 1.f;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) v[t] = v[t] * inv * w[t];
-    }
     return v;
 }
+
+// v times the RMSNorm gain of chunk c (w, or 1 + w).
+template <int C>
+__device__ __forceinline__ f32x4_t gain_in(const RawIn<C>& r, int c, const Fuse& F, f32x4_t v)
+{
+    f32x4_t w = r.w[c];
+    if (F.flags & BRIK_JOB_GAIN_ONE_PLUS) w = w + 1.f;
+    return v * w;
+}
+
+__device__ __forceinline__ float sumsq4(f32x4_t v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
 
 // body(i, loads) for i = threadIdx.x, + blockDim.x, ... < n over chunks of 4C floats, in that order.
 // The loads of SB consecutive trips are issued together before any is used, so a thread pays one
@@ -170,17 +176,36 @@ __device__ __forceinline__ void batched_in(const float* __restrict__ x, const Fu
     }
 }
 
-// Sum of squares of this thread's share of the (gated) row, accumulated in ascending chunk order.
-template <int SB>
-__device__ __forceinline__ float row_ss(const float* __restrict__ x, const Fuse& F, int K)
+// RMSNorm in staging: the factor inv = 1 / sqrt(sum v^2 / K + eps) (v the gated row) is one scalar
+// per row, and a row's result is linear in its input (sum X q and the min term sum x alike), so the
+// image holds v * gain without inv and the row's result is multiplied by inv afterwards. One pass over
+// x then yields both the image and the sum of squares.
+//
+// End of a staging pass: the flag (nonzero if any thread saw a non-finite value, `bad`) and inv from
+// the threads' partial sums of squares `ss` (1 without a norm). A zero, infinite or NaN factor raises
+// the flag too: the exact path applies it per element, as the reference does. thread 0 wrote flag = 0
+// before the pass; the 1s are written after the first barrier, so they cannot race it. Ends with a
+// barrier after which flag and inv hold their final values.
+__device__ __forceinline__ void stage_finish(int* flag, float* inv, const Fuse& F, int K, float ss, int bad)
 {
-    const Fuse G{F.gate, nullptr, 0.f, F.flags};
-    float ss = 0.f;
-    batched_in<SB, 1>(x, G, K >> 2, [&](int, const RawIn<1>& r) {
-        const f32x4_t v = apply_in<1>(r, 0, G, 1.f);
-        ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-    });
-    return ss;
+    if (F.norm_w) {
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if ((threadIdx.x & 63) == 0) inv[1 + (threadIdx.x >> 6)] = ss;
+    }
+    const bool wave_bad = __any(bad);
+    __syncthreads();
+    if (wave_bad && (threadIdx.x & 63) == 0) *flag = 1;
+    if (threadIdx.x == 0) {
+        float f = 1.f;
+        if (F.norm_w) {
+            float t = 0.f;
+            for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += inv[1 + w];
+            f = 1.f / sqrtf(t / (float)K + F.eps);
+            if (!(f > 0.f && f < __builtin_inff())) *flag = 1;
+        }
+        *inv = f;
+    }
+    __syncthreads();
 }
 
 __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h, int& m, int& l)
@@ -204,23 +229,16 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
     }
     if (threadIdx.x < 24) ((uint32_t*)(S.limbs + 96 * G))[threadIdx.x] = 0u;   // the zero group
     const int nq = K >> 2;
-    float inv = 1.f;
-    if (F.norm_w) {
-        // sum of squares of the (gated) row: per thread, per wave, then across the block's waves
-        float ss = row_ss<SB>(x, F, K);
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-        if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
-        __syncthreads();
-        float t = 0.f;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += S.inv[1 + w];
-        inv = 1.f / sqrtf(t / (float)K + F.eps);
-    }
-    if (threadIdx.x == 0) *S.inv = inv;
-    __syncthreads();
+    float ss = 0.f;
+    int bad = 0;
     // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
     // every body is entered by whole 8-lane groups, so the DPP group reductions see full groups
     batched_in<SB, 1>(x, F, nq, [&](int i, const RawIn<1>& r) {
-        const f32x4_t v = apply_in<1>(r, 0, F, inv);
+        f32x4_t v = apply_in<1>(r, 0, F);
+        if (F.norm_w) {
+            ss += sumsq4(v);
+            v = gain_in<1>(r, 0, F, v);
+        }
         const int g = i >> 3, c = i & 7;
         const float p = sum8((v.x + v.y) + (v.z + v.w));
         const float a = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
@@ -229,7 +247,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
         (void)frexpf(a, &e);                 // a < 2^e, so |x * 2^(22-e)| < 2^22
         const int sh = 22 - e;
         if (c == 0) S.xse[g] = float2{p, __builtin_bit_cast(float, -sh)};
-        if (!finite) *S.flag = 1;
+        bad |= !finite;
         int hh[4], mm[4], ll[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) split_limbs(v[t], sh, finite, hh[t], mm[t], ll[t]);
@@ -267,7 +285,7 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
             }
         }
     });
-    __syncthreads();
+    stage_finish(S.flag, S.inv, F, K, ss, bad);
 }
 
 // ---- q4: x as six signed 4-bit digit planes ---------------------------------------------------
@@ -357,24 +375,18 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
     const int G = S.G;
     if (threadIdx.x == 0) *S.flag = 0;
     if (threadIdx.x < 7) *(u32x4_t*)(S.base + 112 * G + 16 * threadIdx.x) = u32x4_t{0u, 0u, 0u, 0u};
-    float inv = 1.f;
-    if (F.norm_w) {
-        float ss = row_ss<SB>(x, F, K);
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-        if ((threadIdx.x & 63) == 0) S.inv[1 + (threadIdx.x >> 6)] = ss;
-        __syncthreads();
-        float t = 0.f;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += S.inv[1 + w];
-        inv = 1.f / sqrtf(t / (float)K + F.eps);
-    }
-    if (threadIdx.x == 0) *S.inv = inv;
-    __syncthreads();
+    float ss = 0.f;
+    int bad = 0;
     // every body is entered by whole quads (blockDim % 4 == 0, K/8 % 4 == 0), so the DPP group
     // reductions see full groups
     const int n8 = K >> 3;
     batched_in<(SB > 1 ? SB - 1 : 1), 2>(x, F, n8, [&](int i, const RawIn<2>& r) {
-        const f32x4_t v0 = apply_in<2>(r, 0, F, inv);
-        const f32x4_t v1 = apply_in<2>(r, 1, F, inv);
+        f32x4_t v0 = apply_in<2>(r, 0, F), v1 = apply_in<2>(r, 1, F);
+        if (F.norm_w) {
+            ss += sumsq4(v0) + sumsq4(v1);
+            v0 = gain_in<2>(r, 0, F, v0);
+            v1 = gain_in<2>(r, 1, F, v1);
+        }
         const int g = i >> 2, j = i & 3;
         const float p = sum4(((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)));
         const float a = max4(fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
@@ -398,9 +410,9 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
 #pragma unroll
         for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
         if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, 0};
-        if (!finite) *S.flag = 1;
+        bad |= !finite;
     });
-    __syncthreads();
+    stage_finish(S.flag, S.inv, F, K, ss, bad);
 }
 
 }  // namespace brik
