@@ -340,9 +340,11 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 // 216-matrix layer set are faster with variant 0, N <= 4096 and the K = 9728 down projection with
 // variant 5; the K = 896 q8 FFN shape with variant 0.
 // q4: large launches (the 36-layer set: 98k rows) stream whole rows per step with variant 7 (16
-// lanes x 5 groups = a K = 2560 row, 2 rows per team); rows of K >= 4096 alone take variant 5;
-// launches of a layer's gate/up size (8k-24k rows) variant 0; small ones the one-row-per-team form
-// of variant 8, which gives twice the blocks of variant 7.
+// lanes x 5 groups = a K = 2560 row, 2 rows per team); rows of K >= 8192 alone (a down projection)
+// the one-row-per-team whole-row form of variant 8 (10.4 us against 11.0 us with variant 5 for
+// Qwen3-4B's fused down launch); rows of K >= 4096 variant 5; launches of a layer's gate/up size
+// (8k-24k rows) variant 0; 4k-8k rows (a layer's q/k/v) variant 1 (7.3 us against 7.9 us with
+// variant 8); smaller ones variant 8, which gives twice the blocks of variant 7.
 // q3 is bound by its unpacking (2-bit and 1-bit planes merged to bytes, ~35 VALU per row and group):
 // large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (cfg 3)
 // measured 45 us against 47-51 us with variant 0 and 52-58 us with the whole-row variants.
@@ -353,8 +355,10 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
     if (staged && f == F_Q3) return 7;
     if (f == F_Q4) {
         if (rows >= 96L * 256) return 7;
+        if (kmin >= 8192) return 8;
         if (kmin >= 4096) return 5;
-        return rows >= 32L * 256 ? 0 : 8;
+        if (rows >= 32L * 256) return 0;
+        return rows >= 16L * 256 ? 1 : 8;
     }
     if (f == F_Q3 && rows >= 96L * 256) return 3;
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
