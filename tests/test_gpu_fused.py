@@ -182,3 +182,29 @@ def test_prestaged_large_plan(gpu, fmt):
             else:
                 assert normwise_rel(y, r) <= TOL
     plan.destroy()
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
+def test_norm_degenerate_factor(gpu, fmt):
+    """A zero row with eps = 0 has the RMSNorm factor 1 / sqrt(0) = inf, and the reference's
+    x * inv * g is 0 * inf = NaN in every element (rmsnormCpu, kernels.ts:3395-3404): every output
+    is NaN. The staged image leaves the factor out and scales each row's result by it, so such a
+    factor has to take the per-element path instead. A second job of the same plan, with a finite
+    factor, stays on the fast path."""
+    K, N = 512, 300
+    t = synth.tensor(fmt, 60, N, K)
+    w = synth.normal(61, K) * 0.5 + 1
+    x2 = synth.normal(62, K)
+    zero = np.zeros(K, np.float32)
+    zb, xb2, wb = gpu.up(zero), gpu.up(x2), gpu.up(w)
+    y1, y2 = gpu.up(np.zeros(N, np.float32)), gpu.up(np.zeros(N, np.float32))
+    plan = gpu.ctx.gemv_plan(fmt, [job(gpu, fmt, t, zb, y1, K, N, norm_w=wb, eps=0.0),
+                                   job(gpu, fmt, t, xb2, y2, K, N, norm_w=wb, eps=0.0)])
+    plan.run()
+    a, b = gpu.ctx.download(y1, np.float32, N), gpu.ctx.download(y2, np.float32, N)
+    plan.destroy()
+    with np.errstate(all="ignore"):
+        r1 = oracle_mm(fmt, O.rmsnorm(zero, w, 1, K, 0.0, False), t, K, N)
+        r2 = oracle_mm(fmt, O.rmsnorm(x2, w, 1, K, 0.0, False), t, K, N)
+    assert np.isnan(r1).all() and np.isnan(a).all()
+    assert normwise_rel(b, r2) <= TOL
