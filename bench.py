@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""bench.py — q4 decode GEMV HBM GB/s at Qwen3-4B shapes on one MI355X (+ the other BASELINE configs).
+"""bench.py — q4 decode GEMV HBM GB/s at Qwen3-4B shapes on one MI355X (+ the other benchmarked configurations).
 
 Headline (``value``): the full Qwen3-4B q4 GEMV layer set at M=1 (K=2560 -> N in {4096, 1024, 1024,
 9728, 9728}; K=9728 -> N=2560) for all 36 layers — 216 matrices, 2.04 GB of distinct packed weights,

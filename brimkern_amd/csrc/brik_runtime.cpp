@@ -217,12 +217,12 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 // GEMM block tile (index into kGemmTiles).
 // Dense (E == 0): the tile with the smallest modelled makespan, rounds x tile area x a small-tile
 // penalty, where rounds = ceil(blocks / CUs) (every block of a round runs on its own compute unit).
-// A 256-column tile runs as its 8-wave form (two waves per SIMD): measured on the cfg 4 shape
+// A 256-column tile runs as its 8-wave form (two waves per SIMD): measured on the M = 512, K = 2560, N = 9728 prefill shape
 // (M = 512, K = 2560, N = 9728) with cold weights 44.9 us against 47.5 us for 96 x 256 with 4 waves,
 // and 5-10 % faster at every other row count.
 // Expert-grouped (MoE): 256 columns, 8 waves; 64-row tiles when rows are long (K >= 1024: each block
 // then streams enough weight per launch to amortize its latency-bound steps), else 32-row tiles.
-// Measured on cfg 5 (64 experts, 22-47 rows each): gate/up (K = 2048, N = 768) 35 us with 64-row
+// Measured on a 64-expert MoE layer (22-47 rows each): gate/up (K = 2048, N = 768) 35 us with 64-row
 // tiles against 43-45 us with 32-row tiles; down (K = 768, N = 2048) 36 us with 32-row tiles
 // against 45 us with 64-row tiles.
 int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
@@ -346,12 +346,12 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 // (8k-24k rows) variant 0; 4k-8k rows (a layer's q/k/v) variant 1 (7.3 us against 7.9 us with
 // variant 8); smaller ones variant 8, which gives twice the blocks of variant 7.
 // q3 is bound by its unpacking (2-bit and 1-bit planes merged to bytes, ~35 VALU per row and group):
-// large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (cfg 3)
+// large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (N = 151936, K = 2560)
 // measured 45 us against 47-51 us with variant 0 and 52-58 us with the whole-row variants.
 int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
-    // with x staged once per call, q3 streams whole rows too (cfg 3: 42.8 us against 45 us)
+    // with x staged once per call, q3 streams whole rows too (the q3 LM head: 42.8 us against 45 us)
     if (staged && f == F_Q3) return 7;
     if (f == F_Q4) {
         if (rows >= 96L * 256) return 7;

@@ -206,7 +206,7 @@ void oracle_matmul_t_q3(const float *x, const uint32_t *lo, const uint32_t *hi, 
     matmul_rows(FMT_Q3, x, lo, hi, sc, mn, M, K, N, y, absden, threads);
 }
 
-/* ---- MoE expert-grouped matmul (no reference counterpart) -------------
+/* ---- MoE expert-grouped matmul (no reference counterpart; the benchmarked 64-expert MoE layer) -------------
  * The reference has no MoE. The oracle applies the reference matmul above per expert:
  * rows [row_off[e], row_off[e+1]) of x_sorted times deq(W_e)^T, where W is a stacked q4 tensor
  * [E, N, K] in one .brik blob (expert e's nibbles start at e*N*K/2, its scales/mins at e*N*K/32). */

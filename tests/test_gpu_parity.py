@@ -73,13 +73,13 @@ def test_golden_moe(gpu):
     assert normwise_rel(y, m["y"]) <= REL_TOL
 
 
-# ---- dequant bit-exactness at full BASELINE sizes ----------------------------------------
+# ---- dequant bit-exactness at the full benchmark sizes ----------------------------------------
 
 @pytest.mark.parametrize("fmt,N,K,seed", [
-    ("q8", 4864, 896, 1),        # cfg 1
-    ("q4", 9728, 2560, 2),       # cfg 2 gate/up, cfg 4
-    ("q4", 2560, 9728, 3),       # cfg 2 down
-    ("q3", 151936, 2560, 4),     # cfg 3 LM head
+    ("q8", 4864, 896, 1),        # Qwen2.5-0.5B FFN
+    ("q4", 9728, 2560, 2),       # Qwen3-4B gate/up (also the prefill GEMM weight)
+    ("q4", 2560, 9728, 3),       # Qwen3-4B down
+    ("q3", 151936, 2560, 4),     # Qwen3-4B q3 LM head
 ])
 def test_dequant_bit_exact(gpu, fmt, N, K, seed):
     t = synth.tensor(fmt, seed, N, K)
@@ -102,12 +102,12 @@ def test_one_hot_gemv_is_dequant_column(gpu, fmt):
         assert np.array_equal(y.ravel().view(np.uint32), deq[:, k].copy().view(np.uint32)), f"k={k}"
 
 
-# ---- decode GEMV at the BASELINE shapes -------------------------------------------------
+# ---- decode GEMV at the benchmark shapes -------------------------------------------------
 
 GEMV_SHAPES = [
-    ("q8", 896, 4864),                                     # cfg 1 (Qwen2.5-0.5B FFN)
-    ("q4", 2560, 4096), ("q4", 2560, 1024), ("q4", 2560, 9728), ("q4", 9728, 2560),   # cfg 2
-    ("q3", 2560, 151936),                                  # cfg 3 (Qwen3-4B LM head)
+    ("q8", 896, 4864),                                     # Qwen2.5-0.5B FFN
+    ("q4", 2560, 4096), ("q4", 2560, 1024), ("q4", 2560, 9728), ("q4", 9728, 2560),   # Qwen3-4B layer set
+    ("q3", 2560, 151936),                                  # Qwen3-4B LM head
 ]
 
 
@@ -149,7 +149,7 @@ def test_gemv_variants(gpu, fmt, variant):
 # ---- prefill GEMM and small-M -----------------------------------------------------------
 
 @pytest.mark.parametrize("fmt,M,K,N", [
-    ("q4", 512, 2560, 9728),     # cfg 4
+    ("q4", 512, 2560, 9728),     # Qwen3-4B prefill, M = 512
     ("q8", 64, 896, 4864),
     ("q3", 48, 2560, 4096),
     ("q4", 2, 2560, 1024), ("q4", 5, 128, 6), ("q4", 17, 96, 65), ("q8", 3, 64, 130), ("q3", 65, 160, 33),
@@ -191,10 +191,10 @@ def test_forced_paths_agree(gpu, fmt):
     check(gpu.matmul(fmt, x[:K], planes, 1, K, N), r[:1], den[:1], REL_TOL)
 
 
-# ---- MoE expert-grouped q4 (cfg 5) ------------------------------------------------------
+# ---- MoE expert-grouped q4 (64 experts) ------------------------------------------------------
 
 @pytest.mark.parametrize("which", ["gate", "down"])
-def test_moe_cfg5(gpu, which):
+def test_moe_e64(gpu, which):
     T, H, E, F, TOPK = 256, 2048, 64, 768, 8
     K, N = (H, F) if which == "gate" else (F, H)
     rows, row_off = synth.moe_routing(77, T, E, TOPK)
