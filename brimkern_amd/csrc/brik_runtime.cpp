@@ -119,6 +119,9 @@ struct brik_gemv_plan {
 struct brik_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    // the context's workspace generation when the capture ended: the recorded launches hold the
+    // workspace addresses of that moment
+    unsigned long long ws_generation = 0;
 };
 
 struct brik_ctx {
@@ -142,6 +145,9 @@ struct brik_ctx {
     void* cws = nullptr;   // convolution workspace: the [pixels, Cout] GEMM output (grow-only)
     size_t cws_bytes = 0;
     bool graph_capturing = false;
+    // bumped whenever a context workspace is freed and reallocated (ensure_buf): a graph recorded
+    // before that replays addresses that are no longer the context's, so brik_graph_launch refuses it
+    unsigned long long ws_generation = 0;
     char err[512] = {0};
 };
 
@@ -265,6 +271,7 @@ int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
         HIP_TRY(c, hipFree(buf));
         buf = nullptr;
         have = 0;
+        ++c->ws_generation;
     }
     bytes = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
     HIP_TRY(c, hipMalloc(&buf, bytes));
@@ -1071,6 +1078,7 @@ int brik_graph_end(brik_ctx* c, brik_graph** out)
         delete g;
         return fail(c, BRIK_EHIP, "graph_end: %s", hipGetErrorString(e));
     }
+    g->ws_generation = c->ws_generation;
     *out = g;
     return BRIK_OK;
 }
@@ -1078,6 +1086,9 @@ int brik_graph_end(brik_ctx* c, brik_graph** out)
 int brik_graph_launch(brik_ctx* c, const brik_graph* g)
 {
     if (!c || !g) return BRIK_EINVAL;
+    if (g->ws_generation != c->ws_generation)
+        return fail(c, BRIK_EINVAL, "graph_launch: a context workspace was reallocated after this graph was "
+                                    "recorded (a larger call ran since); record the graph again");
     HIP_TRY(c, hipSetDevice(c->device));
     HIP_TRY(c, hipGraphLaunch(g->exec, c->stream));
     return BRIK_OK;

@@ -17,9 +17,10 @@
 //      reads are free of bank conflicts. W goes straight from global memory into the MFMA B operand:
 //      each lane loads two whole groups of one column per step and dequantizes them in registers 8
 //      codes at a time, one slice ahead of the MFMAs that consume them. The dequant is packed f16: a
-//      code q placed in the mantissa of 1024.0h reads as 1024 + q (or 1024 + 16 q one nibble higher,
-//      which the scale s / 16 undoes), and one packed subtract and one packed FMA give the dequantized
-//      pair (q s + m); the code pairs (j, j + 4) this produces from 8 packed codes fix the
+//      low nibble q placed in the mantissa of 1024.0h reads as 1024 + q, and a high nibble left in
+//      place (bits 4-7) in the mantissa of 64.0h reads as 64 + q; one packed subtract and one packed
+//      FMA then give the dequantized pair (q s + m), rounded once to f16 whatever the scale; the
+//      code pairs (j, j + 4) this produces from 8 packed codes fix the
 //      [0 4 1 5 2 6 3 7] order. Scales and mins are staged in LDS per 4 steps by coalesced loads. The
 //      epilogue multiplies by rscale[m] (exact) and stores y through LDS with 16-byte stores.
 // f16 (not bf16) operands: 11-bit significands keep the normwise error near 3e-4, inside the 1e-3
@@ -297,32 +298,37 @@ struct Loader {
 };
 
 // Dequantize 8 codes to 4 packed f16 pairs (codes j and j + 4 in pair j). A code q placed in the
-// mantissa of 1024.0h reads as 1024 + q (or 1024 + 16 q one nibble higher, which the scale s / 16
-// undoes); one packed subtract and one packed FMA give the dequantized pair (q s + m). The pairs
-// (j, j + 4) match the [0 4 1 5 2 6 3 7] order of the staged x.
+// mantissa of a power of two 2^E whose mantissa unit is 1 at the code's bit position reads as
+// 2^E + q: 1024.0h (unit 1 at bit 0) for a code in bits 0-3, 64.0h (unit 1/16 at bit 0, so 1 at
+// bit 4) for a code left in bits 4-7. One packed subtract (exact) and one packed FMA then give the
+// dequantized pair (q s + m), rounded once, with the f16 scale itself: no scale is rescaled, so
+// every normal or subnormal scale is used exactly. The pairs (j, j + 4) match the
+// [0 4 1 5 2 6 3 7] order of the staged x.
 // Mask and exponent constants of the dequantization, held in VGPRs so that a mask-and-insert is one
 // v_and_or_b32 (a VOP3 instruction here takes no literal operand, and with literals the compiler
 // emits a v_and_b32 / v_or_b32 pair instead).
 struct DeqConst {
-    uint32_t lo4, hi4, e1024, lo2;
+    uint32_t lo4, hi4, e1024, lo2, e64;
     __device__ __forceinline__ static DeqConst make()
     {
-        DeqConst k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x00030003u};
-        asm volatile("" : "+v"(k.lo4), "+v"(k.hi4), "+v"(k.e1024), "+v"(k.lo2));
+        DeqConst k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x00030003u, 0x54005400u};
+        asm volatile("" : "+v"(k.lo4), "+v"(k.hi4), "+v"(k.e1024), "+v"(k.lo2), "+v"(k.e64));
         return k;
     }
 };
 
-// q4: the low nibble of each byte lands on the mantissa units, the high nibble 16 units up.
-__device__ __forceinline__ u32x4_t deq8_q4(uint32_t w, half2_t s2, half2_t s2_16, half2_t m2, const DeqConst& k)
+// q4: the low nibble of each byte on the mantissa units of 1024.0h, the high nibble in place on
+// those of 64.0h.
+__device__ __forceinline__ u32x4_t deq8_q4(uint32_t w, half2_t s2, half2_t m2, const DeqConst& k)
 {
     const half2_t k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+    const half2_t k64 = {(_Float16)64.f, (_Float16)64.f};
     const uint32_t w8 = w >> 8;
     u32x4_t r;
     r[0] = as_u32(__builtin_elementwise_fma(as_h2((w & k.lo4) | k.e1024) - k1024, s2, m2));
-    r[1] = as_u32(__builtin_elementwise_fma(as_h2((w & k.hi4) | k.e1024) - k1024, s2_16, m2));
+    r[1] = as_u32(__builtin_elementwise_fma(as_h2((w & k.hi4) | k.e64) - k64, s2, m2));
     r[2] = as_u32(__builtin_elementwise_fma(as_h2((w8 & k.lo4) | k.e1024) - k1024, s2, m2));
-    r[3] = as_u32(__builtin_elementwise_fma(as_h2((w8 & k.hi4) | k.e1024) - k1024, s2_16, m2));
+    r[3] = as_u32(__builtin_elementwise_fma(as_h2((w8 & k.hi4) | k.e64) - k64, s2, m2));
     return r;
 }
 
@@ -357,10 +363,10 @@ __device__ __forceinline__ u32x4_t deq8_q8(uint32_t w, uint32_t w2, half2_t s2)
     return r;
 }
 
-// Per-group scale operands of one column block for the current step: packed splats of the scale,
-// scale / 16 (q4 high nibbles) and min of groups e = 0, 1.
+// Per-group scale operands of one column block for the current step: packed splats of the scale and
+// min of groups e = 0, 1.
 struct GroupOps {
-    half2_t s2[2], s16[2], m2[2];
+    half2_t s2[2], m2[2];
     DeqConst k;
 };
 
@@ -373,9 +379,7 @@ __device__ __forceinline__ GroupOps group_ops(const WCodes<FMT>& f, const DeqCon
     for (int e = 0; e < 2; ++e) {
         const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)f.s[e]);
         const _Float16 m = __builtin_bit_cast(_Float16, (uint16_t)f.m[e]);
-        const _Float16 s16 = s * (_Float16)0.0625f;     // exact for normal scales >= 2^-10
         o.s2[e] = half2_t{s, s};
-        o.s16[e] = half2_t{s16, s16};
         o.m2[e] = half2_t{m, m};
     }
     return o;
@@ -388,7 +392,7 @@ __device__ __forceinline__ half8_t b_frag(const WCodes<FMT>& f, const GroupOps& 
     const int e = sl >> 2, c = sl & 3;
     u32x4_t o;
     if constexpr (FMT == FMT_Q4) {
-        o = deq8_q4(f.w[sl], g.s2[e], g.s16[e], g.m2[e], g.k);
+        o = deq8_q4(f.w[sl], g.s2[e], g.m2[e], g.k);
     } else if constexpr (FMT == FMT_Q8) {
         o = deq8_q8(f.w[2 * sl], f.w[2 * sl + 1], g.s2[e]);
     } else {

@@ -187,7 +187,11 @@ int brik_lm_head_topk_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, cons
  * may change between replays. While a capture is open, brik_alloc / brik_free, copies, brik_sync,
  * plan creation and calls that would grow a context workspace fail with BRIK_EINVAL (make the same
  * calls once before capturing); after such an error, close the capture with brik_graph_end and
- * destroy what it returns. One capture per context at a time. */
+ * destroy what it returns. One capture per context at a time.
+ * A graph also holds the addresses of the context workspaces it used. An ordinary call after the
+ * capture that needs a larger workspace frees and reallocates it; brik_graph_launch then refuses the
+ * older graph with BRIK_EINVAL (nothing is enqueued): record it again. Buffers the caller passed
+ * (and plans) must outlive every graph that recorded them. */
 typedef struct brik_graph brik_graph;
 int brik_graph_begin(brik_ctx *ctx);
 int brik_graph_end(brik_ctx *ctx, brik_graph **out);

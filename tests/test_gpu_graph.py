@@ -94,3 +94,46 @@ def test_capture_refuses_workspace_growth_and_copies(gpu):
     ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
     ctx.sync()
     assert np.isfinite(ctx.download(ym, np.float32, M * N)).all()
+
+
+def test_replay_after_workspace_reallocation_is_refused(gpu):
+    """A graph records the context workspace's address; an eager call that needs a larger workspace
+    frees and reallocates it, after which replaying the old graph would touch freed memory. The
+    library refuses that launch (no GPU work is enqueued) and a graph recorded afterwards replays."""
+    ctx = gpu.ctx
+    K, N, M = 256, 64, 16
+    t = synth.q4_tensor(140, N, K)
+    nib, sc, mn = gpu.planes("q4", t)
+    xm = gpu.up(synth.normal(141, M * K))
+    ym = gpu.up(np.zeros(M * N, np.float32))
+    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+    ctx.sync()
+    ctx.graph_begin()
+    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+    old = ctx.graph_end()
+    # 128 MiB of staged activation rows (M_big x K_big halves): more than any earlier call of the session
+    M_big, K_big = 16384, 4096
+    xb = gpu.up(np.zeros(M_big * K_big, np.float32))
+    yb = gpu.up(np.zeros(M_big * 32, np.float32))
+    tb = synth.q4_tensor(142, 32, K_big)
+    ctx.matmul_t_q4(xb, *gpu.planes("q4", tb), yb, M_big, K_big, 32)
+    ctx.sync()
+    try:
+        with pytest.raises(BrikError) as e:
+            old.launch()
+        assert e.value.code == BRIK_EINVAL
+    finally:
+        old.destroy()
+    ctx.graph_begin()
+    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+    new = ctx.graph_end()
+    try:
+        ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+        ctx.sync()
+        eager = ctx.download(ym, np.float32, M * N)
+        ctx.h2d(ym, np.full(M * N, np.nan, np.float32))
+        new.launch()
+        ctx.sync()
+        assert np.array_equal(ctx.download(ym, np.float32, M * N), eager)
+    finally:
+        new.destroy()
