@@ -1,9 +1,10 @@
 """Build recipe for the native parts of brimkern_amd (no cmake / node-gyp needed).
 
 1. ``csrc/kernels/brik_kernels.hip`` -> ``_build/brik_gfx950.hsaco``  (hipcc --genco, gfx950 only)
-2. ``csrc/brik_runtime.cpp`` + ``csrc/brik_embed.S`` (embeds the code object) -> ``libbrik.so``
-   (the C ABI declared in ``include/brik.h``)
-3. ``csrc/brik_napi.cc`` -> ``js/brik.node`` (Node N-API addon over libbrik.so, rpath $ORIGIN/..)
+2. ``csrc/brik_scratch.hip`` -> ``_build/brik_scratch.o`` (hipcc -c: the no-allocation scratch array)
+3. ``csrc/brik_runtime.cpp`` + ``csrc/brik_embed.S`` (embeds the code object) + that object ->
+   ``libbrik.so`` (the C ABI declared in ``include/brik.h``)
+4. ``csrc/brik_napi.cc`` -> ``js/brik.node`` (Node N-API addon over libbrik.so, rpath $ORIGIN/..)
 
 Run ``python -m brimkern_amd.build`` or call :func:`build`.
 """
@@ -21,6 +22,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 NODE_INC = "/usr/include/node"
 
 HSACO = os.path.join(BUILD, "brik_gfx950.hsaco")
+SCRATCH_OBJ = os.path.join(BUILD, "brik_scratch.o")
 LIB = os.path.join(PKG, "libbrik.so")
 ADDON = os.path.join(PKG, "js", "brik.node")
 
@@ -46,12 +48,23 @@ def build_hsaco(verbose=False):
     return HSACO
 
 
+def build_scratch(verbose=False):
+    """``csrc/brik_scratch.hip`` (the fixed device scratch of the no-allocation entry point and its
+    address lookup) as a HIP object, linked into libbrik.so."""
+    os.makedirs(BUILD, exist_ok=True)
+    tmp = SCRATCH_OBJ + ".tmp"
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", *HIP_DEVICE_FLAGS, "-Wall",
+          "-o", tmp, os.path.join(CSRC, "brik_scratch.hip")], verbose)
+    os.replace(tmp, SCRATCH_OBJ)
+    return SCRATCH_OBJ
+
+
 def build_lib(verbose=False):
     tmp = LIB + ".tmp"
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
           f'-DBRIK_HSACO_PATH="{HSACO}"',
-          os.path.join(CSRC, "brik_runtime.cpp"), os.path.join(CSRC, "brik_embed.S"),
+          os.path.join(CSRC, "brik_runtime.cpp"), os.path.join(CSRC, "brik_embed.S"), SCRATCH_OBJ,
           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
           "-Wl,--no-undefined", "-o", tmp], verbose)
     os.replace(tmp, LIB)
@@ -72,6 +85,7 @@ def build_addon(verbose=False):
 
 def build(verbose=False):
     build_hsaco(verbose)
+    build_scratch(verbose)
     build_lib(verbose)
     build_addon(verbose)
 

@@ -37,6 +37,7 @@ SIGNATURES = {
     "brik_matmul_t_q8": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_matmul_t_q3": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
+    "brik_matmul_t_q4_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_moe_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "brik_dequant_q8_f32": (_I, [_P, _P, _P, _P, _Z]),
     "brik_dequant_q4_f32": (_I, [_P, _P, _P, _P, _P, _Z]),
@@ -66,6 +67,7 @@ SIGNATURES = {
                                   _P]),
 }
 BRIK_TOPK_MAX = 64
+BRIK_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 FMT_CODES = {"q8": 8, "q4": 4, "q3": 3}
 
@@ -233,6 +235,11 @@ class Context:
     def matmul_t_q4(self, x, nib, sc, mn, y, M, K, N):
         self._check(self.lib.brik_matmul_t_q4(self.handle, _addr(x), _addr(nib), _addr(sc), _addr(mn),
                                               _addr(y), M, K, N))
+
+    def matmul_t_q4_noalloc(self, x, nib, sc, mn, y, M, K, N):
+        """:meth:`matmul_t_q4` on the library's fixed per-device scratch: no device allocation."""
+        self._check(self.lib.brik_matmul_t_q4_noalloc(self.handle, _addr(x), _addr(nib), _addr(sc), _addr(mn),
+                                                      _addr(y), M, K, N))
 
     def matmul_t_q3(self, x, lo, hi, sc, mn, y, M, K, N):
         self._check(self.lib.brik_matmul_t_q3(self.handle, _addr(x), _addr(lo), _addr(hi), _addr(sc),

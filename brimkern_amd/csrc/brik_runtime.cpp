@@ -19,6 +19,8 @@
 
 extern "C" const unsigned char brik_hsaco_begin[];
 extern "C" const unsigned char brik_hsaco_end[];
+// brik_scratch.hip: device address of the fixed scratch array on the current device (a hipError_t)
+extern "C" int brik_scratch_resolve(int device, void** out, size_t* bytes);
 
 namespace {
 
@@ -144,6 +146,11 @@ struct brik_ctx {
     size_t sws_bytes = 0;
     void* cws = nullptr;   // convolution workspace: the [pixels, Cout] GEMM output (grow-only)
     size_t cws_bytes = 0;
+    // the device's fixed scratch array (brik_scratch.hip), resolved at creation; scratch_err holds the
+    // hipError_t of a failed resolution, which only the no-allocation entry point reports
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
+    int scratch_err = 0;
     bool graph_capturing = false;
     // bumped whenever a context workspace is freed and reallocated (ensure_buf): a graph recorded
     // before that replays addresses that are no longer the context's, so brik_graph_launch refuses it
@@ -279,7 +286,27 @@ int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
     return BRIK_OK;
 }
 
-int ensure_ws(brik_ctx* c, size_t bytes) { return ensure_buf(c, c->ws, c->ws_bytes, bytes); }
+// Device memory a call uses beyond its inputs and outputs. By default the context workspaces above
+// (grown with hipMalloc on demand); the no-allocation entry point passes a fixed buffer instead, and
+// a call that would need more than it holds fails before anything is enqueued.
+struct Scratch {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+int take_scratch(brik_ctx* c, const Scratch* fixed, void*& buf, size_t& have, size_t bytes, void*& out)
+{
+    if (!fixed) {
+        HIP_TRY_RC(ensure_buf(c, buf, have, bytes));
+        out = buf;
+        return BRIK_OK;
+    }
+    if (bytes > fixed->bytes)
+        return fail(c, BRIK_EINVAL, "no-allocation call: needs %zu bytes of scratch, the fixed buffer holds %zu",
+                    bytes, fixed->bytes);
+    out = fixed->p;
+    return BRIK_OK;
+}
 
 // y[0, n) = 0 on the context stream (a kernel, so graph capture records no memset node).
 int fill_zero(brik_ctx* c, float* y, size_t n)
@@ -291,16 +318,25 @@ int fill_zero(brik_ctx* c, float* y, size_t n)
     return launch(c, K_FILL_ZERO, (unsigned)blocks, 1, 256, 0, args);
 }
 
-// Workspace for `rows` staged f16 activation rows of K (padded to Kp) and their row scales.
-int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*& rscale)
+// Bytes of `rows` staged f16 activation rows of K (padded to Kp halves) and their row scales.
+size_t gemm_stage_bytes(long rows, long K, long& Kp)
 {
     Kp = (K + kGemmKPad - 1) / kGemmKPad * kGemmKPad;
+    return (size_t)rows * Kp * 2 + 4 * (size_t)rows;
+}
+
+// Workspace for `rows` staged f16 activation rows of K (padded to Kp) and their row scales.
+int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*& rscale,
+                  const Scratch* fixed = nullptr)
+{
+    const size_t bytes = gemm_stage_bytes(rows, K, Kp);
     const size_t xbytes = (size_t)rows * Kp * 2;
     if (xbytes >= (1ull << 31))
         return fail(c, BRIK_EINVAL, "matmul: %d rows x K=%d exceed the 2 GiB staged-activation limit", rows, K);
-    HIP_TRY_RC(ensure_ws(c, xbytes + 4 * (size_t)rows));
-    xh = static_cast<uint16_t*>(c->ws);
-    rscale = reinterpret_cast<float*>(static_cast<char*>(c->ws) + xbytes);
+    void* p = nullptr;
+    HIP_TRY_RC(take_scratch(c, fixed, c->ws, c->ws_bytes, bytes, p));
+    xh = static_cast<uint16_t*>(p);
+    rscale = reinterpret_cast<float*>(static_cast<char*>(p) + xbytes);
     return BRIK_OK;
 }
 
@@ -324,13 +360,13 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
 // tile kernel.
 int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
-         float* y, int rows, int K, int N, const int* row_off, int E)
+         float* y, int rows, int K, int N, const int* row_off, int E, const Scratch* fixed = nullptr)
 {
     if (K == 0) return fill_zero(c, y, (size_t)rows * N);   // empty sums
     long Kp;
     uint16_t* xh;
     float* rscale;
-    HIP_TRY_RC(gemm_stage_ws(c, rows, K, Kp, xh, rscale));
+    HIP_TRY_RC(gemm_stage_ws(c, rows, K, Kp, xh, rscale, fixed));
     int Mi = rows, Ki = K, Kpi = (int)Kp;
     {
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
@@ -372,7 +408,7 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
 }
 
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
-           const void* mn, float* y, int M, int K, int N)
+           const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr)
 {
     if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
     // A large q4 / q3 matrix at M = 1 (an LM head) stages x once per call (brik_gemv_stage1_<fmt>, one
@@ -399,15 +435,16 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     if (use_gemv) {
         const unsigned char* staged = nullptr;
         if (stage1) {
-            HIP_TRY_RC(ensure_buf(c, c->sws, c->sws_bytes, (gemv_lds(K, f) + 15) & ~(size_t)15));
-            staged = static_cast<const unsigned char*>(c->sws);
-            void* sargs[] = {&x, &Ki, &c->sws};
+            void* img = nullptr;
+            HIP_TRY_RC(take_scratch(c, fixed, c->sws, c->sws_bytes, (gemv_lds(K, f) + 15) & ~(size_t)15, img));
+            staged = static_cast<const unsigned char*>(img);
+            void* sargs[] = {&x, &Ki, &img};
             HIP_TRY_RC(launch(c, f == F_Q4 ? K_GEMV_STAGE1_Q4 : K_GEMV_STAGE1_Q3, 1, 1, kStageThreads, 0, sargs));
         }
         void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged};
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
-    return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0);
+    return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0, fixed);
 }
 
 // ---- sampling pre-work -------------------------------------------------------------------------
@@ -534,6 +571,8 @@ int brik_create(int device, brik_ctx** out)
                 max_threads < (int)kGemmTiles[t].threads())
                 return bail(BRIK_EMODULE);
         }
+    // the fixed scratch of brik_matmul_t_q4_noalloc, with this device current (once per device)
+    c->scratch_err = brik_scratch_resolve(device, &c->scratch, &c->scratch_bytes);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);
     if (hipEventCreate(&c->ev_begin) != hipSuccess || hipEventCreate(&c->ev_end) != hipSuccess)
         return bail(BRIK_EHIP);
@@ -618,6 +657,18 @@ int brik_matmul_t_q4(brik_ctx* c, const float* x, const uint8_t* nib, const uint
     int r = check_mm(c, "matmul_t_q4", x, nib, nullptr, sc, mn, y, M, K, N, F_Q4);
     if (r != BRIK_OK || M == 0 || N == 0) return r;
     return matmul(c, F_Q4, x, nib, nullptr, sc, mn, y, M, K, N);
+}
+
+int brik_matmul_t_q4_noalloc(brik_ctx* c, const float* x, const uint8_t* nib, const uint16_t* sc,
+                             const uint16_t* mn, float* y, int M, int K, int N)
+{
+    int r = check_mm(c, "matmul_t_q4_noalloc", x, nib, nullptr, sc, mn, y, M, K, N, F_Q4);
+    if (r != BRIK_OK || M == 0 || N == 0) return r;
+    if (!c->scratch)
+        return fail(c, BRIK_EHIP, "matmul_t_q4_noalloc: the scratch array has no device address (%s)",
+                    hipGetErrorString((hipError_t)c->scratch_err));
+    const Scratch fixed{c->scratch, c->scratch_bytes};
+    return matmul(c, F_Q4, x, nib, nullptr, sc, mn, y, M, K, N, &fixed);
 }
 
 int brik_matmul_t_q3(brik_ctx* c, const float* x, const uint32_t* lo, const uint32_t* hi,

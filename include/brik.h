@@ -83,6 +83,20 @@ int brik_matmul_t_q4(brik_ctx *ctx, const float *x, const uint8_t *nibbles, cons
 int brik_matmul_t_q3(brik_ctx *ctx, const float *x, const uint32_t *lo, const uint32_t *hi,
                      const uint16_t *scales, const uint16_t *mins, float *y, int M, int K, int N);
 
+/* brik_matmul_t_q4 without any device allocation. No counterpart exists in the reference (WebGPU
+ * callers never manage device memory themselves); it is for callers that cannot allocate: code under
+ * HIP graph capture, serving loops and harnesses that forbid hipMalloc. Same arguments, kernels and
+ * results as brik_matmul_t_q4 (bit-identical), but the staging memory it needs (M >= 2: the f16
+ * activation rows, 2 * M * roundup(K, 256) + 4 * M bytes; M == 1 with N >= 24576: the staged
+ * activation image, about 3.5 * K bytes) comes from a fixed per-device scratch array of
+ * BRIK_NOALLOC_SCRATCH_BYTES held by the library until the process ends, never from hipMalloc.
+ * A call needing more than that returns BRIK_EINVAL before anything is enqueued. Every call on one
+ * GPU shares that GPU's array (contexts included): calls that overlap on one GPU (two streams or two
+ * contexts in flight at once) race; calls on one context's stream are ordered and do not. */
+#define BRIK_NOALLOC_SCRATCH_BYTES (16u << 20)
+int brik_matmul_t_q4_noalloc(brik_ctx *ctx, const float *x, const uint8_t *nibbles, const uint16_t *scales,
+                             const uint16_t *mins, float *y, int M, int K, int N);
+
 /* Expert-grouped q4 matmul (MoE). No counterpart exists in the reference (it has no MoE); this is
  * the per-expert application of matmul_t_q4 over a token list sorted by expert:
  *   for e in [0, E): y_sorted[r, :] = x_sorted[r, :] . deq(W_e)^T  for r in [row_off[e], row_off[e+1])
