@@ -41,6 +41,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+from brimkern_amd.capi import BRIK_OPT_PATH, PATH_AUTO, PATH_GEMV, PATH_GEMM  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
@@ -58,12 +59,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+ROTATE_BYTES = 512 << 20        # distinct weight copies a per-call timing cycles through: 2x the MALL
+SMALL_M = (2, 4, 8, 15)
+
+
+def synth_rows(K, M):
+    from brimkern_amd import synth
+    return synth.normal(900 + K, M * K)
+
+
 class Replicas:
     """``count`` device copies (distinct addresses) of one packed tensor; returns plane addresses."""
 
     def __init__(self, ctx, fmt, t, count):
         from brimkern_amd import layout
-        self.fmt, self.N, self.K = fmt, t["N"], t["K"]
+        self.fmt, self.N, self.K, self.tensor = fmt, t["N"], t["K"], t
         blob = layout.pack(fmt, t)
         self.stride = (blob.size + 255) // 256 * 256
         self.buf = ctx.alloc(self.stride * count)
@@ -136,26 +146,43 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
     reps, xa, xd, ybuf, nbytes = b["reps"], b["xa"], b["xd"], b["ybuf"], b["nbytes"]
     settle(ctx, lambda i: plan.run(), settle_s)
     ms = time_loop(ctx, lambda i: plan.run(), steps, warmup)
-    # per-shape single launches, rotating over the layers' copies
-    single = {}
-    for name, K, N in QWEN3_4B:
-        r = reps[name]
-        yb = ctx.alloc(4 * N)
-        x = xd if K == 9728 else xa
-
-        def one(i, r=r, x=x, yb=yb, K=K, N=N):
-            nib, sc, mn = r.planes(i % layers)
-            ctx.matmul_t_q4(x, nib, sc, mn, yb, 1, K, N)
-        lms = time_loop(ctx, one, 4 * layers, layers)
-        b = q_bytes("q4", N, K) + 4 * K + 4 * N
-        single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1)}
-        ctx.free(yb)
     plan.destroy()
+    # per-shape single launches and small-M calls, each rotating over distinct weight copies totalling
+    # at least twice the 256 MB last-level cache (so every call streams its weights from HBM)
+    single, small_m = {}, {}
+    for name, K, N in QWEN3_4B:
+        tb = q_bytes("q4", N, K)
+        count = max(layers, -(-ROTATE_BYTES // tb))
+        extra = Replicas(ctx, "q4", reps[name].tensor, count) if count > layers else reps[name]
+        x = xd if K == 9728 else xa
+        xm = ctx.upload(synth_rows(K, max(SMALL_M)))
+        yb = ctx.alloc(4 * N * max(SMALL_M))
+
+        def one(i, M=1, r=extra, yb=yb, K=K, N=N, count=count):
+            nib, sc, mn = r.planes(i % count)
+            ctx.matmul_t_q4(x if M == 1 else xm, nib, sc, mn, yb, M, K, N)
+        lms = time_loop(ctx, one, max(4 * layers, count), count)
+        b = tb + 4 * K + 4 * N
+        single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1),
+                                       "copies": count}
+        for M in SMALL_M:
+            row = {}
+            for label, path in (("auto", PATH_AUTO), ("gemv", PATH_GEMV), ("gemm", PATH_GEMM)):
+                ctx.set_option(BRIK_OPT_PATH, path)
+                ms_m = time_loop(ctx, lambda i, M=M: one(i, M), count, count // 4)
+                row[label + "_us"] = round(ms_m * 1e3, 2)
+            ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
+            row["weight_GBps"] = round(tb / (row["auto_us"] * 1e-6) / 1e9, 1)
+            small_m.setdefault(f"M{M}", {})[f"{name}_K{K}_N{N}"] = row
+        if extra is not reps[name]:
+            ctx.free(extra.buf)
+        ctx.free(xm)
+        ctx.free(yb)
     fused = decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay)
     for r in reps.values():
         ctx.free(r.buf)
     ctx.free(ybuf)
-    return ms, nbytes, single, fused
+    return ms, nbytes, single, fused, small_m
 
 
 def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
@@ -525,10 +552,14 @@ def main():
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
-    ms, nbytes, single, fused = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle,
-                                               not args.no_graph)
+    ms, nbytes, single, fused, small_m = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle,
+                                                        not args.no_graph)
     value = nbytes / (ms * 1e-3) / 1e9
-    extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused}
+    extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused,
+             "small_m_qwen3_4b": dict(small_m, note="matmul_t_q4 at M rows per call (the reference's "
+                                      "matmul_t_q4_tiled range, 2 <= M < 16, plus M = 15): the routed path (auto), "
+                                      "the GEMV re-streaming W per row and the MFMA GEMM; weight_GBps = W bytes "
+                                      "(read once) / auto time")}
     if not args.no_extra:
         log("bench: cfg1 q8 GEMV")
         extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)

@@ -65,14 +65,17 @@ const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 constexpr int kGroup = 32;
 // GEMM block tiles (BM rows x 32 TN NW columns, NW waves), in the order of BRIK_GEMM_FMT in gemm.hip:
 // brik_gemm_<fmt>_<BM>x<TN> (NW = 4) and brik_gemm_<fmt>_<BM>x<TN>w8 (NW = 8).
+// pf: steps of W prefetched ahead (kernel suffix p<pf> when above 1)
 struct GemmTile {
-    int bm, tn, nw;
+    int bm, tn, nw, pf;
     int bn() const { return 32 * tn * nw; }
     unsigned threads() const { return 64u * (unsigned)nw; }
 };
-constexpr GemmTile kGemmTiles[] = {{128, 2, 4}, {128, 1, 4}, {128, 3, 4}, {64, 2, 4}, {64, 1, 4}, {64, 3, 4},
-                                   {32, 2, 4},  {32, 1, 4},  {32, 3, 4},  {96, 2, 4}, {96, 1, 4}, {96, 3, 4},
-                                   {128, 1, 8}, {96, 1, 8},  {64, 1, 8},  {32, 1, 8}, {64, 2, 8}};
+constexpr GemmTile kGemmTiles[] = {{128, 2, 4, 1}, {128, 1, 4, 1}, {128, 3, 4, 1}, {64, 2, 4, 1}, {64, 1, 4, 1},
+                                   {64, 3, 4, 1},  {32, 2, 4, 1},  {32, 1, 4, 1},  {32, 3, 4, 1}, {96, 2, 4, 1},
+                                   {96, 1, 4, 1},  {96, 3, 4, 1},  {128, 1, 8, 1}, {96, 1, 8, 1}, {64, 1, 8, 1},
+                                   {32, 1, 8, 1},  {64, 2, 8, 1},  {32, 1, 8, 4},  {64, 1, 8, 3}, {32, 1, 4, 4},
+                                   {64, 1, 4, 3},  {32, 1, 8, 2},  {64, 1, 8, 2}};
 constexpr int kNumGemmTiles = sizeof(kGemmTiles) / sizeof(kGemmTiles[0]);
 constexpr unsigned kCUs = 256;                 // MI355X compute units
 constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
@@ -138,6 +141,8 @@ struct brik_ctx {
     int opt_path = 0;
     int opt_variant = 0;   // 0 auto, else 1 + index into kGemvVariants
     int opt_tile = 0;      // 0 auto, else 1 + index into kGemmTiles
+    int opt_plan_stage = 0;  // plans: 0 auto, 1 in-block staging, 2 staging launch
+    int opt_plan_sets = 0;   // plans: 0 auto, else row sets per block
     void* ws = nullptr;    // GEMM workspace: f16 activation rows, then per-row scales (grow-only)
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
@@ -241,9 +246,10 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
-    auto find = [](int bm, int tn, int nw) {
+    auto find = [](int bm, int tn, int nw, int pf = 1) {
         for (int t = 0; t < kNumGemmTiles; ++t)
-            if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == tn && kGemmTiles[t].nw == nw) return t;
+            if (kGemmTiles[t].bm == bm && kGemmTiles[t].tn == tn && kGemmTiles[t].nw == nw && kGemmTiles[t].pf == pf)
+                return t;
         return 0;
     };
     if (E > 0) return find(K >= 1024 ? 64 : 32, 1, 8);
@@ -251,7 +257,7 @@ int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
     double best_cost = 0;
     for (int t = 0; t < kNumGemmTiles; ++t) {
         GemmTile g = kGemmTiles[t];
-        if (g.nw != 4) continue;
+        if (g.nw != 4 || g.pf != 1) continue;
         const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn());
         const double rounds = std::ceil(blocks / kCUs);
         const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
@@ -407,6 +413,23 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
 
+// M >= 2: whether the GEMV (grid.y = M: every activation row streams W again, rows after the first
+// mostly from the 256 MB last-level cache) is expected to beat the MFMA GEMM. Cost model fitted on the
+// Qwen3-4B q4 shapes at M = 2..64 (time above the launch cost, us): GEMV ~ M * W bytes / 7.5 TB/s
+// (q3: 4.5, bound by its unpacking); GEMM ~ max(0.65 us per 128-deep K step, which is what its few-row
+// tiles spend in issue latency on one wave per SIMD, 2MNK at 1 PFLOP/s). Measured crossovers: K = 2560,
+// N = 4096 at M ~ 15; N = 9728 at M ~ 7; N = 1024 past M = 32; K = 9728, N = 2560 at M ~ 20-30.
+bool gemv_cheaper(Fmt f, long M, long K, long N)
+{
+    const double nk = (double)N * K;
+    const double wbytes = f == F_Q4 ? nk * (0.5 + 4.0 / kGroup) : f == F_Q8 ? nk * (1.0 + 2.0 / kGroup)
+                                                                            : nk * (0.375 + 4.0 / kGroup);
+    const double gemv_us = (double)M * wbytes / (f == F_Q3 ? 4.5e6 : 7.5e6);
+    const double steps = (double)((K + 2 * 128 - 1) / (2 * 128) * 2);
+    const double gemm_us = std::max(0.65 * steps, 2.0 * M * nk / 1e9);
+    return gemv_us < gemm_us;
+}
+
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr)
 {
@@ -424,7 +447,8 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     // the MFMA GEMM reads scales in 16-group chunks, so a matrix of fewer than 16 groups (N * K < 512)
     // always takes the GEMV path (which handles any M)
     const bool tiny = (long)N * (K / kGroup) < 16;
-    bool use_gemv = ((M == 1 || tiny) && gemv_fits);
+    // a forced GEMM tile asks for the GEMM
+    bool use_gemv = (M == 1 || tiny || (c->opt_tile == 0 && gemv_cheaper(f, M, K, N))) && gemv_fits;
     if (c->opt_path == 1) {
         if (!gemv_fits) return fail(c, BRIK_EINVAL, "forced GEMV: K=%d exceeds the LDS staging limit", K);
         use_gemv = true;
@@ -562,8 +586,10 @@ int brik_create(int device, brik_ctx** out)
     for (int f = 0; f < 3; ++f)
         for (int t = 0; t < kNumGemmTiles; ++t) {
             char name[64];
-            snprintf(name, sizeof name, "brik_gemm_%s_%dx%d%s", kFmtNames[f], kGemmTiles[t].bm, kGemmTiles[t].tn,
-                     kGemmTiles[t].nw == 8 ? "w8" : "");
+            char pf[16] = "";
+            if (kGemmTiles[t].pf > 1) snprintf(pf, sizeof pf, "p%d", kGemmTiles[t].pf);
+            snprintf(name, sizeof name, "brik_gemm_%s_%dx%d%s%s", kFmtNames[f], kGemmTiles[t].bm, kGemmTiles[t].tn,
+                     kGemmTiles[t].nw == 8 ? "w8" : "", pf);
             if (hipModuleGetFunction(&c->gemm[f][t], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
             // the launch shape the runtime uses must fit the kernel's compiled bounds
             int max_threads = 0;
@@ -942,7 +968,7 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
     std::vector<brik_gemv_job_ex> sorted(njobs);
     std::vector<uint32_t> start(njobs + 1, 0), rpbs(njobs);
     std::vector<long> sets(njobs);
-    const bool prestage = rows >= kPrestageRows;
+    const bool prestage = c->opt_plan_stage ? c->opt_plan_stage == 2 : rows >= kPrestageRows;
     // the lane partials of a block's row sets stay within the 16 KiB the per-job LDS check reserves
     long maxsets = (long)(kPlanPartialLds / kGemvVariants[v].extra_lds(rpi));
     const long capsets = prestage ? kPrestageMaxSets : kPlanMaxSets;
@@ -963,6 +989,8 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
         if (blocks >= kPlanMinBlocks || maxsets == 1) break;
         for (int k = 0; k < njobs; ++k) sets[k] = (sets[k] + 1) / 2;
     }
+    if (c->opt_plan_sets > 0)
+        for (int k = 0; k < njobs; ++k) sets[k] = c->opt_plan_sets < maxsets ? c->opt_plan_sets : maxsets;
     size_t lds = 0;
     for (int k = 0; k < njobs; ++k) {
         const brik_gemv_job& b = sorted[k].job;
@@ -1189,6 +1217,14 @@ int brik_set_option(brik_ctx* c, int key, int value)
         if (value < 0 || value > kNumGemmTiles)
             return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMM_TILE: %d not in 0..%d", value, kNumGemmTiles);
         c->opt_tile = value;
+        return BRIK_OK;
+    case BRIK_OPT_PLAN_STAGE:
+        if (value < 0 || value > 2) return fail(c, BRIK_EINVAL, "BRIK_OPT_PLAN_STAGE: %d not in 0..2", value);
+        c->opt_plan_stage = value;
+        return BRIK_OK;
+    case BRIK_OPT_PLAN_SETS:
+        if (value < 0 || value > 64) return fail(c, BRIK_EINVAL, "BRIK_OPT_PLAN_SETS: %d not in 0..64", value);
+        c->opt_plan_sets = value;
         return BRIK_OK;
     default:
         return fail(c, BRIK_EINVAL, "unknown option %d", key);

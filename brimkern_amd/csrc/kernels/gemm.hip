@@ -12,10 +12,11 @@
 //      columns over all BM rows and runs v_mfma_f32_32x32x16_f16 (f32 accumulation), which issues at
 //      full rate from one wave per SIMD and hides about six VALU instructions of the same wave beside
 //      each MFMA; with 8 waves two share each SIMD. A K
-//      step is 128 (four quantization groups, 8 MFMA slices of 16). x goes through LDS: three
-//      buffers filled two steps ahead by direct global->LDS loads, XOR-swizzled so that the A-fragment
-//      reads are free of bank conflicts. W goes straight from global memory into the MFMA B operand:
-//      each lane loads two whole groups of one column per step and dequantizes them in registers 8
+//      step is 128 (four quantization groups, 8 MFMA slices of 16). x goes through LDS: PF + 2
+//      buffers filled PF + 1 steps ahead by direct global->LDS loads, XOR-swizzled so that the
+//      A-fragment reads are free of bank conflicts. W goes straight from global memory into the MFMA B
+//      operand: each lane loads two whole groups of one column per step, PF steps ahead (PF = 1 for the
+//      dense tiles, more for the latency-bound few-row tiles), and dequantizes them in registers 8
 //      codes at a time, one slice ahead of the MFMAs that consume them. The dequant is packed f16: a
 //      low nibble q placed in the mantissa of 1024.0h reads as 1024 + q, and a high nibble left in
 //      place (bits 4-7) in the mantissa of 64.0h reads as 64 + q; one packed subtract and one packed
@@ -137,20 +138,27 @@ constexpr int XROW = GK * 2;         // bytes of one x row per step in LDS (16 c
 // lane, and the dequantization of one 16-k slice of a column block feeds TM MFMAs. The 32x32x16 MFMA
 // (32 cycles) issues at full rate from a single wave and leaves room for about six VALU instructions
 // of the same wave beside each one, which is what the dequantization needs at TM = 4.
-// x steps go through three LDS buffers of BM rows x 256 bytes, filled by direct global->LDS loads two
-// steps ahead. The 16-byte chunk c of row r sits at position c ^ (r & 15) of the row, so the 16 rows
+// x steps go through PF + 2 LDS buffers of BM rows x 256 bytes, filled by direct global->LDS loads
+// PF + 1 steps ahead (PF below). The 16-byte chunk c of row r sits at position c ^ (r & 15) of the row, so the 16 rows
 // that one 16-lane phase of an A-fragment read touches hit 16 different bank groups.
 // Scales and mins go through LDS too, a chunk of 4 steps (16 groups, 32 bytes of each column) at a
 // time, double buffered: the block loads them with 32-byte-per-column global->LDS loads (2 lanes per
 // column) instead of every lane fetching its own 2-byte values from a different cache line.
-template <int FMT, int BM_, int TN_, int NW_ = 4>
+// PF: how many steps ahead the W codes are loaded (a register ring of PF + 1 steps); the x buffers
+// then number PF + 2, filled PF + 1 steps ahead. Loads complete in issue order, so waiting for the x
+// of the next step also waits for every W load issued before it: W runs PF steps ahead only when x
+// runs further ahead still. A launch of few blocks (few rows per expert, small M) is bound by the
+// memory latency of each step, and PF > 1 keeps several steps of W in flight; a launch of many blocks
+// per CU (the dense prefill) hides the latency across blocks and keeps PF = 1.
+template <int FMT, int BM_, int TN_, int NW_ = 4, int PF_ = 1>
 struct Tile {
-    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 32, NW = NW_;
+    static constexpr int BM = BM_, TN = TN_, TM = BM_ / 32, NW = NW_, PF = PF_;
     static constexpr int BN = 32 * TN_ * NW_;
     static constexpr int NT = 64 * NW_;
     static constexpr int XI = BM_ / (4 * NW_);           // 16-byte x chunks per thread per step
     static constexpr int XBUF = BM_ * XROW;               // one x buffer
-    static constexpr int A_BYTES = 3 * XBUF;
+    static constexpr int XQ = PF_ + 2;                    // x buffers
+    static constexpr int A_BYTES = XQ * XBUF;
     static constexpr int PLANES = FMT == FMT_Q8 ? 1 : 2;  // scales (and mins)
     static constexpr int SPLANE = BN * 32;                // one plane of one scale chunk
     static constexpr int SBUF = PLANES * SPLANE;          // one scale chunk
@@ -161,8 +169,14 @@ struct Tile {
     static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 2 && TM % 2 == 0 ? 2 : 1;
     static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
     static constexpr int SMEM = MAIN > RF * C_BYTES ? MAIN : RF * C_BYTES;
+    // vector-memory loads per step: W codes, then the x chunks
+    static constexpr int W_OPS = (FMT == FMT_Q4 ? 2 : 4) * TN_;
+    // loads a wave may still have in flight once the x of the next step has landed: the W and x of the
+    // PF - 1 steps issued after it, and the W of the current step
+    static constexpr int VM_NEXT_X = (PF_ - 1) * (W_OPS + XI) + W_OPS;
     static_assert(BM_ % 32 == 0 && TN_ >= 1 && (NW_ == 4 || NW_ == 8) && BM_ % (4 * NW_) == 0 && TM % RF == 0 &&
-                  SMEM <= 160 * 1024, "tile shape");
+                  SMEM <= 160 * 1024 && PF_ >= 1 && VM_NEXT_X < 64 && XI + (PF_ - 1) * (W_OPS + XI) < 64,
+                  "tile shape");
 };
 
 // K mapping of a step (128 k = 8 slices of 16, one MFMA each): lane half h = lane >> 5, slice s and
@@ -191,6 +205,7 @@ struct Loader {
     static constexpr int TN = T::TN, XI = T::XI, NSD = T::NSD;
     static constexpr int CODE_OPS = FMT == FMT_Q4 ? 2 : 4;
     static constexpr int W_OPS = CODE_OPS * TN;
+    static_assert(W_OPS == T::W_OPS, "load count");
     static constexpr int OPS = W_OPS + XI;
     static constexpr int WS = 2;                              // slices that issue the W loads
     static constexpr int XS = 4;                              // first slice of the x loads (the barrier)
@@ -430,29 +445,30 @@ __device__ __forceinline__ void step_barrier()
 
 // One step of the multiply loop, 8 slices. On entry a[0] and b[0] hold the operands of slice 0,
 // prepared by the previous step. Slice sl reads and dequantizes the operands of slice sl + 1 while its
-// MFMAs run; slices 6-7 prepare slice 0 of the next step (its scales, codes and x). Loads: W codes of
-// step t + 1 in slices 0-1; at slice 4 the wave waits for the loads of earlier steps (x step t + 1
-// among them) and meets the other waves at the barrier, after which x step t + 1 may be read and the
-// buffer of step t - 1 refilled: x step t + 2 goes there over slices 4-7, and at the first step of a
-// scale chunk the next chunk is loaded.
+// MFMAs run; slices 6-7 prepare slice 0 of the next step (its scales, codes in wn, and x). Loads: W
+// codes of step t + PF into wl in slices 0-1; at slice 4 the wave waits for the loads of earlier steps
+// (x step t + 1 among them) and meets the other waves at the barrier, after which x step t + 1 may be
+// read and the buffer of step t - 1 refilled: x step t + PF + 1 goes there over slices 4-7, and at the
+// first step of a scale chunk the next chunk is loaded. With PF = 1, wn and wl are the same registers.
 template <int FMT, class T>
 __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_t (&aoff)[8], uint32_t abuf,
                                          uint32_t anext, const WCodes<FMT> (&wc)[T::TN], const GroupOps (&go)[T::TN],
                                          half8_t (&a)[2][T::TM], half8_t (&b)[2][T::TN],
                                          floatx16_t (&acc)[T::TM][T::TN], Loader<FMT, T>& ld,
-                                         WCodes<FMT> (&wn)[T::TN], GroupOps (&gn)[T::TN], int t, int xstep,
-                                         uint32_t xbuf, bool schunk, int sv, uint32_t sdst, uint32_t snext, int lane)
+                                         WCodes<FMT> (&wn)[T::TN], WCodes<FMT> (&wl)[T::TN], GroupOps (&gn)[T::TN],
+                                         int t, int xstep, uint32_t xbuf, bool schunk, int sv, uint32_t sdst,
+                                         uint32_t snext, int lane)
 {
     constexpr int TM = T::TM, TN = T::TN;
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) {
         const int cur = sl & 1, nxt = cur ^ 1;
         if (sl == Loader<FMT, T>::XS) {
-            wait_vm<Loader<FMT, T>::W_OPS>();
+            wait_vm<T::VM_NEXT_X>();
             step_barrier();
             if (schunk) ld.scale_chunk(sv, sdst);
         }
-        ld.issue(sl, wn, xstep, xbuf);
+        ld.issue(sl, wl, xstep, xbuf);
         if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
         if (sl < 7) {
 #pragma unroll
@@ -592,53 +608,71 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // Prologue: W codes of step 0 into registers, scale chunk 0 and x steps 0 and 1 into LDS, then
-    // the operands of slice 0 of step 0.
-    WCodes<FMT> wc[TN], wn_[TN];
+    // Prologue, in the order the steps keep: W codes of step 0 into registers, scale chunk 0, x steps 0
+    // and 1 into LDS, then W of step s and x of step s + 1 for s = 1 .. PF - 1; then the operands of
+    // slice 0 of step 0. W step s sits in slot s of a ring of PF + 1 register sets, x step s in LDS
+    // buffer s mod (PF + 2). Steps past the end are clamped (their loads are never used).
+    constexpr int R = T::PF + 1;
+    WCodes<FMT> wr[R][TN];
     GroupOps go[TN], gn[TN];
     half8_t a[2][TM], b[2][TN];
     ld.begin(0);
 #pragma unroll
-    for (int u = 0; u < ld.W_OPS; ++u) ld.op(u, wc, 0, 0);
+    for (int u = 0; u < ld.W_OPS; ++u) ld.op(u, wr[0], 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     ld.scale_chunk(0, T::S_OFF);
 #pragma unroll
-    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wc, 0, 0);
+    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wr[0], 0, 0);
 #pragma unroll
-    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wc, 1, T::XBUF);
-    wait_vm<XI>();
+    for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wr[0], min(1, steps - 1), T::XBUF);
+#pragma unroll
+    for (int s = 1; s < T::PF; ++s) {
+        ld.begin(min(s, steps - 1));
+#pragma unroll
+        for (int u = 0; u < ld.W_OPS; ++u) ld.op(u, wr[s], 0, 0);
+#pragma unroll
+        for (int u = ld.W_OPS; u < ld.OPS; ++u) ld.op(u, wr[s], min(s + 1, steps - 1), (s + 1) * T::XBUF);
+    }
+    // x step 0 (and scale chunk 0) landed: at most x step 1 and the PF - 1 later (W, x) pairs in flight
+    wait_vm<XI + (T::PF - 1) * (T::W_OPS + XI)>();
     step_barrier();
-    ld.read_scales(wc, 0, T::S_OFF, lane);
+    ld.read_scales(wr[0], 0, T::S_OFF, lane);
     const DeqConst dk = DeqConst::make();
 #pragma unroll
     for (int i = 0; i < TM; ++i) a[0][i] = *(const half8_t*)(smem + aoff[0] + i * 32 * XROW);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        go[j] = group_ops<FMT>(wc[j], dk);
-        b[0][j] = b_frag<FMT>(wc[j], go[j], 0);
+        go[j] = group_ops<FMT>(wr[0][j], dk);
+        b[0][j] = b_frag<FMT>(wr[0][j], go[j], 0);
     }
 
-    // Step t multiplies x step t (LDS buffer b0) by W step t (wc); b1 holds x step t + 1, b2 the buffer
-    // of step t - 1, refilled with x step t + 2 once every wave is past the barrier of step t. Loads
-    // past the end are clamped, and the operands prepared for step `steps` are not used.
-    uint32_t b0 = 0, b1 = T::XBUF, b2 = 2 * T::XBUF;
+    // Step t multiplies x step t (LDS buffer xq) by W step t (ring slot t mod R); it loads W step
+    // t + PF into slot (t + PF) mod R and, once every wave is past its barrier, x step t + PF + 1 into
+    // the buffer of step t - 1. The loop body runs R steps so that the ring slots are fixed registers.
+    // Loads past the end are clamped, and the operands prepared for step `steps` are not used.
     const int nchunks = (steps + 3) / 4;
+    uint32_t xq = 0;
     int t = 0;
     do {     // steps >= 2: no loop guard for the prologue loads to sink past
-        ld.begin(min(t + 1, steps - 1));
-        const int v = t >> 2;
-        mma_step<FMT, T>(smem, aoff, b0, b1, wc, go, a, b, acc, ld, wn_, gn, t, min(t + 2, steps - 1), b2,
-                         (t & 3) == 0, min(v + 1, nchunks - 1), T::S_OFF + ((v + 1) & 1) * T::SBUF,
-                         T::S_OFF + (((t + 1) >> 2) & 1) * T::SBUF, lane);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            wc[j] = wn_[j];
-            go[j] = gn[j];
+        for (int r = 0; r < R; ++r) {
+            ld.begin(min(t + T::PF, steps - 1));
+            const int v = t >> 2;
+            const uint32_t x1 = xq + 1 == (uint32_t)T::XQ ? 0u : xq + 1;     // buffer of step t + 1
+            const uint32_t xf = xq == 0 ? (uint32_t)T::XQ - 1 : xq - 1;       // buffer of step t - 1
+            mma_step<FMT, T>(smem, aoff, xq * T::XBUF, x1 * T::XBUF, wr[r], go, a, b, acc, ld, wr[(r + 1) % R],
+                             wr[(r + T::PF) % R], gn, t, min(t + T::PF + 1, steps - 1), xf * T::XBUF,
+                             (t & 3) == 0, min(v + 1, nchunks - 1), T::S_OFF + ((v + 1) & 1) * T::SBUF,
+                             T::S_OFF + (((t + 1) >> 2) & 1) * T::SBUF, lane);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) go[j] = gn[j];
+            xq = x1;
+            ++t;
+            // steps is even, so a two-step body never stops half way
+            if (R > 2 && r + 1 < R && t >= steps) break;
         }
-        const uint32_t bt = b0; b0 = b1; b1 = b2; b2 = bt;
-        ++t;
     } while (t < steps);
-    // the clamped loads of the last two steps may still be writing LDS, which the epilogue reuses
+    // the clamped loads of the last steps may still be writing LDS, which the epilogue reuses
     wait_vm<0>();
     lds_barrier();
 
@@ -680,16 +714,19 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 
 // Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN, 256 threads = 4 waves) and
 // brik_gemm_<fmt>_<BM>x<TN>w8 (BM x 256 TN, 512 threads = 8 waves); the runtime picks the tile.
-#define BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, NW_, SUFFIX)                                                    \
+#define BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, NW_, PF_, SUFFIX)                                               \
     extern "C" __global__ __launch_bounds__(64 * NW_) void brik_gemm_##FMTN##_##BM_##x##TN_##SUFFIX(      \
         const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
         float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E)               \
     {                                                                                                     \
-        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E);      \
+        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
     }
-#define BRIK_GEMM(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, )
-#define BRIK_GEMM8(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, w8)
+#define BRIK_GEMM(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, 1, )
+#define BRIK_GEMM8(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, 1, w8)
+// prefetching tiles: brik_gemm_<fmt>_<BM>x<TN>[w8]p<PF>
+#define BRIK_GEMMP(FMTN, FMT, BM_, TN_, PF_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, PF_, p##PF_)
+#define BRIK_GEMM8P(FMTN, FMT, BM_, TN_, PF_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, PF_, w8p##PF_)
 
 // Tiles in the order of the runtime's table: (BM, TN[, 8 waves]).
 #define BRIK_GEMM_FMT(FMTN, FMT)                                                       \
@@ -698,7 +735,9 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     BRIK_GEMM(FMTN, FMT, 32, 2) BRIK_GEMM(FMTN, FMT, 32, 1) BRIK_GEMM(FMTN, FMT, 32, 3)    \
     BRIK_GEMM(FMTN, FMT, 96, 2) BRIK_GEMM(FMTN, FMT, 96, 1) BRIK_GEMM(FMTN, FMT, 96, 3)    \
     BRIK_GEMM8(FMTN, FMT, 128, 1) BRIK_GEMM8(FMTN, FMT, 96, 1) BRIK_GEMM8(FMTN, FMT, 64, 1) \
-    BRIK_GEMM8(FMTN, FMT, 32, 1) BRIK_GEMM8(FMTN, FMT, 64, 2)
+    BRIK_GEMM8(FMTN, FMT, 32, 1) BRIK_GEMM8(FMTN, FMT, 64, 2)                              \
+    BRIK_GEMM8P(FMTN, FMT, 32, 1, 4) BRIK_GEMM8P(FMTN, FMT, 64, 1, 3) BRIK_GEMMP(FMTN, FMT, 32, 1, 4) \
+    BRIK_GEMMP(FMTN, FMT, 64, 1, 3) BRIK_GEMM8P(FMTN, FMT, 32, 1, 2) BRIK_GEMM8P(FMTN, FMT, 64, 1, 2)
 
 BRIK_GEMM_FMT(q4, FMT_Q4)
 BRIK_GEMM_FMT(q8, FMT_Q8)

@@ -292,8 +292,14 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
                                     1 128x256, 2 128x128, 3 128x384, 4 64x256, 5 64x128, 6 64x384,
                                     7 32x256, 8 32x128, 9 32x384, 10 96x256, 11 96x128, 12 96x384
                                     (4 waves); 13 128x256, 14 96x256, 15 64x256, 16 32x256,
-                                    17 64x512 (8 waves) */
-#define BRIK_GEMM_TILES 17
+                                    17 64x512 (8 waves); with W prefetched P steps ahead: 18 32x256 P4,
+                                    19 64x256 P3 (8 waves), 20 32x128 P4, 21 64x128 P3 (4 waves),
+                                    22 32x256 P2, 23 64x256 P2 (8 waves) */
+#define BRIK_GEMM_TILES 23
+#define BRIK_OPT_PLAN_STAGE 4    /* grouped GEMV plans created from now on: 0 auto, 1 stage x in every block,
+                                    2 stage each distinct input once per run (a staging launch) */
+#define BRIK_OPT_PLAN_SETS 5     /* grouped GEMV plans created from now on: 0 auto, else row sets per block
+                                    (capped by the LDS the lane partials may use) */
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus

@@ -155,20 +155,41 @@ def test_gemv_variants(gpu, fmt, variant):
     ("q4", 2, 2560, 1024), ("q4", 5, 128, 6), ("q4", 17, 96, 65), ("q8", 3, 64, 130), ("q3", 65, 160, 33),
 ])
 def test_gemm_parity(gpu, fmt, M, K, N):
+    """The automatic choice (small M may take the GEMV, see test_small_m_routing) and the forced MFMA
+    GEMM, each against the oracle."""
     t = synth.tensor(fmt, 31 + M, N, K)
     x = synth.normal(32 + M, M * K)
     planes = gpu.planes(fmt, t)
-    y = gpu.matmul(fmt, x, planes, M, K, N)
     r, den = oracle_mm(fmt, x, t, M, K, N)
+    check(gpu.matmul(fmt, x, planes, M, K, N), r, den, REL_TOL)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
+    check(gpu.matmul(fmt, x, planes, M, K, N), r, den, REL_TOL)
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 8, 15, 16, 32])
+@pytest.mark.parametrize("K,N", [(2560, 4096), (2560, 9728), (9728, 2560), (2560, 1024)])
+def test_small_m_routing(gpu, M, K, N):
+    """Small M at the Qwen3-4B shapes, on whichever path the runtime picks (the GEMV re-streaming W per
+    row, or the MFMA GEMM): held to the GEMM's 1e-3 bar, and to the GEMV's 1e-5 when the result is
+    that accurate (the GEMV path)."""
+    t = synth.q4_tensor(700 + M, N, K)
+    x = synth.normal(701 + M, M * K)
+    planes = gpu.planes("q4", t)
+    y = gpu.matmul("q4", x, planes, M, K, N)
+    r, den = oracle_mm("q4", x, t, M, K, N)
     check(y, r, den, REL_TOL)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 1)
+    check(gpu.matmul("q4", x, planes, M, K, N), r, den, GEMV_TOL)
 
 
+@pytest.mark.parametrize("K", [96, 1056])
 @pytest.mark.parametrize("tile", range(1, BRIK_GEMM_TILES + 1))
 @pytest.mark.parametrize("fmt", ["q8", "q4", "q3"])
-def test_gemm_every_tile(gpu, fmt, tile):
+def test_gemm_every_tile(gpu, fmt, tile, K):
     # ragged in M and N (partial row and column tiles), 9 column tiles of 128: one full XCD-ordered
-    # group of 8 plus the row-major remainder
-    M, K, N = 130, 96, 1100
+    # group of 8 plus the row-major remainder; K = 96 is the shortest pipeline (2 steps), K = 1056 runs
+    # 10 steps, which is not a multiple of the W register ring of the prefetching tiles (3 to 5 slots)
+    M, N = 130, 1100
     t = synth.tensor(fmt, 35, N, K)
     x = synth.normal(36, M * K)
     planes = gpu.planes(fmt, t)
@@ -208,6 +229,25 @@ def test_moe_e64(gpu, which):
     planes = gpu.planes("q4", t)
     xb, rb = gpu.up(np.ascontiguousarray(x)), gpu.up(row_off)
     yb = gpu.up(np.zeros(R * N, np.float32))
+    gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
+    y = gpu.ctx.download(yb, np.float32, R * N)
+    r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
+    assert normwise_rel(y, r) <= REL_TOL
+
+
+@pytest.mark.parametrize("tile", range(0, BRIK_GEMM_TILES + 1))
+def test_moe_every_tile(gpu, tile):
+    """Every tile on an expert-grouped launch with uneven experts (one of 0 rows, some above 64) and a
+    K of 24 steps (the prefetching tiles' rings wrap several times)."""
+    E, K, N = 12, 1536 * 2, 160
+    row_off = np.array([0, 3, 3, 40, 110, 111, 150, 230, 250, 251, 300, 330, 332], np.int32)
+    R = int(row_off[-1])
+    t = synth.q4_tensor(92, E * N, K)
+    x = synth.normal(93, R * K)
+    planes = gpu.planes("q4", t)
+    gpu.ctx.set_option(BRIK_OPT_GEMM_TILE, tile)
+    xb, rb = gpu.up(x), gpu.up(row_off)
+    yb = gpu.up(np.full(R * N, np.nan, np.float32))
     gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
     y = gpu.ctx.download(yb, np.float32, R * N)
     r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)

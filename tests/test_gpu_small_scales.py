@@ -49,6 +49,7 @@ def oracle_mm(fmt, x, t, M):
 def test_gemm_tiny_scales(gpu, fmt, M, K, N):
     t = tiny_tensor(fmt, 810 + M, N, K)
     x = synth.normal(811 + M, M * K)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)          # the MFMA GEMM
     y = gpu.matmul(fmt, x, gpu.planes(fmt, t), M, K, N)
     r, den = oracle_mm(fmt, x, t, M)
     check(y, r, den)
@@ -74,6 +75,7 @@ def test_gemm_zero_scales(gpu):
     sc[::3] = 0
     t = dict(t, sc=sc)
     x = synth.normal(831, M * K)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
     y = gpu.matmul("q4", x, gpu.planes("q4", t), M, K, N)
     r, den = oracle_mm("q4", x, t, M)
     check(y, r, den)
@@ -97,6 +99,7 @@ def test_gemm_on_gpu_encoded_small_weights(gpu):
     s = t["sc"].view(np.float16).astype(np.float32)
     assert (s < 2.0 ** -10).mean() > 0.1
     x = synth.normal(841, M * K)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
     y = gpu.matmul("q4", x, planes, M, K, N)
     r, den = oracle_mm("q4", x, t, M)
     check(y, r, den)
