@@ -41,7 +41,7 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
-from brimkern_amd.capi import BRIK_OPT_PATH, PATH_AUTO, PATH_GEMV, PATH_GEMM  # noqa: E402
+from brimkern_amd.capi import BRIK_OPT_PATH, BRIK_OPT_SPLITK, PATH_AUTO, PATH_GEMV, PATH_GEMM  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16
@@ -167,11 +167,14 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
                                        "copies": count}
         for M in SMALL_M:
             row = {}
-            for label, path in (("auto", PATH_AUTO), ("gemv", PATH_GEMV), ("gemm", PATH_GEMM)):
+            for label, path, sk in (("auto", PATH_AUTO, 0), ("gemv", PATH_GEMV, 0), ("tiled", PATH_GEMM, 1),
+                                    ("splitk", PATH_GEMM, 2)):
                 ctx.set_option(BRIK_OPT_PATH, path)
+                ctx.set_option(BRIK_OPT_SPLITK, sk)
                 ms_m = time_loop(ctx, lambda i, M=M: one(i, M), count, count // 4)
                 row[label + "_us"] = round(ms_m * 1e3, 2)
             ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
+            ctx.set_option(BRIK_OPT_SPLITK, 0)
             row["weight_GBps"] = round(tb / (row["auto_us"] * 1e-6) / 1e9, 1)
             small_m.setdefault(f"M{M}", {})[f"{name}_K{K}_N{N}"] = row
         if extra is not reps[name]:
@@ -557,9 +560,9 @@ def main():
     value = nbytes / (ms * 1e-3) / 1e9
     extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused,
              "small_m_qwen3_4b": dict(small_m, note="matmul_t_q4 at M rows per call (the reference's "
-                                      "matmul_t_q4_tiled range, 2 <= M < 16, plus M = 15): the routed path (auto), "
-                                      "the GEMV re-streaming W per row and the MFMA GEMM; weight_GBps = W bytes "
-                                      "(read once) / auto time")}
+                                      "matmul_t_q4_tiled range 2 <= M < 16): the routed path (auto), the GEMV "
+                                      "re-streaming W per row, the tiled MFMA GEMM and the split-K MFMA GEMM; "
+                                      "weight_GBps = W bytes (read once) / auto time")}
     if not args.no_extra:
         log("bench: cfg1 q8 GEMV")
         extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)

@@ -33,6 +33,7 @@ enum Kern {
     K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT,
     K_GEMV_F16W_V8, K_GEMV_F16W_V4, K_GEMM_F16W,
     K_GEMV_STAGE_Q8, K_GEMV_STAGE_Q4, K_GEMV_STAGE_Q3, K_GEMV_STAGE1_Q4, K_GEMV_STAGE1_Q3,
+    K_SPLITK_REDUCE,
     K_COUNT
 };
 
@@ -45,6 +46,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_conv2d_direct_q8", "brik_conv2d_direct_q4", "brik_xprep_im2col_f16", "brik_conv_out",
     "brik_gemv_f16w_v8", "brik_gemv_f16w_v4", "brik_gemm_f16w",
     "brik_gemv_stage_q8", "brik_gemv_stage_q4", "brik_gemv_stage_q3", "brik_gemv_stage1_q4", "brik_gemv_stage1_q3",
+    "brik_splitk_reduce",
 };
 
 // GEMV variants {team, r, u, d}, in the order of BRIK_GEMV_FMT in gemv.hip: TEAM lanes per row team,
@@ -136,6 +138,7 @@ struct brik_ctx {
     hipFunction_t gemv[3][kNumGemvVariants] = {};
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
     hipFunction_t gemm[3][kNumGemmTiles] = {};
+    hipFunction_t gemm_sk[3][3] = {};      // split-K few-row kernels, KSL = 2, 4, 8
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
     int opt_path = 0;
@@ -143,6 +146,7 @@ struct brik_ctx {
     int opt_tile = 0;      // 0 auto, else 1 + index into kGemmTiles
     int opt_plan_stage = 0;  // plans: 0 auto, 1 in-block staging, 2 staging launch
     int opt_plan_sets = 0;   // plans: 0 auto, else row sets per block
+    int opt_splitk = 0;      // few-row GEMMs: 0 auto, 1 never split-K, 2 split-K whenever it applies
     void* ws = nullptr;    // GEMM workspace: f16 activation rows, then per-row scales (grow-only)
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
@@ -151,6 +155,9 @@ struct brik_ctx {
     size_t sws_bytes = 0;
     void* cws = nullptr;   // convolution workspace: the [pixels, Cout] GEMM output (grow-only)
     size_t cws_bytes = 0;
+    void* pws = nullptr;   // split-K partial tiles [slice][row][column] f32 (grow-only)
+    size_t pws_bytes = 0;
+
     // the device's fixed scratch array (brik_scratch.hip), resolved at creation; scratch_err holds the
     // hipError_t of a failed resolution, which only the no-allocation entry point reports
     void* scratch = nullptr;
@@ -346,10 +353,100 @@ int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*&
     return BRIK_OK;
 }
 
+// M >= 2 (dense): the cheapest of three paths by a cost model fitted on the Qwen3-4B q4 shapes at
+// M = 2..64 (us per call, launches included):
+// GEMV (grid.y = M: every activation row streams W again, rows after the first mostly from the 256 MB
+// last-level cache): 5 + M * W bytes / 7.5 TB/s (q3: 4.5, bound by its unpacking).
+// Tiled GEMM: 5 + max(0.65 us per 128-deep K step, which is what its few-row tiles spend in issue
+// latency on one wave per SIMD, 2MNK at 1 PFLOP/s).
+// Split-K (few rows, below): ~9 us of launches (x staging, the kernel, the slice sum), 0.15 us per K step,
+// W at about 2.5 TB/s and 0.15 us per row, fitted on the same shapes at M = 2..64; it beats the tiled GEMM
+// at every such point (e.g. M = 32, K = 9728, N = 2560: 30 us against 94), and the GEMV for M >= 8-16
+// except on small matrices (N = 1024 up to M ~ 32). The tiled GEMM keeps M > 64.
+enum SmallMPath { SM_GEMV, SM_SPLITK, SM_TILED };
+constexpr long kSplitKMaxRows = 64;
+
+SmallMPath small_m_path(Fmt f, long M, long K, long N)
+{
+    const double nk = (double)N * K;
+    const double wbytes = f == F_Q4 ? nk * (0.5 + 4.0 / kGroup) : f == F_Q8 ? nk * (1.0 + 2.0 / kGroup)
+                                                                            : nk * (0.375 + 4.0 / kGroup);
+    const double steps = (double)((K + 2 * 128 - 1) / (2 * 128) * 2);
+    const double gemv_us = 5.0 + (double)M * wbytes / (f == F_Q3 ? 4.5e6 : 7.5e6);
+    const double tiled_us = 5.0 + std::max(0.65 * steps, 2.0 * M * nk / 1e9);
+    const double sk_us = M <= kSplitKMaxRows ? 9.0 + 0.15 * steps + wbytes / 2.5e6 + 0.15 * M : 1e30;
+    if (gemv_us <= sk_us && gemv_us <= tiled_us) return SM_GEMV;
+    return sk_us <= tiled_us ? SM_SPLITK : SM_TILED;
+}
+
+bool gemv_cheaper(Fmt f, long M, long K, long N) { return small_m_path(f, M, K, N) == SM_GEMV; }
+
+// Split-K few-row kernel (brik_gemm_sk_<fmt>_k<KSL>): 32 x 128 tiles, each over K slices of at most
+// KSL steps of 128. The slices are sized so the launch has about 1024 blocks (four per CU): the largest
+// KSL of {8, 4, 2} that still gives that many, then as many slices as the K steps need.
+constexpr int kSkTarget = 1024;
+struct SplitK {
+    int k;               // index of KSL in {2, 4, 8}
+    unsigned gx, gy, gz;
+};
+
+SplitK splitk_shape(long rows, int K, int N, int E)
+{
+    const long steps = (K + 255) / 256 * 2;
+    SplitK p;
+    p.gx = (unsigned)((N + 127) / 128);
+    p.gy = (unsigned)((rows + 31) / 32 + E);
+    const long tiles = (long)p.gx * p.gy;
+    const long want = (kSkTarget + tiles - 1) / tiles;           // slices wanted
+    p.k = 0;
+    for (int k = 2; k >= 0; --k)
+        if ((steps + (2 << k) - 1) / (2 << k) >= want || k == 0) { p.k = k; break; }
+    p.gz = (unsigned)((steps + (2 << p.k) - 1) / (2 << p.k));
+    return p;
+}
+
+// Whether a GEMM takes the split-K kernel: dense launches of few rows where the cost model above prefers
+// it, unless a tile is forced, the no-allocation entry point runs it (no workspace) or the option says
+// so. Expert-grouped launches keep the tiled kernel: on the 64-expert layer (20-50 rows per expert)
+// split-K measured slower (gate 62 us against 42, down 50 against 35: experts past 32 rows read their
+// weights twice, and the two-slice gate adds the slice sum).
+bool use_splitk(const brik_ctx* c, Fmt f, long rows, int K, int N, int E, const Scratch* fixed)
+{
+    if (fixed || c->opt_tile > 0 || c->opt_splitk == 1) return false;
+    if (c->opt_splitk == 2) return true;
+    return E == 0 && rows <= kSplitKMaxRows && small_m_path(f, rows, K, N) == SM_SPLITK;
+}
+
+int gemm_splitk(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
+                const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E)
+{
+    const SplitK p = splitk_shape(rows, K, N, E);
+    float* part = nullptr;
+    if (p.gz > 1) {
+        void* pw = nullptr;
+        HIP_TRY_RC(take_scratch(c, nullptr, c->pws, c->pws_bytes, (size_t)p.gz * rows * N * 4, pw));
+        part = static_cast<float*>(pw);
+    }
+    int Mi = rows, Ki = K, Ni = N, Ei = E;
+    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &part};
+    hipFunction_t fn = c->gemm_sk[fmt_index(f)][p.k];
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipModuleLaunchKernel(fn, p.gx, p.gy, p.gz, 256, 1, 1, 0, c->stream, args, nullptr));
+    if (p.gz == 1) return BRIK_OK;
+    // the slices' partial tiles, summed in slice order
+    size_t n = (size_t)rows * N;
+    int ks = (int)p.gz;
+    const size_t blocks = ((n + 3) / 4 + 255) / 256;
+    void* rargs[] = {&part, &y, &n, &ks};
+    return launch(c, K_SPLITK_REDUCE, (unsigned)(blocks < 2048 ? blocks : 2048), 1, 256, 0, rargs);
+}
+
 // The tile kernel over staged rows: dense when row_off is null, expert-grouped otherwise.
 int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
-             const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E)
+             const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E,
+             const Scratch* fixed = nullptr)
 {
+    if (use_splitk(c, f, rows, K, N, E, fixed)) return gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E);
     int Mi = rows, Ki = K, Ni = N, Ei = E;
     const int t = gemm_tile(c, rows, N, K, E);
     const GemmTile& gt = kGemmTiles[t];
@@ -378,7 +475,7 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
         HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
     }
-    return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E);
+    return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed);
 }
 
 // GEMV variant for a launch over `rows` rows in total (one matrix or a plan's jobs) with shortest row
@@ -413,22 +510,6 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
 
-// M >= 2: whether the GEMV (grid.y = M: every activation row streams W again, rows after the first
-// mostly from the 256 MB last-level cache) is expected to beat the MFMA GEMM. Cost model fitted on the
-// Qwen3-4B q4 shapes at M = 2..64 (time above the launch cost, us): GEMV ~ M * W bytes / 7.5 TB/s
-// (q3: 4.5, bound by its unpacking); GEMM ~ max(0.65 us per 128-deep K step, which is what its few-row
-// tiles spend in issue latency on one wave per SIMD, 2MNK at 1 PFLOP/s). Measured crossovers: K = 2560,
-// N = 4096 at M ~ 15; N = 9728 at M ~ 7; N = 1024 past M = 32; K = 9728, N = 2560 at M ~ 20-30.
-bool gemv_cheaper(Fmt f, long M, long K, long N)
-{
-    const double nk = (double)N * K;
-    const double wbytes = f == F_Q4 ? nk * (0.5 + 4.0 / kGroup) : f == F_Q8 ? nk * (1.0 + 2.0 / kGroup)
-                                                                            : nk * (0.375 + 4.0 / kGroup);
-    const double gemv_us = (double)M * wbytes / (f == F_Q3 ? 4.5e6 : 7.5e6);
-    const double steps = (double)((K + 2 * 128 - 1) / (2 * 128) * 2);
-    const double gemm_us = std::max(0.65 * steps, 2.0 * M * nk / 1e9);
-    return gemv_us < gemm_us;
-}
 
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr)
@@ -599,6 +680,13 @@ int brik_create(int device, brik_ctx** out)
         }
     // the fixed scratch of brik_matmul_t_q4_noalloc, with this device current (once per device)
     c->scratch_err = brik_scratch_resolve(device, &c->scratch, &c->scratch_bytes);
+    constexpr int kSkl[3] = {2, 4, 8};
+    for (int f = 0; f < 3; ++f)
+        for (int k = 0; k < 3; ++k) {
+            char name[64];
+            snprintf(name, sizeof name, "brik_gemm_sk_%s_k%d", kFmtNames[f], kSkl[k]);
+            if (hipModuleGetFunction(&c->gemm_sk[f][k], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+        }
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return bail(BRIK_EHIP);
     if (hipEventCreate(&c->ev_begin) != hipSuccess || hipEventCreate(&c->ev_end) != hipSuccess)
         return bail(BRIK_EHIP);
@@ -619,6 +707,7 @@ void brik_destroy(brik_ctx* c)
     if (c->tws) (void)hipFree(c->tws);
     if (c->sws) (void)hipFree(c->sws);
     if (c->cws) (void)hipFree(c->cws);
+    if (c->pws) (void)hipFree(c->pws);
     if (c->module) (void)hipModuleUnload(c->module);
     delete c;
 }
@@ -1221,6 +1310,10 @@ int brik_set_option(brik_ctx* c, int key, int value)
     case BRIK_OPT_PLAN_STAGE:
         if (value < 0 || value > 2) return fail(c, BRIK_EINVAL, "BRIK_OPT_PLAN_STAGE: %d not in 0..2", value);
         c->opt_plan_stage = value;
+        return BRIK_OK;
+    case BRIK_OPT_SPLITK:
+        if (value < 0 || value > 2) return fail(c, BRIK_EINVAL, "BRIK_OPT_SPLITK: %d not in 0..2", value);
+        c->opt_splitk = value;
         return BRIK_OK;
     case BRIK_OPT_PLAN_SETS:
         if (value < 0 || value > 64) return fail(c, BRIK_EINVAL, "BRIK_OPT_PLAN_SETS: %d not in 0..64", value);

@@ -132,6 +132,59 @@ namespace {
 constexpr int GK = 128;              // K per pipeline step: four quantization groups
 constexpr int XROW = GK * 2;         // bytes of one x row per step in LDS (16 chunks of 16 bytes)
 
+// The expert and rows of pair y of an expert-grouped launch, whose pairs are the BM-row tiles of
+// experts 0, 1, ... in order. Wave 0 reads row_off 64 experts at a time (one per lane, vector loads),
+// scans the tile counts across the wave and publishes the expert that holds pair y through LDS: a few
+// dozen instructions and one memory round trip, where walking the experts one by one costs a dependent
+// scalar load per expert. Every thread of the block calls it (it ends with a barrier). Returns false,
+// for the whole block, when y is past the last pair; offsets that decrease count as empty experts and
+// rows are clipped to M, so a malformed table cannot send stores past row M.
+template <int BM>
+__device__ __forceinline__ bool find_expert_tile(const int* __restrict__ row_off, int E, int y, int M, int& e,
+                                                 int& m0, int& m_end)
+{
+    __shared__ int res[3];
+    if (threadIdx.x < 64) {
+        const int lane = (int)threadIdx.x;
+        int carry = 0, found = -1, fm0 = 0, fend = 0;
+        for (int base = 0; base < E && found < 0; base += 64) {     // uniform across wave 0
+            const int ex = base + lane;
+            int lo = 0, hi = 0, tiles = 0;
+            if (ex < E) {
+                lo = row_off[ex];
+                hi = row_off[ex + 1];
+                tiles = hi > lo ? (hi - lo + BM - 1) / BM : 0;
+            }
+            int incl = tiles;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += v;
+            }
+            incl += carry;
+            const int excl = incl - tiles;
+            const unsigned long long own = __ballot(ex < E && y >= excl && y < incl);
+            if (own) {
+                const int src = __ffsll((long long)own) - 1;
+                found = __shfl(ex, src, 64);
+                fm0 = __shfl(lo + (y - excl) * BM, src, 64);
+                fend = __shfl(min(hi, M), src, 64);
+            }
+            carry = __shfl(incl, 63, 64);
+        }
+        if (lane == 0) {
+            res[0] = found;
+            res[1] = fm0;
+            res[2] = fend;
+        }
+    }
+    __syncthreads();
+    e = res[0];
+    m0 = res[1];
+    m_end = res[2];
+    return e >= 0 && m0 >= 0 && m0 < m_end;
+}
+
 // Block tile: BM rows x 32 TN NW columns, NW waves (4: one per SIMD, 8: two per SIMD); wave w owns
 // columns [32 TN w, 32 TN (w + 1)) of all BM rows as TM = BM / 32 row blocks x TN column blocks of
 // v_mfma_f32_32x32x16_f16, so each W element of the block is loaded and dequantized by exactly one
@@ -710,6 +763,182 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     }
 }
 
+// ---- 3. split-K GEMM for few rows ---------------------------------------------------------------
+// A launch with few rows per weight column (small M, or an expert's 20-50 routed rows) has too little
+// MFMA work to hide the dequantization behind: the tiled kernel above then runs one wave per SIMD on
+// the few blocks its tiles give, each paying the issue latency of ~150 VALU instructions per K step
+// (measured: ~0.65 us per step whatever the prefetch depth). This kernel spreads the same work over
+// many small blocks instead: a block owns 32 rows x 128 columns (4 waves, one 32-column MFMA block
+// each) over a slice of at most KSL K steps. It issues every load of its slice at once (W codes,
+// scales and mins into registers, the f16 x rows of the slice into LDS), waits once, and runs the
+// slice's MFMAs without a barrier; several blocks per CU overlap one block's loads with another's
+// arithmetic. With more than one slice (gridDim.z) every block writes its partial tile to `part`
+// ([slice][row][column] f32, already times the row scale) and brik_splitk_reduce, the next launch on
+// the stream, sums the slices in order into y: the result does not depend on which block finishes
+// first. (Summing in the last block of each tile instead, behind device-scope fences and a counter,
+// measured several times slower: every fence writes back and invalidates an XCD's L2.)
+constexpr int SK_BM = 32, SK_BN = 128;
+
+template <int FMT, int KSL>
+__device__ __forceinline__ void gemm_sk_body(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
+                                             const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
+                                             const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
+                                             float* __restrict__ y, int M, int K, int N,
+                                             const int* __restrict__ row_off, int E, float* __restrict__ part)
+{
+    constexpr int SBUF = SK_BM * XROW;                   // one step of x rows in LDS
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[KSL * SBUF];
+
+    const int G = K / BRIK_GROUP;
+    const int Kp = (K + 2 * GK - 1) / (2 * GK) * (2 * GK);
+    const int steps = Kp / GK;
+    const int KS = (int)gridDim.z, slice = (int)blockIdx.z;
+    const int t0 = slice * KSL;
+    const int nst = min(KSL, steps - t0);                // >= 1: the host sizes gridDim.z so
+    const int n0 = (int)blockIdx.x * SK_BN;
+    int m0, m_end = M, e = 0;
+    if (row_off) {
+        // the whole block, and the same for every slice of the tile
+        if (!find_expert_tile<SK_BM>(row_off, E, (int)blockIdx.y, M, e, m0, m_end)) return;
+    } else {
+        m0 = (int)blockIdx.y * SK_BM;
+        if (m0 >= M) return;
+    }
+
+    const size_t wel = (size_t)N * K;
+    const size_t gbase = (size_t)e * N * G;
+    const brsrc_t rx = make_rsrc(xh, (uint32_t)((size_t)M * Kp * 2));
+    brsrc_t r0, r1 = rx;
+    if constexpr (FMT == FMT_Q8) {
+        r0 = make_rsrc(p0 + (size_t)e * wel, (uint32_t)wel);
+    } else if constexpr (FMT == FMT_Q4) {
+        r0 = make_rsrc(p0 + (size_t)e * wel / 2, (uint32_t)(wel / 2));
+    } else {
+        r0 = make_rsrc(p0 + (size_t)e * wel / 4, (uint32_t)(wel / 4));
+        r1 = make_rsrc(p1 + (size_t)e * wel / 8, (uint32_t)(wel / 8));
+    }
+    const uint32_t sgroups = (uint32_t)((size_t)(row_off ? E : 1) * N * G);
+    const brsrc_t rsc = make_rsrc(sc, sgroups * 2);
+    const brsrc_t rmn = FMT == FMT_Q8 ? rsc : make_rsrc(mn, sgroups * 2);
+
+    const int tid = (int)threadIdx.x, lane = tid & 63, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ncol = n0 + wave * 32 + (lane & 31);        // this lane's column (D layout and B operand)
+    const uint32_t colg = (uint32_t)(min(ncol, N - 1) * G);
+    const uint32_t sgb = (uint32_t)gbase + colg;
+
+    // every load of the slice: W codes, scales and mins of each step (lane half h holds groups
+    // 4t + 2h and 4t + 2h + 1 of its column), then the x rows of each step into LDS
+    WCodes<FMT> wr[KSL];
+    uint32_t gs[KSL];                                    // first group of the lane's pair, per step
+#pragma unroll
+    for (int t = 0; t < KSL; ++t) {
+        const int g0 = 4 * min(t0 + t, steps - 1) + 2 * h;
+        gs[t] = (uint32_t)g0;
+        const uint32_t ga = colg + (uint32_t)min(g0, G - 1), gb = colg + (uint32_t)min(g0 + 1, G - 1);
+        WCodes<FMT>& f = wr[t];
+        if constexpr (FMT == FMT_Q4) {
+            const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(r0, ga * 16, 0, 0);
+            const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(r0, gb * 16, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { f.w[j] = a[j]; f.w[4 + j] = b[j]; }
+        } else if constexpr (FMT == FMT_Q8) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r0, (k >> 1 ? gb : ga) * 32 + 16 * (k & 1), 0, 0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) f.w[4 * k + j] = v[j];
+            }
+        } else {
+            const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(r0, ga * 8, 0, 0);
+            const u32x2_t b = __builtin_amdgcn_raw_buffer_load_b64(r0, gb * 8, 0, 0);
+            f.w[0] = a.x; f.w[1] = a.y; f.w[2] = b.x; f.w[3] = b.y;
+            f.w[4] = __builtin_amdgcn_raw_buffer_load_b32(r1, ga * 4, 0, 0);
+            f.w[5] = __builtin_amdgcn_raw_buffer_load_b32(r1, gb * 4, 0, 0);
+        }
+        const uint32_t sa = sgb + (uint32_t)min(g0, G - 1), sb = sgb + (uint32_t)min(g0 + 1, G - 1);
+        f.s[0] = __builtin_amdgcn_raw_buffer_load_b16(rsc, sa * 2, 0, 0);
+        f.s[1] = __builtin_amdgcn_raw_buffer_load_b16(rsc, sb * 2, 0, 0);
+        if constexpr (FMT != FMT_Q8) {
+            f.m[0] = __builtin_amdgcn_raw_buffer_load_b16(rmn, sa * 2, 0, 0);
+            f.m[1] = __builtin_amdgcn_raw_buffer_load_b16(rmn, sb * 2, 0, 0);
+        } else {
+            f.m[0] = f.m[1] = 0u;
+        }
+    }
+    // x: step t of the slice fills LDS bytes [t SBUF, (t + 1) SBUF), 32 rows x 256 bytes, as eight
+    // 1 KiB direct loads (16 bytes per lane: row 4 i + (lane >> 4), stored chunk lane & 15, which holds
+    // logical chunk (lane & 15) ^ (row & 15)); wave w issues i = w and w + 4. Rows past the tile's end
+    // repeat a live row.
+#pragma unroll
+    for (int t = 0; t < KSL; ++t) {
+        const int tt = min(t0 + t, steps - 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int i = 4 * j + wave;
+            const int r = 4 * i + (lane >> 4);
+            const int m = min(m0 + r, m_end - 1);
+            const uint32_t off = (uint32_t)((size_t)m * Kp + (size_t)tt * GK + (((lane & 15) ^ (r & 15)) * 8)) * 2;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(smem + t * SBUF + i * 1024), 16, off, 0, 0, 0);
+        }
+    }
+    // every load above stays ahead of the wait: the loaded registers are consumed here (an empty asm),
+    // so no load can be sunk down to the step that uses it (each step would then pay a memory round
+    // trip), not even into the steps that run only when the slice is that long
+#pragma unroll
+    for (int t = 0; t < KSL; ++t) {
+#pragma unroll
+        for (int j = 0; j < (int)(sizeof(wr[t].w) / 4); ++j) asm volatile("" ::"v"(wr[t].w[j]));
+        asm volatile("" ::"v"(wr[t].s[0]), "v"(wr[t].s[1]), "v"(wr[t].m[0]), "v"(wr[t].m[1]));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vm<0>();
+    step_barrier();
+
+    uint32_t aoff[8];
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) aoff[sl] = (uint32_t)((lane & 31) * XROW + (((8 * h + sl) ^ (lane & 15)) * 16));
+    const DeqConst dk = DeqConst::make();
+    floatx16_t acc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[q][r] = 0.f;
+#pragma unroll
+    for (int t = 0; t < KSL; ++t) {
+        if (t >= nst) break;                             // uniform: the last slice may be shorter
+        // groups past the row end: scale and min 0 (their x is zero padding as well)
+        WCodes<FMT> f = wr[t];
+        const bool la = (int)gs[t] < G, lb = (int)gs[t] + 1 < G;
+        f.s[0] = la ? f.s[0] : 0u; f.s[1] = lb ? f.s[1] : 0u;
+        f.m[0] = la ? f.m[0] : 0u; f.m[1] = lb ? f.m[1] : 0u;
+        const GroupOps go = group_ops<FMT>(f, dk);
+#pragma unroll
+        for (int sl = 0; sl < 8; ++sl) {
+            const half8_t a = *(const half8_t*)(smem + t * SBUF + aoff[sl]);
+            const half8_t b = b_frag<FMT>(f, go, sl);
+            acc[sl & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[sl & 1], 0, 0, 0);
+        }
+    }
+
+    // D layout of a 32x32 tile: lane holds column lane & 31, register r row 8 (r >> 2) + 4 h + (r & 3)
+    const bool colok = ncol < N;
+    if (KS == 1) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (colok && m < m_end) y[(size_t)m * N + ncol] = (acc[0][r] + acc[1][r]) * rscale[m];
+        }
+        return;
+    }
+    float* const P = part + (size_t)slice * M * N;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (colok && m < m_end) P[(size_t)m * N + ncol] = (acc[0][r] + acc[1][r]) * rscale[m];
+    }
+}
+
 }  // namespace
 
 // Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN, 256 threads = 4 waves) and
@@ -742,3 +971,40 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
 BRIK_GEMM_FMT(q4, FMT_Q4)
 BRIK_GEMM_FMT(q8, FMT_Q8)
 BRIK_GEMM_FMT(q3, FMT_Q3)
+
+// Split-K few-row kernels: brik_gemm_sk_<fmt>_k<KSL> (32 x 128 tiles, 256 threads, K slices of at most
+// KSL steps of 128); grid (column tiles, row tiles or expert row-tile pairs, slices).
+#define BRIK_GEMM_SK(FMTN, FMT, KSL_)                                                                     \
+    extern "C" __global__ __launch_bounds__(256) void brik_gemm_sk_##FMTN##_k##KSL_(                       \
+        const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
+        const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
+        float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E,               \
+        float* __restrict__ part)                                                                         \
+    {                                                                                                     \
+        gemm_sk_body<FMT, KSL_>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E, part);                 \
+    }
+// y[i] = sum over slices q = 0 .. ks - 1, in that order, of part[q * n + i], for i < n (n = rows x N of a
+// split-K launch); float4 accesses when n % 4 == 0.
+extern "C" __global__ __launch_bounds__(256) void brik_splitk_reduce(const float* __restrict__ part,
+                                                                    float* __restrict__ y, size_t n, int ks)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if ((n & 3) == 0) {
+        const size_t n4 = n / 4;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+            f32x4_t v = *(const f32x4_t*)(part + 4 * i);
+            for (int q = 1; q < ks; ++q) v = v + *(const f32x4_t*)(part + (size_t)q * n + 4 * i);
+            *(f32x4_t*)(y + 4 * i) = v;
+        }
+        return;
+    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float v = part[i];
+        for (int q = 1; q < ks; ++q) v += part[(size_t)q * n + i];
+        y[i] = v;
+    }
+}
+
+BRIK_GEMM_SK(q4, FMT_Q4, 2) BRIK_GEMM_SK(q4, FMT_Q4, 4) BRIK_GEMM_SK(q4, FMT_Q4, 8)
+BRIK_GEMM_SK(q8, FMT_Q8, 2) BRIK_GEMM_SK(q8, FMT_Q8, 4) BRIK_GEMM_SK(q8, FMT_Q8, 8)
+BRIK_GEMM_SK(q3, FMT_Q3, 2) BRIK_GEMM_SK(q3, FMT_Q3, 4) BRIK_GEMM_SK(q3, FMT_Q3, 8)

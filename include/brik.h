@@ -300,6 +300,8 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
                                     2 stage each distinct input once per run (a staging launch) */
 #define BRIK_OPT_PLAN_SETS 5     /* grouped GEMV plans created from now on: 0 auto, else row sets per block
                                     (capped by the LDS the lane partials may use) */
+#define BRIK_OPT_SPLITK 6        /* MFMA GEMMs of few rows (expert-grouped, or at most 64 rows): 0 auto,
+                                    1 never use the split-K kernel, 2 use it whenever no tile is forced */
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus
