@@ -15,6 +15,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libbrik.so")
 
 BRIK_OK, BRIK_EINVAL, BRIK_EALIGN, BRIK_EHIP, BRIK_ENOMEM, BRIK_ENODEV, BRIK_EMODULE = 0, -1, -2, -3, -4, -5, -6
+BRIK_EVALID = -7
 BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT = 1, 2
 BRIK_GEMV_VARIANTS = 9
 BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES = 3, 23
@@ -35,6 +36,11 @@ SIGNATURES = {
     "brik_d2h": (_I, [_P, _P, _P, _Z]),
     "brik_d2d": (_I, [_P, _P, _P, _Z]),
     "brik_sync": (_I, [_P]),
+    "brik_fence_record": (_I, [_P, ctypes.POINTER(_P)]),
+    "brik_fence_d2h": (_I, [_P, _P, _P, _Z]),
+    "brik_fence_error": (ctypes.c_char_p, [_P]),
+    "brik_fence_destroy": (None, [_P]),
+    "brik_self_validate": (_I, [_P, ctypes.c_char_p, _Z]),
     "brik_matmul_t_q8": (_I, [_P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_matmul_t_q3": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
@@ -218,6 +224,22 @@ class Context:
     def sync(self):
         self._check(self.lib.brik_sync(self.handle))
 
+    def fence(self) -> "Fence":
+        """Mark the current end of the stream (brik_fence_record)."""
+        h = _P()
+        self._check(self.lib.brik_fence_record(self.handle, ctypes.byref(h)))
+        return Fence(self, h)
+
+    def self_validate(self):
+        """The load-time kernel checks (brik_self_validate): returns None when every check passes, else
+        the name of the first failing check (BRIK_EVALID); other errors raise."""
+        buf = ctypes.create_string_buffer(64)
+        rc = self.lib.brik_self_validate(self.handle, buf, 64)
+        if rc == BRIK_EVALID:
+            return buf.value.decode()
+        self._check(rc)
+        return None
+
     def set_option(self, key: int, value: int):
         self._check(self.lib.brik_set_option(self.handle, key, value))
 
@@ -327,6 +349,26 @@ class Context:
 
     def f16_to_f32(self, src, out, n):
         self._check(self.lib.brik_f16_to_f32(self.handle, _addr(src), _addr(out), n))
+
+
+class Fence:
+    """A point on the context stream (``brik_fence``): :meth:`d2h` waits for it, then copies to host;
+    safe to call from another thread while the context keeps enqueueing."""
+
+    def __init__(self, ctx: Context, handle):
+        self.ctx, self.handle = ctx, handle
+
+    def d2h(self, src, dtype, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=dtype)
+        rc = self.ctx.lib.brik_fence_d2h(self.handle, _P(out.ctypes.data), _addr(src), out.nbytes)
+        if rc != BRIK_OK:
+            raise BrikError(rc, self.ctx.lib.brik_fence_error(self.handle).decode())
+        return out
+
+    def destroy(self):
+        if self.handle:
+            self.ctx.lib.brik_fence_destroy(self.handle)
+            self.handle = None
 
 
 class Graph:

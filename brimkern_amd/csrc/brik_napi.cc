@@ -115,14 +115,39 @@ bool get_ptr(napi_env env, napi_value v, void** out)
     return true;
 }
 
-bool get_ctx(napi_env env, napi_value v, brik_ctx** out)
+// A context as JS holds it: the library context, and the count of the JS-side objects that keep it
+// alive (the context handle itself, device buffers, plans). It is destroyed when the last one is
+// finalized, so a buffer collected after its context never frees into a destroyed context.
+struct CtxBox {
+    brik_ctx* ctx;
+    long refs;
+    long live_buffers;   // device buffers allocated through allocBuffer and not yet freed
+};
+
+void box_release(CtxBox* b)
+{
+    if (--b->refs == 0) {
+        brik_destroy(b->ctx);
+        delete b;
+    }
+}
+
+bool get_box(napi_env env, napi_value v, CtxBox** out)
 {
     void* p = nullptr;
     if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
         napi_throw_type_error(env, "BRIK_EINVAL", "expected a brik context");
         return false;
     }
-    *out = static_cast<brik_ctx*>(p);
+    *out = static_cast<CtxBox*>(p);
+    return true;
+}
+
+bool get_ctx(napi_env env, napi_value v, brik_ctx** out)
+{
+    CtxBox* b;
+    if (!get_box(env, v, &b)) return false;
+    *out = b->ctx;
     return true;
 }
 
@@ -172,7 +197,7 @@ bool get_bytes(napi_env env, napi_value v, void** data, size_t* len)
     return false;
 }
 
-void ctx_finalize(napi_env, void* data, void*) { brik_destroy(static_cast<brik_ctx*>(data)); }
+void ctx_finalize(napi_env, void* data, void*) { box_release(static_cast<CtxBox*>(data)); }
 
 // ---- context / memory ------------------------------------------------------------------------
 
@@ -193,9 +218,206 @@ napi_value CreateContext(napi_env env, napi_callback_info info)
     if (a.n >= 1 && !get_i32(env, a.v[0], &dev)) return nullptr;
     brik_ctx* ctx = nullptr;
     if (check(env, nullptr, brik_create(dev, &ctx))) return nullptr;
+    CtxBox* box = new CtxBox{ctx, 1, 0};
     napi_value ext;
-    NAPI_CALL(env, napi_create_external(env, ctx, ctx_finalize, nullptr, &ext));
+    if (napi_create_external(env, box, ctx_finalize, nullptr, &ext) != napi_ok) {
+        box_release(box);
+        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+        return nullptr;
+    }
     return ext;
+}
+
+// ---- device buffers owned by JS objects -------------------------------------------------------
+// allocBuffer(ctx, bytes) -> handle: a device allocation freed by freeBuffer(handle) or, if the handle
+// is dropped first, by its finalizer when the garbage collector reclaims it (the reference's
+// destroy()-or-GC buffer lifetime, kernels.ts:903-956). bufferPtr(handle) -> BigInt address.
+struct BufBox {
+    CtxBox* box;
+    void* ptr;
+};
+
+void buf_release(BufBox* b)
+{
+    if (b->ptr) {
+        brik_free(b->box->ctx, b->ptr);   // best effort: a finalizer has no caller to report to
+        b->ptr = nullptr;
+        --b->box->live_buffers;
+    }
+}
+
+void buf_finalize(napi_env, void* data, void*)
+{
+    BufBox* b = static_cast<BufBox*>(data);
+    buf_release(b);
+    box_release(b->box);
+    delete b;
+}
+
+bool get_buf(napi_env env, napi_value v, BufBox** out)
+{
+    void* p = nullptr;
+    if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a device buffer handle");
+        return false;
+    }
+    *out = static_cast<BufBox*>(p);
+    return true;
+}
+
+napi_value AllocBuffer(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 2)) return nullptr;
+    CtxBox* box;
+    size_t bytes;
+    if (!get_box(env, a.v[0], &box) || !get_size(env, a.v[1], &bytes)) return nullptr;
+    void* p = nullptr;
+    if (check(env, box->ctx, brik_alloc(box->ctx, bytes, &p))) return nullptr;
+    BufBox* b = new BufBox{box, p};
+    ++box->refs;
+    ++box->live_buffers;
+    napi_value ext;
+    if (napi_create_external(env, b, buf_finalize, nullptr, &ext) != napi_ok) {
+        buf_finalize(env, b, nullptr);
+        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+        return nullptr;
+    }
+    return ext;
+}
+
+napi_value BufferPtr(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    BufBox* b;
+    if (!get_buf(env, a.v[0], &b)) return nullptr;
+    return make_ptr(env, b->ptr);
+}
+
+napi_value FreeBuffer(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    BufBox* b;
+    if (!get_buf(env, a.v[0], &b)) return nullptr;
+    buf_release(b);
+    return undefined(env);
+}
+
+napi_value LiveBuffers(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    CtxBox* box;
+    if (!get_box(env, a.v[0], &box)) return nullptr;
+    napi_value r;
+    NAPI_CALL(env, napi_create_int64(env, box->live_buffers, &r));
+    return r;
+}
+
+// ---- asynchronous readback ------------------------------------------------------------------------
+// readbackAsync(ctx, src, bytes) -> Promise<ArrayBuffer>: a fence is recorded on the context stream now
+// (after everything enqueued so far, in call order), and a libuv worker waits for it and copies the
+// bytes into a new ArrayBuffer; the promise resolves on the JS thread (rejects with the error code
+// and message on failure), as the reference's mapAsync readback does.
+struct ReadbackWork {
+    napi_async_work work = nullptr;
+    napi_deferred deferred = nullptr;
+    napi_ref buffer = nullptr;
+    void* data = nullptr;
+    const void* src = nullptr;
+    size_t bytes = 0;
+    brik_fence* fence = nullptr;
+    CtxBox* box = nullptr;   // held until completion: the context (and the memory read) outlives the copy
+    int rc = BRIK_OK;
+    std::string msg;
+};
+
+void readback_execute(napi_env, void* data)
+{
+    ReadbackWork* w = static_cast<ReadbackWork*>(data);
+    w->rc = brik_fence_d2h(w->fence, w->data, w->src, w->bytes);
+    if (w->rc != BRIK_OK) w->msg = std::string(code_name(w->rc)) + ": " + brik_fence_error(w->fence);
+}
+
+void readback_complete(napi_env env, napi_status status, void* data)
+{
+    ReadbackWork* w = static_cast<ReadbackWork*>(data);
+    napi_value buf = nullptr;
+    napi_get_reference_value(env, w->buffer, &buf);
+    if (status == napi_ok && w->rc == BRIK_OK && buf) {
+        napi_resolve_deferred(env, w->deferred, buf);
+    } else {
+        const std::string code = w->rc != BRIK_OK ? code_name(w->rc) : "BRIK_NAPI";
+        const std::string msg = w->rc != BRIK_OK ? w->msg : "BRIK_NAPI: readback was cancelled";
+        napi_value c, m, err;
+        napi_create_string_utf8(env, code.c_str(), NAPI_AUTO_LENGTH, &c);
+        napi_create_string_utf8(env, msg.c_str(), NAPI_AUTO_LENGTH, &m);
+        napi_create_error(env, c, m, &err);
+        napi_reject_deferred(env, w->deferred, err);
+    }
+    napi_delete_reference(env, w->buffer);
+    napi_delete_async_work(env, w->work);
+    brik_fence_destroy(w->fence);
+    box_release(w->box);
+    delete w;
+}
+
+napi_value ReadbackAsync(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    CtxBox* box;
+    void* src;
+    size_t bytes;
+    if (!get_box(env, a.v[0], &box) || !get_ptr(env, a.v[1], &src) || !get_size(env, a.v[2], &bytes)) return nullptr;
+    brik_ctx* ctx = box->ctx;
+    ReadbackWork* w = new ReadbackWork();
+    w->src = src;
+    w->bytes = bytes;
+    if (check(env, ctx, brik_fence_record(ctx, &w->fence))) {
+        delete w;
+        return nullptr;
+    }
+    napi_value ab, promise, name;
+    if (napi_create_arraybuffer(env, bytes, &w->data, &ab) != napi_ok ||
+        napi_create_reference(env, ab, 1, &w->buffer) != napi_ok ||
+        napi_create_promise(env, &w->deferred, &promise) != napi_ok ||
+        napi_create_string_utf8(env, "brik.readback", NAPI_AUTO_LENGTH, &name) != napi_ok ||
+        napi_create_async_work(env, nullptr, name, readback_execute, readback_complete, w, &w->work) != napi_ok ||
+        napi_queue_async_work(env, w->work) != napi_ok) {
+        // nothing was queued: undo what was made (a created promise is left pending and unreachable)
+        if (w->work) napi_delete_async_work(env, w->work);
+        if (w->buffer) napi_delete_reference(env, w->buffer);
+        brik_fence_destroy(w->fence);
+        delete w;
+        napi_throw_error(env, "BRIK_NAPI", "readbackAsync: N-API setup failed");
+        return nullptr;
+    }
+    w->box = box;
+    ++box->refs;
+    return promise;
+}
+
+// selfValidate(ctx) -> null when every check passes, else the name of the first failing check
+napi_value SelfValidate(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    char stage[64];
+    const int rc = brik_self_validate(ctx, stage, sizeof stage);
+    if (rc == BRIK_EVALID) {
+        napi_value r;
+        NAPI_CALL(env, napi_create_string_utf8(env, stage, NAPI_AUTO_LENGTH, &r));
+        return r;
+    }
+    if (check(env, ctx, rc)) return nullptr;
+    napi_value n;
+    NAPI_CALL(env, napi_get_null(env, &n));
+    return n;
 }
 
 napi_value Alloc(napi_env env, napi_callback_info info)
@@ -499,14 +721,15 @@ napi_value LmHeadTopK(napi_env env, napi_callback_info info)
 // ---- grouped GEMV plans ----------------------------------------------------------------------
 
 struct PlanBox {
-    brik_ctx* ctx;
+    CtxBox* box;
     brik_gemv_plan* plan;
 };
 
 void plan_finalize(napi_env, void* data, void*)
 {
     PlanBox* b = static_cast<PlanBox*>(data);
-    if (b->plan) brik_gemv_plan_destroy(b->ctx, b->plan);
+    if (b->plan) brik_gemv_plan_destroy(b->box->ctx, b->plan);
+    box_release(b->box);
     delete b;
 }
 
@@ -516,9 +739,10 @@ napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
 {
     Args a;
     if (!get_args(env, info, a, 3)) return nullptr;
-    brik_ctx* ctx;
+    CtxBox* box;
     int32_t fmt;
-    if (!get_ctx(env, a.v[0], &ctx) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    if (!get_box(env, a.v[0], &box) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    brik_ctx* ctx = box->ctx;
     uint32_t n = 0;
     NAPI_CALL(env, napi_get_array_length(env, a.v[2], &n));
     std::vector<brik_gemv_job_ex> jobs(n);
@@ -564,8 +788,14 @@ napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
     }
     brik_gemv_plan* plan = nullptr;
     if (check(env, ctx, brik_gemv_plan_create_ex(ctx, fmt, jobs.data(), (int)n, &plan))) return nullptr;
+    PlanBox* pb = new PlanBox{box, plan};
+    ++box->refs;
     napi_value ext;
-    NAPI_CALL(env, napi_create_external(env, new PlanBox{ctx, plan}, plan_finalize, nullptr, &ext));
+    if (napi_create_external(env, pb, plan_finalize, nullptr, &ext) != napi_ok) {
+        plan_finalize(env, pb, nullptr);
+        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+        return nullptr;
+    }
     return ext;
 }
 
@@ -580,7 +810,7 @@ napi_value GemvPlanRun(napi_env env, napi_callback_info info)
     }
     PlanBox* b = static_cast<PlanBox*>(p);
     if (!b->plan) { napi_throw_error(env, "BRIK_EINVAL", "plan was destroyed"); return nullptr; }
-    if (check(env, b->ctx, brik_gemv_plan_run(b->ctx, b->plan))) return nullptr;
+    if (check(env, b->box->ctx, brik_gemv_plan_run(b->box->ctx, b->plan))) return nullptr;
     return undefined(env);
 }
 
@@ -591,7 +821,7 @@ napi_value GemvPlanDestroy(napi_env env, napi_callback_info info)
     void* p = nullptr;
     if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p) return nullptr;
     PlanBox* b = static_cast<PlanBox*>(p);
-    if (b->plan) brik_gemv_plan_destroy(b->ctx, b->plan);
+    if (b->plan) brik_gemv_plan_destroy(b->box->ctx, b->plan);
     b->plan = nullptr;
     return undefined(env);
 }
@@ -625,6 +855,12 @@ napi_value Init(napi_env env, napi_value exports)
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanRun", nullptr, GemvPlanRun, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanDestroy", nullptr, GemvPlanDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"allocBuffer", nullptr, AllocBuffer, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"bufferPtr", nullptr, BufferPtr, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"freeBuffer", nullptr, FreeBuffer, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"liveBuffers", nullptr, LiveBuffers, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"readbackAsync", nullptr, ReadbackAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"selfValidate", nullptr, SelfValidate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
     };
     napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
     return exports;

@@ -123,6 +123,12 @@ struct brik_gemv_plan {
     size_t inputs_off = 0;        // byte offset of the stage-input table in dev
 };
 
+struct brik_fence {
+    int device = -1;
+    hipEvent_t ev = nullptr;
+    char err[256] = {0};
+};
+
 struct brik_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -609,6 +615,155 @@ int lm_head_topk(brik_ctx* c, const char* who, Fmt f, const float* x, const void
     return topk_passes(c, logits, vocab, recent, n_recent, penalty, softcap, k, ids, vals, pen);
 }
 
+// ---- self-validation (brik_self_validate) --------------------------------------------------------
+// A CPU check inside the library, as the reference's engine carries one (selfValidate,
+// src/lib/webgpu/kernels.ts:2255-2459): it runs the kernels on small seeded problems, downloads the
+// planes the encoder produced and compares each result with an f64 sum over those planes' dequantized
+// values. It never computes anything a caller receives.
+
+uint64_t sv_next(uint64_t& s)
+{
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// uniform in [-1, 1), as the reference's rand() draws Math.random() * 2 - 1
+float sv_unit(uint64_t& s) { return (float)((double)(sv_next(s) >> 11) * (1.0 / 9007199254740992.0) * 2.0 - 1.0); }
+
+// IEEE half -> float (exact), for the downloaded scales and mins
+double sv_f16(uint16_t h)
+{
+    const int e = (h >> 10) & 31, m = h & 1023;
+    const double v = e == 0 ? std::ldexp((double)m, -24) : e == 31 ? (m ? NAN : INFINITY) : std::ldexp(1024.0 + m, e - 25);
+    return (h & 0x8000) ? -v : v;
+}
+
+struct SvPlanes {
+    size_t codes = 0, hi = 0, sc = 0, mn = 0, bytes = 0;   // byte offsets in one blob, and its size
+};
+
+SvPlanes sv_layout(Fmt f, size_t n)
+{
+    SvPlanes p;
+    const size_t g = n / kGroup;
+    const size_t cb = f == F_Q8 ? n : f == F_Q4 ? n / 2 : n / 4;
+    p.codes = 0;
+    p.hi = cb;
+    p.sc = cb + (f == F_Q3 ? n / 8 : 0);
+    p.mn = p.sc + 2 * g;
+    p.bytes = p.mn + (f == F_Q8 ? 0 : 2 * g);
+    return p;
+}
+
+// dequantized element i of a downloaded blob (the format's arithmetic: q * s, or q * s + m rounded
+// once to f32, which is what the reference's dequantize produces)
+float sv_deq(Fmt f, const std::vector<uint8_t>& b, const SvPlanes& p, size_t i)
+{
+    uint16_t sb, mb = 0;
+    std::memcpy(&sb, &b[p.sc + 2 * (i / kGroup)], 2);
+    if (f != F_Q8) std::memcpy(&mb, &b[p.mn + 2 * (i / kGroup)], 2);
+    const double s = sv_f16(sb), m = sv_f16(mb);
+    if (f == F_Q8) return (float)((double)(int8_t)b[p.codes + i] * s);
+    uint32_t q;
+    if (f == F_Q4) {
+        q = (b[p.codes + i / 2] >> (4 * (i & 1))) & 15u;
+    } else {
+        uint32_t lw, hw;
+        std::memcpy(&lw, &b[p.codes + 4 * (i / 16)], 4);
+        std::memcpy(&hw, &b[p.hi + 4 * (i / 32)], 4);
+        q = ((lw >> (2 * (i % 16))) & 3u) | (((hw >> (i % 32)) & 1u) << 2);
+    }
+    return (float)((double)q * s + m);
+}
+
+struct SvBuf {
+    void* p = nullptr;
+    ~SvBuf() { if (p) (void)hipFree(p); }
+};
+
+// One check; returns BRIK_OK, BRIK_EVALID (c->err names the failure) or a HIP / argument error.
+int sv_case(brik_ctx* c, const char* stage, Fmt f, int M, int K, int N, bool moe, bool quant_check, bool relative,
+            uint64_t seed)
+{
+    const size_t nw = (size_t)N * K;
+    const int E = moe ? 4 : 1;
+    const size_t nwe = nw * E;
+    std::vector<float> W(nwe), A((size_t)M * K);
+    for (auto& v : W) v = sv_unit(seed);
+    for (auto& v : A) v = sv_unit(seed);
+    const SvPlanes pl = sv_layout(f, nwe);
+    SvBuf wf, blob, xa, ya, ro;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipMalloc(&wf.p, nwe * 4));
+    HIP_TRY(c, hipMalloc(&blob.p, pl.bytes));
+    HIP_TRY(c, hipMalloc(&xa.p, A.size() * 4));
+    HIP_TRY(c, hipMalloc(&ya.p, (size_t)M * N * 4));
+    HIP_TRY_RC(brik_h2d(c, wf.p, W.data(), nwe * 4));
+    HIP_TRY_RC(brik_h2d(c, xa.p, A.data(), A.size() * 4));
+    auto at = [&](size_t off) { return static_cast<char*>(blob.p) + off; };
+    int r = f == F_Q8 ? brik_quantize_q8(c, (const float*)wf.p, (int8_t*)at(pl.codes), (uint16_t*)at(pl.sc), nwe)
+          : f == F_Q4 ? brik_quantize_q4(c, (const float*)wf.p, (uint8_t*)at(pl.codes), (uint16_t*)at(pl.sc),
+                                         (uint16_t*)at(pl.mn), nwe)
+                      : brik_quantize_q3(c, (const float*)wf.p, (uint32_t*)at(pl.codes), (uint32_t*)at(pl.hi),
+                                         (uint16_t*)at(pl.sc), (uint16_t*)at(pl.mn), nwe);
+    HIP_TRY_RC(r);
+    std::vector<uint8_t> hb(pl.bytes);
+    HIP_TRY_RC(brik_d2h(c, hb.data(), blob.p, pl.bytes));
+    if (quant_check) {
+        // every dequantized weight within half a quantization step of the value it encodes, plus 2^-9
+        // for the f16 rounding of the group's scale and min (at most (1 + range) 2^-11 with |w| < 1)
+        for (size_t i = 0; i < nwe; ++i) {
+            uint16_t sb;
+            std::memcpy(&sb, &hb[pl.sc + 2 * (i / kGroup)], 2);
+            const double d = std::fabs((double)sv_deq(f, hb, pl, i) - (double)W[i]);
+            if (!(d <= 0.5 * sv_f16(sb) * (1.0 + 1e-3) + std::ldexp(1.0, -9)))
+                return fail(c, BRIK_EVALID, "%s: element %zu dequantizes %g away from its input", stage, i, d);
+        }
+        return BRIK_OK;
+    }
+    std::vector<int32_t> off(E + 1);
+    for (int e = 0; e <= E; ++e) off[e] = (int)((long)M * e / E);
+    if (moe) {
+        HIP_TRY(c, hipMalloc(&ro.p, off.size() * 4));
+        HIP_TRY_RC(brik_h2d(c, ro.p, off.data(), off.size() * 4));
+        r = brik_moe_matmul_t_q4(c, (const float*)xa.p, (const int32_t*)ro.p, (const uint8_t*)at(pl.codes),
+                                 (const uint16_t*)at(pl.sc), (const uint16_t*)at(pl.mn), (float*)ya.p, E, M, K, N);
+    } else if (f == F_Q8) {
+        r = brik_matmul_t_q8(c, (const float*)xa.p, (const int8_t*)at(pl.codes), (const uint16_t*)at(pl.sc),
+                             (float*)ya.p, M, K, N);
+    } else if (f == F_Q4) {
+        r = brik_matmul_t_q4(c, (const float*)xa.p, (const uint8_t*)at(pl.codes), (const uint16_t*)at(pl.sc),
+                             (const uint16_t*)at(pl.mn), (float*)ya.p, M, K, N);
+    } else {
+        r = brik_matmul_t_q3(c, (const float*)xa.p, (const uint32_t*)at(pl.codes), (const uint32_t*)at(pl.hi),
+                             (const uint16_t*)at(pl.sc), (const uint16_t*)at(pl.mn), (float*)ya.p, M, K, N);
+    }
+    HIP_TRY_RC(r);
+    std::vector<float> got((size_t)M * N);
+    HIP_TRY_RC(brik_d2h(c, got.data(), ya.p, got.size() * 4));
+    std::vector<float> wd((size_t)N * K);
+    for (int row = 0; row < M; ++row) {
+        const int e = moe ? (int)(std::upper_bound(off.begin(), off.end(), row) - off.begin()) - 1 : 0;
+        if (row == 0 || (moe && row == off[e]))
+            for (size_t i = 0; i < nw; ++i) wd[i] = sv_deq(f, hb, pl, (size_t)e * nw + i);
+        for (int col = 0; col < N; ++col) {
+            double ref = 0, den = 0;
+            for (int k = 0; k < K; ++k) {
+                const double t = (double)A[(size_t)row * K + k] * (double)wd[(size_t)col * K + k];
+                ref += t;
+                den += std::fabs(t);
+            }
+            const double g = got[(size_t)row * N + col];
+            const double tol = relative ? 1e-3 * den : 1e-3;
+            if (!(std::fabs(g - (double)(float)ref) < tol))
+                return fail(c, BRIK_EVALID, "%s: y[%d, %d] = %g, CPU reference %g", stage, row, col, g, (double)(float)ref);
+        }
+    }
+    return BRIK_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -616,6 +771,7 @@ extern "C" {
 const char* brik_strerror(int code)
 {
     switch (code) {
+    case BRIK_EVALID: return "self-validation failed";
     case BRIK_OK: return "ok";
     case BRIK_EINVAL: return "invalid argument";
     case BRIK_EALIGN: return "misaligned pointer";
@@ -1286,6 +1442,92 @@ int brik_timer_end(brik_ctx* c, float* ms)
     HIP_TRY(c, hipEventRecord(c->ev_end, c->stream));
     HIP_TRY(c, hipEventSynchronize(c->ev_end));
     HIP_TRY(c, hipEventElapsedTime(ms, c->ev_begin, c->ev_end));
+    return BRIK_OK;
+}
+
+int brik_fence_record(brik_ctx* c, brik_fence** out)
+{
+    if (!c || !out) return BRIK_EINVAL;
+    *out = nullptr;
+    if (c->graph_capturing) return fail(c, BRIK_EINVAL, "fence: not allowed while a graph capture is open");
+    brik_fence* f = new (std::nothrow) brik_fence();
+    if (!f) return BRIK_ENOMEM;
+    f->device = c->device;
+    hipError_t e = hipSetDevice(c->device);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&f->ev, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(f->ev, c->stream);
+    if (e != hipSuccess) {
+        brik_fence_destroy(f);
+        return fail(c, BRIK_EHIP, "fence: %s", hipGetErrorString(e));
+    }
+    *out = f;
+    return BRIK_OK;
+}
+
+int brik_fence_d2h(brik_fence* f, void* dst, const void* src, size_t bytes)
+{
+    if (!f) return BRIK_EINVAL;
+    if (bytes && (!dst || !src)) {
+        snprintf(f->err, sizeof f->err, "fence_d2h: null pointer");
+        return BRIK_EINVAL;
+    }
+    hipError_t e = hipSetDevice(f->device);
+    if (e == hipSuccess) e = hipEventSynchronize(f->ev);
+    // the context stream is non-blocking, so this copy on the null stream waits for nothing else
+    if (e == hipSuccess && bytes) e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        snprintf(f->err, sizeof f->err, "fence_d2h: %s", hipGetErrorString(e));
+        return BRIK_EHIP;
+    }
+    return BRIK_OK;
+}
+
+const char* brik_fence_error(const brik_fence* f) { return f ? f->err : "null fence"; }
+
+void brik_fence_destroy(brik_fence* f)
+{
+    if (!f) return;
+    if (f->ev) {
+        (void)hipSetDevice(f->device);
+        (void)hipEventDestroy(f->ev);
+    }
+    delete f;
+}
+
+int brik_self_validate(brik_ctx* c, char* stage, size_t cap)
+{
+    if (!c) return BRIK_EINVAL;
+    if (stage && cap) stage[0] = 0;
+    if (c->graph_capturing) return fail(c, BRIK_EINVAL, "self_validate: not allowed while a graph capture is open");
+    struct Check {
+        const char* stage;
+        Fmt f;
+        int M, K, N;
+        bool moe, quant, relative;
+    };
+    // the reference's quantized checks in its order (kernels.ts:2325-2459), then two of this library's
+    const Check checks[] = {
+        {"matmulQ4", F_Q4, 1, 128, 6, false, false, false},
+        {"quantize_q4", F_Q4, 1, 128, 6, false, true, false},
+        {"matmulQ3", F_Q3, 5, 128, 6, false, false, false},
+        {"matmul_q4_tiled", F_Q4, 5, 128, 6, false, false, false},
+        {"matmul_q4_shared", F_Q4, 20, 128, 18, false, false, false},
+        {"matmulQ8", F_Q8, 1, 128, 6, false, false, false},
+        {"quantize_q8", F_Q8, 1, 128, 6, false, true, false},
+        {"matmul_q8_tiled", F_Q8, 5, 128, 6, false, false, false},
+        {"matmul_q8_shared", F_Q8, 20, 128, 18, false, false, false},
+        {"matmul_q4_prefill", F_Q4, 40, 1024, 256, false, false, true},
+        {"moe_matmul_q4", F_Q4, 40, 512, 96, true, false, true},
+    };
+    uint64_t seed = 0x5EEDB41Cull;
+    for (const Check& k : checks) {
+        const int r = sv_case(c, k.stage, k.f, k.M, k.K, k.N, k.moe, k.quant, k.relative, seed);
+        seed += 0x1000;
+        if (r != BRIK_OK) {
+            if (stage && cap) snprintf(stage, cap, "%s", k.stage);
+            return r;
+        }
+    }
     return BRIK_OK;
 }
 

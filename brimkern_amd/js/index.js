@@ -27,8 +27,11 @@
 //                                                    engine.weightFromContainer(parsed, name)
 //
 // Plane arguments may be DeviceBuffers, plane views ({ptr: BigInt}) or BigInt addresses. Errors
-// (bad shapes, K % 32 != 0, misalignment, no device) throw an Error whose .code is "BRIK_E...";
-// the reference validated nothing and let WebGPU fail silently.
+// (bad shapes, K % 32 != 0, misalignment, no device) carry .code "BRIK_E...": the promise-returning
+// methods (the readback ops, top-k, quantizeToBytes, matmulT, selfValidate) reject with them, the
+// device-resident ones (mm, gemvPlan, conv2d, ...) throw; the reference validated nothing and let
+// WebGPU fail silently. DeviceBuffers free their memory on destroy() or, if dropped, when collected.
+//   selfValidate()                      :2255-2459  engine.selfValidate() -> Promise<boolean>, validationFailure
 
 const path = require('path');
 const planes = require('./planes');
@@ -44,17 +47,21 @@ const FMT = { q8: 8, q4: 4, q3: 3 };
 const OPT_PATH = 1;
 const OPT_GEMV_VARIANT = 2;
 
+// A device allocation owned by this object: destroy() frees it at once; if the object is dropped
+// without destroy(), the addon's finalizer frees it when the garbage collector reclaims the handle
+// (the reference releases its buffers through destroy() or lets the GC take them, kernels.ts:903-956).
 class DeviceBuffer {
-  constructor(engine, ptr, size) {
+  constructor(engine, handle, size) {
     this.engine = engine;
-    this.ptr = ptr;       // BigInt device address
-    this.size = size;     // bytes
+    this.handle = handle;                             // addon handle (owns the allocation)
+    this.ptr = engine.native.bufferPtr(handle);       // BigInt device address
+    this.size = size;                                 // bytes
   }
   // A plane view `offset` bytes into the buffer.
   view(offset) { return { ptr: this.ptr + BigInt(offset), buffer: this }; }
   destroy() {
     if (this.ptr !== null) {
-      this.engine.native.free(this.engine.ctx, this.ptr);
+      this.engine.native.freeBuffer(this.handle);
       this.ptr = null;
     }
   }
@@ -82,7 +89,10 @@ class Engine {
   static deviceCount() { return loadNative().deviceCount(); }
 
   // ---- memory ---------------------------------------------------------------------------------
-  alloc(bytes) { return new DeviceBuffer(this, this.native.alloc(this.ctx, Math.max(bytes, 1)), bytes); }
+  alloc(bytes) { return new DeviceBuffer(this, this.native.allocBuffer(this.ctx, Math.max(bytes, 1)), bytes); }
+
+  // Device buffers allocated through this engine and not yet freed (by destroy() or the GC).
+  liveBuffers() { return this.native.liveBuffers(this.ctx); }
 
   // Persistent device copy of raw bytes, padded to a 4-byte multiple (kernels.ts:1032-1042).
   uploadGpuRaw(bytes) {
@@ -102,6 +112,13 @@ class Engine {
   readBack(buf, bytes) {
     const ptr = typeof buf === 'bigint' ? buf : buf.ptr;
     return new Float32Array(this.native.d2h(this.ctx, ptr, bytes));
+  }
+
+  // Asynchronous form (readBack / mapAsync, kernels.ts:244-258): resolves once the work enqueued so far
+  // has run, without blocking the JS thread meanwhile.
+  readBackAsync(buf, bytes) {
+    const ptr = typeof buf === 'bigint' ? buf : buf.ptr;
+    return this.native.readbackAsync(this.ctx, ptr, bytes).then(function (ab) { return new Float32Array(ab); });
   }
 
   // A quantized weight handle from one packed .brik blob: one upload, planes addressed in place.
@@ -127,39 +144,43 @@ class Engine {
   }
 
   // ---- readback ops (reference signatures) -----------------------------------------------------
-  _readback(fn, a, planeArgs, m, k, n) {
+  // Upload a, enqueue the matmul and read y back without blocking the JS thread; a bad argument or a
+  // library error rejects the promise. The temporary buffers are freed after the readback (freeing
+  // them earlier would wait for the stream).
+  async _readback(fn, a, planeArgs, m, k, n) {
     const x = a instanceof Float32Array ? a : Float32Array.from(a);
-    if (x.length !== m * k) {
-      const e = new Error('BRIK_EINVAL: activation has ' + x.length + ' floats, expected m*k = ' + m * k);
-      e.code = 'BRIK_EINVAL';
-      throw e;
-    }
+    if (x.length !== m * k) throw einval('activation has ' + x.length + ' floats, expected m*k = ' + m * k);
     const xb = this.alloc(x.byteLength);
     const yb = this.alloc(m * n * 4);
     try {
       if (x.byteLength) this.native.h2d(this.ctx, xb.ptr, x);
       fn.apply(this.native, [this.ctx, xb.ptr].concat(planeArgs, [yb.ptr, m, k, n]));
-      return this.readBack(yb, m * n * 4);
+      return await this.readBackAsync(yb, m * n * 4);
     } finally {
       xb.destroy();
       yb.destroy();
     }
   }
 
-  matmulQ4(a, nib, sc, mn, m, k, n) {
-    return Promise.resolve(this._readback(this.native.matmulQ4, a, [nib, sc, mn], m, k, n));
-  }
+  matmulQ4(a, nib, sc, mn, m, k, n) { return this._readback(this.native.matmulQ4, a, [nib, sc, mn], m, k, n); }
   matmulQ4Tiled(a, nib, sc, mn, m, k, n) { return this.matmulQ4(a, nib, sc, mn, m, k, n); }
   matmulQ4Shared(a, nib, sc, mn, m, k, n) { return this.matmulQ4(a, nib, sc, mn, m, k, n); }
 
-  matmulQ8(a, codes, sc, m, k, n) {
-    return Promise.resolve(this._readback(this.native.matmulQ8, a, [codes, sc], m, k, n));
-  }
+  matmulQ8(a, codes, sc, m, k, n) { return this._readback(this.native.matmulQ8, a, [codes, sc], m, k, n); }
   matmulQ8Tiled(a, codes, sc, m, k, n) { return this.matmulQ8(a, codes, sc, m, k, n); }
   matmulQ8Shared(a, codes, sc, m, k, n) { return this.matmulQ8(a, codes, sc, m, k, n); }
 
-  matmulQ3(a, lo, hi, sc, mn, m, k, n) {
-    return Promise.resolve(this._readback(this.native.matmulQ3, a, [lo, hi, sc, mn], m, k, n));
+  matmulQ3(a, lo, hi, sc, mn, m, k, n) { return this._readback(this.native.matmulQ3, a, [lo, hi, sc, mn], m, k, n); }
+
+  // The reference's load-time gate (selfValidate, kernels.ts:2255-2459): runs every quantized matmul
+  // check of the library (brik_self_validate) and resolves true, or false with validationFailure set
+  // to the failing check's name, as the reference does (useModelEngine.ts:243-249 refuses the model).
+  async selfValidate() {
+    this.validationFailure = null;
+    const stage = this.native.selfValidate(this.ctx);
+    if (stage === null) return true;
+    this.validationFailure = stage;
+    return false;
   }
 
   // ---- recorded (device-resident) form: recMM ---------------------------------------------------
@@ -204,13 +225,13 @@ class Engine {
   }
 
   // ---- sampling pre-work (decodeTopKQ8) --------------------------------------------------------
-  _topK(run, recent, K) {
+  async _topK(run, recent, K) {
     const ids = Array.from(new Set(recent || []));              // each id once, as the reference's callers do
     const rb = ids.length ? this.uploadGpuRaw(Int32Array.from(ids)) : null;
     const ob = this.alloc(8 * K);
     try {
       run(rb ? rb.ptr : null, ids.length, ob.ptr, ob.ptr + BigInt(4 * K));
-      const raw = new Uint32Array(this.native.d2h(this.ctx, ob.ptr, 8 * K));
+      const raw = new Uint32Array(await this.native.readbackAsync(this.ctx, ob.ptr, 8 * K));
       return { ids: raw.slice(0, K), vals: new Float32Array(raw.buffer.slice(4 * K, 8 * K)) };
     } finally {
       ob.destroy();
@@ -219,27 +240,27 @@ class Engine {
   }
 
   // softcap -> repetition penalty -> top-K on a device logits buffer (modified in place), kernels.ts:1940-1958.
-  logitsTopK(logits, vocab, recent, penalty, softcap, K) {
+  async logitsTopK(logits, vocab, recent, penalty, softcap, K) {
     const k = K === undefined ? 64 : K;
     const nat = this.native, ctx = this.ctx;
-    return Promise.resolve(this._topK(function (rec, nrec, ids, vals) {
+    return this._topK(function (rec, nrec, ids, vals) {
       nat.logitsTopK(ctx, logits, rec, ids, vals, vocab, nrec, k, penalty || 0, softcap || 0);
-    }, recent, k));
+    }, recent, k);
   }
 
   // decodeTopKQ8's LM head and passes (kernels.ts:1934-1968) for one row x (Float32Array[d] or device
   // buffer): one launch for the whole vocab (no tiling), then the passes; K ids + values come back.
-  lmHeadTopK(x, w, d, vocab, recent, penalty, softcap, K) {
+  async lmHeadTopK(x, w, d, vocab, recent, penalty, softcap, K) {
     const k = K === undefined ? 64 : K;
     const nat = this.native, ctx = this.ctx;
     const xb = (x instanceof Float32Array || Array.isArray(x)) ? this.uploadGpuRaw(Float32Array.from(x)) : null;
     const xp = xb ? xb.ptr : x;
     const fmt = w.q3 ? FMT.q3 : w.nib ? FMT.q4 : FMT.q8;
     try {
-      return Promise.resolve(this._topK(function (rec, nrec, ids, vals) {
+      return await this._topK(function (rec, nrec, ids, vals) {
         nat.lmHeadTopK(ctx, fmt, xp, w.nib || w.codes || w.lo, w.hi || null, w.sc, w.mn || null, rec, ids, vals,
           d, vocab, nrec, k, penalty || 0, softcap || 0);
-      }, recent, k));
+      }, recent, k);
     } finally {
       if (xb) xb.destroy();
     }
@@ -260,7 +281,7 @@ class Engine {
   // on the GPU first). `dtype`: 'q8' | 'q4' | 'q3'. The work runs in chunks of `chunkOverride`
   // elements (default 2^26), rounded to whole groups (whole 512-element blocks for quant sources),
   // so the device holds one chunk at a time; any chunking gives the same bytes.
-  quantizeToBytes(type, data, nElems, dtype, chunkOverride) {
+  async quantizeToBytes(type, data, nElems, dtype, chunkOverride) {
     const src = toBytes(data);
     if (!FMT[dtype]) throw einval('quantizeToBytes: unknown dtype ' + dtype);
     if (!(nElems >= 0) || nElems % 32 !== 0) throw einval('quantizeToBytes: nElems ' + nElems + ' is not a multiple of 32');
@@ -269,7 +290,7 @@ class Engine {
     if (need < 0) throw einval('quantizeToBytes: unsupported source type ' + type);
     if (src.byteLength < need) throw einval('quantizeToBytes: ' + type + ' data has ' + src.byteLength + ' bytes, need ' + need);
     const out = new Uint8Array(planes.byteLength(dtype, nElems));
-    if (nElems === 0) return Promise.resolve(out);
+    if (nElems === 0) return out;
     const unit = quantSrc ? 512 : 32;
     let chunk = chunkOverride === undefined ? (1 << 26) : chunkOverride;
     chunk = Math.max(unit, Math.floor(chunk / unit) * unit);
@@ -301,10 +322,10 @@ class Engine {
         const names = Object.keys(outOffs);
         nat.quantize(ctx, FMT[dtype], f32.ptr, dst(names[0]), dtype === 'q3' ? dst('hi') : null, dst('sc'),
           dtype === 'q8' ? null : dst('mn'), ce);
-        names.forEach(function (p) {
+        for (const p of names) {
           const len = ce * perElem[p];
-          out.set(new Uint8Array(nat.d2h(ctx, dst(p), len)), outOffs[p][0] + e0 * perElem[p]);
-        });
+          out.set(new Uint8Array(await nat.readbackAsync(ctx, dst(p), len)), outOffs[p][0] + e0 * perElem[p]);
+        }
       }
     } finally {
       f32.destroy();
@@ -312,7 +333,7 @@ class Engine {
       if (stage) stage.destroy();
       if (w) this.destroyWeight(w);
     }
-    return Promise.resolve(out);
+    return out;
   }
 
   // f32ToQ8Gpu / f32ToQ4Gpu (kernels.ts:986-1010) and the q3 analogue: a device f32 buffer of nElems
@@ -337,9 +358,9 @@ class Engine {
   // matmulT with an f16 weight (kernels.ts:410-426 -> MATMUL_T_F16W): w is a device buffer / address of
   // N x K IEEE f16 values (uploadGpuRaw of the raw bytes). f32 weights (wF16 false) are outside this
   // library and throw BRIK_EINVAL.
-  matmulT(a, w, m, k, n, wF16) {
+  async matmulT(a, w, m, k, n, wF16) {
     if (!wF16) throw einval('matmulT: only f16 weights (wF16 = true) are handled here');
-    return Promise.resolve(this._readback(this.native.matmulF16W, a, [w], m, k, n));
+    return this._readback(this.native.matmulF16W, a, [w], m, k, n);
   }
 
   // Device-resident form of matmulT with an f16 weight.

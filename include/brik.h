@@ -43,6 +43,7 @@ extern "C" {
 #define BRIK_ENOMEM (-4)   /* device allocation failed */
 #define BRIK_ENODEV (-5)   /* no such device / no gfx950 device */
 #define BRIK_EMODULE (-6)  /* the embedded gfx950 code object failed to load */
+#define BRIK_EVALID (-7)   /* brik_self_validate: a kernel disagreed with the CPU reference */
 
 typedef struct brik_ctx brik_ctx;
 
@@ -65,6 +66,35 @@ int brik_d2h(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
 int brik_d2d(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Wait for all work enqueued on the context's stream. */
 int brik_sync(brik_ctx *ctx);
+
+/* ---- asynchronous readback ------------------------------------------------------------------
+ * The reference's readback ops resolve through mapAsync without blocking the JS thread
+ * (readBack, src/lib/webgpu/kernels.ts:244-258; run, :381-390). A fence marks the current end of the
+ * context stream: brik_fence_record enqueues it (call order = stream order, like queue.submit);
+ * brik_fence_d2h waits for it and then copies `bytes` of device memory (of the context's device,
+ * complete once the fence is reached) into host memory. brik_fence_d2h and brik_fence_destroy do not
+ * touch the context, so they may run on another thread while the context keeps enqueueing work
+ * (one thread per fence at a time). Not allowed while a graph capture is open. */
+typedef struct brik_fence brik_fence;
+int brik_fence_record(brik_ctx *ctx, brik_fence **out);
+int brik_fence_d2h(brik_fence *fence, void *dst, const void *src, size_t bytes);
+const char *brik_fence_error(const brik_fence *fence);
+void brik_fence_destroy(brik_fence *fence);
+
+/* ---- load-time self-validation ----------------------------------------------------------------
+ * The reference refuses to load a model when any of its quantized-matmul kernels disagrees with its
+ * CPU reference (selfValidate, src/lib/webgpu/kernels.ts:2255-2265, quantized checks :2325-2459;
+ * enforced at src/app/useModelEngine.ts:243-249). This runs the same checks on this library's kernels,
+ * in the reference's order and shapes (matmulQ4 m=1 k=128 n=6, quantize_q4, matmulQ3 m=5,
+ * matmul_q4_tiled m=5, matmul_q4_shared m=20 n=18, matmulQ8, quantize_q8, matmul_q8_tiled,
+ * matmul_q8_shared), plus a prefill-sized q4 GEMM (m=40 k=1024 n=256) and an expert-grouped q4 call:
+ * weights in [-1, 1) encoded by brik_quantize_*, activations in [-1, 1) (a fixed seed), results
+ * against an f64 sum over the downloaded planes' dequantized values with the reference's tolerance
+ * (|got - ref| < 1e-3; 1e-3 * sum |a w| for the two MFMA-sized checks), the encoders against the
+ * quantization bound (every dequantized weight within half a step of its input). Returns BRIK_OK, or
+ * BRIK_EVALID with the name of the first failing check in `stage` (and the message), or an allocation
+ * / HIP error. Uses its own device memory (about 2 MB), freed before it returns. */
+int brik_self_validate(brik_ctx *ctx, char *stage, size_t stage_cap);
 
 /* ---- quantized matmuls --------------------------------------------------------------------
  * Replace matmulQ8 / matmulQ8Tiled / matmulQ8Shared (kernels.ts:1140-1169), matmulQ4 /

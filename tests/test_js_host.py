@@ -24,7 +24,8 @@ pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
 EXPORTS = ["deviceCount", "createContext", "alloc", "free", "h2d", "d2h", "sync", "setOption", "timerBegin",
            "timerEnd", "matmulQ8", "matmulQ4", "matmulQ3", "moeMatmulQ4", "dequantQ8", "dequantQ4", "dequantQ3",
            "gemvPlanCreate", "gemvPlanRun", "gemvPlanDestroy", "logitsTopK", "lmHeadTopK", "quantize",
-           "f16ToF32", "conv2d", "matmulF16W"]
+           "f16ToF32", "conv2d", "matmulF16W", "allocBuffer", "bufferPtr", "freeBuffer", "liveBuffers",
+           "readbackAsync", "selfValidate"]
 
 
 def node(script, timeout=120):
@@ -62,3 +63,14 @@ def test_js_engine_parity_on_gpu():
     assert r.returncode == 0, r.stdout + r.stderr
     res = json.loads(r.stdout.strip().splitlines()[-1])
     assert res["failed"] == 0 and res["checks"] >= 20
+
+
+@pytest.mark.gpu
+def test_js_engine_async_and_lifetime_on_gpu():
+    """Readbacks through fences off the JS thread, rejection instead of throwing, finalizers freeing
+    dropped device buffers (and keeping their context alive), selfValidate passing."""
+    r = subprocess.run([NODE, "--expose-gc", os.path.join(ROOT, "tests", "js", "engine_async.js")], cwd=ROOT,
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["failed"] == 0 and res["checks"] >= 14
