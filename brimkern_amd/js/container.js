@@ -1,32 +1,33 @@
 'use strict';
-// The single-file .brik container and its shard layout, as the reference reads and writes them
-// (src/lib/brik/container.ts, codec.ts:62-98, convert.ts:37-89, loader.ts:57-66, format.ts:6-8,
-// 87-90), so that a .brik file made by either side loads in the other:
+// The single-file .brik container: reader, writer and the shard layout of a converted model, with the
+// file bytes of the reference's writer (src/lib/brik/container.ts, codec.ts:62-98, convert.ts:37-89,
+// loader.ts:57-66, format.ts:6-8) so that a file made on either side loads on the other.
 //
-//   [0, 4)          magic "BRIK"
-//   [4, 8)          version, u32 LE (1)
-//   [8, 12)         manifest byte length L, u32 LE
-//   [12, 12 + L)    manifest JSON (UTF-8)
-//   [alignUp(12 + L, 16), ...)   the data section: shard bytes in ascending shard-id order
+//   bytes [0, 4)        "BRIK"
+//         [4, 8)        format version, u32 little-endian (1)
+//         [8, 12)       L = manifest length in bytes, u32 little-endian
+//         [12, 12 + L)  manifest, JSON.stringify of the manifest object, UTF-8
+//         [D, end)      data section, D = 12 + L rounded up to 16: the shards back to back by id
 //
-// A tensor's absolute file offset is dataStart + shardBase[shard] + offset; every tensor starts on a
-// 16-byte boundary of its shard, and shards have 16-byte multiple lengths. Error messages keep the
-// reference's text, so callers that match on them see the same errors.
+// Inside a shard every tensor starts on a 16-byte boundary and the shard's length is a multiple of 16,
+// so every tensor of the file is 16-byte aligned. A tensor lives at D + base(shard) + offset.
 //
-// Quantized tensors are stored as the packed planes (packQ8 / packQ4 / packQ3 bytes); this module
-// does not encode values itself: engine.quantizeToBytes (GPU) produces them.
+// The module is built on one placement routine (`place`) used at both levels: tensors inside a shard
+// (16-byte runs) and shards inside the data section (runs already 16-byte multiples). Error messages
+// are the reference's, word for word, so callers that match on them see the same errors. Values are
+// not encoded here: quantized tensors arrive as packed planes (engine.quantizeToBytes).
 
 const BRIK_VERSION = 1;
 const BRIK_ALIGN = 16;
-const MAGIC = 'BRIK';
-const HEADER_FIXED = 12;
+const MAGIC = [0x42, 0x52, 0x49, 0x4b];   // "BRIK"
+const FIXED = 12;                          // magic + version + manifest length
 
 function alignUp(n, align) {
   const a = align === undefined ? BRIK_ALIGN : align;
   return Math.ceil(n / a) * a;
 }
 
-function brikDataStart(manifestByteLength) { return alignUp(HEADER_FIXED + manifestByteLength); }
+function brikDataStart(manifestByteLength) { return alignUp(FIXED + manifestByteLength); }
 
 function asBytes(data) {
   if (data instanceof Uint8Array) return data;
@@ -35,137 +36,148 @@ function asBytes(data) {
   throw new TypeError('expected bytes (TypedArray / ArrayBuffer)');
 }
 
-// container.ts:30-58
-function serializeBrik(manifest, shards) {
-  const manifestBytes = Buffer.from(JSON.stringify(manifest), 'utf8');
-  const dataStart = brikDataStart(manifestBytes.length);
-  const ordered = manifest.shards.slice().sort(function (a, b) { return a.id - b.id; });
-  const byFile = new Map(shards.map(function (s) { return [s.file, asBytes(s.bytes)]; }));
-  let dataLen = 0;
-  ordered.forEach(function (sh) {
-    const bytes = byFile.get(sh.file);
-    if (!bytes) throw new Error('shard manquant : ' + sh.file);
-    if (bytes.length !== sh.byteLength) {
-      throw new Error('taille de shard incohérente pour ' + sh.file + ' : ' + bytes.length + ' ≠ ' + sh.byteLength);
-    }
-    dataLen += sh.byteLength;
-  });
-  const out = new Uint8Array(dataStart + dataLen);
-  for (let i = 0; i < MAGIC.length; i++) out[i] = MAGIC.charCodeAt(i);
-  const dv = new DataView(out.buffer);
-  dv.setUint32(4, BRIK_VERSION, true);
-  dv.setUint32(8, manifestBytes.length, true);
-  out.set(manifestBytes, HEADER_FIXED);
-  let off = dataStart;
-  ordered.forEach(function (sh) {
-    out.set(byFile.get(sh.file), off);
-    off += sh.byteLength;
-  });
-  return out;
+// Runs of the given lengths laid end to end, each starting on a multiple of `align`: their start
+// offsets and the end of the last one.
+function place(lengths, align) {
+  const at = new Array(lengths.length);
+  let end = 0;
+  for (let i = 0; i < lengths.length; i++) {
+    at[i] = alignUp(end, align);
+    end = at[i] + lengths[i];
+  }
+  return { at: at, end: end };
 }
 
-// container.ts:71-81: header + manifest from the leading bytes of a file
+function byId(shards) { return shards.slice().sort(function (a, b) { return a.id - b.id; }); }
+
+// ---- reading --------------------------------------------------------------------------------------
+
+// The fixed header and the manifest, from the leading bytes of a file (parseBrikHeader, container.ts:71-81).
 function parseBrikHeader(data) {
-  const bytes = asBytes(data);
-  if (bytes.length < HEADER_FIXED) throw new Error('BRIK: fichier tronqué (en-tête)');
-  const magic = String.fromCharCode(bytes[0], bytes[1], bytes[2], bytes[3]);
-  if (magic !== MAGIC) throw new Error('BRIK: sceau magique absent (' + magic + ')');
-  const dv = new DataView(bytes.buffer, bytes.byteOffset, bytes.byteLength);
-  const version = dv.getUint32(4, true);
-  const manifestLen = dv.getUint32(8, true);
-  if (HEADER_FIXED + manifestLen > bytes.length) throw new Error('BRIK: manifeste tronqué');
-  const text = Buffer.from(bytes.buffer, bytes.byteOffset + HEADER_FIXED, manifestLen).toString('utf8');
-  return { manifest: JSON.parse(text), version: version, dataStart: brikDataStart(manifestLen) };
+  const b = asBytes(data);
+  if (b.length < FIXED) throw new Error('BRIK: fichier tronqué (en-tête)');
+  const seal = String.fromCharCode(b[0], b[1], b[2], b[3]);
+  if (MAGIC.some(function (c, i) { return b[i] !== c; })) throw new Error('BRIK: sceau magique absent (' + seal + ')');
+  const dv = new DataView(b.buffer, b.byteOffset, FIXED);
+  const length = dv.getUint32(8, true);
+  if (length > b.length - FIXED) throw new Error('BRIK: manifeste tronqué');
+  const json = Buffer.from(b.buffer, b.byteOffset + FIXED, length).toString('utf8');
+  return { manifest: JSON.parse(json), version: dv.getUint32(4, true), dataStart: brikDataStart(length) };
 }
 
-// container.ts:84-87
+// The header plus `data`, a view of the data section (parseBrik, container.ts:84-87).
 function parseBrik(data) {
-  const bytes = asBytes(data);
-  const h = parseBrikHeader(bytes);
-  return { manifest: h.manifest, version: h.version, dataStart: h.dataStart, data: bytes.subarray(h.dataStart) };
+  const b = asBytes(data);
+  const h = parseBrikHeader(b);
+  h.data = b.subarray(h.dataStart);
+  return h;
 }
 
-// loader.ts:57-66: byte offset of each shard in the data section, indexed by shard id
+// Byte offset of each shard in the data section, indexed by shard id (loader.ts:57-66).
 function computeShardBases(shards) {
-  const ordered = shards.slice().sort(function (a, b) { return a.id - b.id; });
+  const ordered = byId(shards);
+  const p = place(ordered.map(function (s) { return s.byteLength; }), 1);
   const bases = [];
-  let off = 0;
-  ordered.forEach(function (sh) {
-    bases[sh.id] = off;
-    off += sh.byteLength;
-  });
+  ordered.forEach(function (s, i) { bases[s.id] = p.at[i]; });
   return bases;
 }
 
-// The bytes of one tensor of a parsed file (a view, no copy), with its manifest entry.
+// One tensor of a parsed file: its manifest entry and a view of its bytes (no copy).
 function tensorBytes(parsed, name) {
-  const e = parsed.manifest.tensors[name];
-  if (!e) throw new Error('BRIK: tenseur absent : ' + name);
-  const base = computeShardBases(parsed.manifest.shards)[e.shard];
-  const start = base + e.offset;
-  if (base === undefined || start + e.byteLength > parsed.data.length) throw new Error('BRIK: tenseur tronqué : ' + name);
-  return { entry: e, bytes: parsed.data.subarray(start, start + e.byteLength) };
+  const entry = parsed.manifest.tensors[name];
+  if (!entry) throw new Error('BRIK: tenseur absent : ' + name);
+  const base = computeShardBases(parsed.manifest.shards)[entry.shard];
+  const from = base + entry.offset, to = from + entry.byteLength;
+  if (base === undefined || to > parsed.data.length) throw new Error('BRIK: tenseur tronqué : ' + name);
+  return { entry: entry, bytes: parsed.data.subarray(from, to) };
 }
 
-// codec.ts:62-98: tensors [{name, dtype, shape, bytes | data (f32 only), nElems}] into one shard,
-// each 16-byte aligned, the shard length padded to 16.
-function packShard(tensors, shardId) {
-  const encoded = tensors.map(function (t) {
-    let bytes = t.bytes;
-    if (!bytes) {
-      if (t.dtype !== 'f32' || !t.data) throw new Error('packShard: ' + t.name + ' needs pre-encoded bytes for dtype ' + t.dtype);
-      bytes = Float32Array.from(t.data);
+// ---- writing --------------------------------------------------------------------------------------
+
+// The file bytes for a manifest and its shards [{file, bytes}] (serializeBrik, container.ts:30-58):
+// every shard the manifest lists must be supplied at the length it declares.
+function serializeBrik(manifest, shards) {
+  const supplied = {};
+  shards.forEach(function (s) { supplied[s.file] = asBytes(s.bytes); });
+  const table = byId(manifest.shards).map(function (s) {
+    const bytes = Object.prototype.hasOwnProperty.call(supplied, s.file) ? supplied[s.file] : null;
+    if (!bytes) throw new Error('shard manquant : ' + s.file);
+    if (bytes.length !== s.byteLength) {
+      throw new Error('taille de shard incohérente pour ' + s.file + ' : ' + bytes.length + ' ≠ ' + s.byteLength);
     }
-    bytes = asBytes(bytes);
-    const nElems = t.nElems !== undefined ? t.nElems : t.data ? t.data.length
-      : t.shape.reduce(function (a, b) { return a * b; }, 1);
-    return { t: t, bytes: bytes, nElems: nElems };
+    return bytes;
   });
-  let total = 0;
-  encoded.forEach(function (e) { total = alignUp(total) + e.bytes.length; });
-  const buffer = new Uint8Array(alignUp(total));
+  const json = Buffer.from(JSON.stringify(manifest), 'utf8');
+  const start = brikDataStart(json.length);
+  const section = place(table.map(function (b) { return b.length; }), 1);
+  const file = new Uint8Array(start + section.end);
+  file.set(MAGIC, 0);
+  const dv = new DataView(file.buffer);
+  dv.setUint32(4, BRIK_VERSION, true);
+  dv.setUint32(8, json.length, true);
+  file.set(json, FIXED);
+  table.forEach(function (b, i) { file.set(b, start + section.at[i]); });
+  return file;
+}
+
+function elementCount(t) {
+  if (t.nElems !== undefined) return t.nElems;
+  if (t.data) return t.data.length;
+  let n = 1;
+  for (const d of t.shape) n *= d;
+  return n;
+}
+
+// Tensors [{name, dtype, shape, bytes | data (f32 only), nElems}] placed into one shard on 16-byte
+// boundaries, the shard padded to 16 (packShard, codec.ts:62-98): {buffer, entries by name}.
+function packShard(tensors, shardId) {
+  const payloads = tensors.map(function (t) {
+    if (t.bytes) return asBytes(t.bytes);
+    if (t.dtype !== 'f32' || !t.data) throw new Error('packShard: ' + t.name + ' needs pre-encoded bytes for dtype ' + t.dtype);
+    return asBytes(Float32Array.from(t.data));
+  });
+  const p = place(payloads.map(function (b) { return b.length; }), BRIK_ALIGN);
+  const buffer = new Uint8Array(alignUp(p.end));
   const entries = {};
-  let cursor = 0;
-  encoded.forEach(function (e) {
-    cursor = alignUp(cursor);
-    buffer.set(e.bytes, cursor);
-    entries[e.t.name] = { dtype: e.t.dtype, shape: e.t.shape, nElems: e.nElems, shard: shardId, offset: cursor,
-      byteLength: e.bytes.length };
-    cursor += e.bytes.length;
+  tensors.forEach(function (t, i) {
+    buffer.set(payloads[i], p.at[i]);
+    entries[t.name] = { dtype: t.dtype, shape: t.shape, nElems: elementCount(t), shard: shardId, offset: p.at[i],
+      byteLength: payloads[i].length };
   });
   return { buffer: buffer, entries: entries };
 }
 
-// convert.ts:37-52: one shard per transformer block ("blk.<i>."), everything else in shard 0
-function shardFile(id) { return 'shard-' + String(id).padStart(4, '0') + '.brik'; }
-function groupKey(name) {
-  const m = /^blk\.(\d+)\./.exec(name);
+// Shard grouping of a converted model (convert.ts:37-89): the tensors of transformer block i
+// ("blk.<i>.") form shard "layer-<i, 4 digits>", all others the "shared" shard; shard ids follow
+// "shared" first, then the group names in string order; shard files are "shard-<id, 4 digits>.brik".
+const BLOCK = /^blk\.(\d+)\./;
+function groupOf(name) {
+  const m = BLOCK.exec(name);
   return m ? 'layer-' + m[1].padStart(4, '0') : 'shared';
 }
-function orderShardKeys(keys) {
-  return keys.slice().sort(function (a, b) { return a === 'shared' ? -1 : b === 'shared' ? 1 : a.localeCompare(b); });
+function groupRank(a, b) {
+  if (a === b) return 0;
+  if (a === 'shared') return -1;
+  if (b === 'shared') return 1;
+  return a.localeCompare(b);
 }
 
-// convert.ts:54-89: {model, arch, chat, tokenizer, tensors} -> {manifest, shards}
+// {model, arch, chat, tokenizer, tensors} -> {manifest, shards: [{file, bytes}]} (assembleBrik)
 function assembleBrik(input) {
-  const groups = new Map();
+  const groups = {};
   input.tensors.forEach(function (t) {
-    const k = groupKey(t.name);
-    if (!groups.has(k)) groups.set(k, []);
-    groups.get(k).push(t);
-  });
-  const tensors = {};
-  const shards = [];
-  const shardMeta = [];
-  orderShardKeys(Array.from(groups.keys())).forEach(function (key, shardId) {
-    const packed = packShard(groups.get(key), shardId);
-    Object.assign(tensors, packed.entries);
-    const file = shardFile(shardId);
-    shards.push({ file: file, bytes: packed.buffer });
-    shardMeta.push({ id: shardId, file: file, byteLength: packed.buffer.length });
+    const g = groupOf(t.name);
+    (groups[g] || (groups[g] = [])).push(t);
   });
   const manifest = { format: 'brik', version: BRIK_VERSION, model: input.model, arch: input.arch, chat: input.chat,
-    tokenizer: input.tokenizer, shards: shardMeta, tensors: tensors };
+    tokenizer: input.tokenizer, shards: [], tensors: {} };
+  const shards = Object.keys(groups).sort(groupRank).map(function (g, id) {
+    const packed = packShard(groups[g], id);
+    const file = 'shard-' + String(id).padStart(4, '0') + '.brik';
+    Object.keys(packed.entries).forEach(function (n) { manifest.tensors[n] = packed.entries[n]; });
+    manifest.shards.push({ id: id, file: file, byteLength: packed.buffer.length });
+    return { file: file, bytes: packed.buffer };
+  });
   return { manifest: manifest, shards: shards };
 }
 

@@ -167,3 +167,44 @@ def test_python_and_js_writers_agree(tmp_path):
     for name, (start, ln) in json.loads(r.stdout).items():
         e, b = C.tensor_bytes(p, name)
         assert bytes(f[start:start + ln]) == bytes(b)
+
+
+def test_js_reader_and_writer_error_messages(tmp_path):
+    """The JS module raises the reference's messages on the same bad inputs as the Python one."""
+    if NODE is None:
+        pytest.skip("node not installed")
+    _, manifest, shards, f = build()
+    (tmp_path / "f.brik").write_bytes(f)
+    mlen = struct.unpack_from("<I", f, 8)[0]
+    script = (
+        "const c = require('./brimkern_amd/js/container'); const fs = require('fs');"
+        f"const f = new Uint8Array(fs.readFileSync({json.dumps(str(tmp_path / 'f.brik'))}));"
+        "function msg(fn) { try { fn(); return null; } catch (e) { return e.message; } }"
+        "const bad = f.slice(); bad[0] = 0; const p = c.parseBrik(f);"
+        "const shards = p.manifest.shards.map(function (s) { const b = c.computeShardBases(p.manifest.shards)[s.id];"
+        " return { file: s.file, bytes: p.data.slice(b, b + s.byteLength) }; });"
+        "const grown = shards.map(function (s, i) { return i === 1 ? { file: s.file, bytes: new Uint8Array(s.bytes.length + 16) } : s; });"
+        "console.log(JSON.stringify({"
+        " magic: msg(function () { c.parseBrikHeader(bad); }),"
+        " header: msg(function () { c.parseBrikHeader(f.subarray(0, 11)); }),"
+        f" manifest: msg(function () {{ c.parseBrikHeader(f.subarray(0, {12 + mlen - 1})); }}),"
+        f" headerOnly: msg(function () {{ c.parseBrikHeader(f.subarray(0, {12 + mlen})); }}),"
+        " tensorCut: msg(function () { c.tensorBytes(c.parseBrik(f.subarray(0, f.length - 40)), 'blk.1.ffn_down.weight'); }),"
+        " tensorGone: msg(function () { c.tensorBytes(p, 'nope'); }),"
+        " missing: msg(function () { c.serializeBrik(p.manifest, shards.slice(1)); }),"
+        " resized: msg(function () { c.serializeBrik(p.manifest, grown); }),"
+        " roundTrip: Buffer.from(c.serializeBrik(p.manifest, shards)).equals(Buffer.from(f)) }));"
+    )
+    r = subprocess.run([NODE, "-e", script], cwd=ROOT, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    m = json.loads(r.stdout)
+    assert m["magic"].startswith("BRIK: sceau magique absent (")
+    assert m["header"] == "BRIK: fichier tronqué (en-tête)"
+    assert m["manifest"] == "BRIK: manifeste tronqué"
+    assert m["headerOnly"] is None
+    assert m["tensorCut"] == "BRIK: tenseur tronqué : blk.1.ffn_down.weight"
+    assert m["tensorGone"] == "BRIK: tenseur absent : nope"
+    assert m["missing"] == f"shard manquant : {manifest['shards'][0]['file']}"
+    s1 = manifest["shards"][1]
+    assert m["resized"] == f"taille de shard incohérente pour {s1['file']} : {s1['byteLength'] + 16} ≠ {s1['byteLength']}"
+    assert m["roundTrip"] is True
