@@ -393,19 +393,28 @@ def moe_cfg5(ctx, steps, warmup):
     yu = ctx.alloc(4 * R * F)
     yd = ctx.alloc(4 * R * H)
 
-    def step(i):
+    def step3(i):
         c = i % copies
         ctx.moe_matmul_t_q4(xg, ro, *reps["gate"].planes(c), yg, E, R, H, F)
         ctx.moe_matmul_t_q4(xg, ro, *reps["up"].planes(c), yu, E, R, H, F)
         ctx.moe_matmul_t_q4(xd, ro, *reps["down"].planes(c), yd, E, R, F, H)
+
+    def step(i):     # gate and up in one launch on one staging of x (brik_moe_matmul_t_q4_x2), then down
+        c = i % copies
+        ctx.moe_matmul_t_q4_x2(xg, ro, reps["gate"].planes(c), yg, reps["up"].planes(c), yu, E, R, H, F)
+        ctx.moe_matmul_t_q4(xd, ro, *reps["down"].planes(c), yd, E, R, F, H)
+    ms3 = time_loop(ctx, step3, max(steps, 6), 3)
     ms = time_loop(ctx, step, max(steps, 6), 3)
     wbytes = 2 * q_bytes("q4", E * F, H) + q_bytes("q4", E * H, F)
     flops = 2.0 * R * (2 * H * F + F * H)
     for bb in list(r.buf for r in reps.values()) + [xg, xd, ro, yg, yu, yd]:
         ctx.free(bb)
     return {"us": round(ms * 1e3, 2), "weight_GBps": round(wbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 2), "rows": int(R),
-            "max_rows_per_expert": int(np.diff(row_off).max()), "min_rows_per_expert": int(np.diff(row_off).min())}
+            "max_rows_per_expert": int(np.diff(row_off).max()), "min_rows_per_expert": int(np.diff(row_off).min()),
+            "launches": "gate+up: brik_xprep_f16 + brik_gemmg_q4 (grid.z = 2); down: brik_xprep_f16 + brik_gemmg_q4",
+            "us_three_calls": round(ms3 * 1e3, 2)}
 
 
 def cpu_model():
@@ -523,6 +532,43 @@ def hbm_traffic(layers):
         return None, None
 
 
+def headline_only(ctx, a):
+    """The headline plan alone: settle, warmup, timed steps (no per-matrix, small-M or F3 extras)."""
+    plan, b = build_layer_plan(ctx, a.layers)
+    settle(ctx, lambda i: plan.run(), a.settle)
+    ms = time_loop(ctx, lambda i: plan.run(), a.steps, a.warmup)
+    plan.destroy()
+    for r in b["reps"].values():
+        ctx.free(r.buf)
+    for bb in (b["xa"], b["xd"], b["ybuf"]):
+        ctx.free(bb)
+    return {"us": round(ms * 1e3, 2), "GBps": round(b["nbytes"] / (ms * 1e-3) / 1e9, 1)}
+
+
+def f3_only(ctx, a):
+    plan, b = build_layer_plan(ctx, a.layers)
+    plan.destroy()
+    out = decode_layers_fused(ctx, b["reps"], a.layers, a.steps, a.warmup, not a.no_graph)
+    for r in b["reps"].values():
+        ctx.free(r.buf)
+    for bb in (b["xa"], b["xd"], b["ybuf"]):
+        ctx.free(bb)
+    return out
+
+
+ONLY = {
+    "headline": headline_only,
+    "f3": f3_only,
+    "cfg1": lambda ctx, a: gemv_single_cfg(ctx, "q8", 896, 4864, 600, a.steps, a.warmup),
+    "cfg3": lambda ctx, a: gemv_single_cfg(ctx, "q3", 2560, 151936, 700, a.steps, a.warmup),
+    "cfg4": lambda ctx, a: gemm_cfg4(ctx, a.steps, a.warmup),
+    "moe": lambda ctx, a: moe_cfg5(ctx, a.steps, a.warmup),
+    "conv": lambda ctx, a: conv_f4(ctx, a.steps, a.warmup),
+    "f16w": lambda ctx, a: f16w_f4(ctx, a.steps, a.warmup),
+    "f1": lambda ctx, a: quantize_f1(ctx, a.steps, a.warmup),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -537,10 +583,20 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="time the fused decoder layers eagerly only (rocprofv3's kernel trace has crashed in "
                          "hipGraphLaunch on the box)")
+    ap.add_argument("--only", choices=sorted(ONLY),
+                    help="run one workload alone and print its result (for profiler runs; not the bench line)")
     ap.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.probe:
         probe(args.layers)
+        return
+    if args.only:
+        from brimkern_amd import Context
+        ctx = Context(0)
+        log(f"bench: {args.only} alone")
+        print(json.dumps({"only": args.only, "steps": args.steps, "warmup": args.warmup,
+                          "result": ONLY[args.only](ctx, args)}), flush=True)
+        ctx.close()
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this path has no multi-GPU form in this build (it would shard "

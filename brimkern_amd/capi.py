@@ -46,6 +46,7 @@ SIGNATURES = {
     "brik_matmul_t_q3": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_matmul_t_q4_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I]),
     "brik_moe_matmul_t_q4": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    "brik_moe_matmul_t_q4_x2": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "brik_dequant_q8_f32": (_I, [_P, _P, _P, _P, _Z]),
     "brik_dequant_q4_f32": (_I, [_P, _P, _P, _P, _P, _Z]),
     "brik_dequant_q3_f32": (_I, [_P, _P, _P, _P, _P, _P, _Z]),
@@ -271,6 +272,12 @@ class Context:
     def moe_matmul_t_q4(self, x, row_off, nib, sc, mn, y, E, R, K, N):
         self._check(self.lib.brik_moe_matmul_t_q4(self.handle, _addr(x), _addr(row_off), _addr(nib),
                                                   _addr(sc), _addr(mn), _addr(y), E, R, K, N))
+
+    def moe_matmul_t_q4_x2(self, x, row_off, a, y_a, b, y_b, E, R, K, N):
+        """Two stacked q4 tensors (``a``, ``b``: (nib, sc, mn) address triples) on the same routed rows,
+        one launch (brik_moe_matmul_t_q4_x2)."""
+        self._check(self.lib.brik_moe_matmul_t_q4_x2(self.handle, _addr(x), _addr(row_off), *map(_addr, a),
+                                                     _addr(y_a), *map(_addr, b), _addr(y_b), E, R, K, N))
 
     def gemv_plan(self, fmt: str, jobs) -> "GemvPlan":
         """jobs: iterable of dicts with x, p0, p1, sc, mn, y (device addresses), K, N, and optionally the

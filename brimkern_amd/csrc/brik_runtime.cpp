@@ -144,6 +144,7 @@ struct brik_ctx {
     hipFunction_t gemv[3][kNumGemvVariants] = {};
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
     hipFunction_t gemm[3][kNumGemmTiles] = {};
+    hipFunction_t gemmg[kNumGemmTiles] = {};    // expert-grouped q4 kernels (brik_gemmg_q4_*)
     hipFunction_t gemm_sk[3][3] = {};      // split-K few-row kernels, KSL = 2, 4, 8
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
@@ -447,31 +448,58 @@ int gemm_splitk(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, con
     return launch(c, K_SPLITK_REDUCE, (unsigned)(blocks < 2048 ? blocks : 2048), 1, 256, 0, rargs);
 }
 
-// The tile kernel over staged rows: dense when row_off is null, expert-grouped otherwise.
+// A second q4 weight tensor multiplied by the same staged rows in the same launch (an MoE layer's gate
+// and up projections): its codes, scales, mins and output.
+struct WeightPair {
+    const void* p0;
+    const void* sc;
+    const void* mn;
+    float* y;
+};
+
+// The tile kernel over staged rows: dense when row_off is null, expert-grouped (q4) otherwise; `pair`
+// (grouped only) adds the second tensor as blockIdx.z == 1.
 int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
              const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E,
-             const Scratch* fixed = nullptr)
+             const Scratch* fixed = nullptr, const WeightPair* pair = nullptr)
 {
-    if (use_splitk(c, f, rows, K, N, E, fixed)) return gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E);
+    if (use_splitk(c, f, rows, K, N, E, fixed)) {
+        HIP_TRY_RC(gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E));
+        if (!pair) return BRIK_OK;
+        return gemm_splitk(c, f, xh, rscale, pair->p0, p1, pair->sc, pair->mn, pair->y, rows, K, N, row_off, E);
+    }
     int Mi = rows, Ki = K, Ni = N, Ei = E;
     const int t = gemm_tile(c, rows, N, K, E);
     const GemmTile& gt = kGemmTiles[t];
     const int bn = gt.bn();
-    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
-    if (!row_off)
+    if (!row_off) {
+        void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
         return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, gt.threads(), 0,
                          args);
+    }
+    if (f != F_Q4) return fail(c, BRIK_EINVAL, "expert-grouped GEMM: q4 weights only");
     // blockIdx.y enumerates (expert, row tile) pairs: at most ceil(rows / BM) + E of them
-    return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(N, bn), gemm_tiles(rows, gt.bm) + (unsigned)E,
-                     gt.threads(), 0, args);
+    const void* p0b = pair ? pair->p0 : p0;
+    const void* scb = pair ? pair->sc : sc;
+    const void* mnb = pair ? pair->mn : mn;
+    float* yb = pair ? pair->y : y;
+    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &p0b, &scb, &mnb, &yb};
+    const unsigned gx = gemm_tiles(N, bn), gy = gemm_tiles(rows, gt.bm) + (unsigned)E, gz = pair ? 2u : 1u;
+    HIP_TRY(c, hipSetDevice(c->device));
+    HIP_TRY(c, hipModuleLaunchKernel(c->gemmg[t], gx, gy, gz, gt.threads(), 1, 1, 0, c->stream, args, nullptr));
+    return BRIK_OK;
 }
 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
 // tile kernel.
 int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc, const void* mn,
-         float* y, int rows, int K, int N, const int* row_off, int E, const Scratch* fixed = nullptr)
+         float* y, int rows, int K, int N, const int* row_off, int E, const Scratch* fixed = nullptr,
+         const WeightPair* pair = nullptr)
 {
-    if (K == 0) return fill_zero(c, y, (size_t)rows * N);   // empty sums
+    if (K == 0) {                                           // empty sums
+        if (pair) HIP_TRY_RC(fill_zero(c, pair->y, (size_t)rows * N));
+        return fill_zero(c, y, (size_t)rows * N);
+    }
     long Kp;
     uint16_t* xh;
     float* rscale;
@@ -481,7 +509,7 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
         HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
     }
-    return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed);
+    return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed, pair);
 }
 
 // GEMV variant for a launch over `rows` rows in total (one matrix or a plan's jobs) with shortest row
@@ -833,6 +861,13 @@ int brik_create(int device, brik_ctx** out)
             if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->gemm[f][t]) != hipSuccess ||
                 max_threads < (int)kGemmTiles[t].threads())
                 return bail(BRIK_EMODULE);
+            if (f != fmt_index(F_Q4)) continue;
+            snprintf(name, sizeof name, "brik_gemmg_q4_%dx%d%s%s", kGemmTiles[t].bm, kGemmTiles[t].tn,
+                     kGemmTiles[t].nw == 8 ? "w8" : "", pf);
+            if (hipModuleGetFunction(&c->gemmg[t], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+            if (hipFuncGetAttribute(&max_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, c->gemmg[t]) != hipSuccess ||
+                max_threads < (int)kGemmTiles[t].threads())
+                return bail(BRIK_EMODULE);
         }
     // the fixed scratch of brik_matmul_t_q4_noalloc, with this device current (once per device)
     c->scratch_err = brik_scratch_resolve(device, &c->scratch, &c->scratch_bytes);
@@ -950,22 +985,38 @@ int brik_matmul_t_q3(brik_ctx* c, const float* x, const uint32_t* lo, const uint
     return matmul(c, F_Q3, x, lo, hi, sc, mn, y, M, K, N);
 }
 
-int brik_moe_matmul_t_q4(brik_ctx* c, const float* x, const int32_t* row_off, const uint8_t* nib,
-                         const uint16_t* sc, const uint16_t* mn, float* y, int E, int R, int K, int N)
+static int moe(brik_ctx* c, const char* who, const float* x, const int32_t* row_off, const uint8_t* nib,
+               const uint16_t* sc, const uint16_t* mn, float* y, const WeightPair* pair, int E, int R, int K, int N)
 {
     if (!c) return BRIK_EINVAL;
-    if (E < 0 || R < 0) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: negative E=%d or R=%d", E, R);
-    int r = check_mm(c, "moe_matmul_t_q4", x, nib, nullptr, sc, mn, y, R, K, N, F_Q4);
+    if (E < 0 || R < 0) return fail(c, BRIK_EINVAL, "%s: negative E=%d or R=%d", who, E, R);
+    int r = check_mm(c, who, x, nib, nullptr, sc, mn, y, R, K, N, F_Q4);
+    if (r == BRIK_OK && pair)
+        r = check_mm(c, who, x, pair->p0, nullptr, pair->sc, pair->mn, pair->y, R, K, N, F_Q4);
     if (r != BRIK_OK || R == 0 || N == 0 || E == 0) return r;
-    if (!row_off) return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: row_off is null");
-    if (!aligned(row_off, 4)) return fail(c, BRIK_EALIGN, "moe_matmul_t_q4: row_off must be 4-byte aligned");
-    if (K == 0) return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
+    if (!row_off) return fail(c, BRIK_EINVAL, "%s: row_off is null", who);
+    if (!aligned(row_off, 4)) return fail(c, BRIK_EALIGN, "%s: row_off must be 4-byte aligned", who);
+    if (K == 0) return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E, nullptr, pair);
     // the scale and min planes of all experts are addressed through one resource, in 16-group chunks
     const unsigned long long groups = (unsigned long long)E * N * (K / kGroup);
     if (groups < 16 || groups * 2 >= (1ull << 32))
-        return fail(c, BRIK_EINVAL, "moe_matmul_t_q4: E*N*K = %llu weight elements is outside [512, 2^35)",
+        return fail(c, BRIK_EINVAL, "%s: E*N*K = %llu weight elements is outside [512, 2^35)", who,
                     groups * kGroup);
-    return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E);
+    return gemm(c, F_Q4, x, nib, nullptr, sc, mn, y, R, K, N, row_off, E, nullptr, pair);
+}
+
+int brik_moe_matmul_t_q4(brik_ctx* c, const float* x, const int32_t* row_off, const uint8_t* nib,
+                         const uint16_t* sc, const uint16_t* mn, float* y, int E, int R, int K, int N)
+{
+    return moe(c, "moe_matmul_t_q4", x, row_off, nib, sc, mn, y, nullptr, E, R, K, N);
+}
+
+int brik_moe_matmul_t_q4_x2(brik_ctx* c, const float* x, const int32_t* row_off, const uint8_t* nib_a,
+                            const uint16_t* sc_a, const uint16_t* mn_a, float* y_a, const uint8_t* nib_b,
+                            const uint16_t* sc_b, const uint16_t* mn_b, float* y_b, int E, int R, int K, int N)
+{
+    const WeightPair pair{nib_b, sc_b, mn_b, y_b};
+    return moe(c, "moe_matmul_t_q4_x2", x, row_off, nib_a, sc_a, mn_a, y_a, &pair, E, R, K, N);
 }
 
 static int dequant(brik_ctx* c, Kern k, const char* who, void** args, size_t n, const void* p0,

@@ -22,16 +22,17 @@
 //      place (bits 4-7) in the mantissa of 64.0h reads as 64 + q; one packed subtract and one packed
 //      FMA then give the dequantized pair (q s + m), rounded once to f16 whatever the scale; the
 //      code pairs (j, j + 4) this produces from 8 packed codes fix the
-//      [0 4 1 5 2 6 3 7] order. Scales and mins are staged in LDS per 4 steps by coalesced loads. The
-//      epilogue multiplies by rscale[m] (exact) and stores y through LDS with 16-byte stores.
+//      [0 4 1 5 2 6 3 7] order. Scales and mins are staged in LDS a few steps at a time by coalesced
+//      loads. The epilogue multiplies by rscale[m] (exact) and stores y through LDS with 16-byte stores.
 // f16 (not bf16) operands: 11-bit significands keep the normwise error near 3e-4, inside the 1e-3
 // bar; bf16's 8 bits would not. The row scaling removes f16's range limit on activations.
 //
-// Dense mode (row_off == nullptr): a 1-D grid ordered so the M tiles of one N tile go to the same
-// XCD (blocks are dealt to the 8 XCDs round-robin) and share its L2 for the weight tile. Grouped
-// (MoE) mode: rows of x / y are sorted by expert; expert e owns rows [row_off[e], row_off[e+1]) and
-// weight slice e of a stacked [E, N, K] q-tensor; blockIdx.y enumerates (expert, BM-row tile)
-// pairs and blocks past the last pair exit.
+// Dense kernels (brik_gemm_*): a 1-D grid ordered so the M tiles of one N tile go to the same XCD
+// (blocks are dealt to the 8 XCDs round-robin) and share its L2 for the weight tile. Grouped (MoE)
+// kernels (brik_gemmg_q4_*): rows of x / y are sorted by expert; expert e owns rows
+// [row_off[e], row_off[e+1]) and weight slice e of a stacked [E, N, K] q-tensor; blockIdx.y enumerates
+// (expert, BM-row tile) pairs, blocks past the last pair exit, and blockIdx.z picks one of two weight
+// tensors multiplied by the same rows.
 #include "common.h"
 
 namespace {
@@ -179,9 +180,11 @@ __device__ __forceinline__ bool find_expert_tile(const int* __restrict__ row_off
         }
     }
     __syncthreads();
-    e = res[0];
-    m0 = res[1];
-    m_end = res[2];
+    // block-uniform values read from LDS land in VGPRs: move them to scalar registers, or every buffer
+    // resource built from them would be a per-lane value (a waterfall loop around each buffer load)
+    e = __builtin_amdgcn_readfirstlane(res[0]);
+    m0 = __builtin_amdgcn_readfirstlane(res[1]);
+    m_end = __builtin_amdgcn_readfirstlane(res[2]);
     return e >= 0 && m0 >= 0 && m0 < m_end;
 }
 
@@ -194,9 +197,9 @@ __device__ __forceinline__ bool find_expert_tile(const int* __restrict__ row_off
 // x steps go through PF + 2 LDS buffers of BM rows x 256 bytes, filled by direct global->LDS loads
 // PF + 1 steps ahead (PF below). The 16-byte chunk c of row r sits at position c ^ (r & 15) of the row, so the 16 rows
 // that one 16-lane phase of an A-fragment read touches hit 16 different bank groups.
-// Scales and mins go through LDS too, a chunk of 4 steps (16 groups, 32 bytes of each column) at a
-// time, double buffered: the block loads them with 32-byte-per-column global->LDS loads (2 lanes per
-// column) instead of every lane fetching its own 2-byte values from a different cache line.
+// Scales and mins go through LDS too, a chunk of SCH steps (SG groups, 2 SG bytes of each column) at
+// a time, double buffered: the block loads them with coalesced 16-byte-per-lane global->LDS loads
+// instead of every lane fetching its own 2-byte values from a different cache line.
 // PF: how many steps ahead the W codes are loaded (a register ring of PF + 1 steps); the x buffers
 // then number PF + 2, filled PF + 1 steps ahead. Loads complete in issue order, so waiting for the x
 // of the next step also waits for every W load issued before it: W runs PF steps ahead only when x
@@ -213,9 +216,17 @@ struct Tile {
     static constexpr int XQ = PF_ + 2;                    // x buffers
     static constexpr int A_BYTES = XQ * XBUF;
     static constexpr int PLANES = FMT == FMT_Q8 ? 1 : 2;  // scales (and mins)
-    static constexpr int SPLANE = BN * 32;                // one plane of one scale chunk
+    // scale chunks: SG groups (SCH = SG / 4 steps) of every column of the block, SG * 2 bytes per column
+    // and plane; loaded 16 bytes per lane, LPC lanes per column. A chunk loaded at the first step of the
+    // previous chunk must have landed when the last step of that chunk reads it, SCH - 1 steps later:
+    // the wait of a step covers the loads issued PF steps before it, so SCH >= PF + 1. Small chunks
+    // keep the LDS of a block small (two blocks of the 64-row 8-wave tile fit a CU with SG = 8).
+    // The chunk is also a whole number of 1024-byte load instructions per wave.
+    static constexpr bool sg_fits(int sg) { return sg / 4 >= PF_ + 1 && (PLANES * BN * sg * 2) % (NW_ * 1024) == 0; }
+    static constexpr int SG = sg_fits(8) ? 8 : sg_fits(16) ? 16 : 32, SCH = SG / 4, LPC = SG / 8;
+    static constexpr int SPLANE = BN * SG * 2;            // one plane of one scale chunk
     static constexpr int SBUF = PLANES * SPLANE;          // one scale chunk
-    static constexpr int NSD = PLANES * TN_;              // scale-chunk load instructions per wave
+    static constexpr int NSD = PLANES * SPLANE / 1024 / NW_;   // scale-chunk load instructions per wave
     static constexpr int S_OFF = A_BYTES;                 // scale chunks follow the x buffers
     static constexpr int CLD = BN + 4;                    // epilogue staging row stride (floats)
     static constexpr int C_BYTES = 32 * CLD * 4;          // one 32-row block
@@ -228,6 +239,7 @@ struct Tile {
     // PF - 1 steps issued after it, and the W of the current step
     static constexpr int VM_NEXT_X = (PF_ - 1) * (W_OPS + XI) + W_OPS;
     static_assert(BM_ % 32 == 0 && TN_ >= 1 && (NW_ == 4 || NW_ == 8) && BM_ % (4 * NW_) == 0 && TM % RF == 0 &&
+                  SCH >= PF_ + 1 && NSD * NW_ * 1024 == PLANES * SPLANE &&
                   SMEM <= 160 * 1024 && PF_ >= 1 && VM_NEXT_X < 64 && XI + (PF_ - 1) * (W_OPS + XI) < 64,
                   "tile shape");
 };
@@ -252,7 +264,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 // column block the code loads of W step t + 1, in slices 0-1; then, after the barrier in slice 4, the
 // direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (NW i + w), +1024)
 // of the buffer, 16 bytes per lane: row 4 (NW i + w) + (lane >> 4), stored chunk lane & 15) over slices
-// 4-7. Every fourth step also loads the next scale chunk, in slice 4.
+// 4-7. The first step of every scale chunk (every SCH steps) also loads the next chunk, in slice 4.
 template <int FMT, class T>
 struct Loader {
     static constexpr int TN = T::TN, XI = T::XI, NSD = T::NSD;
@@ -267,7 +279,7 @@ struct Loader {
     brsrc_t p0, p1, rsc, rmn, rx;
     uint32_t colg[TN], sg[TN], xoff[XI];
     int h, G, wave;
-    uint32_t slim;                 // last scale-chunk start that ends inside the plane (groups - 16)
+    uint32_t slim;                 // last scale-chunk start that ends inside the plane (groups - SG)
     unsigned char* lds;
     // scale-chunk loads: flat group index of this lane's column for instruction k, and its LDS offset
     // within a chunk buffer
@@ -321,16 +333,18 @@ struct Loader {
             if (slice_of(u) == sl) op(u, f, xstep, xbuf);
     }
 
-    // Scale chunk v (groups 16 v .. 16 v + 15 of every column of the block) into the chunk buffer at
-    // byte offset `buf`: instruction k of wave w covers plane (NW k + w) / (BN / 32), columns
-    // 32 ((NW k + w) % (BN / 32)) + lane / 2, 16 bytes (8 groups) per lane. A chunk that would run past the end of the
-    // plane is moved back to end inside it; the reader shifts its index by the same amount.
+    // Scale chunk v (groups SG v .. SG v + SG - 1 of every column of the block) into the chunk buffer at
+    // byte offset `buf`: instruction k of wave w covers plane (NW k + w) / CPI and the 64 / LPC columns
+    // that follow (NW k + w) % CPI times as many (CPI = instructions per plane), 16 bytes (8 groups)
+    // per lane, LPC lanes per column. A chunk that would run past the end of the plane is moved back
+    // to end inside it; the reader shifts its index by the same amount.
     __device__ __forceinline__ void scale_chunk(int v, uint32_t buf)
     {
+        constexpr int CPI = T::SPLANE / 1024;
 #pragma unroll
         for (int k = 0; k < NSD; ++k) {
-            const uint32_t plane = (uint32_t)(T::NW * k + wave) / (T::BN / 32);
-            const uint32_t off = (min(sdc[k] + 16 * v, slim) + 8 * (threadIdx.x & 1)) * 2;
+            const uint32_t plane = (uint32_t)(T::NW * k + wave) / CPI;
+            const uint32_t off = (min(sdc[k] + T::SG * v, slim) + 8 * (threadIdx.x % T::LPC)) * 2;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(plane ? rmn : rsc, (lds_void_t*)(lds + buf + sdst[k]), 16,
                                                      off, 0, 0, 0);
         }
@@ -342,15 +356,15 @@ struct Loader {
     {
         const int g0 = 4 * t + 2 * h;
         const bool la = g0 < G, lb = g0 + 1 < G;
-        const uint32_t F0 = 16 * (uint32_t)(t >> 2);
+        const uint32_t F0 = T::SG * (uint32_t)(t / T::SCH);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const uint32_t F = sg[j] + F0;
             // shift of a moved chunk; a live group's position is at most 15, and the clamp keeps reads of
             // dead groups (masked below) within the chunk buffer and its 64-byte pad
-            const uint32_t pos = min((F - min(F, slim)) + 4 * (t & 3) + 2 * h, 15u);
+            const uint32_t pos = min((F - min(F, slim)) + 4 * (t % T::SCH) + 2 * h, (uint32_t)T::SG - 1);
             const uint32_t col = (uint32_t)(wave * 32 * TN + 32 * j + (lane & 31));
-            const unsigned char* ps = lds + buf + col * 32 + pos * 2;
+            const unsigned char* ps = lds + buf + col * (T::SG * 2) + pos * 2;
             const uint32_t s0 = *(const uint16_t*)ps, s1 = *(const uint16_t*)(ps + 2);
             f[j].s[0] = la ? s0 : 0u;
             f[j].s[1] = lb ? s1 : 0u;
@@ -555,7 +569,9 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
     }
 }
 
-template <int FMT, class T>
+// GROUPED: the expert-grouped (MoE) form, a separate instantiation so that the dense kernels hold
+// none of its code; blockIdx.y enumerates (expert, row tile) pairs, found by the block-wide lookup.
+template <int FMT, class T, bool GROUPED>
 __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
                                           const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                           const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
@@ -570,19 +586,10 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     const int steps = Kp / GK;                 // even, >= 2
     int m0, m_end = M, n0, e = 0;
 
-    if (row_off) {
+    if constexpr (GROUPED) {
         n0 = blockIdx.x * BN;
-        int remaining = blockIdx.y;
-        for (; e < E; ++e) {
-            const int cnt = row_off[e + 1] - row_off[e];
-            const int tiles = (cnt + BM - 1) / BM;
-            if (remaining < tiles) break;
-            remaining -= tiles;
-        }
-        if (e >= E) return;     // uniform across the block, before any barrier
-        m0 = row_off[e] + remaining * BM;
-        m_end = min(row_off[e + 1], M);     // a malformed table cannot push stores past row M
-        if (m0 < 0 || m0 >= m_end) return;
+        // uniform across the block (the lookup ends with a barrier), before any other barrier
+        if (!find_expert_tile<BM>(row_off, E, (int)blockIdx.y, M, e, m0, m_end)) return;
     } else {
         const int nMT = (M + BM - 1) / BM, nNT = (N + BN - 1) / BN;
         const int b = blockIdx.x, gsz = 8 * nMT;
@@ -615,7 +622,7 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         r0 = make_rsrc(p0 + (size_t)e * wel / 4, (uint32_t)(wel / 4));
         r1 = make_rsrc(p1 + (size_t)e * wel / 8, (uint32_t)(wel / 8));
     }
-    const uint32_t sgroups = (uint32_t)((size_t)(row_off ? E : 1) * N * G);
+    const uint32_t sgroups = (uint32_t)((size_t)(GROUPED ? E : 1) * N * G);
     rsc = make_rsrc(sc, sgroups * 2);
     if constexpr (FMT != FMT_Q8) rmn = make_rsrc(mn, sgroups * 2);
 
@@ -645,11 +652,12 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         ld.sg[j] = (uint32_t)gbase + ld.colg[j];   // the same group in the whole scale plane
     }
     // scale chunks (the host routes planes of fewer than 16 groups elsewhere)
-    ld.slim = sgroups - 16;
+    ld.slim = sgroups - T::SG;
 #pragma unroll
     for (int k = 0; k < T::NSD; ++k) {
-        const int gi = T::NW * k + wave, cb = gi % (BN / 32), plane = gi / (BN / 32);
-        ld.sdc[k] = (uint32_t)gbase + (uint32_t)(min(n0 + 32 * cb + (lane >> 1), N - 1) * G);
+        constexpr int CPI = T::SPLANE / 1024, COLS = 64 / T::LPC;   // instructions per plane, columns each
+        const int gi = T::NW * k + wave, cb = gi % CPI, plane = gi / CPI;
+        ld.sdc[k] = (uint32_t)gbase + (uint32_t)(min(n0 + COLS * cb + lane / T::LPC, N - 1) * G);
         ld.sdst[k] = (uint32_t)(plane * T::SPLANE + cb * 1024);
     }
 
@@ -703,20 +711,20 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     // t + PF into slot (t + PF) mod R and, once every wave is past its barrier, x step t + PF + 1 into
     // the buffer of step t - 1. The loop body runs R steps so that the ring slots are fixed registers.
     // Loads past the end are clamped, and the operands prepared for step `steps` are not used.
-    const int nchunks = (steps + 3) / 4;
+    const int nchunks = (steps + T::SCH - 1) / T::SCH;
     uint32_t xq = 0;
     int t = 0;
     do {     // steps >= 2: no loop guard for the prologue loads to sink past
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             ld.begin(min(t + T::PF, steps - 1));
-            const int v = t >> 2;
+            const int v = t / T::SCH;
             const uint32_t x1 = xq + 1 == (uint32_t)T::XQ ? 0u : xq + 1;     // buffer of step t + 1
             const uint32_t xf = xq == 0 ? (uint32_t)T::XQ - 1 : xq - 1;       // buffer of step t - 1
             mma_step<FMT, T>(smem, aoff, xq * T::XBUF, x1 * T::XBUF, wr[r], go, a, b, acc, ld, wr[(r + 1) % R],
                              wr[(r + T::PF) % R], gn, t, min(t + T::PF + 1, steps - 1), xf * T::XBUF,
-                             (t & 3) == 0, min(v + 1, nchunks - 1), T::S_OFF + ((v + 1) & 1) * T::SBUF,
-                             T::S_OFF + (((t + 1) >> 2) & 1) * T::SBUF, lane);
+                             t % T::SCH == 0, min(v + 1, nchunks - 1), T::S_OFF + ((v + 1) & 1) * T::SBUF,
+                             T::S_OFF + (((t + 1) / T::SCH) & 1) * T::SBUF, lane);
 #pragma unroll
             for (int j = 0; j < TN; ++j) go[j] = gn[j];
             xq = x1;
@@ -942,35 +950,56 @@ __device__ __forceinline__ void gemm_sk_body(const uint16_t* __restrict__ xh, co
 }  // namespace
 
 // Kernel names: brik_gemm_<fmt>_<BM>x<TN> (block tile BM x 128 TN, 256 threads = 4 waves) and
-// brik_gemm_<fmt>_<BM>x<TN>w8 (BM x 256 TN, 512 threads = 8 waves); the runtime picks the tile.
-#define BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, NW_, PF_, SUFFIX)                                               \
+// brik_gemm_<fmt>_<BM>x<TN>w8 (BM x 256 TN, 512 threads = 8 waves), with p<PF> for the prefetching
+// tiles; the runtime picks the tile. Dense kernels ignore row_off / E.
+#define BRIK_GEMM_DENSE(FMTN, FMT, BM_, TN_, NW_, PF_, SUFFIX)                                            \
     extern "C" __global__ __launch_bounds__(64 * NW_) void brik_gemm_##FMTN##_##BM_##x##TN_##SUFFIX(      \
         const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
         float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E)               \
     {                                                                                                     \
-        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
+        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, false>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
     }
-#define BRIK_GEMM(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, 1, )
-#define BRIK_GEMM8(FMTN, FMT, BM_, TN_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, 1, w8)
-// prefetching tiles: brik_gemm_<fmt>_<BM>x<TN>[w8]p<PF>
-#define BRIK_GEMMP(FMTN, FMT, BM_, TN_, PF_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 4, PF_, p##PF_)
-#define BRIK_GEMM8P(FMTN, FMT, BM_, TN_, PF_) BRIK_GEMM_NW(FMTN, FMT, BM_, TN_, 8, PF_, w8p##PF_)
+// Expert-grouped kernels, q4 only: brik_gemmg_q4_<tile>. Blocks with blockIdx.z == 1 multiply the
+// second matrix (codes p0b, scales scb, mins mnb, into yb) by the same staged rows: the gate and up
+// projections of an MoE layer in one launch. Experts hold few rows, so a launch has few blocks per
+// CU, each bound by the latency of its steps: the narrow 8-wave tiles (BM <= 64, one column block per
+// wave, PF = 1) are held to 128 VGPRs so that two blocks share a CU.
+constexpr int grouped_waves_per_eu(int bm, int tn, int nw, int pf) { return bm <= 64 && tn == 1 && nw == 8 && pf == 1 ? 4 : 1; }
+#define BRIK_GEMM_GROUPED(FMTN, FMT, BM_, TN_, NW_, PF_, SUFFIX)                                          \
+    extern "C" __global__ __launch_bounds__(64 * NW_)                                                     \
+    __attribute__((amdgpu_waves_per_eu(grouped_waves_per_eu(BM_, TN_, NW_, PF_))))                                 \
+    void brik_gemmg_##FMTN##_##BM_##x##TN_##SUFFIX(                                                       \
+        const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
+        const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
+        float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E,               \
+        const uint8_t* __restrict__ p0b, const uint16_t* __restrict__ scb, const uint16_t* __restrict__ mnb, \
+        float* __restrict__ yb)                                                                           \
+    {                                                                                                     \
+        if (blockIdx.z) {                                                                                 \
+            p0 = p0b;                                                                                     \
+            sc = scb;                                                                                     \
+            mn = mnb;                                                                                     \
+            y = yb;                                                                                       \
+        }                                                                                                 \
+        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, true>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
+    }
 
-// Tiles in the order of the runtime's table: (BM, TN[, 8 waves]).
-#define BRIK_GEMM_FMT(FMTN, FMT)                                                       \
-    BRIK_GEMM(FMTN, FMT, 128, 2) BRIK_GEMM(FMTN, FMT, 128, 1) BRIK_GEMM(FMTN, FMT, 128, 3) \
-    BRIK_GEMM(FMTN, FMT, 64, 2) BRIK_GEMM(FMTN, FMT, 64, 1) BRIK_GEMM(FMTN, FMT, 64, 3)    \
-    BRIK_GEMM(FMTN, FMT, 32, 2) BRIK_GEMM(FMTN, FMT, 32, 1) BRIK_GEMM(FMTN, FMT, 32, 3)    \
-    BRIK_GEMM(FMTN, FMT, 96, 2) BRIK_GEMM(FMTN, FMT, 96, 1) BRIK_GEMM(FMTN, FMT, 96, 3)    \
-    BRIK_GEMM8(FMTN, FMT, 128, 1) BRIK_GEMM8(FMTN, FMT, 96, 1) BRIK_GEMM8(FMTN, FMT, 64, 1) \
-    BRIK_GEMM8(FMTN, FMT, 32, 1) BRIK_GEMM8(FMTN, FMT, 64, 2)                              \
-    BRIK_GEMM8P(FMTN, FMT, 32, 1, 4) BRIK_GEMM8P(FMTN, FMT, 64, 1, 3) BRIK_GEMMP(FMTN, FMT, 32, 1, 4) \
-    BRIK_GEMMP(FMTN, FMT, 64, 1, 3) BRIK_GEMM8P(FMTN, FMT, 32, 1, 2) BRIK_GEMM8P(FMTN, FMT, 64, 1, 2)
+// Tiles in the order of the runtime's table: (BM, TN, waves, PF, name suffix).
+#define BRIK_GEMM_TILE_LIST(X, FMTN, FMT)                                                                     \
+    X(FMTN, FMT, 128, 2, 4, 1, ) X(FMTN, FMT, 128, 1, 4, 1, ) X(FMTN, FMT, 128, 3, 4, 1, )                \
+    X(FMTN, FMT, 64, 2, 4, 1, ) X(FMTN, FMT, 64, 1, 4, 1, ) X(FMTN, FMT, 64, 3, 4, 1, )                   \
+    X(FMTN, FMT, 32, 2, 4, 1, ) X(FMTN, FMT, 32, 1, 4, 1, ) X(FMTN, FMT, 32, 3, 4, 1, )                   \
+    X(FMTN, FMT, 96, 2, 4, 1, ) X(FMTN, FMT, 96, 1, 4, 1, ) X(FMTN, FMT, 96, 3, 4, 1, )                   \
+    X(FMTN, FMT, 128, 1, 8, 1, w8) X(FMTN, FMT, 96, 1, 8, 1, w8) X(FMTN, FMT, 64, 1, 8, 1, w8)            \
+    X(FMTN, FMT, 32, 1, 8, 1, w8) X(FMTN, FMT, 64, 2, 8, 1, w8)                                           \
+    X(FMTN, FMT, 32, 1, 8, 4, w8p4) X(FMTN, FMT, 64, 1, 8, 3, w8p3) X(FMTN, FMT, 32, 1, 4, 4, p4)         \
+    X(FMTN, FMT, 64, 1, 4, 3, p3) X(FMTN, FMT, 32, 1, 8, 2, w8p2) X(FMTN, FMT, 64, 1, 8, 2, w8p2)
 
-BRIK_GEMM_FMT(q4, FMT_Q4)
-BRIK_GEMM_FMT(q8, FMT_Q8)
-BRIK_GEMM_FMT(q3, FMT_Q3)
+BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q4, FMT_Q4)
+BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q8, FMT_Q8)
+BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q3, FMT_Q3)
+BRIK_GEMM_TILE_LIST(BRIK_GEMM_GROUPED, q4, FMT_Q4)
 
 // Split-K few-row kernels: brik_gemm_sk_<fmt>_k<KSL> (32 x 128 tiles, 256 threads, K slices of at most
 // KSL steps of 128); grid (column tiles, row tiles or expert row-tile pairs, slices).

@@ -139,6 +139,15 @@ int brik_moe_matmul_t_q4(brik_ctx *ctx, const float *x_sorted, const int32_t *ro
                          const uint8_t *nibbles, const uint16_t *scales, const uint16_t *mins,
                          float *y_sorted, int E, int R, int K, int N);
 
+/* Two expert-stacked q4 tensors of the same shape [E, N, K] on the same routed rows (an MoE layer's
+ * gate and up projections): y_a = x . deq(W_a)^T and y_b = x . deq(W_b)^T per expert, as two
+ * brik_moe_matmul_t_q4 calls would give them bit for bit, with one staging of x and one launch. No
+ * reference counterpart (the reference has no MoE path); same requirements as brik_moe_matmul_t_q4. */
+int brik_moe_matmul_t_q4_x2(brik_ctx *ctx, const float *x_sorted, const int32_t *row_off,
+                            const uint8_t *nibbles_a, const uint16_t *scales_a, const uint16_t *mins_a,
+                            float *y_a, const uint8_t *nibbles_b, const uint16_t *scales_b,
+                            const uint16_t *mins_b, float *y_b, int E, int R, int K, int N);
+
 /* ---- grouped decode GEMV plans -------------------------------------------------------------
  * The reference records a whole decoder layer, 7 recMM calls, into one command encoder and submits
  * once (recordLayerKV, src/lib/webgpu/kernels.ts:1690-1744; decodeTopKQ8 :1908-1969). A plan is the
