@@ -573,6 +573,18 @@ napi_value MoeMatmulQ4(napi_env env, napi_callback_info info)   // (ctx, x, rowO
     return undefined(env);
 }
 
+napi_value MoeMatmulQ4x2(napi_env env, napi_callback_info info)
+// (ctx, x, rowOff, nibA, scA, mnA, yA, nibB, scB, mnB, yB, E, R, K, N)
+{
+    brik_ctx* c; void* p[10]; int32_t i[4];
+    if (!parse(env, info, &c, p, 10, i, 4)) return nullptr;
+    if (check(env, c, brik_moe_matmul_t_q4_x2(c, (const float*)p[0], (const int32_t*)p[1], (const uint8_t*)p[2],
+                                              (const uint16_t*)p[3], (const uint16_t*)p[4], (float*)p[5],
+                                              (const uint8_t*)p[6], (const uint16_t*)p[7], (const uint16_t*)p[8],
+                                              (float*)p[9], i[0], i[1], i[2], i[3]))) return nullptr;
+    return undefined(env);
+}
+
 napi_value DequantQ8(napi_env env, napi_callback_info info)   // (ctx, codes, sc, out, n)
 {
     brik_ctx* c; void* p[3]; int32_t i[1];
@@ -843,6 +855,7 @@ napi_value Init(napi_env env, napi_value exports)
         {"matmulQ4", nullptr, MatmulQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"matmulQ3", nullptr, MatmulQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"moeMatmulQ4", nullptr, MoeMatmulQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"moeMatmulQ4x2", nullptr, MoeMatmulQ4x2, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ8", nullptr, DequantQ8, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ4", nullptr, DequantQ4, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"dequantQ3", nullptr, DequantQ3, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

@@ -203,6 +203,12 @@ class Engine {
     return ySorted;
   }
 
+  // Two stacked [E, N, K] q4 weights on the same routed rows (an MoE layer's gate and up), one launch.
+  moeMatmulQ4x2(xSorted, rowOff, wa, ya, wb, yb, E, R, K, N) {
+    this.native.moeMatmulQ4x2(this.ctx, xSorted, rowOff, wa.nib, wa.sc, wa.mn, ya, wb.nib, wb.sc, wb.mn, yb, E, R, K, N);
+    return [ya, yb];
+  }
+
   // Grouped decode GEMV plan: jobs [{x, w, y, K, N}] (one format), executed by one launch per run().
   // Optional per job, the fusions of brik_gemv_job_ex (the ops recordLayerKV records around recMM,
   // kernels.ts:1701-1741): norm (RMSNorm gain buffer), eps, onePlus (Gemma 1 + w gain), gate (the

@@ -257,6 +257,43 @@ async function main() {
     wb.destroy();
   }
 
+  // 11. expert-grouped q4 (moeMatmulQ4 / moeMatmulQ4x2): per-expert rows against the JS sum over the
+  // dequantized expert slice; the two-tensor call equals two single calls bit for bit
+  {
+    const r = rng(4321);
+    const E = 3, K = 128, N = 40, rowOff = [0, 5, 5, 12], R = 12;
+    const mk = async function () {
+      const wm = Float32Array.from({ length: E * N * K }, function () { return r() * 2 - 1; });
+      const bytes = await engine.quantizeToBytes('F32', new Uint8Array(wm.buffer), E * N * K, 'q4');
+      return { bytes: bytes, h: engine.weightFromBlob('q4', bytes, E * N * K) };
+    };
+    const wa = await mk(), wb = await mk();
+    const xv = Float32Array.from({ length: R * K }, function () { return r() * 2 - 1; });
+    const xb = engine.uploadGpu(xv), rb = engine.uploadGpuRaw(Int32Array.from(rowOff));
+    const ys = [0, 1, 2, 3].map(function () { return engine.alloc(R * N * 4); });
+    engine.moeMatmulQ4(xb, rb, wa.h, ys[0], E, R, K, N);
+    engine.moeMatmulQ4(xb, rb, wb.h, ys[1], E, R, K, N);
+    engine.moeMatmulQ4x2(xb, rb, wa.h, ys[2], wb.h, ys[3], E, R, K, N);
+    const got = [];
+    for (const y of ys) got.push(await engine.readBackAsync(y, R * N * 4));
+    const same = function (a, b) { return a.every(function (v, i) { return Object.is(v, b[i]); }); };
+    check('moeMatmulQ4x2 equals two moeMatmulQ4 calls', same(got[0], got[2]) && same(got[1], got[3]), {});
+    [[wa, got[0]], [wb, got[1]]].forEach(function (pair, t) {
+      const wd = cpuref.dequantize('q4', cpuref.planes('q4', pair[0].bytes, E * N * K), E * N * K);
+      let worst = 0;
+      for (let e = 0; e < E; e++) {
+        const m = rowOff[e + 1] - rowOff[e];
+        if (!m) continue;
+        const ref = cpuref.matmulRef(xv.subarray(rowOff[e] * K, rowOff[e + 1] * K), wd.subarray(e * N * K, (e + 1) * N * K), m, K, N);
+        worst = Math.max(worst, normwise(pair[1].subarray(rowOff[e] * N, rowOff[e + 1] * N), ref));
+      }
+      check('moeMatmulQ4 tensor ' + t + ' vs JS per-expert sum', worst <= 1e-3, { rel: worst });
+    });
+    [xb, rb].concat(ys).forEach(function (b) { b.destroy(); });
+    engine.destroyWeight(wa.h);
+    engine.destroyWeight(wb.h);
+  }
+
   const failed = results.filter(function (r) { return !r.ok; }).length;
   process.stdout.write(JSON.stringify({ checks: results.length, failed: failed }) + '\n');
   process.exit(failed === 0 ? 0 : 1);

@@ -25,7 +25,7 @@ EXPORTS = ["deviceCount", "createContext", "alloc", "free", "h2d", "d2h", "sync"
            "timerEnd", "matmulQ8", "matmulQ4", "matmulQ3", "moeMatmulQ4", "dequantQ8", "dequantQ4", "dequantQ3",
            "gemvPlanCreate", "gemvPlanRun", "gemvPlanDestroy", "logitsTopK", "lmHeadTopK", "quantize",
            "f16ToF32", "conv2d", "matmulF16W", "allocBuffer", "bufferPtr", "freeBuffer", "liveBuffers",
-           "readbackAsync", "selfValidate"]
+           "readbackAsync", "selfValidate", "moeMatmulQ4x2"]
 
 
 def node(script, timeout=120):
