@@ -359,7 +359,7 @@ def f16w_f4(ctx, steps, warmup, cache_bytes=768 << 20):
                         "frac": round(b1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies},
             "gemm_M512": {"us": round(msm * 1e3, 2), "TFLOPs": round(tf, 1),
                           "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)},
-            "kernels": "brik_gemv_f16w_v8 (M = 1); brik_xprep_f16 + brik_gemm_f16w (M = 512)"}
+            "kernels": "brik_gemv_f16w_v8 (M = 1); brik_xprep_f16 + brik_gemm_f16_96x1w8 (M = 512)"}
 
 
 def gemm_cfg4(ctx, steps, warmup):

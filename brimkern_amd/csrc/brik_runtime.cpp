@@ -79,6 +79,7 @@ constexpr GemmTile kGemmTiles[] = {{128, 2, 4, 1}, {128, 1, 4, 1}, {128, 3, 4, 1
                                    {32, 1, 8, 1},  {64, 2, 8, 1},  {32, 1, 8, 4},  {64, 1, 8, 3}, {32, 1, 4, 4},
                                    {64, 1, 4, 3},  {32, 1, 8, 2},  {64, 1, 8, 2}};
 constexpr int kNumGemmTiles = sizeof(kGemmTiles) / sizeof(kGemmTiles[0]);
+
 constexpr unsigned kCUs = 256;                 // MI355X compute units
 constexpr long kGemmKPad = 256;                // staged activation rows are padded to this many halves
 constexpr size_t kGemvMaxLds = 64 * 1024;      // dynamic LDS budget of one GEMV block
@@ -145,6 +146,7 @@ struct brik_ctx {
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
     hipFunction_t gemm[3][kNumGemmTiles] = {};
     hipFunction_t gemmg[kNumGemmTiles] = {};    // expert-grouped q4 kernels (brik_gemmg_q4_*)
+    hipFunction_t gemm_f16[kNumGemmTiles] = {};   // f16-weight tiles (TN = 1, PF = 1 only; others null)
     hipFunction_t gemm_sk[3][3] = {};      // split-K few-row kernels, KSL = 2, 4, 8
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr, ev_end = nullptr;
@@ -872,6 +874,13 @@ int brik_create(int device, brik_ctx** out)
                 max_threads < (int)kGemmTiles[t].threads())
                 return bail(BRIK_EMODULE);
         }
+    for (int t = 0; t < kNumGemmTiles; ++t) {
+        const GemmTile& g = kGemmTiles[t];
+        if (g.tn != 1 || g.pf != 1) continue;
+        char name[64];
+        snprintf(name, sizeof name, "brik_gemm_f16_%dx1%s", g.bm, g.nw == 8 ? "w8" : "");
+        if (hipModuleGetFunction(&c->gemm_f16[t], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+    }
     // the fixed scratch of brik_matmul_t_q4_noalloc, with this device current (once per device)
     c->scratch_err = brik_scratch_resolve(device, &c->scratch, &c->scratch_bytes);
     constexpr int kSkl[3] = {2, 4, 8};
@@ -1211,6 +1220,36 @@ int brik_matmul_t_f16w(brik_ctx* c, const float* x, const uint16_t* w, float* y,
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};
         HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((M + 3) / 4), 1, 256, 0, args));
     }
+    if (K % kGroup == 0) {
+        // the tiled MFMA GEMM with f16 weights (TN = 1 tiles): a forced tile, or the one of fewest
+        // 256-CU rounds x tile area, as the quantized GEMM picks its dense tiles
+        int best = -1;
+        if (c->opt_tile > 0) {
+            best = c->opt_tile - 1;
+            if (!c->gemm_f16[best]) return fail(c, BRIK_EINVAL, "matmul_t_f16w: tile %d has no f16 form", c->opt_tile);
+        } else {
+            double best_cost = 0;
+            for (int t = 0; t < kNumGemmTiles; ++t) {
+                const GemmTile& g = kGemmTiles[t];
+                if (!c->gemm_f16[t] || g.nw != 8) continue;
+                const double rounds = std::ceil((double)gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn()) / kCUs);
+                const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
+                const double cost = rounds * g.bm * (double)g.bn() * penalty;
+                if (best < 0 || cost < best_cost) {
+                    best = t;
+                    best_cost = cost;
+                }
+            }
+        }
+        const GemmTile& g = kGemmTiles[best];
+        const void* none = nullptr;
+        const int* no_rows = nullptr;
+        int Ei = 0;
+        void* targs[] = {&xh, &rscale, &w, &none, &none, &none, &y, &Mi, &Ki, &Ni, &no_rows, &Ei};
+        return launch_fn(c, c->gemm_f16[best], gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn()), 1, g.threads(), 0,
+                         targs);
+    }
+    // K % 32 != 0: the LDS-tiled kernel (K steps of 32 with zero-filled tails)
     void* args[] = {&xh, &rscale, &w, &y, &Mi, &Ki, &Ni, &Kpi};
     return launch(c, K_GEMM_F16W, (unsigned)((N + 127) / 128), (unsigned)((M + 63) / 64), 256, 0, args);
 }

@@ -6,7 +6,7 @@
 #define BRIK_GROUP 32
 
 // Plane formats: the value is the code's bit width, as in the reference's q8web/q4web/q3web.
-enum { FMT_Q8 = 8, FMT_Q4 = 4, FMT_Q3 = 3 };
+enum { FMT_Q8 = 8, FMT_Q4 = 4, FMT_Q3 = 3, FMT_F16 = 16 };   // F16: IEEE half weights (the MFMA GEMM only)
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));

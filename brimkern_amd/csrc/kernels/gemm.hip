@@ -216,7 +216,7 @@ struct Tile {
     static constexpr int XBUF = BM_ * XROW;               // one x buffer
     static constexpr int XQ = PF_ + 2;                    // x buffers
     static constexpr int A_BYTES = XQ * XBUF;
-    static constexpr int PLANES = FMT == FMT_Q8 ? 1 : 2;  // scales (and mins)
+    static constexpr int PLANES = FMT == FMT_Q8 ? 1 : FMT == FMT_F16 ? 0 : 2;  // scales (and mins); f16 has none
     // scale chunks: SG groups (SCH = SG / 4 steps) of every column of the block, SG * 2 bytes per column
     // and plane; loaded 16 bytes per lane, LPC lanes per column. A chunk loaded at the first step of the
     // previous chunk must have landed when the last step of that chunk reads it, SCH - 1 steps later:
@@ -235,7 +235,7 @@ struct Tile {
     static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
     static constexpr int SMEM = MAIN > RF * C_BYTES ? MAIN : RF * C_BYTES;
     // vector-memory loads per step: W codes, then the x chunks
-    static constexpr int W_OPS = (FMT == FMT_Q4 ? 2 : 4) * TN_;
+    static constexpr int W_OPS = (FMT == FMT_Q4 ? 2 : FMT == FMT_F16 ? 8 : 4) * TN_;
     // loads a wave may still have in flight once the x of the next step has landed: the W and x of the
     // PF - 1 steps issued after it, and the W of the current step
     static constexpr int VM_NEXT_X = (PF_ - 1) * (W_OPS + XI) + W_OPS;
@@ -252,10 +252,11 @@ struct Tile {
 
 // Per lane and 32-column block: the codes of two groups of one column, and their f16 scale and min
 // bits (one group per register, low half). Words: q4 2 x 4 nibble dwords; q8 2 x 8 code dwords; q3
-// 2 x 2 dwords of 2-bit fields, then 2 dwords of high bits (one byte per 8 codes).
+// 2 x 2 dwords of 2-bit fields, then 2 dwords of high bits (one byte per 8 codes); f16 2 x 16 dwords of
+// halves in k order.
 template <int FMT>
 struct WCodes {
-    uint32_t w[FMT == FMT_Q8 ? 16 : FMT == FMT_Q4 ? 8 : 6];
+    uint32_t w[FMT == FMT_F16 ? 32 : FMT == FMT_Q8 ? 16 : FMT == FMT_Q4 ? 8 : 6];
     uint32_t s[2], m[2];
 };
 
@@ -269,7 +270,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 template <int FMT, class T>
 struct Loader {
     static constexpr int TN = T::TN, XI = T::XI, NSD = T::NSD;
-    static constexpr int CODE_OPS = FMT == FMT_Q4 ? 2 : 4;
+    static constexpr int CODE_OPS = FMT == FMT_Q4 ? 2 : FMT == FMT_F16 ? 8 : 4;
     static constexpr int W_OPS = CODE_OPS * TN;
     static_assert(W_OPS == T::W_OPS, "load count");
     static constexpr int OPS = W_OPS + XI;
@@ -285,13 +286,16 @@ struct Loader {
     // scale-chunk loads: flat group index of this lane's column for instruction k, and its LDS offset
     // within a chunk buffer
     uint32_t sdc[NSD], sdst[NSD];
-    // of the W step being loaded: clamped group indices
+    // of the W step being loaded: clamped group indices, and (f16) whether each group is live
     uint32_t ia[TN], ib[TN];
+    bool la, lb;
 
     __device__ __forceinline__ void begin(int wstep)
     {
         const int g0 = 4 * wstep + 2 * h;
         const uint32_t ga = (uint32_t)min(g0, G - 1), gb = (uint32_t)min(g0 + 1, G - 1);
+        la = g0 < G;
+        lb = g0 + 1 < G;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             ia[j] = colg[j] + ga;
@@ -312,6 +316,14 @@ struct Loader {
         if constexpr (FMT == FMT_Q4) {
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, (k ? ib[j] : ia[j]) * 16, 0, 0);
             w.w[4 * k + 0] = v.x; w.w[4 * k + 1] = v.y; w.w[4 * k + 2] = v.z; w.w[4 * k + 3] = v.w;
+        } else if constexpr (FMT == FMT_F16) {
+            // 16 bytes (8 halves) k of the 64-byte group: a dead group (past the row end, clamped to a
+            // live one for the load) reads as zeros, so an Inf or NaN weight there cannot meet the zero
+            // padding of x
+            const bool live = (k >> 2) ? lb : la;
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, ((k >> 2) ? ib[j] : ia[j]) * 64 + 16 * (k & 3), 0, 0);
+            w.w[4 * k + 0] = live ? v.x : 0u; w.w[4 * k + 1] = live ? v.y : 0u;
+            w.w[4 * k + 2] = live ? v.z : 0u; w.w[4 * k + 3] = live ? v.w : 0u;
         } else if constexpr (FMT == FMT_Q8) {
             const uint32_t g = (k >> 1) ? ib[j] : ia[j];
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, g * 32 + 16 * (k & 1), 0, 0);
@@ -476,6 +488,13 @@ __device__ __forceinline__ half8_t b_frag(const WCodes<FMT>& f, const GroupOps& 
     u32x4_t o;
     if constexpr (FMT == FMT_Q4) {
         o = deq8_q4(f.w[sl], g.s2[e], g.m2[e], g.k);
+    } else if constexpr (FMT == FMT_F16) {
+        // halves w0 .. w7 (dwords d0 .. d3) -> pairs (w0 w4) (w1 w5) (w2 w6) (w3 w7), the staged x order
+        const uint32_t* d = f.w + 4 * sl;
+        o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);
+        o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);
+        o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);
+        o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);
     } else if constexpr (FMT == FMT_Q8) {
         o = deq8_q8(f.w[2 * sl], f.w[2 * sl + 1], g.s2[e]);
     } else {
@@ -537,7 +556,8 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
             if (schunk) ld.scale_chunk(sv, sdst);
         }
         ld.issue(sl, wl, xstep, xbuf);
-        if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
+        if constexpr (FMT != FMT_F16)
+            if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
         if (sl < 7) {
 #pragma unroll
             for (int i = 0; i < TM; ++i) a[nxt][i] = *(const half8_t*)(lds + abuf + aoff[sl + 1] + i * 32 * XROW);
@@ -559,7 +579,7 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
         // the next slice's A reads first, then each MFMA with a share of the dequantization; the
         // scheduling barrier keeps every slice's reads one slice ahead of their use
-        constexpr int VALU_PER = (FMT == FMT_Q8 ? 12 : 16) * TN / (TM * TN);
+        constexpr int VALU_PER = (FMT == FMT_F16 ? 4 : FMT == FMT_Q8 ? 12 : 16) * TN / (TM * TN);
         __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
 #pragma unroll
         for (int g = 0; g < TM * TN; ++g) {
@@ -615,7 +635,10 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     const size_t gbase = (size_t)e * N * G;    // flat group offset of the expert slice
     const brsrc_t rx = make_rsrc(xh, (uint32_t)((size_t)M * Kp * 2));
     brsrc_t r0, r1 = rx, rsc, rmn = rx;
-    if constexpr (FMT == FMT_Q8) {
+    if constexpr (FMT == FMT_F16) {
+        static_assert(!GROUPED, "f16 weights: dense only");
+        r0 = make_rsrc(p0, (uint32_t)(wel * 2));
+    } else if constexpr (FMT == FMT_Q8) {
         r0 = make_rsrc(p0 + (size_t)e * wel, (uint32_t)wel);
     } else if constexpr (FMT == FMT_Q4) {
         r0 = make_rsrc(p0 + (size_t)e * wel / 2, (uint32_t)(wel / 2));
@@ -624,8 +647,8 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         r1 = make_rsrc(p1 + (size_t)e * wel / 8, (uint32_t)(wel / 8));
     }
     const uint32_t sgroups = (uint32_t)((size_t)(GROUPED ? E : 1) * N * G);
-    rsc = make_rsrc(sc, sgroups * 2);
-    if constexpr (FMT != FMT_Q8) rmn = make_rsrc(mn, sgroups * 2);
+    rsc = make_rsrc(sc, FMT == FMT_F16 ? 0u : sgroups * 2);
+    if constexpr (FMT != FMT_Q8) rmn = make_rsrc(mn, FMT == FMT_F16 ? 0u : sgroups * 2);
 
     const int tid = threadIdx.x, lane = tid & 63;
     Loader<FMT, T> ld;
@@ -698,7 +721,7 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     // x step 0 (and scale chunk 0) landed: at most x step 1 and the PF - 1 later (W, x) pairs in flight
     wait_vm<XI + (T::PF - 1) * (T::W_OPS + XI)>();
     step_barrier();
-    ld.read_scales(wr[0], 0, T::S_OFF, lane);
+    if constexpr (FMT != FMT_F16) ld.read_scales(wr[0], 0, T::S_OFF, lane);
     const DeqConst dk = DeqConst::make();
 #pragma unroll
     for (int i = 0; i < TM; ++i) a[0][i] = *(const half8_t*)(smem + aoff[0] + i * 32 * XROW);
@@ -1001,6 +1024,12 @@ BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q4, FMT_Q4)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q8, FMT_Q8)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q3, FMT_Q3)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_GROUPED, q4, FMT_Q4)
+// f16 weights (the reference's MATMUL_T_F16W for M > 1, K % 32 == 0): the one-column-block tiles,
+// brik_gemm_f16_<BM>x1[w8]; the codes are the weights, so there is nothing to dequantize
+BRIK_GEMM_DENSE(f16, FMT_F16, 128, 1, 8, 1, w8) BRIK_GEMM_DENSE(f16, FMT_F16, 96, 1, 8, 1, w8)
+BRIK_GEMM_DENSE(f16, FMT_F16, 64, 1, 8, 1, w8) BRIK_GEMM_DENSE(f16, FMT_F16, 32, 1, 8, 1, w8)
+BRIK_GEMM_DENSE(f16, FMT_F16, 128, 1, 4, 1, ) BRIK_GEMM_DENSE(f16, FMT_F16, 96, 1, 4, 1, )
+BRIK_GEMM_DENSE(f16, FMT_F16, 64, 1, 4, 1, ) BRIK_GEMM_DENSE(f16, FMT_F16, 32, 1, 4, 1, )
 
 // Split-K few-row kernels: brik_gemm_sk_<fmt>_k<KSL> (32 x 128 tiles, 256 threads, K slices of at most
 // KSL steps of 128); grid (column tiles, row tiles or expert row-tile pairs, slices).
