@@ -485,11 +485,13 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
     const void* scb = pair ? pair->sc : sc;
     const void* mnb = pair ? pair->mn : mn;
     float* yb = pair ? pair->y : y;
-    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &p0b, &scb, &mnb, &yb};
-    const unsigned gx = gemm_tiles(N, bn), gy = gemm_tiles(rows, gt.bm) + (unsigned)E, gz = pair ? 2u : 1u;
-    HIP_TRY(c, hipSetDevice(c->device));
-    HIP_TRY(c, hipModuleLaunchKernel(c->gemmg[t], gx, gy, gz, gt.threads(), 1, 1, 0, c->stream, args, nullptr));
-    return BRIK_OK;
+    int mats = pair ? 2 : 1;
+    void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &p0b, &scb, &mnb, &yb, &mats};
+    // 1-D grid: (pairs rounded up to a multiple of 8) x column tiles x matrices; the kernel decodes the
+    // index so that every block of one pair lands on one XCD
+    const unsigned pairs = gemm_tiles(rows, gt.bm) + (unsigned)E;
+    const unsigned blocks = (pairs + 7) / 8 * 8 * gemm_tiles(N, bn) * (unsigned)mats;
+    return launch_fn(c, c->gemmg[t], blocks, 1, gt.threads(), 0, args);
 }
 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the

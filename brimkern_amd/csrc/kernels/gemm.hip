@@ -592,12 +592,13 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
 
 // GROUPED: the expert-grouped (MoE) form, a separate instantiation so that the dense kernels hold
 // none of its code; blockIdx.y enumerates (expert, row tile) pairs, found by the block-wide lookup.
+// gtile / gcol (grouped only): this block's (expert, row tile) pair and column tile.
 template <int FMT, class T, bool GROUPED>
 __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
                                           const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                           const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
                                           float* __restrict__ y, int M, int K, int N,
-                                          const int* __restrict__ row_off, int E)
+                                          const int* __restrict__ row_off, int E, int gtile = 0, int gcol = 0)
 {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, XI = T::XI, NT = T::NT;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
@@ -608,9 +609,9 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     int m0, m_end = M, n0, e = 0;
 
     if constexpr (GROUPED) {
-        n0 = blockIdx.x * BN;
+        n0 = gcol * BN;
         // uniform across the block (the lookup ends with a barrier), before any other barrier
-        if (!find_expert_tile<BM>(row_off, E, (int)blockIdx.y, M, e, m0, m_end)) return;
+        if (!find_expert_tile<BM>(row_off, E, gtile, M, e, m0, m_end)) return;
     } else {
         const int nMT = (M + BM - 1) / BM, nNT = (N + BN - 1) / BN;
         const int b = blockIdx.x, gsz = 8 * nMT;
@@ -984,9 +985,13 @@ __device__ __forceinline__ void gemm_sk_body(const uint16_t* __restrict__ xh, co
     {                                                                                                     \
         gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, false>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
     }
-// Expert-grouped kernels, q4 only: brik_gemmg_q4_<tile>. Blocks with blockIdx.z == 1 multiply the
-// second matrix (codes p0b, scales scb, mins mnb, into yb) by the same staged rows: the gate and up
-// projections of an MoE layer in one launch. Experts hold few rows, so a launch has few blocks per
+// Expert-grouped kernels, q4 only: brik_gemmg_q4_<tile>, a 1-D grid over (pair, column tile, matrix)
+// with `mats` matrices: the second (codes p0b, scales scb, mins mnb, into yb) is multiplied by the same
+// staged rows (the gate and up projections of an MoE layer in one launch). Blocks are dealt to the 8
+// XCDs round-robin by linear index, so the index is decoded to put every block of one (expert, row
+// tile) pair, all its column tiles of both matrices, on the same XCD, back to back: the pair's staged
+// rows then come from HBM once and stay in that XCD's L2 for all of them. Indices past the last pair
+// (the grid is rounded up to a multiple of 8 pairs) exit. Experts hold few rows, so a launch has few blocks per
 // CU, each bound by the latency of its steps: the narrow 8-wave tiles (BM <= 64, one column block per
 // wave, PF = 1) are held to 128 VGPRs so that two blocks share a CU.
 constexpr int grouped_waves_per_eu(int bm, int tn, int nw, int pf) { return bm <= 64 && tn == 1 && nw == 8 && pf == 1 ? 4 : 1; }
@@ -998,15 +1003,20 @@ constexpr int grouped_waves_per_eu(int bm, int tn, int nw, int pf) { return bm <
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
         float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E,               \
         const uint8_t* __restrict__ p0b, const uint16_t* __restrict__ scb, const uint16_t* __restrict__ mnb, \
-        float* __restrict__ yb)                                                                           \
+        float* __restrict__ yb, int mats)                                                                 \
     {                                                                                                     \
-        if (blockIdx.z) {                                                                                 \
+        using T_ = Tile<FMT, BM_, TN_, NW_, PF_>;                                                         \
+        const int per = (N + T_::BN - 1) / T_::BN * mats;   /* blocks of one pair */                      \
+        const int s = (int)(blockIdx.x >> 3), r = s % per;                                                \
+        const int gtile = s / per * 8 + (int)(blockIdx.x & 7);                                            \
+        if (gtile >= (M + BM_ - 1) / BM_ + E) return;                                                     \
+        if (r % mats) {                                                                                   \
             p0 = p0b;                                                                                     \
             sc = scb;                                                                                     \
             mn = mnb;                                                                                     \
             y = yb;                                                                                       \
         }                                                                                                 \
-        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, true>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
+        gemm_body<FMT, T_, true>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E, gtile, r / mats);   \
     }
 
 // Tiles in the order of the runtime's table: (BM, TN, waves, PF, name suffix).
