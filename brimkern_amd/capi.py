@@ -19,7 +19,7 @@ BRIK_EVALID = -7
 BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT = 1, 2
 BRIK_GEMV_VARIANTS = 9
 BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES = 3, 23
-BRIK_OPT_PLAN_STAGE, BRIK_OPT_PLAN_SETS, BRIK_OPT_SPLITK = 4, 5, 6
+BRIK_OPT_PLAN_STAGE, BRIK_OPT_PLAN_SETS, BRIK_OPT_SPLITK, BRIK_OPT_GEMV_BLOCKS = 4, 5, 6, 7
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # every exported symbol of include/brik.h with (restype, argtypes)

@@ -105,7 +105,7 @@ enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
 // LDS bytes of a staged activation row (xprep.h), per group plus one zero group: q8 / q3 96 limb
 // bytes, an f32 sum and an int32 exponent; q4 96 bytes of digit planes and 16 bytes of sums and
 // exponent. Then a flag, the RMSNorm factor and 16 reduction slots, 80 bytes (BRIK_XSTAGE_TAIL).
-size_t gemv_lds(int K, Fmt f) { return (size_t)(f == F_Q4 ? 112 : 104) * (K / kGroup + 1) + 80; }
+size_t gemv_lds(int K, Fmt f) { return (size_t)(f == F_Q8 ? 104 : 112) * (K / kGroup + 1) + 80; }
 int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 }  // namespace
@@ -156,6 +156,7 @@ struct brik_ctx {
     int opt_plan_stage = 0;  // plans: 0 auto, 1 in-block staging, 2 staging launch
     int opt_plan_sets = 0;   // plans: 0 auto, else row sets per block
     int opt_splitk = 0;      // few-row GEMMs: 0 auto, 1 never split-K, 2 split-K whenever it applies
+    int opt_gemv_blocks = 0; // single-matrix GEMV: 0 auto, else grid cap
     void* ws = nullptr;    // GEMM workspace: f16 activation rows, then per-row scales (grow-only)
     size_t ws_bytes = 0;
     void* tws = nullptr;   // top-k workspace: lane maxima, then LM-head logits (grow-only)
@@ -563,7 +564,8 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     const int v = gemv_variant(c, f, N, K, stage1);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
-    const unsigned gx = sets < kGemvMaxBlocks ? sets : kGemvMaxBlocks;
+    const unsigned cap = c->opt_gemv_blocks > 0 ? (unsigned)c->opt_gemv_blocks : kGemvMaxBlocks;
+    const unsigned gx = sets < cap ? sets : cap;
     const size_t lds = gemv_lds(K, f) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
     const bool gemv_fits = lds <= kGemvMaxLds;
     // the MFMA GEMM reads scales in 16-group chunks, so a matrix of fewer than 16 groups (N * K < 512)
@@ -1655,6 +1657,11 @@ int brik_set_option(brik_ctx* c, int key, int value)
     case BRIK_OPT_PLAN_SETS:
         if (value < 0 || value > 64) return fail(c, BRIK_EINVAL, "BRIK_OPT_PLAN_SETS: %d not in 0..64", value);
         c->opt_plan_sets = value;
+        return BRIK_OK;
+    case BRIK_OPT_GEMV_BLOCKS:
+        if (value < 0 || value > (int)kGemvMaxBlocks)
+            return fail(c, BRIK_EINVAL, "BRIK_OPT_GEMV_BLOCKS: %d not in 0..%u", value, kGemvMaxBlocks);
+        c->opt_gemv_blocks = value;
         return BRIK_OK;
     default:
         return fail(c, BRIK_EINVAL, "unknown option %d", key);

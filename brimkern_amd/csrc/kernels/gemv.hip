@@ -6,9 +6,9 @@
 // Arithmetic. The group scale factors out of the dot product:
 //   y_n = sum_g [ s_ng * sum_{k in g} x_k q_nk + m_ng * sum_{k in g} x_k ].
 // x is staged once per block as 24-bit block floating point (xprep.h), so sum x_k q_nk is an exact
-// int32 dot product, rescaled once per group: for q8 and q3 of int8 limbs with the codes unpacked to
-// bytes (v_dot4_i32_i8); for q4 of signed 4-bit digits with the packed nibbles as loaded
-// (v_dot8_i32_i4), which leaves no unpacking at all.
+// int32 dot product, rescaled once per group: for q8 of int8 limbs with the int8 codes as loaded
+// (v_dot4_i32_i8); for q4 and q3 of signed 4-bit digits with the codes as signed nibbles
+// (v_dot8_i32_i4): the q4 nibbles as loaded, the q3 ones assembled from its 2-bit and 1-bit planes.
 // A one-hot x reproduces deq(W) bit-exactly: the single product s*q*2^21 and its rescale are exact
 // and the final fmaf(m, 1, s*q) rounds q*s + m once, as the reference's dequantize does.
 //
@@ -89,33 +89,13 @@ __device__ __forceinline__ void load_grp(Grp<FMT>& d, const Rs& rs, uint32_t gi,
     d.s = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (gi + gconst) * 2, gstep * 2, 0);
 }
 
-// The group's 32 codes as 8 dwords of bytes, in brik::code_pos order.
+// The group's 32 q8 codes as 8 dwords of bytes, in element order (the staged limbs' order).
 template <int FMT>
 __device__ __forceinline__ void unpack(const Grp<FMT>& d, uint32_t (&b)[8])
 {
-    if constexpr (FMT == FMT_Q4) {
+    static_assert(FMT == FMT_Q8, "q4 and q3 run on code nibbles (code_nibbles)");
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            b[2 * j] = d.w[j] & 0x0f0f0f0fu;
-            b[2 * j + 1] = (d.w[j] >> 4) & 0x0f0f0f0fu;
-        }
-    } else if constexpr (FMT == FMT_Q8) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) { b[j] = d.w0[j]; b[4 + j] = d.w1[j]; }
-    } else {
-        // lo words L0 (codes 0..15) and L1 (16..31), 2 bits per code; hi word, 1 bit per code.
-        // Byte dword s holds codes s, s+8, s+16, s+24. The 2-bit fields of codes s and s+8 (s < 4)
-        // sit in bytes 0 and 2 of L0, of codes s+16 and s+24 in bytes 0 and 2 of L1; for s >= 4 in
-        // bytes 1 and 3.
-        const uint32_t p0 = __builtin_amdgcn_perm(d.l.y, d.l.x, 0x06040200u);   // L0.b0 L0.b2 L1.b0 L1.b2
-        const uint32_t p1 = __builtin_amdgcn_perm(d.l.y, d.l.x, 0x07050301u);   // L0.b1 L0.b3 L1.b1 L1.b3
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const uint32_t lo = ((s < 4 ? p0 : p1) >> (2 * (s & 3))) & 0x03030303u;
-            const uint32_t hi = ((d.h >> s) & 0x01010101u) << 2;
-            b[s] = lo | hi;
-        }
-    }
+    for (int j = 0; j < 4; ++j) { b[j] = d.w0[j]; b[4 + j] = d.w1[j]; }
 }
 
 // sum_{k in g} x_k q_k * 2^-(e_g - 22) as exact int32 limb dot products, combined in f32.
@@ -276,19 +256,56 @@ struct Work {
     }
 };
 
-// q4 on v_dot8_i32_i4: x as signed 4-bit digit planes (xprep.h, xstage_d), codes as loaded. Per
-// (row, group): 4 XORs make the codes signed nibbles q - 8, 24 dot8 run the Horner chain over the six
-// digit planes (most significant first, shifting by 4 between planes; the last shift also adds the
-// staged 8 * sum X that undoes the -8), then one conversion, one exact rescale and two FMAs.
+// Bit k of the two bytes of h that `sel` picks (v_perm selector: bytes at 0 and 2, zeros between) to
+// bit 2k: the 16-bit Morton spread, its first step done by the byte permute.
+__device__ __forceinline__ uint32_t spread16(uint32_t h, uint32_t sel)
+{
+    uint32_t t = __builtin_amdgcn_perm(0u, h, sel);
+    t = (t | (t << 4)) & 0x0F0F0F0Fu;
+    t = (t | (t << 2)) & 0x33333333u;
+    return (t | (t << 1)) & 0x55555555u;
+}
+
+__device__ __forceinline__ uint32_t bit_insert(uint32_t mask, uint32_t a, uint32_t b)
+{
+    return (a & mask) | (b & ~mask);     // v_bfi_b32
+}
+
+// A group's codes as four words of signed nibbles in the digit-plane order of the format (xprep.h
+// digit_elem). q4: the code words as loaded, XOR 0x8 per nibble (q - 8; the staged 8 sum X undoes it).
+// q3: lo word L (elements 16h .. 16h+15, 2 bits each) masked with 0x33333333 leaves the even elements
+// in nibbles, L >> 2 the odd ones; the hi word spread to every other bit (element e's bit at 2e within
+// its half) puts an even element's hi bit at nibble bit 2 after a shift by 2, an odd element's where it
+// is. 14 instructions for the two spreads, 8 for the four words, instead of merging the planes into
+// eight byte words (~35).
+template <int FMT>
+__device__ __forceinline__ void code_nibbles(const Grp<FMT>& d, uint32_t (&c)[4])
+{
+    if constexpr (FMT == FMT_Q4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = d.w[j] ^ 0x88888888u;
+    } else {
+        const uint32_t s0 = spread16(d.h, 0x0c010c00u), s1 = spread16(d.h, 0x0c030c02u);
+        c[0] = bit_insert(0x33333333u, d.l.x, s0 << 2);
+        c[1] = bit_insert(0x33333333u, d.l.x >> 2, s0);
+        c[2] = bit_insert(0x33333333u, d.l.y, s1 << 2);
+        c[3] = bit_insert(0x33333333u, d.l.y >> 2, s1);
+    }
+}
+
+// q4 and q3 on v_dot8_i32_i4: x as signed 4-bit digit planes (xprep.h, xstage_d), codes as signed
+// nibbles (code_nibbles). Per (row, group): 24 dot8 run the Horner chain over the six digit planes
+// (most significant first, shifting by 4 between planes; for q4 the last shift also adds the staged
+// 8 * sum X that undoes the -8), then one conversion, one exact rescale and two FMAs.
 // The dot products use the clamping form: no partial sum can overflow, so the value is the same,
 // and the compiler keeps the chain as written instead of splitting it into six sums.
-template <int TEAM, int R, int U>
-struct Work<FMT_Q4, TEAM, R, U> {
+template <int FMT, int TEAM, int R, int U>
+struct WorkD {
     static constexpr int RPI = (256 / TEAM) * R;
     static constexpr int PARTS = TEAM;
     static constexpr int NACC = R;
     static constexpr int UG = U;
-    typedef Grp<FMT_Q4> Data[U][R];
+    typedef Grp<FMT> Data[U][R];
     Rs rs;
     int G, r0, r1, rstep, B, lane, team;
     float* part;
@@ -299,7 +316,7 @@ struct Work<FMT_Q4, TEAM, R, U> {
     static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_d_bytes(K); }
     static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
     {
-        brik::xstage_d<STAGE_TRIPS>(x, S, K, F);
+        brik::xstage_d<FMT, STAGE_TRIPS>(x, S, K, F);
     }
 
     __device__ __forceinline__ void init()
@@ -312,7 +329,7 @@ struct Work<FMT_Q4, TEAM, R, U> {
     __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
 
     template <bool EVEN>
-    __device__ __forceinline__ void issue(Grp<FMT_Q4> (&d)[U][R], int p, int b) const
+    __device__ __forceinline__ void issue(Grp<FMT> (&d)[U][R], int p, int b) const
     {
         const int n = n0(p);
 #pragma unroll
@@ -321,17 +338,17 @@ struct Work<FMT_Q4, TEAM, R, U> {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if constexpr (EVEN) {
-                    load_grp<FMT_Q4>(d[u][r], rs, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
+                    load_grp<FMT>(d[u][r], rs, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
                 } else {
                     const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
-                    load_grp<FMT_Q4>(d[u][r], rs, row + g, 0u, 0u);
+                    load_grp<FMT>(d[u][r], rs, row + g, 0u, 0u);
                 }
             }
         }
     }
 
     template <bool EVEN>
-    __device__ __forceinline__ void consume(const Grp<FMT_Q4> (&d)[U][R], const XS& S, int p, int b,
+    __device__ __forceinline__ void consume(const Grp<FMT> (&d)[U][R], const XS& S, int p, int b,
                                             float (&acc)[R]) const
     {
 #pragma unroll
@@ -350,12 +367,11 @@ struct Work<FMT_Q4, TEAM, R, U> {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 uint32_t c[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) c[j] = d[u][r].w[j] ^ 0x88888888u;
+                code_nibbles<FMT>(d[u][r], c);
                 int v = 0;
 #pragma unroll
                 for (int n = 5; n >= 0; --n) {
-                    if (n == 0) v = (v << 4) + xs.z;
+                    if (n == 0 && FMT == FMT_Q4) v = (v << 4) + xs.z;
                     else if (n != 5) v <<= 4;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) v = __builtin_amdgcn_sdot8((int)c[j], (int)L[n][j], v, true);
@@ -369,6 +385,11 @@ struct Work<FMT_Q4, TEAM, R, U> {
         for (int r = 0; r < R; ++r) part[(p * RPI + team * R + r) * TEAM + lane] = acc[r];
     }
 };
+
+template <int TEAM, int R, int U>
+struct Work<FMT_Q4, TEAM, R, U> : WorkD<FMT_Q4, TEAM, R, U> {};
+template <int TEAM, int R, int U>
+struct Work<FMT_Q3, TEAM, R, U> : WorkD<FMT_Q3, TEAM, R, U> {};
 
 // Exact path for a row holding Inf/NaN: 16 teams of 16 lanes; in every row set (rows
 // base + [0, RPI), base = r0, r0 + rstep, ...) team t takes rows t, t + 16, ... (any RPI, also below 16).

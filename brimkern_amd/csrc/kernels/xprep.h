@@ -6,10 +6,12 @@
 // The dot products with the integer weight codes then run on v_dot4_i32_i8 (four int8 MACs per lane
 // per instruction, exact int32 sums), and the group's result is rescaled by 2^(e_g - 22) in f32.
 // Relative to the group's largest element this keeps 22 bits, about f32's 24-bit significand.
+// This byte-limb image serves q8 (int8 codes); q4 and q3 use the digit-plane image further below
+// (the same X, written as six 4-bit digits for v_dot8_i32_i4).
 //
 // LDS layout for K = 32 * G, group-major so a group's limbs are reached with immediate offsets:
 //   limbs: group g (0 <= g <= G) occupies bytes [96g, 96g + 96): limb t (0 = h, 1 = m, 2 = l) at
-//          96g + 32t, its 32 bytes in the byte order the format's code unpacking produces (code_pos),
+//          96g + 32t, its 32 bytes in element order (the order of the q8 code bytes),
 //          the two 16-byte halves swapped when bit 3 of g is set (so lanes reading groups g and g + 8
 //          in one instruction hit different banks). Group G is all zeros: consumers point groups past
 //          the end of a row at it, which zeroes their contribution without a select;
@@ -29,20 +31,6 @@
 #include "../../../include/brik.h"   // BRIK_JOB_* flags
 
 namespace brik {
-
-// Byte position, inside a group's 32 limb bytes (before the half swap), of group element e.
-//   q8: codes are already bytes in element order.
-//   q4: code dword j (elements 8j..8j+7) unpacks to two byte dwords: (w & 0x0f0f0f0f) holds elements
-//       8j, 8j+2, 8j+4, 8j+6 and ((w >> 4) & 0x0f0f0f0f) holds 8j+1, 8j+3, 8j+5, 8j+7; they are
-//       byte dwords 2j and 2j+1.
-//   q3: byte dword s (0..7) holds codes s, s+8, s+16, s+24 (see unpack in gemv.hip).
-template <int FMT>
-__device__ __forceinline__ int code_pos(int e)
-{
-    if constexpr (FMT == FMT_Q8) return e;
-    else if constexpr (FMT == FMT_Q4) return ((2 * (e >> 3) + (e & 1)) << 2) + ((e & 7) >> 1);
-    else return ((e & 7) << 2) + (e >> 3);
-}
 
 __device__ __forceinline__ int half_swap(int g) { return ((g >> 3) & 1) << 4; }
 
@@ -222,6 +210,7 @@ __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h
 template <int FMT, int SB>
 __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K, const Fuse& F)
 {
+    static_assert(FMT == FMT_Q8, "q4 and q3 stage digit planes (xstage_d)");
     const int G = S.G;
     if (threadIdx.x == 0) {
         *S.flag = 0;
@@ -253,37 +242,15 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
         for (int t = 0; t < 4; ++t) split_limbs(v[t], sh, finite, hh[t], mm[t], ll[t]);
         int8_t* base = S.limbs + 96 * g;
         const int hs = half_swap(g);
-        if constexpr (FMT == FMT_Q8) {
-            // elements 4c..4c+3 are byte dword c of every limb
-            const int pos = (4 * c) ^ hs;
-            auto pack = [](const int (&b)[4]) {
-                return (uint32_t)(b[0] & 0xff) | ((uint32_t)(b[1] & 0xff) << 8) | ((uint32_t)(b[2] & 0xff) << 16) |
-                       ((uint32_t)(b[3] & 0xff) << 24);
-            };
-            *(uint32_t*)(base + pos) = pack(hh);
-            *(uint32_t*)(base + 32 + pos) = pack(mm);
-            *(uint32_t*)(base + 64 + pos) = pack(ll);
-        } else if constexpr (FMT == FMT_Q4) {
-            // elements 4c..4c+3 give bytes (c&1)*2 and +1 of byte dwords 2j (even elements) and
-            // 2j+1 (odd elements), j = c/2: two 16-bit stores per limb
-            const int j = c >> 1, bo = (c & 1) * 2;
-            const int pe = ((8 * j) + bo) ^ hs, po = ((8 * j + 4) + bo) ^ hs;
-            auto st = [&](int8_t* lb, const int (&b)[4]) {
-                *(uint16_t*)(lb + pe) = (uint16_t)((b[0] & 0xff) | ((b[2] & 0xff) << 8));
-                *(uint16_t*)(lb + po) = (uint16_t)((b[1] & 0xff) | ((b[3] & 0xff) << 8));
-            };
-            st(base, hh);
-            st(base + 32, mm);
-            st(base + 64, ll);
-        } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int pos = code_pos<FMT>(4 * c + t) ^ hs;
-                base[pos] = (int8_t)hh[t];
-                base[32 + pos] = (int8_t)mm[t];
-                base[64 + pos] = (int8_t)ll[t];
-            }
-        }
+        // elements 4c..4c+3 are byte dword c of every limb
+        const int pos = (4 * c) ^ hs;
+        auto pack = [](const int (&b)[4]) {
+            return (uint32_t)(b[0] & 0xff) | ((uint32_t)(b[1] & 0xff) << 8) | ((uint32_t)(b[2] & 0xff) << 16) |
+                   ((uint32_t)(b[3] & 0xff) << 24);
+        };
+        *(uint32_t*)(base + pos) = pack(hh);
+        *(uint32_t*)(base + 32 + pos) = pack(mm);
+        *(uint32_t*)(base + 64 + pos) = pack(ll);
     });
     stage_finish(S.flag, S.inv, F, K, ss, bad);
 }
@@ -295,10 +262,16 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
 //   X = sum_n d_n 16^n, d_n in [-8, 7].
 // (X + 0x888888) holds the digits offset by 8 in its six nibbles, so XOR 0x888888 of it leaves each
 // d_n as a signed nibble: two instructions per element. Digit plane n of a group is 16 bytes, eight
-// nibbles per dword in element order (nibble i of dword j is element 8j + i), the order of the q4
-// codes themselves (element 2i is the low nibble of byte i).
-// The codes enter the dot products as signed nibbles q - 8 (XOR 0x8 per nibble); the group term is
-// sum X q = sum_n 16^n (d_n . (q - 8)) + 8 sum X, every step an exact int32 (|sum X q| < 15 * 2^27).
+// nibbles per dword, in the element order of the format's code nibbles (digit_elem):
+//   q4: nibble i of dword j is element 8j + i, the order of the q4 codes themselves (element 2i is the
+//       low nibble of byte i). The codes enter the dot products as signed nibbles q - 8 (XOR 0x8 per
+//       nibble); the group term is sum X q = sum_n 16^n (d_n . (q - 8)) + 8 sum X, every step an exact
+//       int32 (|sum X q| < 15 * 2^27).
+//   q3: nibble i of dword j is element 16 (j >> 1) + 2i + (j & 1): the order in which the 2-bit plane's
+//       fields fall into nibbles when a lo word is masked with 0x33333333 (even elements) or shifted
+//       right by 2 first (odd elements); the hi bit of each is inserted at bit 2 of its nibble (gemv.hip).
+//       The codes 0..7 are nonnegative signed nibbles as they are: sum X q = sum_n 16^n (d_n . q)
+//       (|sum X q| < 7 * 2^27).
 //
 // LDS layout, group-major so every read uses an immediate offset: group g (0 <= g <= G) occupies
 // bytes [112g, 112g + 112): digit plane n at 112g + 16n (n < 6), then {f32 sum of the group's x,
@@ -367,9 +340,16 @@ __device__ __forceinline__ void nibble_transpose8(const uint32_t (&a)[8], uint32
     }
 }
 
+// Element of a group at nibble i of digit-plane dword j (see above).
+template <int FMT>
+__host__ __device__ __forceinline__ int digit_elem(int j, int i)
+{
+    return FMT == FMT_Q3 ? 16 * (j >> 1) + 2 * i + (j & 1) : 8 * j + i;
+}
+
 // Stage x[0..K) (16-byte aligned, K % 32 == 0) as digit planes: one thread per 8 consecutive elements,
 // a quad of lanes per group. All threads of the block call it; ends with a barrier.
-template <int SB>
+template <int FMT, int SB>
 __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XStageD& S, int K, const Fuse& F)
 {
     const int G = S.G;
@@ -405,10 +385,24 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
         }
         sx = sum4i(sx);
         uint32_t w[8];
-        nibble_transpose8(dg, w);
         unsigned char* gb = S.base + 112 * g;
+        if constexpr (FMT == FMT_Q3) {
+            // thread j holds elements 8j .. 8j+7: the even ones are nibbles 4(j&1) .. +3 of dword 2(j>>1),
+            // the odd ones the same nibbles of dword 2(j>>1)+1; transposed in the order 0 2 4 6 1 3 5 7
+            // every digit plane word splits into those two 16-bit halves
+            const uint32_t eo[8] = {dg[0], dg[2], dg[4], dg[6], dg[1], dg[3], dg[5], dg[7]};
+            nibble_transpose8(eo, w);
+            const int de = 8 * (j >> 1) + 2 * (j & 1), dodd = de + 4;   // byte offsets in a plane
 #pragma unroll
-        for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
+            for (int n = 0; n < 6; ++n) {
+                *(uint16_t*)(gb + 16 * n + de) = (uint16_t)w[n];
+                *(uint16_t*)(gb + 16 * n + dodd) = (uint16_t)(w[n] >> 16);
+            }
+        } else {
+            nibble_transpose8(dg, w);
+#pragma unroll
+            for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
+        }
         if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, 0};
         bad |= !finite;
     });

@@ -341,6 +341,8 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
                                     (capped by the LDS the lane partials may use) */
 #define BRIK_OPT_SPLITK 6        /* MFMA GEMMs of few rows (expert-grouped, or at most 64 rows): 0 auto,
                                     1 never use the split-K kernel, 2 use it whenever no tile is forced */
+#define BRIK_OPT_GEMV_BLOCKS 7   /* single-matrix GEMV launches: 0 auto, else at most this many blocks
+                                    (each block then loops over several row sets) */
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
 #ifdef __cplusplus
