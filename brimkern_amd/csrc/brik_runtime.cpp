@@ -255,11 +255,10 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 // A 256-column tile runs as its 8-wave form (two waves per SIMD): measured on the M = 512, K = 2560, N = 9728 prefill shape
 // (M = 512, K = 2560, N = 9728) with cold weights 44.9 us against 47.5 us for 96 x 256 with 4 waves,
 // and 5-10 % faster at every other row count.
-// Expert-grouped (MoE): 256 columns, 8 waves; 64-row tiles when rows are long (K >= 1024: each block
-// then streams enough weight per launch to amortize its latency-bound steps), else 32-row tiles.
-// Measured on a 64-expert MoE layer (22-47 rows each): gate/up (K = 2048, N = 768) 35 us with 64-row
-// tiles against 43-45 us with 32-row tiles; down (K = 768, N = 2048) 36 us with 32-row tiles
-// against 45 us with 64-row tiles.
+// Expert-grouped (MoE): 64 rows x 256 columns, 8 waves. Measured on a 64-expert MoE layer (22-47 rows
+// each) with the XCD-grouped grid, every tile forced: gate + up in one launch (K = 2048, N = 768)
+// 67-70 us against 71-117 us for the others; down (K = 768, N = 2048) 30 us against 32-64 us (38 us with
+// the 32-row tile, which was faster before the launches kept each expert's blocks on one XCD).
 int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
@@ -269,7 +268,7 @@ int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
                 return t;
         return 0;
     };
-    if (E > 0) return find(K >= 1024 ? 64 : 32, 1, 8);
+    if (E > 0) return find(64, 1, 8);
     int best = 0;
     double best_cost = 0;
     for (int t = 0; t < kNumGemmTiles; ++t) {
@@ -564,7 +563,10 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     const int v = gemv_variant(c, f, N, K, stage1);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
-    const unsigned cap = c->opt_gemv_blocks > 0 ? (unsigned)c->opt_gemv_blocks : kGemvMaxBlocks;
+    // a launch that copies a staged image (stage1) runs 4 blocks per CU, each looping over its row sets
+    // with the weight loads of the next set in flight (q3 LM head: 39.3 us against 41.2 us with one
+    // block per row set)
+    const unsigned cap = c->opt_gemv_blocks > 0 ? (unsigned)c->opt_gemv_blocks : stage1 ? 4 * kCUs : kGemvMaxBlocks;
     const unsigned gx = sets < cap ? sets : cap;
     const size_t lds = gemv_lds(K, f) + kGemvVariants[v].extra_lds((long)rpi * ((sets + gx - 1) / gx));
     const bool gemv_fits = lds <= kGemvMaxLds;
