@@ -1,6 +1,7 @@
 """Build recipe for the native parts of brimkern_amd (no cmake / node-gyp needed).
 
-1. ``csrc/kernels/brik_kernels.hip`` -> ``_build/brik_gfx950.hsaco``  (hipcc --genco, gfx950 only)
+1. ``csrc/kernels/brik_kernels.hip`` -> ``_build/brik_gfx950.hsaco``  (hipcc --genco, gfx950 only), then
+   ``check_lds_reads.py`` on its disassembly (the GEMM's inline-asm LDS reads)
 2. ``csrc/brik_scratch.hip`` -> ``_build/brik_scratch.o`` (hipcc -c: the no-allocation scratch array)
 3. ``csrc/brik_runtime.cpp`` + ``csrc/brik_embed.S`` (embeds the code object) + that object ->
    ``libbrik.so`` (the C ABI declared in ``include/brik.h``)
@@ -83,8 +84,20 @@ def build_addon(verbose=False):
     return ADDON
 
 
+def check_hsaco(verbose=False):
+    """The GEMM kernels' inline-asm LDS reads must be waited for before their registers are touched
+    (check_lds_reads.py); a violation fails the build."""
+    from brimkern_amd.check_lds_reads import check_file
+    bad = check_file(HSACO)
+    if bad:
+        raise RuntimeError("LDS-read register check failed:\n" + "\n".join(bad[:10]))
+    if verbose:
+        print("+ LDS-read register check: ok", flush=True)
+
+
 def build(verbose=False):
     build_hsaco(verbose)
+    check_hsaco(verbose)
     build_scratch(verbose)
     build_lib(verbose)
     build_addon(verbose)

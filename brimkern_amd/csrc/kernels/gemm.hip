@@ -262,6 +262,39 @@ struct WCodes {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// The multiply loop's LDS reads are inline asm. The compiler treats every direct global->LDS load
+// as a write to LDS of unknown extent, and before any LDS read it emits while such a load may be in
+// flight it waits for the load, that is for every memory load issued before it as well (the W
+// prefetch of the following steps included): a full memory round trip per K step. The pipeline
+// already orders its LDS reads against the direct loads that fill the same buffers (wait_vm before
+// each step barrier), so these reads are issued as asm, invisible to that rule, and their completion
+// is waited for explicitly: lds_wait, then tie on every value read, which orders its uses after the
+// wait.
+__device__ __forceinline__ half8_t ds_read_b128(uint32_t addr)
+{
+    half8_t v;
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ uint32_t ds_read_u16(uint32_t addr)
+{
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"); }
+template <class V>
+__device__ __forceinline__ void tie(V& v)
+{
+    asm volatile("" : "+v"(v));
+}
+
 // The loads of one step, split into ops that the multiply loop spreads over its slices: for each
 // column block the code loads of W step t + 1, in slices 0-1; then, after the barrier in slice 4, the
 // direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (NW i + w), +1024)
@@ -363,28 +396,45 @@ struct Loader {
         }
     }
 
-    // Scales and mins of W step t (chunk buffer at `buf`) into f: groups 4 t + 2 h + e, e = 0, 1; groups
-    // past the row end get 0.
+    // Issue the LDS reads of the scales and mins of W step t (chunk buffer at `buf`) into f: groups
+    // 4 t + 2 h + e, e = 0, 1. The values may be used only after lds_wait and finish_scales.
     __device__ __forceinline__ void read_scales(WCodes<FMT> (&f)[TN], int t, uint32_t buf, int lane)
     {
-        const int g0 = 4 * t + 2 * h;
-        const bool la = g0 < G, lb = g0 + 1 < G;
         const uint32_t F0 = T::SG * (uint32_t)(t / T::SCH);
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const uint32_t F = sg[j] + F0;
             // shift of a moved chunk; a live group's position is at most 15, and the clamp keeps reads of
-            // dead groups (masked below) within the chunk buffer and its 64-byte pad
+            // dead groups (masked in finish_scales) within the chunk buffer and its 64-byte pad
             const uint32_t pos = min((F - min(F, slim)) + 4 * (t % T::SCH) + 2 * h, (uint32_t)T::SG - 1);
             const uint32_t col = (uint32_t)(wave * 32 * TN + 32 * j + (lane & 31));
-            const unsigned char* ps = lds + buf + col * (T::SG * 2) + pos * 2;
-            const uint32_t s0 = *(const uint16_t*)ps, s1 = *(const uint16_t*)(ps + 2);
-            f[j].s[0] = la ? s0 : 0u;
-            f[j].s[1] = lb ? s1 : 0u;
+            const uint32_t ps = lds_addr(lds + buf) + col * (T::SG * 2) + pos * 2;
+            f[j].s[0] = ds_read_u16(ps);
+            f[j].s[1] = ds_read_u16(ps + 2);
             if constexpr (FMT != FMT_Q8) {
-                const uint32_t m0 = *(const uint16_t*)(ps + T::SPLANE), m1 = *(const uint16_t*)(ps + T::SPLANE + 2);
-                f[j].m[0] = la ? m0 : 0u;
-                f[j].m[1] = lb ? m1 : 0u;
+                f[j].m[0] = ds_read_u16(ps + T::SPLANE);
+                f[j].m[1] = ds_read_u16(ps + T::SPLANE + 2);
+            }
+        }
+    }
+
+    // After lds_wait: order the values read by read_scales after the wait, and give groups past the row
+    // end scale and min 0.
+    __device__ __forceinline__ void finish_scales(WCodes<FMT> (&f)[TN], int t)
+    {
+        const int g0 = 4 * t + 2 * h;
+        const bool la = g0 < G, lb = g0 + 1 < G;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            tie(f[j].s[0]);
+            tie(f[j].s[1]);
+            f[j].s[0] = la ? f[j].s[0] : 0u;
+            f[j].s[1] = lb ? f[j].s[1] : 0u;
+            if constexpr (FMT != FMT_Q8) {
+                tie(f[j].m[0]);
+                tie(f[j].m[1]);
+                f[j].m[0] = la ? f[j].m[0] : 0u;
+                f[j].m[1] = lb ? f[j].m[1] : 0u;
             } else {
                 f[j].m[0] = f[j].m[1] = 0u;
             }
@@ -547,9 +597,17 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
                                          uint32_t snext, int lane)
 {
     constexpr int TM = T::TM, TN = T::TN;
+    const uint32_t lbase = lds_addr(lds);
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) {
         const int cur = sl & 1, nxt = cur ^ 1;
+        // the A fragments of this slice (read during the previous one) and, at slice 7, the scales read
+        // at slice 6
+        lds_wait();
+#pragma unroll
+        for (int i = 0; i < TM; ++i) tie(a[cur][i]);
+        if constexpr (FMT != FMT_F16)
+            if (sl == 7) ld.finish_scales(wn, t + 1);
         if (sl == Loader<FMT, T>::XS) {
             wait_vm<T::VM_NEXT_X>();
             step_barrier();
@@ -560,12 +618,12 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
             if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
         if (sl < 7) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) a[nxt][i] = *(const half8_t*)(lds + abuf + aoff[sl + 1] + i * 32 * XROW);
+            for (int i = 0; i < TM; ++i) a[nxt][i] = ds_read_b128(lbase + abuf + aoff[sl + 1] + i * 32 * XROW);
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[nxt][j] = b_frag<FMT>(wc[j], go[j], sl + 1);
         } else {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) a[nxt][i] = *(const half8_t*)(lds + anext + aoff[0] + i * 32 * XROW);
+            for (int i = 0; i < TM; ++i) a[nxt][i] = ds_read_b128(lbase + anext + aoff[0] + i * 32 * XROW);
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 gn[j] = group_ops<FMT>(wn[j], go[j].k);
@@ -580,7 +638,6 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
         // the next slice's A reads first, then each MFMA with a share of the dequantization; the
         // scheduling barrier keeps every slice's reads one slice ahead of their use
         constexpr int VALU_PER = (FMT == FMT_F16 ? 4 : FMT == FMT_Q8 ? 12 : 16) * TN / (TM * TN);
-        __builtin_amdgcn_sched_group_barrier(0x100, TM, 0);
 #pragma unroll
         for (int g = 0; g < TM * TN; ++g) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -725,7 +782,9 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
     if constexpr (FMT != FMT_F16) ld.read_scales(wr[0], 0, T::S_OFF, lane);
     const DeqConst dk = DeqConst::make();
 #pragma unroll
-    for (int i = 0; i < TM; ++i) a[0][i] = *(const half8_t*)(smem + aoff[0] + i * 32 * XROW);
+    for (int i = 0; i < TM; ++i) a[0][i] = ds_read_b128(lds_addr(smem) + aoff[0] + i * 32 * XROW);
+    lds_wait();
+    if constexpr (FMT != FMT_F16) ld.finish_scales(wr[0], 0);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         go[j] = group_ops<FMT>(wr[0][j], dk);
@@ -758,6 +817,15 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
             if (R > 2 && r + 1 < R && t >= steps) break;
         }
     } while (t < steps);
+    // The A fragments the last slice read for a step that does not run: their registers must stay
+    // allocated until those reads have landed, or the epilogue could reuse them while an LDS read is
+    // still to write them.
+    lds_wait();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        tie(a[0][i]);
+        tie(a[1][i]);
+    }
     // the clamped loads of the last steps may still be writing LDS, which the epilogue reuses
     wait_vm<0>();
     lds_barrier();

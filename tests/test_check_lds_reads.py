@@ -1,0 +1,45 @@
+"""The build-time check of the GEMM's inline-asm LDS reads (brimkern_amd/check_lds_reads.py) on
+hand-written disassembly: a register of an LDS read touched before `s_waitcnt lgkmcnt(0)` is reported,
+the same code with the wait first is not, and kernels outside the checked set are skipped."""
+from brimkern_amd.check_lds_reads import check
+
+HEAD = "0000000000001000 <{}>:\n"
+
+
+def body(lines):
+    return "".join(f"\t{l}  // 0000000010{i:02X}: 00000000\n" for i, l in enumerate(lines))
+
+
+def test_touch_before_wait_is_reported():
+    text = HEAD.format("brik_gemm_q4_96x1w8") + body([
+        "ds_read_b128 v[2:5], v44 offset:64",
+        "v_lshlrev_b32_e32 v2, 2, v18",          # reuses v2 while the read may still write it
+        "s_waitcnt lgkmcnt(0)",
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and "v[2]" in bad[0]
+
+
+def test_use_after_wait_is_clean():
+    text = HEAD.format("brik_gemmg_q4_64x1w8") + body([
+        "ds_read_b128 v[2:5], v44",
+        "ds_read_u16 v9, v40 offset:2",
+        "v_and_or_b32 v10, v11, v12, v13",       # unrelated registers
+        "s_waitcnt lgkmcnt(0)",
+        "v_mfma_f32_32x32x16_f16 a[0:15], v[2:5], v[14:17], a[0:15]",
+        "v_mov_b32_e32 v9, 0",
+    ])
+    assert check(text) == []
+
+
+def test_window_spans_branches_and_other_kernels_are_skipped():
+    text = HEAD.format("brik_gemm_q8_64x1") + body([
+        "ds_read_b128 v[6:9], v1",
+        "s_cbranch_scc1 65530",
+        "v_add_u32_e32 v7, s0, v3",               # after the branch, before any wait
+    ]) + HEAD.format("brik_gemm_sk_q4_k4") + body([
+        "ds_read_b128 v[6:9], v1",
+        "v_add_u32_e32 v7, s0, v3",               # compiler-tracked reads: not checked
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and bad[0].startswith("brik_gemm_q8_64x1")
