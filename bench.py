@@ -209,10 +209,12 @@ def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
     plans, nbytes = [], 0
     for l in range(layers):
         x, y = xs[l], xs[l + 1]
+        # gate/up and down as the linked GLU pair: the gate/up launch writes down's staged input
+        glu = ctx.gemv_plan_glu("q4", j("gate", l, tmp["h"], tmp["gate"], norm_w=fn, eps=1e-6),
+                                j("up", l, tmp["h"], tmp["up"], norm_w=fn, eps=1e-6),
+                                j("down", l, tmp["up"], y, gate=tmp["gate"], res=tmp["h"]))
         plans += [ctx.gemv_plan("q4", [j(n, l, x, tmp[n], norm_w=an, eps=1e-6) for n in ("q", "k", "v")]),
-                  ctx.gemv_plan("q4", [j("o", l, attn, tmp["h"], res=x)]),
-                  ctx.gemv_plan("q4", [j(n, l, tmp["h"], tmp[n], norm_w=fn, eps=1e-6) for n in ("gate", "up")]),
-                  ctx.gemv_plan("q4", [j("down", l, tmp["up"], y, gate=tmp["gate"], res=tmp["h"])])]
+                  ctx.gemv_plan("q4", [j("o", l, attn, tmp["h"], res=x)]), *glu]
         nbytes += sum(q_bytes("q4", N, K) for K, N in shapes.values())
 
     def step(i):
@@ -238,7 +240,8 @@ def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
     return {"us_per_layer": round(ms * 1e3 / layers, 2), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "replay": replay,
             "eager_us_per_layer": round(ms_eager * 1e3 / layers, 2), "launches_per_layer": 4, "layers": layers,
-            "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up, swiglu -> down + residual"}
+            "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up (+ staged swiglu image), "
+                     "down (copies the image) + residual"}
 
 
 def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):

@@ -64,6 +64,7 @@ SIGNATURES = {
     "brik_gemv_plan_run": (_I, [_P, _P]),
     "brik_gemv_plan_destroy": (None, [_P, _P]),
     "brik_gemv_plan_create_ex": (_I, [_P, _I, _P, _I, ctypes.POINTER(_P)]),
+    "brik_gemv_plan_create_glu": (_I, [_P, _I, _P, _P, _P, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "brik_graph_begin": (_I, [_P]),
     "brik_graph_end": (_I, [_P, ctypes.POINTER(_P)]),
     "brik_graph_launch": (_I, [_P, _P]),
@@ -296,14 +297,22 @@ class Context:
             return GemvPlan(self, h)
         arr = (GemvJobEx * len(jobs))()
         for i, j in enumerate(jobs):
-            base = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]), _addr(j.get("mn")),
-                           _addr(j["y"]), j["K"], j["N"])
-            flags = (BRIK_JOB_GAIN_ONE_PLUS if j.get("one_plus") else 0) | (BRIK_JOB_ACT_GELU if j.get("gelu") else 0)
-            arr[i] = GemvJobEx(base, _addr(j.get("gate")), _addr(j.get("norm_w")), _addr(j.get("res")),
-                               float(j.get("eps", 1e-6)), flags)
+            arr[i] = _job_ex(j)
         self._check(self.lib.brik_gemv_plan_create_ex(self.handle, FMT_CODES[fmt], ctypes.cast(arr, _P), len(jobs),
                                                       ctypes.byref(h)))
         return GemvPlan(self, h)
+
+    def gemv_plan_glu(self, fmt: str, gate, up, down):
+        """The linked (gate/up, down) plans of ``brik_gemv_plan_create_glu``; each job a dict as for
+        :meth:`gemv_plan`. down must read gate's and up's outputs (``gate=gate["y"]``, ``x=up["y"]``).
+        Returns ``(gate_up_plan, down_plan)``; run them in that order."""
+        jobs = (GemvJobEx * 3)(_job_ex(gate), _job_ex(up), _job_ex(down))
+        hg, hd = _P(), _P()
+        base = ctypes.addressof(jobs)
+        size = ctypes.sizeof(GemvJobEx)
+        self._check(self.lib.brik_gemv_plan_create_glu(self.handle, FMT_CODES[fmt], _P(base), _P(base + size),
+                                                       _P(base + 2 * size), ctypes.byref(hg), ctypes.byref(hd)))
+        return GemvPlan(self, hg), GemvPlan(self, hd)
 
     # ---- recorded launches (HIP graphs) ---------------------------------------------------------
     def graph_begin(self):
@@ -391,6 +400,14 @@ class Graph:
         if self.handle:
             self.ctx.lib.brik_graph_destroy(self.ctx.handle, self.handle)
             self.handle = None
+
+
+def _job_ex(j) -> GemvJobEx:
+    base = GemvJob(_addr(j["x"]), _addr(j["p0"]), _addr(j.get("p1")), _addr(j["sc"]), _addr(j.get("mn")),
+                   _addr(j["y"]), j["K"], j["N"])
+    flags = (BRIK_JOB_GAIN_ONE_PLUS if j.get("one_plus") else 0) | (BRIK_JOB_ACT_GELU if j.get("gelu") else 0)
+    return GemvJobEx(base, _addr(j.get("gate")), _addr(j.get("norm_w")), _addr(j.get("res")),
+                     float(j.get("eps", 1e-6)), flags)
 
 
 class GemvPlan:

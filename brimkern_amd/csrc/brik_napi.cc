@@ -22,6 +22,14 @@ namespace {
             return nullptr;                                                   \
         }                                                                     \
     } while (0)
+// the same in a function returning bool
+#define NAPI_CALL_B(env, call)                                                \
+    do {                                                                      \
+        if ((call) != napi_ok) {                                              \
+            napi_throw_error((env), "BRIK_NAPI", "N-API call failed: " #call); \
+            return false;                                                     \
+        }                                                                     \
+    } while (0)
 
 const char* code_name(int rc)
 {
@@ -745,8 +753,65 @@ void plan_finalize(napi_env, void* data, void*)
     delete b;
 }
 
-// gemvPlanCreate(ctx, fmt, [{x, p0, p1, scales, mins, y, K, N[, gate, normW, res, eps, flags]}, ...]) -> plan
-// (the optional fields are those of brik_gemv_job_ex; a job without them has no fusion)
+// One job object {x, p0, p1, scales, mins, y, K, N[, gate, normW, res, eps, flags]} (the optional fields
+// are those of brik_gemv_job_ex; a job without them has no fusion). False with a pending exception.
+bool get_job(napi_env env, napi_value o, brik_gemv_job_ex* out)
+{
+    static const char* const names[6] = {"x", "p0", "p1", "scales", "mins", "y"};
+    static const char* const fnames[3] = {"gate", "normW", "res"};
+    napi_value f;
+    void* ptrs[6];
+    for (int k = 0; k < 6; ++k) {
+        NAPI_CALL_B(env, napi_get_named_property(env, o, names[k], &f));
+        if (!get_ptr(env, f, &ptrs[k])) return false;
+    }
+    int32_t K, N;
+    NAPI_CALL_B(env, napi_get_named_property(env, o, "K", &f));
+    if (!get_i32(env, f, &K)) return false;
+    NAPI_CALL_B(env, napi_get_named_property(env, o, "N", &f));
+    if (!get_i32(env, f, &N)) return false;
+    void* fp[3] = {nullptr, nullptr, nullptr};
+    for (int k = 0; k < 3; ++k) {
+        bool has = false;
+        NAPI_CALL_B(env, napi_has_named_property(env, o, fnames[k], &has));
+        if (!has) continue;
+        NAPI_CALL_B(env, napi_get_named_property(env, o, fnames[k], &f));
+        if (!get_ptr(env, f, &fp[k])) return false;
+    }
+    float eps = 1e-6f;
+    int32_t flags = 0;
+    bool has = false;
+    NAPI_CALL_B(env, napi_has_named_property(env, o, "eps", &has));
+    if (has) {
+        NAPI_CALL_B(env, napi_get_named_property(env, o, "eps", &f));
+        if (!get_f32(env, f, &eps)) return false;
+    }
+    NAPI_CALL_B(env, napi_has_named_property(env, o, "flags", &has));
+    if (has) {
+        NAPI_CALL_B(env, napi_get_named_property(env, o, "flags", &f));
+        if (!get_i32(env, f, &flags)) return false;
+    }
+    *out = brik_gemv_job_ex{brik_gemv_job{(const float*)ptrs[0], ptrs[1], ptrs[2], (const uint16_t*)ptrs[3],
+                                          (const uint16_t*)ptrs[4], (float*)ptrs[5], K, N},
+                            (const float*)fp[0], (const float*)fp[1], (const float*)fp[2], eps, flags};
+    return true;
+}
+
+// A JS handle owning `plan` (and a reference to the context), or null with a pending exception.
+napi_value wrap_plan(napi_env env, CtxBox* box, brik_gemv_plan* plan)
+{
+    PlanBox* pb = new PlanBox{box, plan};
+    ++box->refs;
+    napi_value ext;
+    if (napi_create_external(env, pb, plan_finalize, nullptr, &ext) != napi_ok) {
+        plan_finalize(env, pb, nullptr);
+        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+        return nullptr;
+    }
+    return ext;
+}
+
+// gemvPlanCreate(ctx, fmt, [job, ...]) -> plan
 napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
 {
     Args a;
@@ -758,57 +823,42 @@ napi_value GemvPlanCreate(napi_env env, napi_callback_info info)
     uint32_t n = 0;
     NAPI_CALL(env, napi_get_array_length(env, a.v[2], &n));
     std::vector<brik_gemv_job_ex> jobs(n);
-    static const char* const names[6] = {"x", "p0", "p1", "scales", "mins", "y"};
-    static const char* const fnames[3] = {"gate", "normW", "res"};
     for (uint32_t j = 0; j < n; ++j) {
-        napi_value o, f;
+        napi_value o;
         NAPI_CALL(env, napi_get_element(env, a.v[2], j, &o));
-        void* ptrs[6];
-        for (int k = 0; k < 6; ++k) {
-            NAPI_CALL(env, napi_get_named_property(env, o, names[k], &f));
-            if (!get_ptr(env, f, &ptrs[k])) return nullptr;
-        }
-        int32_t K, N;
-        NAPI_CALL(env, napi_get_named_property(env, o, "K", &f));
-        if (!get_i32(env, f, &K)) return nullptr;
-        NAPI_CALL(env, napi_get_named_property(env, o, "N", &f));
-        if (!get_i32(env, f, &N)) return nullptr;
-        void* fp[3] = {nullptr, nullptr, nullptr};
-        for (int k = 0; k < 3; ++k) {
-            bool has = false;
-            NAPI_CALL(env, napi_has_named_property(env, o, fnames[k], &has));
-            if (!has) continue;
-            NAPI_CALL(env, napi_get_named_property(env, o, fnames[k], &f));
-            if (!get_ptr(env, f, &fp[k])) return nullptr;
-        }
-        float eps = 1e-6f;
-        int32_t flags = 0;
-        bool has = false;
-        NAPI_CALL(env, napi_has_named_property(env, o, "eps", &has));
-        if (has) {
-            NAPI_CALL(env, napi_get_named_property(env, o, "eps", &f));
-            if (!get_f32(env, f, &eps)) return nullptr;
-        }
-        NAPI_CALL(env, napi_has_named_property(env, o, "flags", &has));
-        if (has) {
-            NAPI_CALL(env, napi_get_named_property(env, o, "flags", &f));
-            if (!get_i32(env, f, &flags)) return nullptr;
-        }
-        jobs[j] = brik_gemv_job_ex{brik_gemv_job{(const float*)ptrs[0], ptrs[1], ptrs[2], (const uint16_t*)ptrs[3],
-                                                 (const uint16_t*)ptrs[4], (float*)ptrs[5], K, N},
-                                   (const float*)fp[0], (const float*)fp[1], (const float*)fp[2], eps, flags};
+        if (!get_job(env, o, &jobs[j])) return nullptr;
     }
     brik_gemv_plan* plan = nullptr;
     if (check(env, ctx, brik_gemv_plan_create_ex(ctx, fmt, jobs.data(), (int)n, &plan))) return nullptr;
-    PlanBox* pb = new PlanBox{box, plan};
-    ++box->refs;
-    napi_value ext;
-    if (napi_create_external(env, pb, plan_finalize, nullptr, &ext) != napi_ok) {
-        plan_finalize(env, pb, nullptr);
-        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+    return wrap_plan(env, box, plan);
+}
+
+// gemvPlanCreateGlu(ctx, fmt, gate, up, down) -> [gateUpPlan, downPlan] (brik_gemv_plan_create_glu)
+napi_value GemvPlanCreateGlu(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 5)) return nullptr;
+    CtxBox* box;
+    int32_t fmt;
+    if (!get_box(env, a.v[0], &box) || !get_i32(env, a.v[1], &fmt)) return nullptr;
+    brik_gemv_job_ex jobs[3];
+    for (int k = 0; k < 3; ++k)
+        if (!get_job(env, a.v[2 + k], &jobs[k])) return nullptr;
+    brik_gemv_plan *gu = nullptr, *dn = nullptr;
+    if (check(env, box->ctx, brik_gemv_plan_create_glu(box->ctx, fmt, &jobs[0], &jobs[1], &jobs[2], &gu, &dn)))
+        return nullptr;
+    napi_value hg = wrap_plan(env, box, gu);
+    if (!hg) {
+        brik_gemv_plan_destroy(box->ctx, dn);
         return nullptr;
     }
-    return ext;
+    napi_value hd = wrap_plan(env, box, dn);
+    if (!hd) return nullptr;
+    napi_value arr;
+    NAPI_CALL(env, napi_create_array_with_length(env, 2, &arr));
+    NAPI_CALL(env, napi_set_element(env, arr, 0, hg));
+    NAPI_CALL(env, napi_set_element(env, arr, 1, hd));
+    return arr;
 }
 
 napi_value GemvPlanRun(napi_env env, napi_callback_info info)
@@ -866,6 +916,7 @@ napi_value Init(napi_env env, napi_value exports)
         {"logitsTopK", nullptr, LogitsTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"lmHeadTopK", nullptr, LmHeadTopK, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanCreate", nullptr, GemvPlanCreate, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"gemvPlanCreateGlu", nullptr, GemvPlanCreateGlu, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanRun", nullptr, GemvPlanRun, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"gemvPlanDestroy", nullptr, GemvPlanDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"allocBuffer", nullptr, AllocBuffer, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

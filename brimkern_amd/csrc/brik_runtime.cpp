@@ -54,15 +54,22 @@ const char* const kKernelNames[K_COUNT] = {
 // (one matrix) and brik_gemvg_<fmt>_... (grouped job table).
 struct GemvVariant {
     int team, r, u, d;
-    int rpi() const { return (256 / team) * r; }      // rows per block iteration
+    constexpr int rpi() const { return (256 / team) * r; }      // rows per block iteration
     // LDS of a block past the staged x: TEAM partial sums for each of `rows` rows
-    size_t extra_lds(long rows) const { return sizeof(float) * (size_t)rows * team; }
+    constexpr size_t extra_lds(long rows) const { return sizeof(float) * (size_t)rows * team; }
 };
 constexpr GemvVariant kGemvVariants[] = {{16, 2, 1, 2}, {16, 2, 1, 3}, {16, 2, 1, 4}, {16, 4, 1, 2},
                                          {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}, {16, 2, 5, 2},
                                          {16, 1, 5, 2}};
 constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]);
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
+// GLU pair kernels brik_gemvp_<fmt>_t16_r2_u1_d2_n512 (q4, q3): 512-thread blocks of 32 teams of 16
+// lanes, each team with one row of gate and the same row of up, so a block covers 32 rows of each (one
+// quantization group of down's input) with as many waves as two blocks of the unpaired gate/up plan.
+constexpr GemvVariant kGluVariant = {16, 2, 1, 2};
+constexpr int kGluThreads = 512;
+constexpr int kGluRows = 32;   // rows of each matrix per block
+static_assert(kGluThreads / kGluVariant.team * kGluVariant.r == 2 * kGluRows, "GLU block rows");
 
 constexpr int kGroup = 32;
 // GEMM block tiles (BM rows x 32 TN NW columns, NW waves), in the order of BRIK_GEMM_FMT in gemm.hip:
@@ -110,18 +117,31 @@ int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 }  // namespace
 
+// A device buffer shared by the two plans of a GLU pair (the staged image of act(gate) * up), freed
+// with the last of them.
+struct SharedBuf {
+    void* ptr = nullptr;
+    int refs = 0;
+};
+
 struct brik_gemv_plan {
     hipFunction_t kernel;
-    // [jobs (brik_gemv_job_ex) | block_start | rows_per_block | stage_off (njobs) | stage inputs]
+    // grouped: [jobs (brik_gemv_job_ex) | block_start | rows_per_block | stage_off (njobs) | stage inputs];
+    // GLU pair: [gate job | up job]
     void* dev = nullptr;
     int njobs = 0;
     unsigned blocks = 0;
     size_t lds = 0;
     // staging pass of a large plan: `ninputs` distinct input rows, staged into `stage`
     hipFunction_t stager = nullptr;
-    void* stage = nullptr;
+    void* stage = nullptr;        // owned, unless `image` holds it
     int ninputs = 0;
     size_t inputs_off = 0;        // byte offset of the stage-input table in dev
+    // GLU pairs: the producer (glu = true) writes the image in `image`, the consumer copies it as its
+    // staged input (stage = image->ptr, no stager)
+    bool glu = false;
+    int act_flags = 0;
+    SharedBuf* image = nullptr;
 };
 
 struct brik_fence {
@@ -144,6 +164,7 @@ struct brik_ctx {
     hipFunction_t fn[K_COUNT] = {};
     hipFunction_t gemv[3][kNumGemvVariants] = {};
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
+    hipFunction_t gemvp[3] = {};                 // GLU pair kernels (q4, q3; q8 has none)
     hipFunction_t gemm[3][kNumGemmTiles] = {};
     hipFunction_t gemmg[kNumGemmTiles] = {};    // expert-grouped q4 kernels (brik_gemmg_q4_*)
     hipFunction_t gemm_f16[kNumGemmTiles] = {};   // f16-weight tiles (TN = 1, PF = 1 only; others null)
@@ -259,7 +280,7 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 // each) with the XCD-grouped grid, every tile forced: gate + up in one launch (K = 2048, N = 768)
 // 67-70 us against 71-117 us for the others; down (K = 768, N = 2048) 30 us against 32-64 us (38 us with
 // the 32-row tile, which was faster before the launches kept each expert's blocks on one XCD).
-int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
+int gemm_tile(brik_ctx* c, long M, long N, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
     auto find = [](int bm, int tn, int nw, int pf = 1) {
@@ -471,7 +492,7 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
         return gemm_splitk(c, f, xh, rscale, pair->p0, p1, pair->sc, pair->mn, pair->y, rows, K, N, row_off, E);
     }
     int Mi = rows, Ki = K, Ni = N, Ei = E;
-    const int t = gemm_tile(c, rows, N, K, E);
+    const int t = gemm_tile(c, rows, N, E);
     const GemmTile& gt = kGemmTiles[t];
     const int bn = gt.bn();
     if (!row_off) {
@@ -859,6 +880,13 @@ int brik_create(int device, brik_ctx** out)
             snprintf(name, sizeof name, "brik_gemvg_%s_t%d_r%d_u%d_d%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d);
             if (hipModuleGetFunction(&c->gemvg[f][v], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
         }
+    for (int f = 1; f < 3; ++f) {
+        char name[64];
+        const GemvVariant& gv = kGluVariant;
+        snprintf(name, sizeof name, "brik_gemvp_%s_t%d_r%d_u%d_d%d_n%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d,
+                 kGluThreads);
+        if (hipModuleGetFunction(&c->gemvp[f], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+    }
     for (int f = 0; f < 3; ++f)
         for (int t = 0; t < kNumGemmTiles; ++t) {
             char name[64];
@@ -1271,15 +1299,9 @@ int brik_f16_to_f32(brik_ctx* c, const uint16_t* src, float* out, size_t n)
     return launch(c, K_F16_TO_F32, (unsigned)(blocks < 8192 ? blocks : 8192), 1, 256, 0, args);
 }
 
-int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out)
+// The per-job checks of a plan (shapes, pointers, alignment, flags, LDS).
+static int check_jobs(brik_ctx* c, Fmt f, const brik_gemv_job_ex* jobs, int njobs)
 {
-    if (!c || !out) return BRIK_EINVAL;
-    *out = nullptr;
-    if (fmt != BRIK_FMT_Q8 && fmt != BRIK_FMT_Q4 && fmt != BRIK_FMT_Q3)
-        return fail(c, BRIK_EINVAL, "gemv_plan: unknown format %d", fmt);
-    if (njobs <= 0 || !jobs) return fail(c, BRIK_EINVAL, "gemv_plan: need at least one job");
-    const Fmt f = Fmt(fmt);
-    int kmax = 0, kmin = 1 << 30;
     for (int j = 0; j < njobs; ++j) {
         const brik_gemv_job& b = jobs[j].job;
         const brik_gemv_job_ex& e = jobs[j];
@@ -1293,8 +1315,27 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
         if (r != BRIK_OK) return r;
         if (gemv_lds(b.K, f) + kPlanPartialLds > kGemvMaxLds)
             return fail(c, BRIK_EINVAL, "gemv_plan: job %d K=%d exceeds the LDS staging limit", j, b.K);
-        kmax = b.K > kmax ? b.K : kmax;
-        kmin = b.K < kmin ? b.K : kmin;
+    }
+    return BRIK_OK;
+}
+
+// A grouped plan over `jobs`. With `image` (the consumer of a GLU pair: one job), the blocks copy that
+// staged image of the job's input instead of staging it, and the plan holds a reference to it.
+static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out,
+                       SharedBuf* image)
+{
+    if (!c || !out) return BRIK_EINVAL;
+    *out = nullptr;
+    if (fmt != BRIK_FMT_Q8 && fmt != BRIK_FMT_Q4 && fmt != BRIK_FMT_Q3)
+        return fail(c, BRIK_EINVAL, "gemv_plan: unknown format %d", fmt);
+    if (njobs <= 0 || !jobs) return fail(c, BRIK_EINVAL, "gemv_plan: need at least one job");
+    const Fmt f = Fmt(fmt);
+    int r0 = check_jobs(c, f, jobs, njobs);
+    if (r0 != BRIK_OK) return r0;
+    int kmax = 0, kmin = 1 << 30;
+    for (int j = 0; j < njobs; ++j) {
+        kmax = jobs[j].job.K > kmax ? jobs[j].job.K : kmax;
+        kmin = jobs[j].job.K < kmin ? jobs[j].job.K : kmin;
     }
     long rows = 0;
     for (int j = 0; j < njobs; ++j) rows += jobs[j].job.N;
@@ -1312,7 +1353,7 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
     std::vector<brik_gemv_job_ex> sorted(njobs);
     std::vector<uint32_t> start(njobs + 1, 0), rpbs(njobs);
     std::vector<long> sets(njobs);
-    const bool prestage = c->opt_plan_stage ? c->opt_plan_stage == 2 : rows >= kPrestageRows;
+    const bool prestage = !image && (c->opt_plan_stage ? c->opt_plan_stage == 2 : rows >= kPrestageRows);
     // the lane partials of a block's row sets stay within the 16 KiB the per-job LDS check reserves
     long maxsets = (long)(kPlanPartialLds / kGemvVariants[v].extra_lds(rpi));
     const long capsets = prestage ? kPrestageMaxSets : kPlanMaxSets;
@@ -1393,11 +1434,99 @@ int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs,
         p->ninputs = (int)inputs.size();
         p->inputs_off = inputs_off;
     }
+    if (image) {
+        p->stage = image->ptr;
+        p->image = image;
+        ++image->refs;
+    }
     p->kernel = c->gemvg[fmt_index(f)][v];
     p->njobs = njobs;
     p->blocks = start[njobs];
     p->lds = lds;
     *out = p;
+    return BRIK_OK;
+}
+
+int brik_gemv_plan_create_ex(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out)
+{
+    return plan_create(c, fmt, jobs, njobs, out, nullptr);
+}
+
+int brik_gemv_plan_create_glu(brik_ctx* c, int fmt, const brik_gemv_job_ex* gate, const brik_gemv_job_ex* up,
+                              const brik_gemv_job_ex* down, brik_gemv_plan** gate_up, brik_gemv_plan** down_plan)
+{
+    if (!c || !gate_up || !down_plan) return BRIK_EINVAL;
+    *gate_up = nullptr;
+    *down_plan = nullptr;
+    if (fmt != BRIK_FMT_Q8 && fmt != BRIK_FMT_Q4 && fmt != BRIK_FMT_Q3)
+        return fail(c, BRIK_EINVAL, "gemv_plan_glu: unknown format %d", fmt);
+    if (!gate || !up || !down) return fail(c, BRIK_EINVAL, "gemv_plan_glu: gate, up and down jobs are required");
+    const brik_gemv_job &g = gate->job, &u = up->job, &d = down->job;
+    if (g.x != u.x || g.K != u.K || g.N != u.N || gate->gate != up->gate || gate->norm_w != up->norm_w ||
+        gate->flags != up->flags || std::memcmp(&gate->eps, &up->eps, sizeof(float)) != 0)
+        return fail(c, BRIK_EINVAL, "gemv_plan_glu: gate and up must share x, K, N and the input fusion");
+    if (g.y == u.y) return fail(c, BRIK_EINVAL, "gemv_plan_glu: gate and up need distinct outputs");
+    if (d.K != g.N || d.x != u.y || down->gate != g.y)
+        return fail(c, BRIK_EINVAL,
+                    "gemv_plan_glu: down must multiply act(gate.y) * up.y (down.gate = gate.y, down.x = up.y, "
+                    "down.K = gate.N)");
+    if (down->norm_w || (down->flags & ~BRIK_JOB_ACT_GELU))
+        return fail(c, BRIK_EINVAL, "gemv_plan_glu: down takes no RMSNorm (flags: BRIK_JOB_ACT_GELU only)");
+    const brik_gemv_job_ex both[2] = {*gate, *up};
+    if (fmt == BRIK_FMT_Q8) {
+        // no q8 pair kernel: the two ordinary plans (down stages its own input)
+        int r = brik_gemv_plan_create_ex(c, fmt, both, 2, gate_up);
+        if (r != BRIK_OK) return r;
+        r = brik_gemv_plan_create_ex(c, fmt, down, 1, down_plan);
+        if (r != BRIK_OK) {
+            brik_gemv_plan_destroy(c, *gate_up);
+            *gate_up = nullptr;
+        }
+        return r;
+    }
+    const Fmt f = Fmt(fmt);
+    int r = check_jobs(c, f, both, 2);
+    if (r == BRIK_OK) r = check_jobs(c, f, down, 1);
+    if (r != BRIK_OK) return r;
+    // the image of down's input: zero groups (group G stays the zero group), then flag 0 and factor 1
+    const size_t ib = (gemv_lds(d.K, f) + 15) & ~(size_t)15;
+    std::vector<unsigned char> host(ib, 0);
+    const size_t tail = (size_t)112 * (d.K / kGroup + 1);
+    const float one = 1.f;
+    std::memcpy(host.data() + tail + 4, &one, sizeof one);
+    SharedBuf* img = new (std::nothrow) SharedBuf();
+    brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();
+    if (!img || !p) {
+        delete img;
+        delete p;
+        return BRIK_ENOMEM;
+    }
+    r = brik_alloc(c, ib, &img->ptr);
+    if (r == BRIK_OK) r = brik_h2d(c, img->ptr, host.data(), ib);
+    if (r == BRIK_OK) r = brik_alloc(c, sizeof both, &p->dev);
+    if (r == BRIK_OK) r = brik_h2d(c, p->dev, both, sizeof both);
+    if (r != BRIK_OK) {
+        brik_free(c, img->ptr);
+        brik_free(c, p->dev);
+        delete img;
+        delete p;
+        return r;
+    }
+    p->glu = true;
+    p->kernel = c->gemvp[fmt_index(f)];
+    p->njobs = 2;
+    p->blocks = (unsigned)(g.N / kGluRows);
+    p->lds = gemv_lds(g.K, f) + kGluVariant.extra_lds(2 * kGluRows);
+    p->act_flags = down->flags & BRIK_JOB_ACT_GELU;
+    p->stage = img->ptr;
+    p->image = img;
+    img->refs = 1;
+    r = plan_create(c, fmt, down, 1, down_plan, img);
+    if (r != BRIK_OK) {
+        brik_gemv_plan_destroy(c, p);
+        return r;
+    }
+    *gate_up = p;
     return BRIK_OK;
 }
 
@@ -1413,13 +1542,20 @@ int brik_gemv_plan_create(brik_ctx* c, int fmt, const brik_gemv_job* jobs, int n
 int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
 {
     if (!c || !p) return BRIK_EINVAL;
+    if (p->glu) {
+        const brik_gemv_job_ex* jobs = (const brik_gemv_job_ex*)p->dev;
+        void* img = p->stage;
+        int af = p->act_flags;
+        void* args[] = {&jobs, &img, &af};
+        return launch_fn(c, p->kernel, p->blocks, 1, kGluThreads, p->lds, args);
+    }
     const brik_gemv_job_ex* jobs = (const brik_gemv_job_ex*)p->dev;
     const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job_ex) * (size_t)p->njobs);
     const uint32_t* rpbs = start + p->njobs + 1;
     const uint32_t* stage_off = rpbs + p->njobs;
     const unsigned char* stage = static_cast<const unsigned char*>(p->stage);
     int nj = p->njobs;
-    if (p->stage) {
+    if (p->stager) {
         // one block per distinct input row; the GEMV launch that follows on the stream reads the images
         const brik_stage_input* inputs =
             reinterpret_cast<const brik_stage_input*>(static_cast<const unsigned char*>(p->dev) + p->inputs_off);
@@ -1436,7 +1572,11 @@ void brik_gemv_plan_destroy(brik_ctx* c, brik_gemv_plan* p)
     if (!p) return;
     if (c) {
         brik_free(c, p->dev);
-        brik_free(c, p->stage);
+        if (!p->image) brik_free(c, p->stage);
+    }
+    if (p->image && --p->image->refs == 0) {
+        if (c) brik_free(c, p->image->ptr);
+        delete p->image;
     }
     delete p;
 }

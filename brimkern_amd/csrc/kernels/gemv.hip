@@ -299,14 +299,20 @@ __device__ __forceinline__ void code_nibbles(const Grp<FMT>& d, uint32_t (&c)[4]
 // 8 * sum X that undoes the -8), then one conversion, one exact rescale and two FMAs.
 // The dot products use the clamping form: no partial sum can overflow, so the value is the same,
 // and the compiler keeps the chain as written instead of splitting it into six sums.
-template <int FMT, int TEAM, int R, int U>
+//
+// P = 2 (GLU pairs): two matrices of equal shape on the same staged x. A team's R rows are then
+// RH = R / 2 rows of the first matrix (rs) followed by the same rows of the second (rs2): row r of
+// the team is row n0(p) + r % RH of matrix r / RH. NT: threads per block.
+template <int FMT, int TEAM, int R, int U, int P = 1, int NT = 256>
 struct WorkD {
-    static constexpr int RPI = (256 / TEAM) * R;
+    static_assert(P == 1 || (P == 2 && R % 2 == 0), "pair rows");
+    static constexpr int RPI = (NT / TEAM) * R;    // rows per block iteration, both matrices together
+    static constexpr int RH = R / P;               // rows per team and matrix
     static constexpr int PARTS = TEAM;
     static constexpr int NACC = R;
     static constexpr int UG = U;
     typedef Grp<FMT> Data[U][R];
-    Rs rs;
+    Rs rs, rs2;
     int G, r0, r1, rstep, B, lane, team;
     float* part;
 
@@ -326,7 +332,7 @@ struct WorkD {
         B = (G + U * TEAM - 1) / (U * TEAM);
     }
     __device__ __forceinline__ bool even() const { return G % (U * TEAM) == 0; }
-    __device__ __forceinline__ int n0(int p) const { return r0 + team * R + p * rstep; }
+    __device__ __forceinline__ int n0(int p) const { return r0 + team * RH + p * rstep; }
 
     template <bool EVEN>
     __device__ __forceinline__ void issue(Grp<FMT> (&d)[U][R], int p, int b) const
@@ -334,14 +340,15 @@ struct WorkD {
         const int n = n0(p);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const uint32_t row = (uint32_t)min(n + r, r1 - 1) * (uint32_t)G;
+            const uint32_t row = (uint32_t)min(n + r % RH, r1 - 1) * (uint32_t)G;
+            const Rs& q = r < RH ? rs : rs2;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if constexpr (EVEN) {
-                    load_grp<FMT>(d[u][r], rs, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
+                    load_grp<FMT>(d[u][r], q, row + (uint32_t)lane, (uint32_t)(TEAM * U * b), (uint32_t)(u * TEAM));
                 } else {
                     const uint32_t g = (uint32_t)min(lane + TEAM * (U * b + u), G - 1);
-                    load_grp<FMT>(d[u][r], rs, row + g, 0u, 0u);
+                    load_grp<FMT>(d[u][r], q, row + g, 0u, 0u);
                 }
             }
         }
@@ -390,18 +397,21 @@ template <int TEAM, int R, int U>
 struct Work<FMT_Q4, TEAM, R, U> : WorkD<FMT_Q4, TEAM, R, U> {};
 template <int TEAM, int R, int U>
 struct Work<FMT_Q3, TEAM, R, U> : WorkD<FMT_Q3, TEAM, R, U> {};
+// GLU pair work (digit-plane formats only)
+template <int FMT, int TEAM, int R, int U, int NT>
+using PairWork = WorkD<FMT, TEAM, R, U, 2, NT>;
 
-// Exact path for a row holding Inf/NaN: 16 teams of 16 lanes; in every row set (rows
-// base + [0, RPI), base = r0, r0 + rstep, ...) team t takes rows t, t + 16, ... (any RPI, also below 16).
+// Exact path for a row holding Inf/NaN: teams of 16 lanes (16 in a 256-thread block); in every row set
+// (rows base + [0, RPI), base = r0, r0 + rstep, ...) team t takes rows t, t + teams, ... (any RPI).
 template <int FMT, int RPI>
 __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Fuse& F, float inv,
                                                 const Planes& P, float* __restrict__ yrow,
                                                 const float* __restrict__ res, int K, int r0, int r1, int rstep)
 {
     const int lane = threadIdx.x % 16;
-    const int team = threadIdx.x / 16;
+    const int team = threadIdx.x / 16, nteams = blockDim.x / 16;
     for (int base = r0; base < r1; base += rstep) {
-        for (int i = team; i < RPI; i += 16) {
+        for (int i = team; i < RPI; i += nteams) {
             const int n = base + i;         // uniform across the team's 16 lanes
             if (n >= r1) break;
             float acc = 0.f;
@@ -426,11 +436,12 @@ __device__ __forceinline__ void stage_copy(const unsigned char* __restrict__ src
 
 // The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
-// With a pre-staged image (`staged`, written by brik_gemv_stage_<fmt>) the block copies it into LDS,
-// issued ahead of the first weight loads so that waiting for it does not wait for them.
+// With a pre-staged image (`staged`, written by brik_gemv_stage_<fmt> or by a GLU pair launch) the
+// block copies it into LDS, issued ahead of the first weight loads so that waiting for it does not
+// wait for them. Returns true, before any step is consumed, if the row holds a value that is not
+// finite: the caller then runs the exact path.
 template <int FMT, class W, int D, bool EVEN>
-__device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
-                                         const Planes& P, float* __restrict__ yrow, const float* __restrict__ res,
+__device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
                                          int K, int S, const unsigned char* __restrict__ staged, unsigned char* lds)
 {
     typename W::Data d[D];
@@ -446,18 +457,20 @@ __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const fl
         bp = wrap ? 0 : bp + 1;
         ip += wrap;
     }
+    int flag;
     if (staged) {
         // every load issued after the copy is one of the D - 1 weight steps above
         brik::wait_vmcnt<(D - 1) * W::NACC * W::UG * LoadsPerGroup<FMT>::v>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        flag = *X.flag;
+        // a GLU pair launch writes the groups of an image but not its flag: each group carries its own
+        // marker (a stager's image carries both)
+        if constexpr (FMT != FMT_Q8) flag |= brik::image_bad(X);
     } else {
         W::stage(x, X, K, F);
+        flag = *X.flag;
     }
-    if (*X.flag) {
-        // exact path: teams of 16 lanes over RPI rows per iteration
-        gemv_rows_exact<FMT, W::RPI>(x, F, *X.inv, P, yrow, res, K, w.r0, w.r1, w.rstep);
-        return;
-    }
+    if (flag) return true;
     float acc[W::NACC] = {};
     int pc = 0, bc = 0;                      // (p, b) of the next step to consume
     int i = 0;
@@ -486,6 +499,7 @@ __device__ __forceinline__ void pipeline(W& w, const typename W::XS& X, const fl
             pc += wrap;
         }
     }
+    return false;
 }
 
 // Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
@@ -506,9 +520,13 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     const int S = nsets * w.B;                                            // steps per lane
     const typename W::XS X = W::xs_layout(lds, K);
     w.part = (float*)(lds + W::xs_bytes(K));
-    if (w.even()) pipeline<FMT, W, D, true>(w, X, x, F, P, yrow, res, K, S, staged, lds);
-    else pipeline<FMT, W, D, false>(w, X, x, F, P, yrow, res, K, S, staged, lds);
-    if (*X.flag) return;
+    const bool exact = w.even() ? pipeline<FMT, W, D, true>(w, X, x, F, K, S, staged, lds)
+                                : pipeline<FMT, W, D, false>(w, X, x, F, K, S, staged, lds);
+    if (exact) {
+        // teams of 16 lanes over RPI rows per iteration
+        gemv_rows_exact<FMT, W::RPI>(x, F, *X.inv, P, yrow, res, K, r0, r1, rstep);
+        return;
+    }
     __syncthreads();
     // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped), times the
     // RMSNorm factor of a fused input (1 otherwise: exact), which the staged image leaves out
@@ -570,6 +588,84 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
                            RPI, lds, stage_base ? stage_base + stage_off[lo] : nullptr);
 }
 
+// GLU pair (brik_gemv_plan_create_glu): rows [r0, r0 + H) of gate (jobs jg) and up (ju), H = RPI / 2,
+// both N x K on one staged x (their common input and fusion), in one row set; then the staged image
+// of act(gate) * up over these rows, which are whole quantization groups of the consumer's K' = N
+// input (H and r0 are multiples of 32): written to img + 112 g for each group g they cover, in the
+// digit-plane layout of xprep.h, bit-identical to what the consumer would stage (stage_group_lanes,
+// the 32-lane form of the code that stages a row in LDS). Each row sum
+// uses the same lane partials, summed in the same order (a rotation by the row index), as the
+// single-matrix path with the same TEAM and U, so gate and up, and with them the image, are
+// bit-identical to those of unpaired plans.
+template <int FMT, class W, int D>
+__device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const brik_gemv_job_ex& ju, int r0,
+                                              unsigned char* __restrict__ img, int act_flags, unsigned char* lds)
+{
+    constexpr int H = W::RPI / 2, RH = W::RH, R = W::NACC, PARTS = W::PARTS;
+    static_assert(H % BRIK_GROUP == 0 && R == 2 * RH, "whole groups per block");
+    const int K = jg.job.K, N = jg.job.N;
+    const Fuse F{jg.gate, jg.norm_w, jg.eps, jg.flags};
+    const Planes Pg{(const uint8_t*)jg.job.p0, (const uint8_t*)jg.job.p1, jg.job.scales, jg.job.mins};
+    const Planes Pu{(const uint8_t*)ju.job.p0, (const uint8_t*)ju.job.p1, ju.job.scales, ju.job.mins};
+    W w;
+    w.G = K / BRIK_GROUP;
+    w.rs = make_rs<FMT>(Pg, N, w.G);
+    w.rs2 = make_rs<FMT>(Pu, N, w.G);
+    w.r0 = r0; w.r1 = min(N, r0 + H); w.rstep = H;
+    w.init();
+    const typename W::XS X = W::xs_layout(lds, K);
+    w.part = (float*)(lds + W::xs_bytes(K));
+    const bool exact = w.even() ? pipeline<FMT, W, D, true>(w, X, jg.job.x, F, K, w.B, nullptr, lds)
+                                : pipeline<FMT, W, D, false>(w, X, jg.job.x, F, K, w.B, nullptr, lds);
+    float* vals = (float*)lds;     // gate then up values of the set; the x image is not read any more
+    if (exact) {
+        gemv_rows_exact<FMT, H>(jg.job.x, F, *X.inv, Pg, jg.job.y, jg.res, K, w.r0, w.r1, H);
+        gemv_rows_exact<FMT, H>(ju.job.x, F, *X.inv, Pu, ju.job.y, ju.res, K, w.r0, w.r1, H);
+        __syncthreads();           // the rows just written are visible to the block
+        for (int q = threadIdx.x; q < 2 * H; q += blockDim.x) {
+            const int n = r0 + q % H;
+            vals[q] = n < N ? (q < H ? jg.job.y : ju.job.y)[n] : 0.f;
+        }
+    } else {
+        __syncthreads();
+        const float inv = *X.inv;      // read by every thread before the values overwrite LDS
+        float v[2] = {0.f, 0.f};
+        int at[2] = {-1, -1};
+        // thread q sums partial row q = team * R + r: row i = team * RH + r % RH of matrix r / RH
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int q = (int)threadIdx.x + k * (int)blockDim.x;
+            if (q < W::RPI) {
+                const int r = q % R, m = r / RH, i = q / R * RH + r % RH;
+                const float* pp = w.part + (size_t)q * PARTS;
+                float s = 0.f;
+#pragma unroll
+                for (int l = 0; l < PARTS; ++l) s += pp[(l + i) % PARTS];
+                s *= inv;
+                const int n = r0 + i;
+                if (n < N) {
+                    const float* res = m ? ju.res : jg.res;
+                    s = res ? res[n] + s : s;
+                    (m ? ju.job.y : jg.job.y)[n] = s;
+                }
+                v[k] = s;
+                at[k] = m * H + i;
+            }
+        }
+        __syncthreads();           // (a tiny row's image tail, inv included, lies under the values)
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+            if (at[k] >= 0) vals[at[k]] = v[k];
+    }
+    __syncthreads();
+    // group g on lanes 0-31 of wave g, lane e holding element e
+    const int g = threadIdx.x >> 6, e = threadIdx.x & 63;
+    if (g < H / BRIK_GROUP && e < BRIK_GROUP) {
+        const float v = brik::act(vals[BRIK_GROUP * g + e], act_flags) * vals[H + BRIK_GROUP * g + e];
+        brik::stage_group_lanes<FMT>(v, img + 112 * (r0 / BRIK_GROUP + g));
+    }
+}
+
 }  // namespace
 
 #define BRIK_GEMV(FMTN, FMT, TEAM, RR, UU, DD)                                                      \
@@ -604,6 +700,20 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __rest
 BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)
 BRIK_GEMV_FMT(q3, FMT_Q3)
+
+// GLU pair launch: jobs[0] = gate, jobs[1] = up; block b (NT threads) runs rows [H b, H b + H) of both,
+// H = RPI / 2, and writes their groups of the image of act(gate) * up to img (act_flags:
+// BRIK_JOB_ACT_GELU or 0). The runtime table (brik_runtime.cpp, kGluVariant) names this shape.
+#define BRIK_GEMV_PAIR(FMTN, FMT, TEAM, RR, UU, DD, NT)                                                   \
+    extern "C" __global__ __launch_bounds__(NT) void brik_gemvp_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD##_n##NT( \
+        const brik_gemv_job_ex* __restrict__ jobs, unsigned char* __restrict__ img, int act_flags)      \
+    {                                                                                                   \
+        extern __shared__ __align__(16) unsigned char lds[];                                            \
+        using W_ = PairWork<FMT, TEAM, RR, UU, NT>;                                                     \
+        gemv_glu_pair<FMT, W_, DD>(jobs[0], jobs[1], (int)blockIdx.x * (W_::RPI / 2), img, act_flags, lds); \
+    }
+BRIK_GEMV_PAIR(q4, FMT_Q4, 16, 2, 1, 2, 512)
+BRIK_GEMV_PAIR(q3, FMT_Q3, 16, 2, 1, 2, 512)
 
 // Staging pass of a large grouped plan: block i (1024 threads) writes the LDS image of input i (x, or
 // its fused transform) to out + in[i].off in the layout a plan block stages (it depends only on the

@@ -275,7 +275,8 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
 //
 // LDS layout, group-major so every read uses an immediate offset: group g (0 <= g <= G) occupies
 // bytes [112g, 112g + 112): digit plane n at 112g + 16n (n < 6), then {f32 sum of the group's x,
-// int32 e_g - 22, int32 8 * sum X, 0} at 112g + 96. Group G is all zeros (the zero group). A team's
+// int32 e_g - 22, int32 8 * sum X, int32 1 if the group holds a value that is not finite, else 0} at
+// 112g + 96. Group G is all zeros (the zero group). A team's
 // lanes read consecutive groups 112 bytes apart, which spreads any 8 of them over distinct banks.
 // Then the flag, the RMSNorm factor and its reduction slots as in the byte-limb layout.
 struct XStageD {
@@ -347,6 +348,57 @@ __host__ __device__ __forceinline__ int digit_elem(int j, int i)
     return FMT == FMT_Q3 ? 16 * (j >> 1) + 2 * i + (j & 1) : 8 * j + i;
 }
 
+// One group's digit planes from its 32 values: the thread at quad position j (lane & 3) holds elements
+// 8j .. 8j+7 in v0, v1; all four lanes of an aligned quad call it together (the group's sum, max and
+// sum X are DPP quad reductions). gb: the group's 112 bytes (LDS, or a staged image in global memory).
+// Writes the planes and {sum x, e - 22, 8 sum X, 1 if a value is not finite else 0}; returns
+// whether the values are all finite (the planes of a group that is not are all zeros).
+template <int FMT>
+__device__ __forceinline__ bool stage_group_d(f32x4_t v0, f32x4_t v1, int j, unsigned char* gb)
+{
+    // The sums below start from the values as rounded: with -ffp-contract=fast the compiler could
+    // otherwise fold a caller's product (act(gate) * up, v * gain) into them as an FMA, and decide
+    // that differently in each kernel that inlines this one, while a GLU pair launch must write the
+    // image its consumer would stage itself.
+    asm volatile("" : "+v"(v0), "+v"(v1));
+    const float p = sum4(((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)));
+    const float a = max4(fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                               fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w)))));
+    const bool finite = __builtin_isfinite(p) && __builtin_isfinite(a);
+    int e = 0;
+    (void)frexpf(a, &e);                 // a < 2^e, so |x * 2^(22-e)| < 2^22
+    const int sh = 22 - e;
+    uint32_t dg[8];
+    int sx = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+        const int X = finite ? (int)__builtin_rintf(ldexpf(t < 4 ? v0[t] : v1[t - 4], sh)) : 0;
+        sx += X;
+        dg[t] = (uint32_t)(X + 0x888888) ^ 0x888888u;   // digit n of X in nibble n, as a signed nibble
+    }
+    sx = sum4i(sx);
+    uint32_t w[8];
+    if constexpr (FMT == FMT_Q3) {
+        // thread j holds elements 8j .. 8j+7: the even ones are nibbles 4(j&1) .. +3 of dword 2(j>>1),
+        // the odd ones the same nibbles of dword 2(j>>1)+1; transposed in the order 0 2 4 6 1 3 5 7
+        // every digit plane word splits into those two 16-bit halves
+        const uint32_t eo[8] = {dg[0], dg[2], dg[4], dg[6], dg[1], dg[3], dg[5], dg[7]};
+        nibble_transpose8(eo, w);
+        const int de = 8 * (j >> 1) + 2 * (j & 1), dodd = de + 4;   // byte offsets in a plane
+#pragma unroll
+        for (int n = 0; n < 6; ++n) {
+            *(uint16_t*)(gb + 16 * n + de) = (uint16_t)w[n];
+            *(uint16_t*)(gb + 16 * n + dodd) = (uint16_t)(w[n] >> 16);
+        }
+    } else {
+        nibble_transpose8(dg, w);
+#pragma unroll
+        for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
+    }
+    if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, finite ? 0 : 1};
+    return finite;
+}
+
 // Stage x[0..K) (16-byte aligned, K % 32 == 0) as digit planes: one thread per 8 consecutive elements,
 // a quad of lanes per group. All threads of the block call it; ends with a barrier.
 template <int FMT, int SB>
@@ -367,46 +419,74 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
             v0 = gain_in<2>(r, 0, F, v0);
             v1 = gain_in<2>(r, 1, F, v1);
         }
-        const int g = i >> 2, j = i & 3;
-        const float p = sum4(((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w)));
-        const float a = max4(fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
-                                   fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w)))));
-        const bool finite = __builtin_isfinite(p) && __builtin_isfinite(a);
-        int e = 0;
-        (void)frexpf(a, &e);                 // a < 2^e, so |x * 2^(22-e)| < 2^22
-        const int sh = 22 - e;
-        uint32_t dg[8];
-        int sx = 0;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const int X = finite ? (int)__builtin_rintf(ldexpf(t < 4 ? v0[t] : v1[t - 4], sh)) : 0;
-            sx += X;
-            dg[t] = (uint32_t)(X + 0x888888) ^ 0x888888u;   // digit n of X in nibble n, as a signed nibble
-        }
-        sx = sum4i(sx);
-        uint32_t w[8];
-        unsigned char* gb = S.base + 112 * g;
-        if constexpr (FMT == FMT_Q3) {
-            // thread j holds elements 8j .. 8j+7: the even ones are nibbles 4(j&1) .. +3 of dword 2(j>>1),
-            // the odd ones the same nibbles of dword 2(j>>1)+1; transposed in the order 0 2 4 6 1 3 5 7
-            // every digit plane word splits into those two 16-bit halves
-            const uint32_t eo[8] = {dg[0], dg[2], dg[4], dg[6], dg[1], dg[3], dg[5], dg[7]};
-            nibble_transpose8(eo, w);
-            const int de = 8 * (j >> 1) + 2 * (j & 1), dodd = de + 4;   // byte offsets in a plane
-#pragma unroll
-            for (int n = 0; n < 6; ++n) {
-                *(uint16_t*)(gb + 16 * n + de) = (uint16_t)w[n];
-                *(uint16_t*)(gb + 16 * n + dodd) = (uint16_t)(w[n] >> 16);
-            }
-        } else {
-            nibble_transpose8(dg, w);
-#pragma unroll
-            for (int n = 0; n < 6; ++n) *(uint32_t*)(gb + 16 * n + 4 * j) = w[n];
-        }
-        if (j == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, 0};
-        bad |= !finite;
+        bad |= !stage_group_d<FMT>(v0, v1, i & 3, S.base + 112 * (i >> 2));
     });
     stage_finish(S.flag, S.inv, F, K, ss, bad);
+}
+
+// The same group image from lanes 0-31 of one wave (all active), lane e holding element e: for a
+// producer that writes a single group at the end of its block, with the group reductions as DPP steps
+// and two lane reads instead of the 8-element-per-lane work of stage_group_d. Every value is
+// bit-identical to stage_group_d's: the group sum follows the same tree, ((e0 + e1) + (e2 + e3)) +
+// ((e4 + e5) + (e6 + e7)) within each 8, then (c0 + c1) + (c2 + c3) (each exchange meets an add's
+// operands in one order or the other, and an IEEE sum is commutative); max and the integer sums are
+// exact in any order.
+template <int FMT>
+__device__ __forceinline__ void stage_group_lanes(float v, unsigned char* gb)
+{
+    asm volatile("" : "+v"(v));   // as in stage_group_d
+    const int e = (int)(threadIdx.x & 63);
+    float p = sum8(v);                                   // c_j in the 8 lanes of chunk j
+    p = BRIK_DPP_ADD(p, DPP_ROW_ROR8);                   // c0 + c1 in lanes 0-15, c2 + c3 in 16-31
+    p = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 0)) +
+        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p), 16));
+    float a = max8(fabsf(v));
+    a = BRIK_DPP_MAX(a, DPP_ROW_ROR8);
+    a = fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0)),
+              __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 16)));
+    const bool finite = __builtin_isfinite(p) && __builtin_isfinite(a);
+    int ex = 0;
+    (void)frexpf(a, &ex);
+    const int sh = 22 - ex;
+    const int X = finite ? (int)__builtin_rintf(ldexpf(v, sh)) : 0;
+    int sx = X;
+    sx += __builtin_amdgcn_mov_dpp(sx, DPP_QUAD_1032, 0xF, 0xF, false);
+    sx += __builtin_amdgcn_mov_dpp(sx, DPP_QUAD_2301, 0xF, 0xF, false);
+    sx += __builtin_amdgcn_mov_dpp(sx, DPP_ROW_HALF_MIRROR, 0xF, 0xF, false);
+    sx += __builtin_amdgcn_mov_dpp(sx, DPP_ROW_ROR8, 0xF, 0xF, false);
+    sx = __builtin_amdgcn_readlane(sx, 0) + __builtin_amdgcn_readlane(sx, 16);
+    const uint32_t dg = (uint32_t)(X + 0x888888) ^ 0x888888u;
+    // nibble i of plane dword j holds element digit_elem(j, i): q4 j = e >> 3, i = e & 7 (the 8 lanes of
+    // a dword are adjacent); q3 j = 2 (e >> 4) + (e & 1), i = (e & 15) >> 1 (the lanes of one parity in
+    // a 16-lane row)
+    const int sl = FMT == FMT_Q3 ? 4 * ((e & 15) >> 1) : 4 * (e & 7);
+    const bool writer = FMT == FMT_Q3 ? (e & 14) == 0 : (e & 7) == 0;
+    const int dw = FMT == FMT_Q3 ? 2 * (e >> 4) + (e & 1) : e >> 3;
+#pragma unroll
+    for (int n = 0; n < 6; ++n) {
+        uint32_t w = ((dg >> (4 * n)) & 0xFu) << sl;
+        if constexpr (FMT == FMT_Q3) {
+            w |= __builtin_amdgcn_mov_dpp(w, 0x122, 0xF, 0xF, false);    // row_ror:2
+            w |= __builtin_amdgcn_mov_dpp(w, DPP_ROW_ROR4, 0xF, 0xF, false);
+            w |= __builtin_amdgcn_mov_dpp(w, DPP_ROW_ROR8, 0xF, 0xF, false);
+        } else {
+            w |= __builtin_amdgcn_mov_dpp(w, DPP_QUAD_1032, 0xF, 0xF, false);
+            w |= __builtin_amdgcn_mov_dpp(w, DPP_QUAD_2301, 0xF, 0xF, false);
+            w |= __builtin_amdgcn_mov_dpp(w, DPP_ROW_HALF_MIRROR, 0xF, 0xF, false);
+        }
+        if (writer) *(uint32_t*)(gb + 16 * n + 4 * dw) = w;
+    }
+    if (e == 0) *(i32x4_t*)(gb + 96) = i32x4_t{__builtin_bit_cast(int, p), -sh, sx * 8, finite ? 0 : 1};
+}
+
+// Whether any of the G groups of a digit-plane image holds a value that is not finite (the marker
+// stage_group_d writes). Called by every thread of the block after the image is in LDS; the
+// block-wide OR ends with a barrier.
+__device__ __forceinline__ int image_bad(const XStageD& S)
+{
+    int bad = 0;
+    for (int g = (int)threadIdx.x; g < S.G; g += (int)blockDim.x) bad |= *(const int*)(S.base + 112 * g + 108);
+    return __syncthreads_or(bad);
 }
 
 }  // namespace brik

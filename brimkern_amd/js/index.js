@@ -50,6 +50,23 @@ const OPT_GEMV_VARIANT = 2;
 // A device allocation owned by this object: destroy() frees it at once; if the object is dropped
 // without destroy(), the addon's finalizer frees it when the garbage collector reclaims the handle
 // (the reference releases its buffers through destroy() or lets the GC take them, kernels.ts:903-956).
+
+// The native job object of a plan job {x, w, y, K, N[, gate, norm, res, eps, onePlus, act]}.
+function jobSpec(j) {
+  const w = j.w;
+  const s = { x: j.x, p0: w.nib || w.codes || w.lo, p1: w.hi || null, scales: w.sc, mins: w.mn || null,
+    y: j.y, K: j.K, N: j.N };
+  if (j.gate) s.gate = j.gate;
+  if (j.norm) s.normW = j.norm;
+  if (j.res) s.res = j.res;
+  if (j.eps !== undefined) s.eps = j.eps;
+  s.flags = (j.onePlus ? 1 : 0) | (j.act === 'gelu' ? 2 : 0);
+  return s;
+}
+
+function planHandle(nat, plan) {
+  return { run: function () { nat.gemvPlanRun(plan); }, destroy: function () { nat.gemvPlanDestroy(plan); } };
+}
 class DeviceBuffer {
   constructor(engine, handle, size) {
     this.engine = engine;
@@ -215,19 +232,18 @@ class Engine {
   // SwiGLU / GeGLU gate buffer, x being "up"), act ('gelu' for GeGLU), res (residual added to y).
   gemvPlan(fmt, jobs) {
     const nat = this.native;
-    const specs = jobs.map(function (j) {
-      const w = j.w;
-      const s = { x: j.x, p0: w.nib || w.codes || w.lo, p1: w.hi || null, scales: w.sc, mins: w.mn || null,
-        y: j.y, K: j.K, N: j.N };
-      if (j.gate) s.gate = j.gate;
-      if (j.norm) s.normW = j.norm;
-      if (j.res) s.res = j.res;
-      if (j.eps !== undefined) s.eps = j.eps;
-      s.flags = (j.onePlus ? 1 : 0) | (j.act === 'gelu' ? 2 : 0);
-      return s;
-    });
-    const plan = nat.gemvPlanCreate(this.ctx, FMT[fmt], specs);
-    return { run: function () { nat.gemvPlanRun(plan); }, destroy: function () { nat.gemvPlanDestroy(plan); } };
+    const plan = nat.gemvPlanCreate(this.ctx, FMT[fmt], jobs.map(jobSpec));
+    return planHandle(nat, plan);
+  }
+
+  // The feed-forward half of a layer as linked plans (brik_gemv_plan_create_glu): gate and up jobs on
+  // one input, then down on act(gate) * up (down.gate = gate.y, down.x = up.y; act: 'gelu' or SiLU).
+  // Returns [gateUp, down]; run them in that order. Outputs equal those of two ordinary plans (within
+  // f32 rounding for gate and up).
+  gemvPlanGlu(fmt, gate, up, down) {
+    const nat = this.native;
+    const pair = nat.gemvPlanCreateGlu(this.ctx, FMT[fmt], jobSpec(gate), jobSpec(up), jobSpec(down));
+    return [planHandle(nat, pair[0]), planHandle(nat, pair[1])];
   }
 
   // ---- sampling pre-work (decodeTopKQ8) --------------------------------------------------------

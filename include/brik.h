@@ -197,6 +197,24 @@ typedef struct brik_gemv_job_ex {
 } brik_gemv_job_ex;
 int brik_gemv_plan_create_ex(brik_ctx *ctx, int fmt, const brik_gemv_job_ex *jobs, int njobs,
                              brik_gemv_plan **out);
+
+/* The feed-forward half of recordLayerKV as a linked pair of plans (kernels.ts:1726-1741: gate and
+ * up on rmsnorm(h), swiglu / geglu, down + residual). Replaces the two plans {gate, up} and {down with
+ * gate = gate.y, x = up.y}: *gate_up runs both projections in one launch, each block computing rows of
+ * the same indices of gate and up (32 of each, one quantization group of down's input), and writes the
+ * staged input image of act(gate.y) * up.y for those rows; *down_plan copies that image instead of
+ * each of its blocks transforming the whole row. down.y is bit-identical to the unlinked down plan's
+ * for the same gate.y and up.y; gate.y and up.y equal the unlinked plan's within f32 rounding (the
+ * RMSNorm factor and the row sums are added up in another order).
+ *   gate, up: equal x, K, N and input fusion (gate, norm_w, eps, flags), distinct y.
+ *   down: down.gate == gate.y, down.x == up.y, down.K == N; no norm_w; flags 0 or BRIK_JOB_ACT_GELU
+ *         (the activation of the image); res allowed.
+ * Run *gate_up before *down_plan (the order of the layer): down reads the image of gate_up's last
+ * run. The plans share that image and may be destroyed in either order. q8 has no pair kernel: for
+ * BRIK_FMT_Q8 the two ordinary plans are returned (down stages its own input). */
+int brik_gemv_plan_create_glu(brik_ctx *ctx, int fmt, const brik_gemv_job_ex *gate, const brik_gemv_job_ex *up,
+                              const brik_gemv_job_ex *down, brik_gemv_plan **gate_up,
+                              brik_gemv_plan **down_plan);
 int brik_gemv_plan_run(brik_ctx *ctx, const brik_gemv_plan *plan);
 void brik_gemv_plan_destroy(brik_ctx *ctx, brik_gemv_plan *plan);
 

@@ -23,7 +23,7 @@ pytestmark = pytest.mark.skipif(NODE is None, reason="node not installed")
 
 EXPORTS = ["deviceCount", "createContext", "alloc", "free", "h2d", "d2h", "sync", "setOption", "timerBegin",
            "timerEnd", "matmulQ8", "matmulQ4", "matmulQ3", "moeMatmulQ4", "dequantQ8", "dequantQ4", "dequantQ3",
-           "gemvPlanCreate", "gemvPlanRun", "gemvPlanDestroy", "logitsTopK", "lmHeadTopK", "quantize",
+           "gemvPlanCreate", "gemvPlanCreateGlu", "gemvPlanRun", "gemvPlanDestroy", "logitsTopK", "lmHeadTopK", "quantize",
            "f16ToF32", "conv2d", "matmulF16W", "allocBuffer", "bufferPtr", "freeBuffer", "liveBuffers",
            "readbackAsync", "selfValidate", "moeMatmulQ4x2"]
 
