@@ -1488,11 +1488,14 @@ int brik_gemv_plan_create_glu(brik_ctx* c, int fmt, const brik_gemv_job_ex* gate
     int r = check_jobs(c, f, both, 2);
     if (r == BRIK_OK) r = check_jobs(c, f, down, 1);
     if (r != BRIK_OK) return r;
-    // the image of down's input: zero groups (group G stays the zero group), then flag 0 and factor 1
+    // the image of down's input: zero groups (group G stays the zero group), then the flag -1 (read the
+    // groups' own markers) and the RMSNorm factor 1
     const size_t ib = (gemv_lds(d.K, f) + 15) & ~(size_t)15;
     std::vector<unsigned char> host(ib, 0);
     const size_t tail = (size_t)112 * (d.K / kGroup + 1);
+    const int32_t scan = -1;
     const float one = 1.f;
+    std::memcpy(host.data() + tail, &scan, sizeof scan);
     std::memcpy(host.data() + tail + 4, &one, sizeof one);
     SharedBuf* img = new (std::nothrow) SharedBuf();
     brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();

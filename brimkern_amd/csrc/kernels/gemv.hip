@@ -463,9 +463,10 @@ __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const fl
         brik::wait_vmcnt<(D - 1) * W::NACC * W::UG * LoadsPerGroup<FMT>::v>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         flag = *X.flag;
-        // a GLU pair launch writes the groups of an image but not its flag: each group carries its own
-        // marker (a stager's image carries both)
-        if constexpr (FMT != FMT_Q8) flag |= brik::image_bad(X);
+        // a GLU pair launch writes the groups of an image but not its flag, which stays -1: each group
+        // then carries its own marker (a stager writes the flag, 0 or 1)
+        if constexpr (FMT != FMT_Q8)
+            if (flag < 0) flag = brik::image_bad(X);
     } else {
         W::stage(x, X, K, F);
         flag = *X.flag;
