@@ -276,11 +276,13 @@ unsigned gemm_tiles(long n, int t) { return (unsigned)((n + t - 1) / t); }
 // A 256-column tile runs as its 8-wave form (two waves per SIMD): measured on the M = 512, K = 2560, N = 9728 prefill shape
 // (M = 512, K = 2560, N = 9728) with cold weights 44.9 us against 47.5 us for 96 x 256 with 4 waves,
 // and 5-10 % faster at every other row count.
-// Expert-grouped (MoE): 64 rows x 256 columns, 8 waves. Measured on a 64-expert MoE layer (22-47 rows
-// each) with the XCD-grouped grid, every tile forced: gate + up in one launch (K = 2048, N = 768)
-// 67-70 us against 71-117 us for the others; down (K = 768, N = 2048) 30 us against 32-64 us (38 us with
-// the 32-row tile, which was faster before the launches kept each expert's blocks on one XCD).
-int gemm_tile(brik_ctx* c, long M, long N, int E)
+// Expert-grouped (MoE): 64-row tiles; 64 x 128 with 4 waves for K >= 2048 (16 or more K steps), else
+// 64 x 256 with 8 waves. Measured on a 64-expert MoE layer (22-47 rows each), every tile forced, per
+// call with the x staging: gate + up in one launch (K = 2048, N = 768) 53.7-55.7 us with the 4-wave
+// tile against 60-65 us with the 8-wave one and 60-96 us for the others; down (K = 768, N = 2048)
+// 29.4-30.6 us with the 8-wave tile against 32.8-33.1 with the 4-wave one and 33-61 us for the others;
+// a single gate (K = 2048, N = 768) the same with either (32.3 / 32.7 us kernel time).
+int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
 {
     if (c->opt_tile > 0) return c->opt_tile - 1;
     auto find = [](int bm, int tn, int nw, int pf = 1) {
@@ -289,21 +291,32 @@ int gemm_tile(brik_ctx* c, long M, long N, int E)
                 return t;
         return 0;
     };
-    if (E > 0) return find(64, 1, 8);
-    int best = 0;
-    double best_cost = 0;
-    for (int t = 0; t < kNumGemmTiles; ++t) {
-        GemmTile g = kGemmTiles[t];
-        if (g.nw != 4 || g.pf != 1) continue;
-        const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn());
-        const double rounds = std::ceil(blocks / kCUs);
-        const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
-        const double cost = rounds * g.bm * (double)g.bn() * penalty;
-        if (best_cost == 0 || cost < best_cost) {
-            best = t;
-            best_cost = cost;
+    if (E > 0) return K >= 2048 ? find(64, 1, 4) : find(64, 1, 8);
+    // the modelled makespan over the 4-wave tiles, or (only256) over the 256-column ones
+    auto pick = [&](bool only256, double& blocks_of_best) {
+        int best = 0;
+        double best_cost = 0;
+        for (int t = 0; t < kNumGemmTiles; ++t) {
+            GemmTile g = kGemmTiles[t];
+            if (g.nw != 4 || g.pf != 1 || (only256 && (g.tn != 2 || g.bm < 64))) continue;
+            const double blocks = (double)gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn());
+            const double rounds = std::ceil(blocks / kCUs);
+            const double penalty = g.bm == 128 ? 1.0 : g.bm == 96 ? 1.1 : g.bm == 64 ? 1.3 : 1.8;
+            const double cost = rounds * g.bm * (double)g.bn() * penalty;
+            if (best_cost == 0 || cost < best_cost) {
+                best = t;
+                best_cost = cost;
+                blocks_of_best = blocks;
+            }
         }
-    }
+        return best;
+    };
+    // Launches of at least one round of 64- to 128-row 256-column tiles keep to those (8-wave forms): on
+    // K = 2560, N = 9728 at M = 1024 and 2048 the all-tile model picked a 128 x 128 tile that ran 90 and
+    // 155-167 us against 80-81 us (96 x 256) and 139.5 us (128 x 256).
+    double blocks = 0;
+    int best = pick(true, blocks);
+    if (blocks < kCUs) best = pick(false, blocks);
     const GemmTile& g = kGemmTiles[best];
     return g.tn == 2 ? find(g.bm, 1, 8) : best;     // the 8-wave form of a 256-column tile
 }
@@ -492,7 +505,7 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
         return gemm_splitk(c, f, xh, rscale, pair->p0, p1, pair->sc, pair->mn, pair->y, rows, K, N, row_off, E);
     }
     int Mi = rows, Ki = K, Ni = N, Ei = E;
-    const int t = gemm_tile(c, rows, N, E);
+    const int t = gemm_tile(c, rows, N, K, E);
     const GemmTile& gt = kGemmTiles[t];
     const int bn = gt.bn();
     if (!row_off) {
