@@ -167,6 +167,7 @@ struct brik_ctx {
     hipFunction_t gemvp[3] = {};                 // GLU pair kernels (q4, q3; q8 has none)
     hipFunction_t gemm[3][kNumGemmTiles] = {};
     hipFunction_t gemmg[kNumGemmTiles] = {};    // expert-grouped q4 kernels (brik_gemmg_q4_*)
+    hipFunction_t gemmg_adapt[2] = {};           // brik_gemmg_q4_64a (4 waves), brik_gemmg_q4_64aw8 (8 waves)
     hipFunction_t gemm_f16[kNumGemmTiles] = {};   // f16-weight tiles (TN = 1, PF = 1 only; others null)
     hipFunction_t gemm_sk[3][3] = {};      // split-K few-row kernels, KSL = 2, 4, 8
     hipStream_t stream = nullptr;
@@ -525,7 +526,13 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
     // index so that every block of one pair lands on one XCD
     const unsigned pairs = gemm_tiles(rows, gt.bm) + (unsigned)E;
     const unsigned blocks = (pairs + 7) / 8 * 8 * gemm_tiles(N, bn) * (unsigned)mats;
-    return launch_fn(c, c->gemmg[t], blocks, 1, gt.threads(), 0, args);
+    // the 8-wave 64-row tile runs as its adaptive form (an expert tile of at most 32 live rows takes the
+    // 32-row body): MoE down (K = 768, N = 2048) 28.4 -> 26.7 us kernel time. The 4-wave form measured
+    // slower on gate + up in one launch (52.0 -> 54.9 us), its 32-row body being bound by the same
+    // dequantization work per block, so that one runs as given; so does a forced tile.
+    hipFunction_t fn = c->gemmg[t];
+    if (c->opt_tile <= 0 && gt.bm == 64 && gt.tn == 1 && gt.pf == 1 && gt.nw == 8) fn = c->gemmg_adapt[1];
+    return launch_fn(c, fn, blocks, 1, gt.threads(), 0, args);
 }
 
 // MFMA GEMM over `rows` activation rows: stage x as scaled f16 rows in the workspace, then run the
@@ -921,6 +928,9 @@ int brik_create(int device, brik_ctx** out)
                 max_threads < (int)kGemmTiles[t].threads())
                 return bail(BRIK_EMODULE);
         }
+    if (hipModuleGetFunction(&c->gemmg_adapt[0], c->module, "brik_gemmg_q4_64a") != hipSuccess ||
+        hipModuleGetFunction(&c->gemmg_adapt[1], c->module, "brik_gemmg_q4_64aw8") != hipSuccess)
+        return bail(BRIK_EMODULE);
     for (int t = 0; t < kNumGemmTiles; ++t) {
         const GemmTile& g = kGemmTiles[t];
         if (g.tn != 1 || g.pf != 1) continue;

@@ -650,42 +650,19 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
 // GROUPED: the expert-grouped (MoE) form, a separate instantiation so that the dense kernels hold
 // none of its code; blockIdx.y enumerates (expert, row tile) pairs, found by the block-wide lookup.
 // gtile / gcol (grouped only): this block's (expert, row tile) pair and column tile.
+// One block tile: rows [m0, min(m0 + BM, m_end)) and columns [n0, n0 + BN) of y, with weight slice e
+// (GROUPED) of the planes, in `smem` (T::SMEM bytes, 1024-byte aligned).
 template <int FMT, class T, bool GROUPED>
-__device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
-                                          const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
-                                          const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
-                                          float* __restrict__ y, int M, int K, int N,
-                                          const int* __restrict__ row_off, int E, int gtile = 0, int gcol = 0)
+__device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_t* __restrict__ xh,
+                                              const float* __restrict__ rscale, const uint8_t* __restrict__ p0,
+                                              const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
+                                              const uint16_t* __restrict__ mn, float* __restrict__ y, int M, int K,
+                                              int N, int E, int e, int m0, int m_end, int n0)
 {
-    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, XI = T::XI, NT = T::NT;
-    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
-
+    constexpr int BN = T::BN, TM = T::TM, TN = T::TN, XI = T::XI, NT = T::NT;
     const int G = K / BRIK_GROUP;
     const int Kp = (K + 2 * GK - 1) / (2 * GK) * (2 * GK);
     const int steps = Kp / GK;                 // even, >= 2
-    int m0, m_end = M, n0, e = 0;
-
-    if constexpr (GROUPED) {
-        n0 = gcol * BN;
-        // uniform across the block (the lookup ends with a barrier), before any other barrier
-        if (!find_expert_tile<BM>(row_off, E, gtile, M, e, m0, m_end)) return;
-    } else {
-        const int nMT = (M + BM - 1) / BM, nNT = (N + BN - 1) / BN;
-        const int b = blockIdx.x, gsz = 8 * nMT;
-        const int grp = b / gsz, full = nNT / 8;
-        int mt, nt;
-        if (grp < full) {
-            const int w = b - grp * gsz;
-            nt = grp * 8 + (w & 7);
-            mt = w >> 3;
-        } else {
-            const int w = b - full * gsz;
-            nt = full * 8 + w / nMT;
-            mt = w % nMT;
-        }
-        m0 = mt * BM;
-        n0 = nt * BN;
-    }
 
     // buffer resources: the staged x rows of this launch; the W planes of this matrix (expert slice);
     // the scales and mins of the whole (stacked) plane
@@ -862,6 +839,63 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
             }
         }
     }
+}
+
+template <int FMT, class T, bool GROUPED>
+__device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
+                                          const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
+                                          const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
+                                          float* __restrict__ y, int M, int K, int N,
+                                          const int* __restrict__ row_off, int E, int gtile = 0, int gcol = 0)
+{
+    constexpr int BM = T::BM, BN = T::BN;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
+    int m0, m_end = M, n0, e = 0;
+    if constexpr (GROUPED) {
+        n0 = gcol * BN;
+        // uniform across the block (the lookup ends with a barrier), before any other barrier
+        if (!find_expert_tile<BM>(row_off, E, gtile, M, e, m0, m_end)) return;
+    } else {
+        const int nMT = (M + BM - 1) / BM, nNT = (N + BN - 1) / BN;
+        const int b = blockIdx.x, gsz = 8 * nMT;
+        const int grp = b / gsz, full = nNT / 8;
+        int mt, nt;
+        if (grp < full) {
+            const int w = b - grp * gsz;
+            nt = grp * 8 + (w & 7);
+            mt = w >> 3;
+        } else {
+            const int w = b - full * gsz;
+            nt = full * 8 + w / nMT;
+            mt = w % nMT;
+        }
+        m0 = mt * BM;
+        n0 = nt * BN;
+    }
+    gemm_tile_run<FMT, T, GROUPED>(smem, xh, rscale, p0, p1, sc, mn, y, M, K, N, E, e, m0, m_end, n0);
+}
+
+// Expert-grouped tile of TL::BM rows that runs the TS::BM-row body (the same columns and waves) when
+// its expert tile holds no more live rows than that: an expert's last (or only) row tile is often
+// about half full, and the smaller body skips the MFMAs, A-fragment reads and x loads of the empty
+// 32-row block. The pairs are those of the TL::BM tiling.
+template <int FMT, class TL, class TS>
+__device__ __forceinline__ void gemm_grouped_adaptive(const uint16_t* __restrict__ xh, const float* __restrict__ rscale,
+                                                      const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
+                                                      const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
+                                                      float* __restrict__ y, int M, int K, int N,
+                                                      const int* __restrict__ row_off, int E, int gtile, int gcol)
+{
+    static_assert(TL::BN == TS::BN && TL::NT == TS::NT && TS::BM < TL::BM, "adaptive tile pair");
+    constexpr int SM = TL::SMEM > TS::SMEM ? TL::SMEM : TS::SMEM;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[SM];
+    int e = 0, m0 = 0, m_end = M;
+    if (!find_expert_tile<TL::BM>(row_off, E, gtile, M, e, m0, m_end)) return;
+    const int n0 = gcol * TL::BN;
+    if (m_end - m0 <= TS::BM)
+        gemm_tile_run<FMT, TS, true>(smem, xh, rscale, p0, p1, sc, mn, y, M, K, N, E, e, m0, m_end, n0);
+    else
+        gemm_tile_run<FMT, TL, true>(smem, xh, rscale, p0, p1, sc, mn, y, M, K, N, E, e, m0, m_end, n0);
 }
 
 // ---- 3. split-K GEMM for few rows ---------------------------------------------------------------
@@ -1102,6 +1136,35 @@ BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q4, FMT_Q4)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q8, FMT_Q8)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_DENSE, q3, FMT_Q3)
 BRIK_GEMM_TILE_LIST(BRIK_GEMM_GROUPED, q4, FMT_Q4)
+
+// Adaptive expert-grouped kernels (gemm_grouped_adaptive): brik_gemmg_q4_64a<suffix> runs a 64-row tile
+// whose expert tile has at most 32 live rows as the 32-row tile of the same columns and waves.
+#define BRIK_GEMM_GROUPED_ADAPTIVE(NW_, SUFFIX)                                                           \
+    extern "C" __global__ __launch_bounds__(64 * NW_)                                                     \
+    __attribute__((amdgpu_waves_per_eu(grouped_waves_per_eu(64, 1, NW_, 1))))                            \
+    void brik_gemmg_q4_64a##SUFFIX(                                                                       \
+        const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
+        const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
+        float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E,               \
+        const uint8_t* __restrict__ p0b, const uint16_t* __restrict__ scb, const uint16_t* __restrict__ mnb, \
+        float* __restrict__ yb, int mats)                                                                 \
+    {                                                                                                     \
+        using TL_ = Tile<FMT_Q4, 64, 1, NW_, 1>;                                                          \
+        using TS_ = Tile<FMT_Q4, 32, 1, NW_, 1>;                                                          \
+        const int per = (N + TL_::BN - 1) / TL_::BN * mats;                                               \
+        const int s = (int)(blockIdx.x >> 3), r = s % per;                                                \
+        const int gtile = s / per * 8 + (int)(blockIdx.x & 7);                                            \
+        if (gtile >= (M + 63) / 64 + E) return;                                                           \
+        if (r % mats) {                                                                                   \
+            p0 = p0b;                                                                                     \
+            sc = scb;                                                                                     \
+            mn = mnb;                                                                                     \
+            y = yb;                                                                                       \
+        }                                                                                                 \
+        gemm_grouped_adaptive<FMT_Q4, TL_, TS_>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E, gtile, r / mats); \
+    }
+BRIK_GEMM_GROUPED_ADAPTIVE(4, )
+BRIK_GEMM_GROUPED_ADAPTIVE(8, w8)
 // f16 weights (the reference's MATMUL_T_F16W for M > 1, K % 32 == 0): the one-column-block tiles,
 // brik_gemm_f16_<BM>x1[w8]; the codes are the weights, so there is nothing to dequantize
 BRIK_GEMM_DENSE(f16, FMT_F16, 128, 1, 8, 1, w8) BRIK_GEMM_DENSE(f16, FMT_F16, 96, 1, 8, 1, w8)
