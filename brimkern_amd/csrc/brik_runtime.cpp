@@ -551,8 +551,8 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     HIP_TRY_RC(gemm_stage_ws(c, rows, K, Kp, xh, rscale, fixed));
     int Mi = rows, Ki = K, Kpi = (int)Kp;
     {
-        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one wave per row
-        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
+        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one block per row, at most 65536 blocks
+        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)(rows < 65536 ? rows : 65536), 1, 256, 0, args));
     }
     return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed, pair);
 }
@@ -1275,7 +1275,7 @@ int brik_matmul_t_f16w(brik_ctx* c, const float* x, const uint16_t* w, float* y,
     int Kpi = (int)Kp;
     {
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};
-        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)((M + 3) / 4), 1, 256, 0, args));
+        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)(M < 65536 ? M : 65536), 1, 256, 0, args));
     }
     if (K % kGroup == 0) {
         // the tiled MFMA GEMM with f16 weights (TN = 1 tiles): a forced tile, or the one of fewest

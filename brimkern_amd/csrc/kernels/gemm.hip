@@ -38,7 +38,7 @@
 
 namespace {
 
-constexpr int XPREP_MAXC = 20;  // 8-float chunks per lane held in registers by the one-pass x staging
+constexpr int XPREP_MAXC = 20;  // 8-float chunks per lane held in registers by one-wave-per-row staging (im2col)
 
 __device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
@@ -70,31 +70,39 @@ __device__ __forceinline__ half8_t to_h8(f32x4_t a, f32x4_t b, float up)
 
 // ---- 1. activation staging ----------------------------------------------------------------------
 
-// One wave per row, four rows per block. Rows of up to 64 * XPREP_MAXC 8-float chunks are read once
-// into registers; longer rows are read twice.
-extern "C" __global__ __launch_bounds__(256) void brik_xprep_f16(const float* __restrict__ x,
-                                                                 uint16_t* __restrict__ xh,
-                                                                 float* __restrict__ rscale, int M, int K,
-                                                                 int Kp)
+// One 256-thread block per row, a grid of at most 65536 blocks looping over the rows (a launch of few
+// rows still fills the CUs: the 512 rows of the prefill shape are 512 blocks, against 128 of one wave
+// per row, which ran 6.2 us for 7.9 MB). Rows of up to 256 * XPREP_BCH 8-float chunks are read once
+// into registers; longer rows are read twice. The row maximum is exact in any order, so the output
+// does not depend on how the row is split.
+constexpr int XPREP_BCH = 4;
+
+__device__ __forceinline__ void xprep_row(const float* __restrict__ x, uint16_t* __restrict__ xh,
+                                          float* __restrict__ rscale, int m, int K, int Kp, float* wmax)
 {
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (m >= M) return;     // a whole wave; no block-level synchronisation follows
-    const int lane = threadIdx.x & 63;
+    const int tid = threadIdx.x;
     const float* xr = x + (size_t)m * K;
     uint16_t* hr = xh + (size_t)m * Kp;
     const int nch = K / 8, nchp = Kp / 8;
+    // the block's maximum of the threads' mx, then the power-of-two scale that fits the row into f16
+    // (the barrier after the reads of wmax keeps the next row's writes behind them)
     auto scale_of = [&](float mx, float& up) {
+        mx = wave_max(mx);
+        if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        __syncthreads();
         int e = 15;                                                    // zero / non-finite rows: scale 1
         if (mx > 0.f && mx <= 3.4028235e38f) (void)frexpf(mx, &e);    // mx = f * 2^e, f in [0.5, 1)
         up = ldexpf(1.f, 15 - e);
-        if (lane == 0) rscale[m] = ldexpf(1.f, e - 15);
+        if (tid == 0) rscale[m] = ldexpf(1.f, e - 15);
     };
-    if (nchp <= 64 * XPREP_MAXC) {
-        f32x4_t a[XPREP_MAXC], b[XPREP_MAXC];
+    if (nchp <= 256 * XPREP_BCH) {
+        f32x4_t a[XPREP_BCH], b[XPREP_BCH];
         float mx = 0.f;
 #pragma unroll
-        for (int i = 0; i < XPREP_MAXC; ++i) {
-            const int c = lane + 64 * i;
+        for (int i = 0; i < XPREP_BCH; ++i) {
+            const int c = tid + 256 * i;
             a[i] = b[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
             if (c < nch) {
                 a[i] = *(const f32x4_t*)(xr + c * 8);
@@ -102,22 +110,22 @@ extern "C" __global__ __launch_bounds__(256) void brik_xprep_f16(const float* __
             }
         }
 #pragma unroll
-        for (int i = 0; i < XPREP_MAXC; ++i) mx = fmaxf(mx, absmax8(a[i], b[i]));
+        for (int i = 0; i < XPREP_BCH; ++i) mx = fmaxf(mx, absmax8(a[i], b[i]));
         float up;
-        scale_of(wave_max(mx), up);
+        scale_of(mx, up);
 #pragma unroll
-        for (int i = 0; i < XPREP_MAXC; ++i) {
-            const int c = lane + 64 * i;
+        for (int i = 0; i < XPREP_BCH; ++i) {
+            const int c = tid + 256 * i;
             if (c < nchp) *(half8_t*)(hr + c * 8) = to_h8(a[i], b[i], up);
         }
         return;
     }
     float mx = 0.f;
-    for (int c = lane; c < nch; c += 64)
+    for (int c = tid; c < nch; c += 256)
         mx = fmaxf(mx, absmax8(*(const f32x4_t*)(xr + c * 8), *(const f32x4_t*)(xr + c * 8 + 4)));
     float up;
-    scale_of(wave_max(mx), up);
-    for (int c = lane; c < nchp; c += 64) {
+    scale_of(mx, up);
+    for (int c = tid; c < nchp; c += 256) {
         f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
         if (c < nch) {
             a = *(const f32x4_t*)(xr + c * 8);
@@ -125,6 +133,16 @@ extern "C" __global__ __launch_bounds__(256) void brik_xprep_f16(const float* __
         }
         *(half8_t*)(hr + c * 8) = to_h8(a, b, up);
     }
+}
+
+extern "C" __global__ __launch_bounds__(256) void brik_xprep_f16(const float* __restrict__ x,
+                                                                 uint16_t* __restrict__ xh,
+                                                                 float* __restrict__ rscale, int M, int K,
+                                                                 int Kp)
+{
+    __shared__ float wmax[4];
+    for (int m = blockIdx.x; m < M; m += gridDim.x)     // the same for the whole block
+        xprep_row(x, xh, rscale, m, K, Kp, wmax);
 }
 
 // ---- 2. GEMM ------------------------------------------------------------------------------------
