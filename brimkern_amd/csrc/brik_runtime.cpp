@@ -30,7 +30,7 @@ enum Kern {
     K_TOPK_PREP, K_TOPK_SELECT,
     K_FILL_ZERO,
     K_QUANT_Q8, K_QUANT_Q4, K_QUANT_Q3, K_F16_TO_F32,
-    K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT,
+    K_CONV_Q8, K_CONV_Q4, K_XPREP_IM2COL, K_CONV_OUT, K_CONV_CHANMAX, K_XPREP_IM2COL3,
     K_GEMV_F16W_V8, K_GEMV_F16W_V4, K_GEMM_F16W,
     K_GEMV_STAGE_Q8, K_GEMV_STAGE_Q4, K_GEMV_STAGE_Q3, K_GEMV_STAGE1_Q4, K_GEMV_STAGE1_Q3,
     K_SPLITK_REDUCE,
@@ -44,6 +44,7 @@ const char* const kKernelNames[K_COUNT] = {
     "brik_fill_zero",
     "brik_encode_q8", "brik_encode_q4", "brik_encode_q3", "brik_f16_decode",
     "brik_conv2d_direct_q8", "brik_conv2d_direct_q4", "brik_xprep_im2col_f16", "brik_conv_out",
+    "brik_conv_chanmax", "brik_xprep_im2col3_f16",
     "brik_gemv_f16w_v8", "brik_gemv_f16w_v4", "brik_gemm_f16w",
     "brik_gemv_stage_q8", "brik_gemv_stage_q4", "brik_gemv_stage_q3", "brik_gemv_stage1_q4", "brik_gemv_stage1_q3",
     "brik_splitk_reduce",
@@ -1194,7 +1195,10 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
         (mn && !aligned(mn, 2)) || !aligned(p0, 16))
         return fail(c, BRIK_EALIGN, "%s: inp / bias 4-byte, out and the code plane 16-byte, scales / mins 2-byte "
                     "aligned", who);
-    const bool gemm_ok = K % kGroup == 0 && Cout * (K / kGroup) >= 16 && K <= (1 << 30);
+    // the GEMM's im2col staging addresses the input (and pad rows and columns before it) through a
+    // 32-bit buffer offset: fewer than 2^29 elements
+    const bool gemm_ok = K % kGroup == 0 && Cout * (K / kGroup) >= 16 && K <= (1 << 30) &&
+                         (long long)Cin * H * W + (long long)pad * (W + 1) < (1ll << 29) && kh <= 64 && kw <= 64;
     bool use_gemm = gemm_ok && M >= 64;
     if (c->opt_path == 1) use_gemm = false;
     else if (c->opt_path == 2 && gemm_ok) use_gemm = true;
@@ -1214,12 +1218,27 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
     uint16_t* xh;
     float* rscale;
     HIP_TRY_RC(gemm_stage_ws(c, rows, Kint, Kp, xh, rscale));
-    HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, (size_t)M * Cout * 4));
+    // conv workspace: the GEMM output [M, Cout], then the channel maxima of the input [H W]
+    const size_t yt_bytes = ((size_t)M * Cout * 4 + 255) & ~(size_t)255;
+    HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, yt_bytes + (size_t)H * W * 4));
     float* yt = static_cast<float*>(c->cws);
-    int Kpi = (int)Kp;
+    float* cmax = reinterpret_cast<float*>(static_cast<unsigned char*>(c->cws) + yt_bytes);
+    int Kpi = (int)Kp, HW = H * W;
     {
-        void* args[] = {&inp, &xh, &rscale, (void*)&rows, (void*)&Kint, &Kpi, &Hi, &Wi, &khi, &kwi, &si, &pi, &OWi};
-        HIP_TRY_RC(launch(c, K_XPREP_IM2COL, (unsigned)((rows + 3) / 4), 1, 256, 0, args));
+        void* args[] = {&inp, &cmax, &Ci, &HW};
+        HIP_TRY_RC(launch(c, K_CONV_CHANMAX, (unsigned)((HW + 31) / 32), 1, 1024, 0, args));
+    }
+    if (kh == 3 && kw == 3) {
+        // 64 rows per block, 4 waves of 8 channels (9 chunks of 8 elements) each
+        void* args[] = {&inp, &cmax, &xh, &rscale, (void*)&rows, (void*)&Kint, &Kpi, &Ci, &Hi, &Wi, &si, &pi, &OWi};
+        HIP_TRY_RC(launch(c, K_XPREP_IM2COL3, (unsigned)((rows + 63) / 64), (unsigned)((Kp / 8 + 35) / 36), 256, 0,
+                          args));
+    } else {
+        // 64 rows per block, 4 waves of 8 chunks of 8 elements each
+        void* args[] = {&inp, &cmax, &xh, &rscale, (void*)&rows, (void*)&Kint, &Kpi, &Ci, &Hi, &Wi, &khi, &kwi, &si,
+                        &pi, &OWi};
+        HIP_TRY_RC(launch(c, K_XPREP_IM2COL, (unsigned)((rows + 63) / 64), (unsigned)((Kp / 8 + 31) / 32), 256, 0,
+                          args));
     }
     HIP_TRY_RC(gemm_run(c, f, xh, rscale, p0, nullptr, sc, mn, yt, rows, Kint, Cout, nullptr, 0));
     int P = rows;

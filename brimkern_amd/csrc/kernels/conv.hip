@@ -78,74 +78,207 @@ extern "C" __global__ __launch_bounds__(256) void brik_conv2d_direct_q4(
 // im2col staging for the MFMA GEMM: row m = output pixel (oy, ox) = (m / OW, m % OW), element k =
 // (ci, ky, kx) = (k / (kh kw), (k / kw) % kh, k % kw) is the input tap or 0 outside the image. The row
 // is written exactly as brik_xprep_f16 writes an activation row (power-of-two row scale, f16, the
-// [0 4 1 5 2 6 3 7] order per 8 elements, zero padding to Kp). One wave per row.
-extern "C" __global__ __launch_bounds__(256) void brik_xprep_im2col_f16(
-    const float* __restrict__ inp, uint16_t* __restrict__ xh, float* __restrict__ rscale, int M, int K, int Kp,
-    int H, int W, int kh, int kw, int stride, int pad, int OW)
+// [0 4 1 5 2 6 3 7] order per 8 elements, zero padding to Kp). Two launches:
+//   a. brik_conv_chanmax: cmax[p] = max over the channels of |inp[ci, p]| for every input position p
+//      (half waves along positions, so every load is contiguous; 32 groups split the channels);
+//   b. brik_xprep_im2col_f16: a row's maximum is the maximum of cmax over its kh x kw in-image taps (the
+//      same set of values; out-of-image taps are 0), so no pass over the row is needed for its scale.
+//      Lanes are 64 consecutive pixels and a wave takes 8 consecutive chunks of 8 elements of their
+//      rows: each tap load is contiguous across the wave; the rows go out through LDS, 512 contiguous
+//      bytes per row and store.
+// fmaxf drops NaN here as in brik_xprep_f16. (One wave per row gathering its own taps, the first form,
+// issued 64 scattered 4-byte loads per instruction: 29 us on a 320 x 64 x 64 3 x 3 input.)
+extern "C" __global__ __launch_bounds__(1024) void brik_conv_chanmax(const float* __restrict__ inp,
+                                                                    float* __restrict__ cmax, int Cin, int HW)
 {
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (m >= M) return;     // a whole wave; no block-level synchronisation follows
-    const int lane = threadIdx.x & 63;
+    // 32 positions per block (one per lane of a half wave), 32 channel groups; a thread's loads of
+    // 8 channels at a time are independent, so they are in flight together
+    __shared__ float part[32][33];
+    const int q = threadIdx.x & 31, g = threadIdx.x >> 5;
+    const int p = blockIdx.x * 32 + q;
+    float mx = 0.f;
+    if (p < HW)
+        for (int ci = g; ci < Cin; ci += 256) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = ci + 32 * u < Cin ? fabsf(inp[(size_t)(ci + 32 * u) * HW + p]) : 0.f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) mx = fmaxf(mx, t[u]);
+        }
+    part[g][q] = mx;
+    __syncthreads();
+    if (g == 0 && p < HW) {
+#pragma unroll
+        for (int k = 1; k < 32; ++k) mx = fmaxf(mx, part[k][q]);
+        cmax[p] = mx;
+    }
+}
+
+constexpr int IM2COL_CPT = 8;    // chunks of 8 elements per thread
+
+extern "C" __global__ __launch_bounds__(256) void brik_xprep_im2col_f16(
+    const float* __restrict__ inp, const float* __restrict__ cmax, uint16_t* __restrict__ xh,
+    float* __restrict__ rscale, int M, int K, int Kp, int Cin, int H, int W, int kh, int kw, int stride, int pad,
+    int OW)
+{
+    // w through readfirstlane: the compiler then keeps the tap walk below, uniform per wave, in scalar
+    // registers, and the buffer loads' scalar offset needs no per-lane loop
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // rows past M compute row M - 1 again (in range) and are not written
+    const int m = min((int)blockIdx.x * 64 + lane, M - 1);
     const int oy = m / OW, ox = m % OW, kk = kh * kw;
     const int y0 = oy * stride - pad, x0 = ox * stride - pad;
-    uint16_t* hr = xh + (size_t)m * Kp;
-    const int nch = K / 8, nchp = Kp / 8;
-    // the 8 taps of chunk c, walking (ci, ky, kx) from k = 8 c
-    auto gather = [&](int c, f32x4_t& a, f32x4_t& b) {
-        float v[8];
-        int k = 8 * c, ci = k / kk, r = k - ci * kk, ky = r / kw, kx = r - ky * kw;
+    float mx = 0.f;
+    for (int ky = 0; ky < kh; ++ky) {
+        const int iy = y0 + ky;
+        if (iy < 0 || iy >= H) continue;
+        for (int kx = 0; kx < kw; ++kx) {
+            const int ix = x0 + kx;
+            if (ix >= 0 && ix < W) mx = fmaxf(mx, cmax[iy * W + ix]);
+        }
+    }
+    int e = 15;                                                    // zero / non-finite rows: scale 1
+    if (mx > 0.f && mx <= 3.4028235e38f) (void)frexpf(mx, &e);    // mx = f * 2^e, f in [0.5, 1)
+    const float up = ldexpf(1.f, 15 - e);
+    if (blockIdx.y == 0 && w == 0 && (int)blockIdx.x * 64 + lane < M) rscale[m] = ldexpf(1.f, e - 15);
+    const int nchp = Kp / 8;
+    const int c0 = (blockIdx.y * 4 + w) * IM2COL_CPT;              // the same for the whole wave
+    // Taps through a buffer resource: the per-thread offset is the pixel's corner (y0, x0), the tap's
+    // (ci, ky, kx) offset is uniform (a scalar register, added by the addressing hardware), and a tap
+    // outside the image gets an offset past the end of the buffer, which loads 0 without an access.
+    // The resource starts pad rows and pad columns before the input, so every corner offset is
+    // nonnegative (y0, x0 >= -pad); only taps inside the image are ever addressed. The input has fewer
+    // than 2^29 elements here (the host checks), so the offsets stay below 2^31.
+    const int lead = pad * W + pad;
+    const brsrc_t rin = make_rsrc((const void*)((uintptr_t)inp - (uintptr_t)lead * 4),
+                                  (uint32_t)(((size_t)Cin * H * W + lead) * 4));
+    uint64_t rowbits = 0, colbits = 0;                             // bit ky / kx: the tap row / column is inside
+    for (int ky = 0; ky < kh; ++ky) rowbits |= (uint64_t)(y0 + ky >= 0 && y0 + ky < H) << ky;
+    for (int kx = 0; kx < kw; ++kx) colbits |= (uint64_t)(x0 + kx >= 0 && x0 + kx < W) << kx;
+    const uint32_t vbase = (uint32_t)((y0 * W + x0 + lead) * 4);
+    // every tap of the thread's chunks is loaded before any is converted, so the loads are in flight
+    // together (one memory round trip per thread)
+    float v[IM2COL_CPT][8];
+    {
+        const int k0 = 8 * c0;
+        int ci = k0 / kk, r = k0 - ci * kk, ky = r / kw, kx = r - ky * kw;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int iy = y0 + ky, ix = x0 + kx;
-            v[j] = (iy >= 0 && iy < H && ix >= 0 && ix < W) ? inp[((size_t)ci * H + iy) * W + ix] : 0.f;
-            if (++kx == kw) {
-                kx = 0;
-                if (++ky == kh) {
-                    ky = 0;
-                    ++ci;
+        for (int j = 0; j < IM2COL_CPT; ++j)
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const bool live = 8 * (c0 + j) + t < K;                // uniform; ci < Cin when set
+                const bool in = live && ((rowbits >> ky) & (colbits >> kx) & 1u);
+                const int soff = live ? ((ci * H + ky) * W + kx) * 4 : 0;
+                v[j][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, in ? vbase : 0x80000000u,
+                                                                                       soff, 0));
+                if (++kx == kw) {
+                    kx = 0;
+                    if (++ky == kh) {
+                        ky = 0;
+                        ++ci;
+                    }
                 }
             }
-        }
-        a = f32x4_t{v[0], v[1], v[2], v[3]};
-        b = f32x4_t{v[4], v[5], v[6], v[7]};
-    };
-    auto scale_of = [&](float mx, float& up) {
-        int e = 15;                                                    // zero / non-finite rows: scale 1
-        if (mx > 0.f && mx <= 3.4028235e38f) (void)frexpf(mx, &e);
-        up = ldexpf(1.f, 15 - e);
-        if (lane == 0) rscale[m] = ldexpf(1.f, e - 15);
-    };
-    if (nchp <= 64 * XPREP_MAXC) {
-        f32x4_t a[XPREP_MAXC], b[XPREP_MAXC];
-        float mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < XPREP_MAXC; ++i) {
-            const int c = lane + 64 * i;
-            a[i] = b[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (c < nch) gather(c, a[i], b[i]);
-            mx = fmaxf(mx, absmax8(a[i], b[i]));
-        }
-        float up;
-        scale_of(wave_max(mx), up);
-#pragma unroll
-        for (int i = 0; i < XPREP_MAXC; ++i) {
-            const int c = lane + 64 * i;
-            if (c < nchp) *(half8_t*)(hr + c * 8) = to_h8(a[i], b[i], up);
-        }
-        return;
     }
+    // Rows of the block through LDS: [64 rows][32 chunks] of 16 bytes, chunk c of a row at
+    // (c ^ (row & 31)) so the writes below (8 chunks of one row per lane) and the reads (consecutive
+    // chunks of two rows per wave instruction) are spread over the banks. Each wave then writes 16 rows,
+    // two per instruction, 512 contiguous bytes each: every lane writing its own row instead put 64 rows
+    // 6 KB apart into one instruction (21 us for this launch on the 320 x 64 x 64 3 x 3 input).
+    __shared__ __attribute__((aligned(16))) half8_t tile[64 * 32];
+    const int row = lane, cb = w * IM2COL_CPT;
+#pragma unroll
+    for (int j = 0; j < IM2COL_CPT; ++j)
+        tile[row * 32 + ((cb + j) ^ (row & 31))] =
+            to_h8(f32x4_t{v[j][0], v[j][1], v[j][2], v[j][3]}, f32x4_t{v[j][4], v[j][5], v[j][6], v[j][7]}, up);
+    __syncthreads();
+    const int cc = lane & 31, cblk = blockIdx.y * 32;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int rr = w * 16 + 2 * i + (lane >> 5);                // the wave's rows 16 w .. 16 w + 15
+        const int mm = blockIdx.x * 64 + rr;
+        if (mm < M && cblk + cc < nchp)
+            *(half8_t*)(xh + (size_t)mm * Kp + (cblk + cc) * 8) = tile[rr * 32 + (cc ^ (rr & 31))];
+    }
+}
+
+// The pixel's row scale from the channel maxima of its in-image taps (as brik_xprep_f16 scales a row).
+__device__ __forceinline__ float im2col_scale(const float* __restrict__ cmax, int y0, int x0, int H, int W, int kh,
+                                              int kw, int& e)
+{
     float mx = 0.f;
-    for (int c = lane; c < nch; c += 64) {
-        f32x4_t a, b;
-        gather(c, a, b);
-        mx = fmaxf(mx, absmax8(a, b));
+    for (int ky = 0; ky < kh; ++ky) {
+        const int iy = y0 + ky;
+        if (iy < 0 || iy >= H) continue;
+        for (int kx = 0; kx < kw; ++kx) {
+            const int ix = x0 + kx;
+            if (ix >= 0 && ix < W) mx = fmaxf(mx, cmax[iy * W + ix]);
+        }
     }
-    float up;
-    scale_of(wave_max(mx), up);
-    for (int c = lane; c < nchp; c += 64) {
-        f32x4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-        if (c < nch) gather(c, a, b);
-        *(half8_t*)(hr + c * 8) = to_h8(a, b, up);
+    e = 15;                                                        // zero / non-finite rows: scale 1
+    if (mx > 0.f && mx <= 3.4028235e38f) (void)frexpf(mx, &e);    // mx = f * 2^e, f in [0.5, 1)
+    return ldexpf(1.f, 15 - e);
+}
+
+// 3 x 3 form: a wave takes 8 whole channels of its 64 pixels, 72 taps = 9 chunks of 8 (a window
+// that starts on a channel, so every tap's place in the row is a compile-time constant), a block 32
+// channels. The 9 per-pixel tap offsets (the corner, or past the end for a tap outside the image)
+// are computed once; each load then only adds the uniform offset of its channel and tap, so the walk
+// costs no per-tap arithmetic. The rows go out through LDS as in the generic form.
+constexpr int IM2COL3_CPB = 36;    // chunks per block: 4 waves x 9
+
+extern "C" __global__ __launch_bounds__(256) void brik_xprep_im2col3_f16(
+    const float* __restrict__ inp, const float* __restrict__ cmax, uint16_t* __restrict__ xh,
+    float* __restrict__ rscale, int M, int K, int Kp, int Cin, int H, int W, int stride, int pad, int OW)
+{
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m = min((int)blockIdx.x * 64 + lane, M - 1);        // rows past M: row M - 1, not written
+    const int oy = m / OW, ox = m % OW;
+    const int y0 = oy * stride - pad, x0 = ox * stride - pad;
+    int e;
+    const float up = im2col_scale(cmax, y0, x0, H, W, 3, 3, e);
+    if (blockIdx.y == 0 && w == 0 && (int)blockIdx.x * 64 + lane < M) rscale[m] = ldexpf(1.f, e - 15);
+    // taps through a buffer resource starting pad rows and columns before the input (see the generic
+    // form); the host keeps every offset below 2^31
+    const int lead = pad * W + pad;
+    const brsrc_t rin = make_rsrc((const void*)((uintptr_t)inp - (uintptr_t)lead * 4),
+                                  (uint32_t)(((size_t)Cin * H * W + lead) * 4));
+    const uint32_t vbase = (uint32_t)((y0 * W + x0 + lead) * 4);
+    uint32_t voff[3][3];
+#pragma unroll
+    for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx) {
+            const bool in = y0 + ky >= 0 && y0 + ky < H && x0 + kx >= 0 && x0 + kx < W;
+            voff[ky][kx] = in ? vbase : 0x80000000u;
+        }
+    const int ci0 = (blockIdx.y * 4 + w) * 8;                       // uniform
+    float v[72];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const bool live = ci0 + c < Cin;                            // uniform: channels past Cin are padding
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const int soff = live ? (((ci0 + c) * H + ky) * W + kx) * 4 : 0;
+                v[c * 9 + ky * 3 + kx] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(rin, live ? voff[ky][kx] : 0x80000000u, soff, 0));
+            }
+    }
+    __shared__ __attribute__((aligned(16))) half8_t tile[64 * (IM2COL3_CPB + 1)];
+#pragma unroll
+    for (int c = 0; c < 9; ++c)
+        tile[lane * (IM2COL3_CPB + 1) + w * 9 + c] =
+            to_h8(f32x4_t{v[8 * c], v[8 * c + 1], v[8 * c + 2], v[8 * c + 3]},
+                  f32x4_t{v[8 * c + 4], v[8 * c + 5], v[8 * c + 6], v[8 * c + 7]}, up);
+    __syncthreads();
+    const int nchp = Kp / 8, cblk = blockIdx.y * IM2COL3_CPB;
+    for (int idx = threadIdx.x; idx < 64 * IM2COL3_CPB; idx += 256) {
+        const int rr = idx / IM2COL3_CPB, cc = idx - rr * IM2COL3_CPB;
+        const int mm = blockIdx.x * 64 + rr;
+        if (mm < M && cblk + cc < nchp)
+            *(half8_t*)(xh + (size_t)mm * Kp + (cblk + cc) * 8) = tile[rr * (IM2COL3_CPB + 1) + cc];
     }
 }
 

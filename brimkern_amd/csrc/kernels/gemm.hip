@@ -38,7 +38,6 @@
 
 namespace {
 
-constexpr int XPREP_MAXC = 20;  // 8-float chunks per lane held in registers by one-wave-per-row staging (im2col)
 
 __device__ __forceinline__ half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 __device__ __forceinline__ uint32_t as_u32(half2_t v) { return __builtin_bit_cast(uint32_t, v); }
