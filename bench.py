@@ -564,6 +564,8 @@ ONLY = {
     "f3": f3_only,
     "cfg1": lambda ctx, a: gemv_single_cfg(ctx, "q8", 896, 4864, 600, a.steps, a.warmup),
     "cfg3": lambda ctx, a: gemv_single_cfg(ctx, "q3", 2560, 151936, 700, a.steps, a.warmup),
+    "f2": lambda ctx, a: lm_head_topk_cfg3(ctx, a.steps, a.warmup,
+                                           gemv_single_cfg(ctx, "q3", 2560, 151936, 700, a.steps, a.warmup)["us"]),
     "cfg4": lambda ctx, a: gemm_cfg4(ctx, a.steps, a.warmup),
     "moe": lambda ctx, a: moe_cfg5(ctx, a.steps, a.warmup),
     "conv": lambda ctx, a: conv_f4(ctx, a.steps, a.warmup),

@@ -89,13 +89,20 @@ extern "C" __global__ __launch_bounds__(256) void brik_topk_prep(float* __restri
         }
         __syncthreads();
     }
+    // all 16 loads of a thread first (one memory round trip; four at a time took four)
+    float raw[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const long i = base + 1024 * wave + 64 * j + lane;
+        raw[j] = i < n ? logits[i] : 0.f;
+    }
     uint32_t m = 0u;
-#pragma unroll 4
+#pragma unroll
     for (int j = 0; j < 16; ++j) {
         const int o = 1024 * wave + 64 * j + lane;
         const long i = base + o;
         if (i < n) {
-            float v = logits[i];
+            float v = raw[j];
             const bool p = pen && ((marks[o >> 5] >> (o & 31)) & 1u);
             if (cap > 0.f) v = cap * tanhf(v / cap);
             if (p) v = v > 0.f ? v / penalty : v * penalty;
