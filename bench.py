@@ -336,7 +336,7 @@ def conv_f4(ctx, steps, warmup):
         ctx.free(bb)
     out["shape"] = "Cin 320, 64x64, Cout 320, 3x3, stride 1, pad 1, q4 weight"
     out["frac_of_mfma_peak"] = round(out["implicit_gemm"]["TFLOPs"] / MFMA_F16_PEAK_TFLOPS, 4)
-    out["launches"] = "brik_conv_chanmax + brik_xprep_im2col3_f16 + brik_gemm_q4 + brik_conv_out"
+    out["launches"] = "brik_conv_chanmax + brik_xprep_im2col3_f16 + brik_gemm_q4 (stores [Cout, pixels] + bias)"
     return out
 
 

@@ -497,9 +497,11 @@ struct WeightPair {
 
 // The tile kernel over staged rows: dense when row_off is null, expert-grouped (q4) otherwise; `pair`
 // (grouped only) adds the second tensor as blockIdx.z == 1.
+// trans (dense, not split-K): y is [N, rows], y[n, m] = (x . W^T)[m, n] + tbias[n] (tbias may be null).
 int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
              const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E,
-             const Scratch* fixed = nullptr, const WeightPair* pair = nullptr)
+             const Scratch* fixed = nullptr, const WeightPair* pair = nullptr, const float* tbias = nullptr,
+             int trans = 0)
 {
     if (use_splitk(c, f, rows, K, N, E, fixed)) {
         HIP_TRY_RC(gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E));
@@ -511,7 +513,7 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
     const GemmTile& gt = kGemmTiles[t];
     const int bn = gt.bn();
     if (!row_off) {
-        void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei};
+        void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &tbias, &trans};
         return launch_fn(c, c->gemm[fmt_index(f)][t], gemm_tiles(rows, gt.bm) * gemm_tiles(N, bn), 1, gt.threads(), 0,
                          args);
     }
@@ -1218,11 +1220,14 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
     uint16_t* xh;
     float* rscale;
     HIP_TRY_RC(gemm_stage_ws(c, rows, Kint, Kp, xh, rscale));
-    // conv workspace: the GEMM output [M, Cout], then the channel maxima of the input [H W]
+    // conv workspace: the GEMM output [M, Cout] (only without the fused epilogue), then the channel
+    // maxima of the input [H W]
     const size_t yt_bytes = ((size_t)M * Cout * 4 + 255) & ~(size_t)255;
-    HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, yt_bytes + (size_t)H * W * 4));
+    // the GEMM writes out itself ([Cout, pixels] plus the bias) unless the split-K kernel runs it
+    const bool fused = !use_splitk(c, f, rows, Kint, Cout, 0, nullptr);
+    HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, (fused ? 0 : yt_bytes) + (size_t)H * W * 4));
     float* yt = static_cast<float*>(c->cws);
-    float* cmax = reinterpret_cast<float*>(static_cast<unsigned char*>(c->cws) + yt_bytes);
+    float* cmax = reinterpret_cast<float*>(static_cast<unsigned char*>(c->cws) + (fused ? 0 : yt_bytes));
     int Kpi = (int)Kp, HW = H * W;
     {
         void* args[] = {&inp, &cmax, &Ci, &HW};
@@ -1240,6 +1245,8 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
         HIP_TRY_RC(launch(c, K_XPREP_IM2COL, (unsigned)((rows + 63) / 64), (unsigned)((Kp / 8 + 31) / 32), 256, 0,
                           args));
     }
+    if (fused) return gemm_run(c, f, xh, rscale, p0, nullptr, sc, mn, out, rows, Kint, Cout, nullptr, 0, nullptr, nullptr,
+                               bias, 1);
     HIP_TRY_RC(gemm_run(c, f, xh, rscale, p0, nullptr, sc, mn, yt, rows, Kint, Cout, nullptr, 0));
     int P = rows;
     void* args[] = {&yt, &bias, &out, &P, &Co};
@@ -1320,8 +1327,9 @@ int brik_matmul_t_f16w(brik_ctx* c, const float* x, const uint16_t* w, float* y,
         const GemmTile& g = kGemmTiles[best];
         const void* none = nullptr;
         const int* no_rows = nullptr;
-        int Ei = 0;
-        void* targs[] = {&xh, &rscale, &w, &none, &none, &none, &y, &Mi, &Ki, &Ni, &no_rows, &Ei};
+        int Ei = 0, trans = 0;
+        const float* no_bias = nullptr;
+        void* targs[] = {&xh, &rscale, &w, &none, &none, &none, &y, &Mi, &Ki, &Ni, &no_rows, &Ei, &no_bias, &trans};
         return launch_fn(c, c->gemm_f16[best], gemm_tiles(M, g.bm) * gemm_tiles(N, g.bn()), 1, g.threads(), 0,
                          targs);
     }

@@ -674,7 +674,8 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
                                               const float* __restrict__ rscale, const uint8_t* __restrict__ p0,
                                               const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc,
                                               const uint16_t* __restrict__ mn, float* __restrict__ y, int M, int K,
-                                              int N, int E, int e, int m0, int m_end, int n0)
+                                              int N, int E, int e, int m0, int m_end, int n0,
+                                              const float* __restrict__ tbias = nullptr, int trans = 0)
 {
     constexpr int BN = T::BN, TM = T::TM, TN = T::TN, XI = T::XI, NT = T::NT;
     const int G = K / BRIK_GROUP;
@@ -841,6 +842,30 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
                 for (int r = 0; r < 16; ++r)
                     Cs[(ii * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) * T::CLD + wn + 32 * j + (lane & 31)] = acc[i0 + ii][j][r];
         lds_barrier();
+        if (trans) {
+            // y is [N, M]: y[n, m] = C[m, n] rscale[m] + tbias[n] (one rounding, the product being exact),
+            // 4 consecutive rows of one column per thread and store
+            constexpr int RB = T::RF * 32 / 4;
+            for (int c = tid; c < BN * RB; c += NT) {
+                const int col = c / RB, row = (c % RB) * 4;
+                const int m = m0 + i0 * 32 + row, n = n0 + col;
+                if (m >= m_end || n >= N) continue;
+                const float b = tbias ? tbias[n] : 0.f;
+                f32x4_t v;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    v[k] = m + k < m_end ? Cs[(row + k) * T::CLD + col] * rscale[m + k] + b : 0.f;
+                float* dst = y + (size_t)n * M + m;
+                if ((M & 3) == 0 && m + 3 < m_end) {
+                    *(f32x4_t*)dst = v;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (m + k < m_end) dst[k] = v[k];
+                }
+            }
+            continue;
+        }
         for (int c = tid; c < T::RF * 32 * CH; c += NT) {
             const int row = c / CH, col = (c % CH) * 4;
             const int m = m0 + i0 * 32 + row, n = n0 + col;
@@ -863,7 +888,8 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
                                           const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,
                                           const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
                                           float* __restrict__ y, int M, int K, int N,
-                                          const int* __restrict__ row_off, int E, int gtile = 0, int gcol = 0)
+                                          const int* __restrict__ row_off, int E, int gtile = 0, int gcol = 0,
+                                          const float* __restrict__ tbias = nullptr, int trans = 0)
 {
     constexpr int BM = T::BM, BN = T::BN;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
@@ -889,7 +915,7 @@ __device__ __forceinline__ void gemm_body(const uint16_t* __restrict__ xh, const
         m0 = mt * BM;
         n0 = nt * BN;
     }
-    gemm_tile_run<FMT, T, GROUPED>(smem, xh, rscale, p0, p1, sc, mn, y, M, K, N, E, e, m0, m_end, n0);
+    gemm_tile_run<FMT, T, GROUPED>(smem, xh, rscale, p0, p1, sc, mn, y, M, K, N, E, e, m0, m_end, n0, tbias, trans);
 }
 
 // Expert-grouped tile of TL::BM rows that runs the TS::BM-row body (the same columns and waves) when
@@ -1100,9 +1126,11 @@ __device__ __forceinline__ void gemm_sk_body(const uint16_t* __restrict__ xh, co
     extern "C" __global__ __launch_bounds__(64 * NW_) void brik_gemm_##FMTN##_##BM_##x##TN_##SUFFIX(      \
         const uint16_t* __restrict__ xh, const float* __restrict__ rscale, const uint8_t* __restrict__ p0, \
         const uint8_t* __restrict__ p1, const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, \
-        float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E)               \
+        float* __restrict__ y, int M, int K, int N, const int* __restrict__ row_off, int E,               \
+        const float* __restrict__ tbias, int trans)                                                       \
     {                                                                                                     \
-        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, false>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E); \
+        gemm_body<FMT, Tile<FMT, BM_, TN_, NW_, PF_>, false>(xh, rscale, p0, p1, sc, mn, y, M, K, N, row_off, E, \
+                                                            0, 0, tbias, trans);                         \
     }
 // Expert-grouped kernels, q4 only: brik_gemmg_q4_<tile>, a 1-D grid over (pair, column tile, matrix)
 // with `mats` matrices: the second (codes p0b, scales scb, mins mnb, into yb) is multiplied by the same
