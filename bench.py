@@ -559,8 +559,40 @@ def f3_only(ctx, a):
     return out
 
 
+def library_gemm_reference(ctx, steps, warmup):
+    """A yardstick, not this library's path: hipBLASLt through torch.matmul on the prefill GEMM shape
+    (M = 512, K = 2560, N = 9728) with the weights already in f16 / bf16 (3.2x the q4 bytes, nothing
+    to dequantize), 8 weight copies rotated (400 MB, past the 256 MB last-level cache), CUDA events on
+    torch's stream. torch loads its own HIP runtime, which finds no device once this library's runtime
+    holds it, so this runs in a process without a library context."""
+    import torch
+    M, K, N = 512, 2560, 9728
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = {"shape": f"M={M} K={K} N={N}", "library": "hipBLASLt via torch.matmul, x (M, K) @ W.T, W (N, K)"}
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        x = torch.randn(M, K, device="cuda", dtype=dt, generator=g)
+        ws = [torch.randn(N, K, device="cuda", dtype=dt, generator=g) * 0.05 for _ in range(8)]
+        for i in range(max(warmup, 8)):
+            torch.matmul(x, ws[i % 8].t())
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = max(steps, 8)
+        a.record()
+        for i in range(n):
+            torch.matmul(x, ws[i % 8].t())
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / n
+        tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 2), "TFLOPs": round(tf, 1), "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+        del x, ws
+    torch.cuda.empty_cache()
+    return out
+
+
 ONLY = {
     "headline": headline_only,
+    "blasref": lambda ctx, a: library_gemm_reference(ctx, a.steps, a.warmup),
     "f3": f3_only,
     "cfg1": lambda ctx, a: gemv_single_cfg(ctx, "q8", 896, 4864, 600, a.steps, a.warmup),
     "cfg3": lambda ctx, a: gemv_single_cfg(ctx, "q3", 2560, 151936, 700, a.steps, a.warmup),
@@ -594,6 +626,12 @@ def main():
     args = ap.parse_args()
     if args.probe:
         probe(args.layers)
+        return
+    if args.only == "blasref":
+        # torch's own HIP runtime must be the first to open the device: no library context here
+        log("bench: blasref alone")
+        print(json.dumps({"only": args.only, "steps": args.steps, "warmup": args.warmup,
+                          "result": library_gemm_reference(None, args.steps, args.warmup)}), flush=True)
         return
     if args.only:
         from brimkern_amd import Context

@@ -266,6 +266,8 @@ struct Tile {
 // element i hold the true K index 128 t + 64 h + 8 s + i. A lane half therefore owns groups 4 t + 2 h
 // and 4 t + 2 h + 1 of its column whole (slices 0-3 and 4-7), and one load brings each group's codes.
 // A (x from LDS) and B (W) use the same mapping, so the order of the contraction does not matter.
+// f16 weights use 128 t + 16 s + 8 h + i instead: their loads are not per group, and this mapping
+// makes the two lane halves of a load read adjacent pieces of a weight row.
 
 // Per lane and 32-column block: the codes of two groups of one column, and their f16 scale and min
 // bits (one group per register, low half). Words: q4 2 x 4 nibble dwords; q8 2 x 8 code dwords; q3
@@ -317,6 +319,11 @@ __device__ __forceinline__ void tie(V& v)
 // direct global->LDS loads of x step t + 2 (instruction i of wave w fills bytes [1024 (NW i + w), +1024)
 // of the buffer, 16 bytes per lane: row 4 (NW i + w) + (lane >> 4), stored chunk lane & 15) over slices
 // 4-7. The first step of every scale chunk (every SCH steps) also loads the next chunk, in slice 4.
+// f16 weights: the group index given to a dead group's loads. Its byte offsets, 64 x this = 2^32 - 64
+// up to 2^32 - 1, lie at or past the end of every f16 weight buffer the host accepts (fewer than 2^31
+// elements with K a multiple of 32: at most 2^32 - 64 bytes), so they read zeros.
+constexpr uint32_t kDeadF16Group = 0x03FFFFFFu;
+
 template <int FMT, class T>
 struct Loader {
     static constexpr int TN = T::TN, XI = T::XI, NSD = T::NSD;
@@ -336,12 +343,27 @@ struct Loader {
     // scale-chunk loads: flat group index of this lane's column for instruction k, and its LDS offset
     // within a chunk buffer
     uint32_t sdc[NSD], sdst[NSD];
-    // of the W step being loaded: clamped group indices, and (f16) whether each group is live
+    // of the W step being loaded: clamped group indices, and (f16) whether each group is live. q formats:
+    // the lane half's two groups; f16: the step's four groups (every lane reads from each of them)
     uint32_t ia[TN], ib[TN];
     bool la, lb;
+    uint32_t iq[FMT == FMT_F16 ? 4 : 1][TN];
 
     __device__ __forceinline__ void begin(int wstep)
     {
+        if constexpr (FMT == FMT_F16) {
+            // a group past the row end gets an index whose byte offsets lie past the end of the buffer
+            // resource, so its loads return zeros without touching memory (and an Inf or NaN weight of
+            // the next row cannot meet the zero padding of x); masking the loaded values instead made the
+            // compiler wait for every load right where it was issued
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int g = 4 * wstep + q;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) iq[q][j] = g < G ? colg[j] + (uint32_t)g : kDeadF16Group;
+            }
+            return;
+        }
         const int g0 = 4 * wstep + 2 * h;
         const uint32_t ga = (uint32_t)min(g0, G - 1), gb = (uint32_t)min(g0 + 1, G - 1);
         la = g0 < G;
@@ -367,13 +389,10 @@ struct Loader {
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, (k ? ib[j] : ia[j]) * 16, 0, 0);
             w.w[4 * k + 0] = v.x; w.w[4 * k + 1] = v.y; w.w[4 * k + 2] = v.z; w.w[4 * k + 3] = v.w;
         } else if constexpr (FMT == FMT_F16) {
-            // 16 bytes (8 halves) k of the 64-byte group: a dead group (past the row end, clamped to a
-            // live one for the load) reads as zeros, so an Inf or NaN weight there cannot meet the zero
-            // padding of x
-            const bool live = (k >> 2) ? lb : la;
-            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, ((k >> 2) ? ib[j] : ia[j]) * 64 + 16 * (k & 3), 0, 0);
-            w.w[4 * k + 0] = live ? v.x : 0u; w.w[4 * k + 1] = live ? v.y : 0u;
-            w.w[4 * k + 2] = live ? v.z : 0u; w.w[4 * k + 3] = live ? v.w : 0u;
+            // the 16 bytes (8 halves) of slice k: k-th 16-k piece of the step, lane half h's 8 of them,
+            // in group k >> 1 of the step at byte 32 (k & 1) + 16 h (zeros for a dead group)
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, iq[k >> 1][j] * 64 + 32 * (k & 1) + 16 * h, 0, 0);
+            w.w[4 * k + 0] = v.x; w.w[4 * k + 1] = v.y; w.w[4 * k + 2] = v.z; w.w[4 * k + 3] = v.w;
         } else if constexpr (FMT == FMT_Q8) {
             const uint32_t g = (k >> 1) ? ib[j] : ia[j];
             const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(p0, g * 32 + 16 * (k & 1), 0, 0);
@@ -717,10 +736,16 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
         const int m = min(m0 + r, m_end - 1);      // rows past the tile's end repeat a live row
         ld.xoff[i] = (uint32_t)(m * Kp + (((lane & 15) ^ (r & 15)) * 8)) * 2;
     }
-    // A fragments of slice sl: row lane & 31 of a 32-row block, logical chunk 8 h + sl
+    // A fragments of slice sl: row lane & 31 of a 32-row block, logical chunk 8 h + sl (quantized W: a
+    // lane half owns two whole groups of the step), or 2 sl + h (f16 W: the two lane halves of a slice
+    // read adjacent 16-byte pieces of a weight row, so a load instruction spans 32 rows x 32 bytes
+    // instead of 64 rows' worth of 16-byte pieces)
     uint32_t aoff[8];
 #pragma unroll
-    for (int sl = 0; sl < 8; ++sl) aoff[sl] = (uint32_t)((lane & 31) * XROW + (((8 * h + sl) ^ (lane & 15)) * 16));
+    for (int sl = 0; sl < 8; ++sl) {
+        const int chunk = FMT == FMT_F16 ? 2 * sl + h : 8 * h + sl;
+        aoff[sl] = (uint32_t)((lane & 31) * XROW + ((chunk ^ (lane & 15)) * 16));
+    }
     // W: flat group index of this lane's column in column block j, at group 0
     const int wn = wave * 32 * TN;
 #pragma unroll
