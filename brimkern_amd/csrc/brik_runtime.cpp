@@ -1131,8 +1131,9 @@ int brik_dequant_q3_f32(brik_ctx* c, const uint32_t* lo, const uint32_t* hi, con
     return dequant(c, K_DEQ_Q3, "dequant_q3", args, n, lo, out, 4);
 }
 
-// Encoders: one thread per 32-element group, 256 groups per block iteration; at most 1024 blocks (four per
-// CU), so each wave loops over several iterations and prefetches the next one's data.
+// Encoders: two threads per 32-element group, 128 groups per block iteration; at most 2048 blocks (eight
+// per CU, what their LDS allows), so each wave loops over several iterations and prefetches the next
+// one's data.
 static int quantize(brik_ctx* c, Kern k, const char* who, void** args, size_t n, const float* src,
                     const void* codes, const void* hi, const uint16_t* sc, const uint16_t* mn, bool asym)
 {
@@ -1147,8 +1148,8 @@ static int quantize(brik_ctx* c, Kern k, const char* who, void** args, size_t n,
                     "the q3 hi plane 4-byte", who);
     if (!aligned(sc, 2) || (mn && !aligned(mn, 2)))
         return fail(c, BRIK_EALIGN, "%s: scales/mins must be 2-byte aligned", who);
-    const size_t blocks = (n / kGroup + 255) / 256;
-    return launch(c, k, (unsigned)(blocks < 1024 ? blocks : 1024), 1, 256, 0, args);
+    const size_t blocks = (n / kGroup + 127) / 128;
+    return launch(c, k, (unsigned)(blocks < 2048 ? blocks : 2048), 1, 256, 0, args);
 }
 
 int brik_quantize_q8(brik_ctx* c, const float* src, int8_t* codes, uint16_t* sc, size_t n)

@@ -13,11 +13,13 @@
 // cannot change it; code_fast below decides the rounding of each code in f32 with a proven margin and
 // hands the rare close cases to the f64 path.
 //
-// Layout: one thread per 32-element group. A wave takes 64 consecutive groups (8 KiB of f32): its
-// lanes load them with consecutive 16-byte loads (1 KiB per instruction), stage them in the wave's own
-// LDS rows with a 16-byte pad per group (36 floats; the per-lane reads of 16 bytes at a 144-byte stride
-// hit every bank once per 16 lanes), and each lane then encodes its own group from LDS, so the scan
-// order, the min / max ties and the stores follow the reference's loop.
+// Layout: two lanes per 32-element group, 16 elements each. A wave takes 32 consecutive groups (4 KiB
+// of f32): its lanes load them with consecutive 16-byte loads (1 KiB per instruction), stage them in
+// the wave's own LDS rows with a 16-byte pad per group (36 floats), and each pair of lanes then encodes
+// its group from LDS. The scan order, the min / max ties and the stores follow the reference's loop:
+// each lane scans its half in order and the pair combines the halves keeping the first half's value on
+// ties. Staging 32 groups per wave (18 KiB of LDS per block) lets a CU hold 32 waves, twice what
+// one lane per group (64 groups per wave) allowed.
 #include "common.h"
 
 namespace {
@@ -107,18 +109,21 @@ __device__ __forceinline__ int code_fast(float x, float m, float r, float er, fl
     return q < lo ? lo : q > hi ? hi : q;
 }
 
-constexpr int ENC_GROUPS = 64;           // groups per wave iteration (one per lane)
+constexpr int ENC_GROUPS = 32;           // groups per wave iteration (two lanes each)
 constexpr int ENC_ROW = 36;              // floats per staged group: 32 + a 16-byte pad
+constexpr int ENC_LOADS = ENC_GROUPS * 8 / 64;   // 16-byte loads per lane per wave iteration
+constexpr int ENC_BLOCKS_PER_CU = 8;     // 18 KiB of LDS each: eight blocks (32 waves) per CU
 
-// The wave's groups [g0, g0 + 64) of src, as lane-interleaved float4s: t[i] of lane l is float4
+// The wave's groups [g0, g0 + 32) of src, as lane-interleaved float4s: t[i] of lane l is float4
 // 64 i + l of the range, so each load of the wave reads 1 KiB of consecutive f32. Past the end of
 // src the last float4 is read again (in bounds; those rows are never encoded).
-__device__ __forceinline__ void load_rows(const f32x4_t* __restrict__ src, size_t g0, size_t groups, f32x4_t (&t)[8])
+__device__ __forceinline__ void load_rows(const f32x4_t* __restrict__ src, size_t g0, size_t groups,
+                                          f32x4_t (&t)[ENC_LOADS])
 {
     const int lane = threadIdx.x & 63;
-    const size_t limit = (groups - g0) * 8;           // float4s of this wave iteration that exist
+    const size_t limit = (groups - g0) * 8;           // float4s from g0 to the end of src
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < ENC_LOADS; ++i) {
         const size_t f = (size_t)i * 64 + lane;
         t[i] = src[g0 * 8 + (f < limit ? f : limit - 1)];
     }
@@ -127,11 +132,11 @@ __device__ __forceinline__ void load_rows(const f32x4_t* __restrict__ src, size_
 // Write loaded rows into the wave's own LDS rows (row j = group g0 + j, 16-byte pad per row). Only
 // the wave itself touches its rows, so waiting for its own LDS writes orders them before its reads
 // (no block barrier).
-__device__ __forceinline__ void store_rows(const f32x4_t (&t)[8], float* __restrict__ rows)
+__device__ __forceinline__ void store_rows(const f32x4_t (&t)[ENC_LOADS], float* __restrict__ rows)
 {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < ENC_LOADS; ++i) {
         const int f = i * 64 + lane;
         *reinterpret_cast<f32x4_t*>(rows + (f >> 3) * ENC_ROW + (f & 7) * 4) = t[i];
     }
@@ -140,15 +145,40 @@ __device__ __forceinline__ void store_rows(const f32x4_t (&t)[8], float* __restr
 
 __device__ __forceinline__ f32x4_t row4(const float* row, int i) { return *reinterpret_cast<const f32x4_t*>(row + 4 * i); }
 
-// min and max as the reference's loop finds them: NaN never replaces a value, and of equal values
-// (+0 and -0) the first stays.
-__device__ __forceinline__ void min_max(const float* row, float& mn, float& mx)
+// The value of the other lane of this lane's pair (lane ^ 1): DPP quad_perm [1, 0, 3, 2]. Both lanes of
+// a pair always run together (they hold the same group).
+__device__ __forceinline__ uint32_t pair_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float pair_f32(float v) { return __builtin_bit_cast(float, pair_u32(__builtin_bit_cast(uint32_t, v))); }
+
+// Combine the two halves' results of a scan that keeps the first of equal values: the second half's
+// value replaces the first half's only when `beyond` it. `second`: this lane holds the second half.
+__device__ __forceinline__ float first_min(float own, bool second)
+{
+    const float other = pair_f32(own);
+    const float a = second ? other : own, b = second ? own : other;
+    return b < a ? b : a;
+}
+__device__ __forceinline__ float first_max(float own, bool second)
+{
+    const float other = pair_f32(own);
+    const float a = second ? other : own, b = second ? own : other;
+    return b > a ? b : a;
+}
+
+// min and max of the group as the reference's loop finds them: NaN never replaces a value, and of
+// equal values (+0 and -0) the first stays. Each lane scans its 16 elements in order; the pair then
+// keeps the first half's value unless the second half's is strictly beyond it, which is what the
+// scan over all 32 gives.
+__device__ __forceinline__ void min_max(const float* half, bool second, float& mn, float& mx)
 {
     mn = __builtin_inff();
     mx = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const f32x4_t w = row4(row, i);
+    for (int i = 0; i < 4; ++i) {
+        const f32x4_t w = row4(half, i);
         const float e[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -156,16 +186,19 @@ __device__ __forceinline__ void min_max(const float* row, float& mn, float& mx)
             if (e[j] > mx) mx = e[j];
         }
     }
+    mn = first_min(mn, second);
+    mx = first_max(mx, second);
 }
 
 // The asymmetric (q4 / q3) group header: f16 scale (max - min) / L || 1e-8 and min, their decoded
-// values s (|| 1e-8) and m, and 1 / s.
+// values s (|| 1e-8) and m, and 1 / s. Both lanes of the pair compute it (the same inputs, the same
+// result).
 template <int L>
-__device__ __forceinline__ void asym_header(const float* row, uint32_t& sh, uint32_t& mh, double& s, double& m,
-                                            double& r)
+__device__ __forceinline__ void asym_header(const float* half, bool second, uint32_t& sh, uint32_t& mh, double& s,
+                                            double& m, double& r)
 {
     float mn, mx;
-    min_max(row, mn, mx);
+    min_max(half, second, mn, mx);
     sh = f16_encode(or_tiny(((double)mx - (double)mn) / (double)L));
     mh = f16_encode((double)mn);
     s = or_tiny(f16_decode(sh));
@@ -173,67 +206,78 @@ __device__ __forceinline__ void asym_header(const float* row, uint32_t& sh, uint
     r = 1.0 / s;
 }
 
+// The wave's staging and loop, shared by the encoders: `encode(g, half, second)` encodes the half of
+// group g starting at `half` in LDS (elements 16 second .. 16 second + 15 of the group).
+template <class F>
+__device__ __forceinline__ void encode_groups(const f32x4_t* __restrict__ src, size_t groups, float* lds, F&& encode)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
+    const bool second = lane & 1;
+    const float* half = rows + (lane >> 1) * ENC_ROW + (second ? 16 : 0);
+    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
+    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
+    f32x4_t t[ENC_LOADS];
+    if (g0 < groups) load_rows(src, g0, groups, t);
+    for (; g0 < groups; g0 += stride) {
+        store_rows(t, rows);
+        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
+        const size_t g = g0 + (lane >> 1);
+        if (g < groups) encode(g, half, second);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // this lane's row reads are done
+    }
+}
+
 }  // namespace
 
-// In every encoder a wave iteration stages 64 groups and each lane encodes its own group from its row:
-// the codes with code_fast, word by word, and, in the rare case that a value was unsure, the whole group
-// again with code_exact (the later stores overwrite the earlier words). The loads of the wave's next
-// 64 groups are issued before the encoding, so they overlap it.
+// In every encoder a wave iteration stages 32 groups and each pair of lanes encodes one group, a half
+// each: the codes with code_fast, word by word, and, in the rare case that a value of the group was
+// unsure, the half again with code_exact (the later stores overwrite the earlier words). The loads of
+// the wave's next 32 groups are issued before the encoding, so they overlap it.
 extern "C" __global__ __launch_bounds__(256) void brik_encode_q8(const f32x4_t* __restrict__ src,
                                                                  uint32_t* __restrict__ codes,
                                                                  uint16_t* __restrict__ scales, size_t groups)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
-    const float* row = rows + lane * ENC_ROW;
-    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
-    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
-    f32x4_t t[8];
-    if (g0 < groups) load_rows(src, g0, groups, t);
-    for (; g0 < groups; g0 += stride) {
-        store_rows(t, rows);
-        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
-        const size_t g = g0 + lane;
-        if (g < groups) {
-            float amax = 0.f;
+    encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
+        float amax = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const f32x4_t w = row4(row, i);
-                const float e[4] = {w.x, w.y, w.z, w.w};
+        for (int i = 0; i < 4; ++i) {
+            const f32x4_t w = row4(half, i);
+            const float e[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float a = fabsf(e[j]);
-                    if (a > amax) amax = a;
-                }
-            }
-            const uint32_t sh = f16_encode(or_tiny((double)amax / 127.0));
-            scales[g] = (uint16_t)sh;
-            const double s = or_tiny(f16_decode(sh));
-            const float r = (float)(1.0 / s), er = r * 0x1p-20f;
-            bool unsure = false;
-#pragma unroll 1
-            for (int k = 0; k < 8; ++k) {
-                const f32x4_t w = row4(row, k);
-                const float e[4] = {w.x, w.y, w.z, w.w};
-                uint32_t word = 0u;
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    word |= ((uint32_t)code_fast(e[b], 0.f, r, er, 0.f, -127, 127, unsure) & 0xffu) << (8 * b);
-                codes[g * 8 + k] = word;
-            }
-            if (unsure) {
-#pragma unroll 1
-                for (int k = 0; k < 8; ++k) {
-                    uint32_t word = 0u;
-                    for (int b = 0; b < 4; ++b)
-                        word |= ((uint32_t)code_exact((double)row[4 * k + b], s, -127.0, 127.0) & 0xffu) << (8 * b);
-                    codes[g * 8 + k] = word;
-                }
+            for (int j = 0; j < 4; ++j) {
+                const float a = fabsf(e[j]);
+                if (a > amax) amax = a;
             }
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // this lane's row reads are done
-    }
+        amax = first_max(amax, second);
+        const uint32_t sh = f16_encode(or_tiny((double)amax / 127.0));
+        if (!second) scales[g] = (uint16_t)sh;
+        const double s = or_tiny(f16_decode(sh));
+        const float r = (float)(1.0 / s), er = r * 0x1p-20f;
+        uint32_t* out = codes + g * 8 + (second ? 4 : 0);
+        bool unsure = false;
+#pragma unroll 1
+        for (int k = 0; k < 4; ++k) {
+            const f32x4_t w = row4(half, k);
+            const float e[4] = {w.x, w.y, w.z, w.w};
+            uint32_t word = 0u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                word |= ((uint32_t)code_fast(e[b], 0.f, r, er, 0.f, -127, 127, unsure) & 0xffu) << (8 * b);
+            out[k] = word;
+        }
+        if (unsure || pair_u32(unsure)) {
+#pragma unroll 1
+            for (int k = 0; k < 4; ++k) {
+                uint32_t word = 0u;
+                for (int b = 0; b < 4; ++b)
+                    word |= ((uint32_t)code_exact((double)half[4 * k + b], s, -127.0, 127.0) & 0xffu) << (8 * b);
+                out[k] = word;
+            }
+        }
+    });
 }
 
 extern "C" __global__ __launch_bounds__(256) void brik_encode_q4(const f32x4_t* __restrict__ src,
@@ -242,46 +286,36 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q4(const f32x4_t* 
                                                                  uint16_t* __restrict__ mins, size_t groups)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
-    const float* row = rows + lane * ENC_ROW;
-    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
-    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
-    f32x4_t t[8];
-    if (g0 < groups) load_rows(src, g0, groups, t);
-    for (; g0 < groups; g0 += stride) {
-        store_rows(t, rows);
-        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
-        const size_t g = g0 + lane;
-        if (g < groups) {
-            uint32_t sh, mh;
-            double s, m, r;
-            asym_header<15>(row, sh, mh, s, m, r);
+    encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
+        uint32_t sh, mh;
+        double s, m, r;
+        asym_header<15>(half, second, sh, mh, s, m, r);
+        if (!second) {
             scales[g] = (uint16_t)sh;
             mins[g] = (uint16_t)mh;
-            const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
-            bool unsure = false;
+        }
+        const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
+        uint32_t* out = nibbles + g * 4 + (second ? 2 : 0);
+        bool unsure = false;
 #pragma unroll 1
-            for (int k = 0; k < 4; ++k) {         // element 8 k + b is nibble b of word k (low nibble = even)
-                const f32x4_t a = row4(row, 2 * k), c = row4(row, 2 * k + 1);
-                const float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-                uint32_t word = 0u;
+        for (int k = 0; k < 2; ++k) {         // element 8 k + b of the half is nibble b of word k (low nibble = even)
+            const f32x4_t a = row4(half, 2 * k), c = row4(half, 2 * k + 1);
+            const float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            uint32_t word = 0u;
 #pragma unroll
-                for (int b = 0; b < 8; ++b) word |= (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 15, unsure) << (4 * b);
-                nibbles[g * 4 + k] = word;
-            }
-            if (unsure) {
+            for (int b = 0; b < 8; ++b) word |= (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 15, unsure) << (4 * b);
+            out[k] = word;
+        }
+        if (unsure || pair_u32(unsure)) {
 #pragma unroll 1
-                for (int k = 0; k < 4; ++k) {
-                    uint32_t word = 0u;
-                    for (int b = 0; b < 8; ++b)
-                        word |= (uint32_t)code_exact((double)row[8 * k + b] - m, s, 0.0, 15.0) << (4 * b);
-                    nibbles[g * 4 + k] = word;
-                }
+            for (int k = 0; k < 2; ++k) {
+                uint32_t word = 0u;
+                for (int b = 0; b < 8; ++b)
+                    word |= (uint32_t)code_exact((double)half[8 * k + b] - m, s, 0.0, 15.0) << (4 * b);
+                out[k] = word;
             }
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
+    });
 }
 
 extern "C" __global__ __launch_bounds__(256) void brik_encode_q3(const f32x4_t* __restrict__ src,
@@ -290,61 +324,42 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q3(const f32x4_t* 
                                                                  uint16_t* __restrict__ mins, size_t groups)
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    float* rows = lds + wave * ENC_GROUPS * ENC_ROW;
-    const float* row = rows + lane * ENC_ROW;
-    const size_t stride = (size_t)gridDim.x * 4 * ENC_GROUPS;
-    size_t g0 = ((size_t)blockIdx.x * 4 + wave) * ENC_GROUPS;
-    f32x4_t t[8];
-    if (g0 < groups) load_rows(src, g0, groups, t);
-    for (; g0 < groups; g0 += stride) {
-        store_rows(t, rows);
-        if (g0 + stride < groups) load_rows(src, g0 + stride, groups, t);     // the next rows, in flight meanwhile
-        const size_t g = g0 + lane;
-        if (g < groups) {
-            uint32_t sh, mh;
-            double s, m, r;
-            asym_header<7>(row, sh, mh, s, m, r);
+    encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
+        uint32_t sh, mh;
+        double s, m, r;
+        asym_header<7>(half, second, sh, mh, s, m, r);
+        if (!second) {
             scales[g] = (uint16_t)sh;
             mins[g] = (uint16_t)mh;
-            const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
-            bool unsure = false;
-            uint32_t h = 0u;
-            // half k: elements [16 k, 16 k + 16) -> lo word k (2 low bits each) and hi bits [16 k, 16 k + 16)
-#pragma unroll 1
-            for (int k = 0; k < 2; ++k) {
-                uint32_t l = 0u, hb = 0u;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const f32x4_t w = row4(row, 4 * k + c);
-                    const float e[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const uint32_t q = (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 7, unsure);
-                        l |= (q & 3u) << (2 * (4 * c + b));
-                        hb |= (q >> 2) << (4 * c + b);
-                    }
-                }
-                lo[g * 2 + k] = l;
-                h |= hb << (16 * k);
-            }
-            if (unsure) {
-                h = 0u;
-#pragma unroll 1
-                for (int k = 0; k < 2; ++k) {
-                    uint32_t l = 0u;
-                    for (int i = 0; i < 16; ++i) {
-                        const uint32_t q = (uint32_t)code_exact((double)row[16 * k + i] - m, s, 0.0, 7.0);
-                        l |= (q & 3u) << (2 * i);
-                        h |= (q >> 2) << (16 * k + i);
-                    }
-                    lo[g * 2 + k] = l;
-                }
-            }
-            hi[g] = h;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
+        const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
+        bool unsure = false;
+        // this half: lo word `second` (2 low bits each) and hi bits [16 second, 16 second + 16)
+        uint32_t l = 0u, hb = 0u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const f32x4_t w = row4(half, c);
+            const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t q = (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 7, unsure);
+                l |= (q & 3u) << (2 * (4 * c + b));
+                hb |= (q >> 2) << (4 * c + b);
+            }
+        }
+        if (unsure || pair_u32(unsure)) {
+            l = 0u;
+            hb = 0u;
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t q = (uint32_t)code_exact((double)half[i] - m, s, 0.0, 7.0);
+                l |= (q & 3u) << (2 * i);
+                hb |= (q >> 2) << i;
+            }
+        }
+        lo[g * 2 + (second ? 1 : 0)] = l;
+        const uint32_t other = pair_u32(hb);
+        if (!second) hi[g] = hb | (other << 16);
+    });
 }
 
 // f16 bits -> f32 as the reference's conversion path decodes an F16 tensor before quantizing it

@@ -57,6 +57,15 @@ def adversarial(seed, groups):
     x[224:256] = 1e-30
     x[256:288] = 3e38
     x[288:320] = -np.inf
+    # ties across the halves of a group (the encoders scan each 16-element half on its own lane): a
+    # +0 minimum before a -0 one, a -0 maximum before a +0 one, a first half of NaN, and equal extremes
+    # in both halves
+    x[352:384] = 0.0
+    x[372] = -0.0                                             # min stays +0 (the first zero)
+    x[384:400], x[400:416] = -0.0, 0.0                         # max stays -0, min -0
+    x[416:432], x[432:448] = np.nan, rng.standard_normal(16).astype(np.float32)
+    x[448:480] = 2.5
+    x[452], x[470] = -3.0, -3.0
     x[n - 32:] = rng.standard_normal(32).astype(np.float32) * 1e4
     return x
 
@@ -74,7 +83,7 @@ def gpu_quantize(gpu, fmt, x):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("groups", [1, 51, 1000, 40000])
 def test_quantize_bytes_equal_cpu_encoder(gpu, fmt, groups):
-    x = adversarial(10 + groups, max(groups, 11))[: 32 * groups]
+    x = adversarial(10 + groups, max(groups, 16))[: 32 * groups]
     assert np.array_equal(gpu_quantize(gpu, fmt, x), oracle_bytes(fmt, x))
 
 
@@ -88,7 +97,7 @@ def group_slice(fmt, blob, n, g0, g1):
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_quantize_large_grid_stride(gpu, fmt):
-    # more groups than one launch covers (1024 blocks x 256 groups): blocks loop over the rest; the
+    # more groups than one launch covers (2048 blocks x 128 groups): blocks loop over the rest; the
     # oracle checks the first groups and the last ones, taken by a later pass
     groups = 4096 * 256 + 777
     x = (np.random.default_rng(3).standard_normal(32 * groups) * 2).astype(np.float32)
