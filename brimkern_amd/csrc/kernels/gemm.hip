@@ -295,17 +295,32 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p)
 // each step barrier), so these reads are issued as asm, invisible to that rule, and their completion
 // is waited for explicitly: lds_wait, then tie on every value read, which orders its uses after the
 // wait.
+// OFF is the instruction's 16-bit immediate offset: reads at fixed distances from one base take no
+// address arithmetic of their own.
+template <int OFF = 0>
 __device__ __forceinline__ half8_t ds_read_b128(uint32_t addr)
 {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     half8_t v;
-    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
 }
+template <int OFF = 0>
 __device__ __forceinline__ uint32_t ds_read_u16(uint32_t addr)
 {
+    static_assert(OFF >= 0 && OFF < 65536, "ds offset");
     uint32_t v;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(addr));
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
     return v;
+}
+// The A fragments of one slice: row block i at base + i * 32 rows.
+template <int TM, int I = 0>
+__device__ __forceinline__ void read_a(half8_t (&a)[TM], uint32_t base)
+{
+    if constexpr (I < TM) {
+        a[I] = ds_read_b128<I * 32 * XROW>(base);
+        read_a<TM, I + 1>(a, base);
+    }
 }
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"); }
 template <class V>
@@ -446,10 +461,10 @@ struct Loader {
             const uint32_t col = (uint32_t)(wave * 32 * TN + 32 * j + (lane & 31));
             const uint32_t ps = lds_addr(lds + buf) + col * (T::SG * 2) + pos * 2;
             f[j].s[0] = ds_read_u16(ps);
-            f[j].s[1] = ds_read_u16(ps + 2);
+            f[j].s[1] = ds_read_u16<2>(ps);
             if constexpr (FMT != FMT_Q8) {
-                f[j].m[0] = ds_read_u16(ps + T::SPLANE);
-                f[j].m[1] = ds_read_u16(ps + T::SPLANE + 2);
+                f[j].m[0] = ds_read_u16<T::SPLANE>(ps);
+                f[j].m[1] = ds_read_u16<T::SPLANE + 2>(ps);
             }
         }
     }
@@ -653,13 +668,11 @@ __device__ __forceinline__ void mma_step(const unsigned char* lds, const uint32_
         if constexpr (FMT != FMT_F16)
             if (sl == 6) ld.read_scales(wn, t + 1, snext, lane);
         if (sl < 7) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) a[nxt][i] = ds_read_b128(lbase + abuf + aoff[sl + 1] + i * 32 * XROW);
+            read_a<TM>(a[nxt], lbase + abuf + aoff[sl + 1]);
 #pragma unroll
             for (int j = 0; j < TN; ++j) b[nxt][j] = b_frag<FMT>(wc[j], go[j], sl + 1);
         } else {
-#pragma unroll
-            for (int i = 0; i < TM; ++i) a[nxt][i] = ds_read_b128(lbase + anext + aoff[0] + i * 32 * XROW);
+            read_a<TM>(a[nxt], lbase + anext + aoff[0]);
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 gn[j] = group_ops<FMT>(wn[j], go[j].k);
@@ -801,8 +814,7 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
     step_barrier();
     if constexpr (FMT != FMT_F16) ld.read_scales(wr[0], 0, T::S_OFF, lane);
     const DeqConst dk = DeqConst::make();
-#pragma unroll
-    for (int i = 0; i < TM; ++i) a[0][i] = ds_read_b128(lds_addr(smem) + aoff[0] + i * 32 * XROW);
+    read_a<TM>(a[0], lds_addr(smem) + aoff[0]);
     lds_wait();
     if constexpr (FMT != FMT_F16) ld.finish_scales(wr[0], 0);
 #pragma unroll
