@@ -106,6 +106,7 @@ constexpr long kPrestageRows = 96L * 256;
 constexpr unsigned kStageThreads = 1024;       // threads of a staging block (launch bounds of brik_gemv_stage_*)
 constexpr double kPrestageGroupRows = 8192;
 constexpr long kPrestageMaxSets = 4;
+constexpr long kPrestageMinSets = 2;
 constexpr long kPlanMinBlocks = 1024;          // grouped-plan blocks, at least (while sets > 1)
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
@@ -1414,6 +1415,10 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
         const brik_gemv_job& b = jobs[order[k]].job;
         sorted[k] = jobs[order[k]];
         long s0 = lround(group_rows / ((double)(b.K / kGroup) * rpi));
+        // a block that copies a staged image moves 112 B of it per group against 20 rpi B of q4 weights
+        // per group and row set (17.5 %), so it takes at least two sets: the 36-layer q4 set's K = 9728
+        // blocks (one set by the rule above) went 300.8-301.5 -> 299.3-300.0 us per step
+        if (prestage && s0 < kPrestageMinSets) s0 = kPrestageMinSets;
         sets[k] = s0 < 1 ? 1 : s0 > maxsets ? maxsets : s0;
     }
     for (;;) {
