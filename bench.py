@@ -59,6 +59,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+SINGLE_MIN_LAUNCHES = 1000    # timed launches of a single-matrix GEMV line, at least
 ROTATE_BYTES = 512 << 20        # distinct weight copies a per-call timing cycles through: 2x the MALL
 SMALL_M = (2, 4, 8, 15)
 
@@ -161,7 +162,7 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
         def one(i, M=1, r=extra, yb=yb, K=K, N=N, count=count):
             nib, sc, mn = r.planes(i % count)
             ctx.matmul_t_q4(x if M == 1 else xm, nib, sc, mn, yb, M, K, N)
-        lms = time_loop(ctx, one, max(4 * layers, count), count)
+        lms = time_loop(ctx, one, max(4 * layers, count, SINGLE_MIN_LAUNCHES), count)
         b = tb + 4 * K + 4 * N
         single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1),
                                        "copies": count}
@@ -253,7 +254,10 @@ def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
     x = ctx.upload(synth.normal(seed + 1, K))
     y = ctx.alloc(4 * N)
     fn = {"q8": ctx.matmul_t_q8, "q4": ctx.matmul_t_q4, "q3": ctx.matmul_t_q3}[fmt]
-    ms = time_loop(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies), copies)
+    # at least SINGLE_MIN_LAUNCHES timed launches: the queue starts empty after the warmup's sync, and
+    # over a few hundred launches of a few microseconds that start-up latency still shows in the mean
+    ms = time_loop(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies, SINGLE_MIN_LAUNCHES),
+                   copies)
     b = tb + 4 * K + 4 * N
     for bb in (r.buf, x, y):
         ctx.free(bb)
