@@ -132,10 +132,14 @@ class Engine {
   }
 
   // Asynchronous form (readBack / mapAsync, kernels.ts:244-258): resolves once the work enqueued so far
-  // has run, without blocking the JS thread meanwhile.
+  // has run, without blocking the JS thread meanwhile. The callback refers to `buf`, so a DeviceBuffer
+  // stays reachable (its finalizer cannot free the memory) until the copy out of it has completed.
   readBackAsync(buf, bytes) {
     const ptr = typeof buf === 'bigint' ? buf : buf.ptr;
-    return this.native.readbackAsync(this.ctx, ptr, bytes).then(function (ab) { return new Float32Array(ab); });
+    return this.native.readbackAsync(this.ctx, ptr, bytes).then(function (ab) {
+      void buf;   // a reference from the closure is what keeps the buffer alive
+      return new Float32Array(ab);
+    });
   }
 
   // A quantized weight handle from one packed .brik blob: one upload, planes addressed in place.
