@@ -30,6 +30,7 @@ steady), and the headline is the steady-state rate a decode loop sees.
 """
 import argparse
 import json
+import math
 import os
 import shutil
 import subprocess
@@ -59,7 +60,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-SINGLE_MIN_LAUNCHES = 1000    # timed launches of a single-matrix GEMV line, at least
+MIN_TIMED_MS = 20.0           # timed work of an `extra` line, at least (time_loop_min)
 ROTATE_BYTES = 512 << 20        # distinct weight copies a per-call timing cycles through: 2x the MALL
 SMALL_M = (2, 4, 8, 15)
 
@@ -106,6 +107,16 @@ def time_loop(ctx, fn, steps, warmup):
     ms = ctx.timer_end()
     ctx.sync()
     return ms / steps
+
+
+def time_loop_min(ctx, fn, steps, warmup, min_ms=MIN_TIMED_MS):
+    """time_loop for the `extra` lines: if `steps` calls take less than min_ms, time again with enough
+    calls to fill it. The queue starts empty after the warmup's synchronize, and over a few milliseconds
+    that start-up latency (about 0.1 ms here) still shows in the mean."""
+    ms = time_loop(ctx, fn, steps, warmup)
+    if ms * steps < min_ms:
+        ms = time_loop(ctx, fn, int(math.ceil(min_ms / max(ms, 1e-4))), 0)
+    return ms
 
 
 def settle(ctx, fn, seconds):
@@ -162,7 +173,7 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
         def one(i, M=1, r=extra, yb=yb, K=K, N=N, count=count):
             nib, sc, mn = r.planes(i % count)
             ctx.matmul_t_q4(x if M == 1 else xm, nib, sc, mn, yb, M, K, N)
-        lms = time_loop(ctx, one, max(4 * layers, count, SINGLE_MIN_LAUNCHES), count)
+        lms = time_loop_min(ctx, one, max(4 * layers, count), count)
         b = tb + 4 * K + 4 * N
         single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1),
                                        "copies": count}
@@ -172,7 +183,7 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
                                     ("splitk", PATH_GEMM, 2)):
                 ctx.set_option(BRIK_OPT_PATH, path)
                 ctx.set_option(BRIK_OPT_SPLITK, sk)
-                ms_m = time_loop(ctx, lambda i, M=M: one(i, M), count, count // 4)
+                ms_m = time_loop_min(ctx, lambda i, M=M: one(i, M), count, count // 4)
                 row[label + "_us"] = round(ms_m * 1e3, 2)
             ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
             ctx.set_option(BRIK_OPT_SPLITK, 0)
@@ -254,10 +265,7 @@ def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
     x = ctx.upload(synth.normal(seed + 1, K))
     y = ctx.alloc(4 * N)
     fn = {"q8": ctx.matmul_t_q8, "q4": ctx.matmul_t_q4, "q3": ctx.matmul_t_q3}[fmt]
-    # at least SINGLE_MIN_LAUNCHES timed launches: the queue starts empty after the warmup's sync, and
-    # over a few hundred launches of a few microseconds that start-up latency still shows in the mean
-    ms = time_loop(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies, SINGLE_MIN_LAUNCHES),
-                   copies)
+    ms = time_loop_min(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies), copies)
     b = tb + 4 * K + 4 * N
     for bb in (r.buf, x, y):
         ctx.free(bb)
@@ -277,10 +285,10 @@ def lm_head_topk_cfg3(ctx, steps, warmup, gemv_us, cache_bytes=768 << 20):
     rec = ctx.upload(np.unique((synth.uniform(702, 40) * N).astype(np.int32)))
     nrec = int(rec.nbytes // 4)
     out = ctx.alloc(8 * k)
-    ms = time_loop(ctx, lambda i: ctx.lm_head_topk("q3", x, r.planes(i % copies), K, N, rec, nrec, 1.15, 30.0, k,
+    ms = time_loop_min(ctx, lambda i: ctx.lm_head_topk("q3", x, r.planes(i % copies), K, N, rec, nrec, 1.15, 30.0, k,
                                                   out, out.offset(4 * k)), max(steps, copies), copies)
     logits = ctx.upload(synth.normal(703, N) * 4)
-    ms_p = time_loop(ctx, lambda i: ctx.logits_topk(logits, N, rec, nrec, 1.15, 30.0, k, out, out.offset(4 * k)),
+    ms_p = time_loop_min(ctx, lambda i: ctx.logits_topk(logits, N, rec, nrec, 1.15, 30.0, k, out, out.offset(4 * k)),
                      steps, warmup)
     for bb in (r.buf, x, rec, out, logits):
         ctx.free(bb)
@@ -302,7 +310,7 @@ def quantize_f1(ctx, steps, warmup):
         ob = ctx.alloc(layout.byte_length(fmt, n))
         offs = layout.plane_offsets(fmt, n)
         pl = [ob.offset(offs[p][0]) for p in planes_of[fmt]]
-        ms = time_loop(ctx, lambda i: ctx.quantize(fmt, src[i % 3], pl, n), steps, warmup)
+        ms = time_loop_min(ctx, lambda i: ctx.quantize(fmt, src[i % 3], pl, n), steps, warmup)
         b = 4 * n + layout.byte_length(fmt, n)
         out[fmt] = {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
                     "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "Gelem_per_s": round(n / (ms * 1e-3) / 1e9, 1)}
@@ -333,7 +341,7 @@ def conv_f4(ctx, steps, warmup):
     out = {}
     for name, path, st in (("implicit_gemm", 0, steps), ("direct", 1, max(2, steps // 10))):
         ctx.set_option(BRIK_OPT_PATH, path)
-        ms = time_loop(ctx, lambda i: ctx.conv2d("q4", x, planes, b, y, Cin, H, W, Cout, k, k, 1, 1), st, 2)
+        ms = time_loop_min(ctx, lambda i: ctx.conv2d("q4", x, planes, b, y, Cin, H, W, Cout, k, k, 1, 1), st, 2)
         out[name] = {"us": round(ms * 1e3, 2), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1)}
     ctx.set_option(BRIK_OPT_PATH, 0)
     for bb in (wb, x, b, y):
@@ -356,9 +364,9 @@ def f16w_f4(ctx, steps, warmup, cache_bytes=768 << 20):
     ws = [ctx.upload(w) for _ in range(copies)]
     x = ctx.upload(synth.normal(961, M * K))
     y = ctx.alloc(4 * M * N)
-    ms1 = time_loop(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, 1, K, N), max(steps, copies), copies)
+    ms1 = time_loop_min(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, 1, K, N), max(steps, copies), copies)
     b1 = wbytes + 4 * K + 4 * N
-    msm = time_loop(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, M, K, N), steps, warmup)
+    msm = time_loop_min(ctx, lambda i: ctx.matmul_t_f16w(x, ws[i % copies], y, M, K, N), steps, warmup)
     tf = 2.0 * M * N * K / (msm * 1e-3) / 1e12
     for bb in ws + [x, y]:
         ctx.free(bb)
@@ -376,7 +384,7 @@ def gemm_cfg4(ctx, steps, warmup):
     r = Replicas(ctx, "q4", synth.q4_tensor(300, N, K), copies)
     x = ctx.upload(synth.normal(301, M * K))
     y = ctx.alloc(4 * M * N)
-    ms = time_loop(ctx, lambda i: ctx.matmul_t_q4(x, *r.planes(i % copies), y, M, K, N), max(steps, copies), 4)
+    ms = time_loop_min(ctx, lambda i: ctx.matmul_t_q4(x, *r.planes(i % copies), y, M, K, N), max(steps, copies), 4)
     flops = 2.0 * M * N * K
     for bb in (r.buf, x, y):
         ctx.free(bb)
@@ -410,8 +418,8 @@ def moe_cfg5(ctx, steps, warmup):
         c = i % copies
         ctx.moe_matmul_t_q4_x2(xg, ro, reps["gate"].planes(c), yg, reps["up"].planes(c), yu, E, R, H, F)
         ctx.moe_matmul_t_q4(xd, ro, *reps["down"].planes(c), yd, E, R, F, H)
-    ms3 = time_loop(ctx, step3, max(steps, 6), 3)
-    ms = time_loop(ctx, step, max(steps, 6), 3)
+    ms3 = time_loop_min(ctx, step3, max(steps, 6), 3)
+    ms = time_loop_min(ctx, step, max(steps, 6), 3)
     wbytes = 2 * q_bytes("q4", E * F, H) + q_bytes("q4", E * H, F)
     flops = 2.0 * R * (2 * H * F + F * H)
     for bb in list(r.buf for r in reps.values()) + [xg, xd, ro, yg, yu, yd]:
