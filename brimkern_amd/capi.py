@@ -21,6 +21,7 @@ BRIK_GEMV_VARIANTS = 9
 BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES = 3, 23
 BRIK_OPT_PLAN_STAGE, BRIK_OPT_PLAN_SETS, BRIK_OPT_SPLITK, BRIK_OPT_GEMV_BLOCKS = 4, 5, 6, 7
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+BRIK_PATH_GEMV, BRIK_PATH_GEMV_STAGED, BRIK_PATH_TILED, BRIK_PATH_SPLITK = 1, 2, 3, 4
 
 # every exported symbol of include/brik.h with (restype, argtypes)
 _P, _I, _Z, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(ctypes.c_float)
@@ -28,6 +29,7 @@ SIGNATURES = {
     "brik_create": (_I, [_I, ctypes.POINTER(_P)]),
     "brik_destroy": (None, [_P]),
     "brik_last_error": (ctypes.c_char_p, [_P]),
+    "brik_last_path": (_I, [_P]),
     "brik_strerror": (ctypes.c_char_p, [_I]),
     "brik_device_count": (_I, [ctypes.POINTER(_I)]),
     "brik_alloc": (_I, [_P, _Z, ctypes.POINTER(_P)]),
@@ -244,6 +246,10 @@ class Context:
 
     def set_option(self, key: int, value: int):
         self._check(self.lib.brik_set_option(self.handle, key, value))
+
+    def last_path(self) -> int:
+        """BRIK_PATH_* of the last matmul call on this context (0 before any, or for K = 0)."""
+        return self.lib.brik_last_path(self.handle)
 
     def timer_begin(self):
         self._check(self.lib.brik_timer_begin(self.handle))

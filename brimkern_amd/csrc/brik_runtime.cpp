@@ -156,8 +156,10 @@ struct brik_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     // the context's workspace generation when the capture ended: the recorded launches hold the
-    // workspace addresses of that moment
+    // workspace addresses of that moment. Checked at launch only if the capture used a context
+    // workspace (uses_ws): a graph of plans and no-allocation calls holds none of those addresses.
     unsigned long long ws_generation = 0;
+    bool uses_ws = false;
 };
 
 struct brik_ctx {
@@ -197,7 +199,9 @@ struct brik_ctx {
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
     int scratch_err = 0;
+    int last_path = 0;            // BRIK_PATH_* of the last matmul call (brik_last_path)
     bool graph_capturing = false;
+    bool graph_used_ws = false;   // the open capture recorded a launch on a context workspace
     // bumped whenever a context workspace is freed and reallocated (ensure_buf): a graph recorded
     // before that replays addresses that are no longer the context's, so brik_graph_launch refuses it
     unsigned long long ws_generation = 0;
@@ -328,6 +332,7 @@ int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
 // read the old buffer, so the stream is drained before it is freed.
 int ensure_buf(brik_ctx* c, void*& buf, size_t& have, size_t bytes)
 {
+    if (c->graph_capturing) c->graph_used_ws = true;
     if (have >= bytes) return BRIK_OK;
     if (c->graph_capturing)
         return fail(c, BRIK_EINVAL, "a workspace would grow during graph capture: run the same calls once "
@@ -452,26 +457,52 @@ SplitK splitk_shape(long rows, int K, int N, int E)
 }
 
 // Whether a GEMM takes the split-K kernel: dense launches of few rows where the cost model above prefers
-// it, unless a tile is forced, the no-allocation entry point runs it (no workspace) or the option says
-// so. Expert-grouped launches keep the tiled kernel: on the 64-expert layer (20-50 rows per expert)
-// split-K measured slower (gate 62 us against 42, down 50 against 35: experts past 32 rows read their
-// weights twice, and the two-slice gate adds the slice sum).
-bool use_splitk(const brik_ctx* c, Fmt f, long rows, int K, int N, int E, const Scratch* fixed)
+// it, unless a tile is forced or the option says so. Expert-grouped launches keep the tiled kernel: on
+// the 64-expert layer (20-50 rows per expert) split-K measured slower (gate 62 us against 42, down 50
+// against 35: experts past 32 rows read their weights twice, and the two-slice gate adds the slice sum).
+bool use_splitk(const brik_ctx* c, Fmt f, long rows, int K, int N, int E)
 {
-    if (fixed || c->opt_tile > 0 || c->opt_splitk == 1) return false;
+    if (c->opt_tile > 0 || c->opt_splitk == 1) return false;
     if (c->opt_splitk == 2) return true;
     return E == 0 && rows <= kSplitKMaxRows && small_m_path(f, rows, K, N) == SM_SPLITK;
 }
 
+// Bytes of the split-K partial tiles a GEMM over `rows` rows writes (0: no split-K, or one slice).
+size_t splitk_part_bytes(const brik_ctx* c, Fmt f, long rows, int K, int N, int E)
+{
+    if (!use_splitk(c, f, rows, K, N, E)) return 0;
+    const SplitK p = splitk_shape(rows, K, N, E);
+    return p.gz > 1 ? (size_t)p.gz * rows * N * 4 : 0;
+}
+
+// Offset of the split-K partial tiles in a fixed scratch: after the staged rows, 256-byte aligned.
+size_t splitk_part_off(long rows, int K)
+{
+    long Kp;
+    return (gemm_stage_bytes(rows, K, Kp) + 255) & ~(size_t)255;
+}
+
 int gemm_splitk(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const void* p0, const void* p1,
-                const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E)
+                const void* sc, const void* mn, float* y, int rows, int K, int N, const int* row_off, int E,
+                const Scratch* fixed)
 {
     const SplitK p = splitk_shape(rows, K, N, E);
     float* part = nullptr;
     if (p.gz > 1) {
-        void* pw = nullptr;
-        HIP_TRY_RC(take_scratch(c, nullptr, c->pws, c->pws_bytes, (size_t)p.gz * rows * N * 4, pw));
-        part = static_cast<float*>(pw);
+        const size_t bytes = (size_t)p.gz * rows * N * 4;
+        if (fixed) {
+            // the no-allocation entry point: after the staged rows in the same fixed buffer (gemm checked
+            // that both fit before enqueueing anything)
+            const size_t off = splitk_part_off(rows, K);
+            if (off + bytes > fixed->bytes)
+                return fail(c, BRIK_EINVAL, "no-allocation call: needs %zu bytes of scratch, the fixed buffer "
+                            "holds %zu", off + bytes, fixed->bytes);
+            part = reinterpret_cast<float*>(static_cast<char*>(fixed->p) + off);
+        } else {
+            void* pw = nullptr;
+            HIP_TRY_RC(take_scratch(c, nullptr, c->pws, c->pws_bytes, bytes, pw));
+            part = static_cast<float*>(pw);
+        }
     }
     int Mi = rows, Ki = K, Ni = N, Ei = E;
     void* args[] = {&xh, &rscale, &p0, &p1, &sc, &mn, &y, &Mi, &Ki, &Ni, &row_off, &Ei, &part};
@@ -504,11 +535,14 @@ int gemm_run(brik_ctx* c, Fmt f, const uint16_t* xh, const float* rscale, const 
              const Scratch* fixed = nullptr, const WeightPair* pair = nullptr, const float* tbias = nullptr,
              int trans = 0)
 {
-    if (use_splitk(c, f, rows, K, N, E, fixed)) {
-        HIP_TRY_RC(gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E));
+    if (use_splitk(c, f, rows, K, N, E)) {
+        c->last_path = BRIK_PATH_SPLITK;
+        HIP_TRY_RC(gemm_splitk(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed));
         if (!pair) return BRIK_OK;
-        return gemm_splitk(c, f, xh, rscale, pair->p0, p1, pair->sc, pair->mn, pair->y, rows, K, N, row_off, E);
+        return gemm_splitk(c, f, xh, rscale, pair->p0, p1, pair->sc, pair->mn, pair->y, rows, K, N, row_off, E,
+                           fixed);
     }
+    c->last_path = BRIK_PATH_TILED;
     int Mi = rows, Ki = K, Ni = N, Ei = E;
     const int t = gemm_tile(c, rows, N, K, E);
     const GemmTile& gt = kGemmTiles[t];
@@ -548,6 +582,15 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     if (K == 0) {                                           // empty sums
         if (pair) HIP_TRY_RC(fill_zero(c, pair->y, (size_t)rows * N));
         return fill_zero(c, y, (size_t)rows * N);
+    }
+    if (fixed) {
+        // a fixed scratch holds the staged rows and, for split-K, the partial tiles after them: refuse
+        // before anything is enqueued if they do not fit
+        const size_t pb = splitk_part_bytes(c, f, rows, K, N, E);
+        const size_t need = pb ? splitk_part_off(rows, K) + pb : 0;
+        if (need > fixed->bytes)
+            return fail(c, BRIK_EINVAL, "no-allocation call: needs %zu bytes of scratch (staged rows and split-K "
+                        "partial tiles), the fixed buffer holds %zu", need, fixed->bytes);
     }
     long Kp;
     uint16_t* xh;
@@ -600,6 +643,7 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
            const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr)
 {
+    c->last_path = 0;
     if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
     // A large q4 / q3 matrix at M = 1 (an LM head) stages x once per call (brik_gemv_stage1_<fmt>, one
     // block) and its blocks copy the image instead of each staging x themselves. q8 measured no gain.
@@ -637,6 +681,7 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
             HIP_TRY_RC(launch(c, f == F_Q4 ? K_GEMV_STAGE1_Q4 : K_GEMV_STAGE1_Q3, 1, 1, kStageThreads, 0, sargs));
         }
         void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged};
+        c->last_path = stage1 ? BRIK_PATH_GEMV_STAGED : BRIK_PATH_GEMV;
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
     return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0, fixed);
@@ -869,6 +914,8 @@ const char* brik_strerror(int code)
 
 const char* brik_last_error(const brik_ctx* c) { return c ? c->err : "null context"; }
 
+int brik_last_path(const brik_ctx* c) { return c ? c->last_path : 0; }
+
 int brik_device_count(int* count)
 {
     if (!count) return BRIK_EINVAL;
@@ -1062,6 +1109,7 @@ static int moe(brik_ctx* c, const char* who, const float* x, const int32_t* row_
                const uint16_t* sc, const uint16_t* mn, float* y, const WeightPair* pair, int E, int R, int K, int N)
 {
     if (!c) return BRIK_EINVAL;
+    c->last_path = 0;
     if (E < 0 || R < 0) return fail(c, BRIK_EINVAL, "%s: negative E=%d or R=%d", who, E, R);
     int r = check_mm(c, who, x, nib, nullptr, sc, mn, y, R, K, N, F_Q4);
     if (r == BRIK_OK && pair)
@@ -1226,7 +1274,7 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
     // maxima of the input [H W]
     const size_t yt_bytes = ((size_t)M * Cout * 4 + 255) & ~(size_t)255;
     // the GEMM writes out itself ([Cout, pixels] plus the bias) unless the split-K kernel runs it
-    const bool fused = !use_splitk(c, f, rows, Kint, Cout, 0, nullptr);
+    const bool fused = !use_splitk(c, f, rows, Kint, Cout, 0);
     HIP_TRY_RC(ensure_buf(c, c->cws, c->cws_bytes, (fused ? 0 : yt_bytes) + (size_t)H * W * 4));
     float* yt = static_cast<float*>(c->cws);
     float* cmax = reinterpret_cast<float*>(static_cast<unsigned char*>(c->cws) + (fused ? 0 : yt_bytes));
@@ -1682,6 +1730,7 @@ int brik_graph_begin(brik_ctx* c)
     HIP_TRY(c, hipSetDevice(c->device));
     HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     c->graph_capturing = true;
+    c->graph_used_ws = false;
     return BRIK_OK;
 }
 
@@ -1701,6 +1750,7 @@ int brik_graph_end(brik_ctx* c, brik_graph** out)
         return fail(c, BRIK_EHIP, "graph_end: %s", hipGetErrorString(e));
     }
     g->ws_generation = c->ws_generation;
+    g->uses_ws = c->graph_used_ws;
     *out = g;
     return BRIK_OK;
 }
@@ -1708,7 +1758,7 @@ int brik_graph_end(brik_ctx* c, brik_graph** out)
 int brik_graph_launch(brik_ctx* c, const brik_graph* g)
 {
     if (!c || !g) return BRIK_EINVAL;
-    if (g->ws_generation != c->ws_generation)
+    if (g->uses_ws && g->ws_generation != c->ws_generation)
         return fail(c, BRIK_EINVAL, "graph_launch: a context workspace was reallocated after this graph was "
                                     "recorded (a larger call ran since); record the graph again");
     HIP_TRY(c, hipSetDevice(c->device));

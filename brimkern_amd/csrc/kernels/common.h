@@ -46,6 +46,17 @@ __device__ __forceinline__ brsrc_t make_rsrc(const void* p, uint32_t bytes)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, BRIK_BUF_DWORD3);
 }
 
+// p, with its provenance hidden from the compiler (an empty asm on a uniform value). Loads through a
+// restrict-qualified const pointer are treated as reads of constant memory, which the compiler may
+// reorder freely; through the laundered pointer they stay in program order relative to other memory
+// operations and compiler barriers, where the order in which loads are issued matters.
+template <typename T>
+__device__ __forceinline__ T* launder_uniform(T* p)
+{
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
 // Cache policy of streamed weight loads: non-temporal (nt).
 #define BRIK_AUX_STREAM 2
 

@@ -176,7 +176,8 @@ constexpr int stage_trips(int R, int U) { return U >= 5 && R >= 2 ? 1 : 4; }
 
 template <int FMT, int TEAM, int R, int U>
 struct Work {
-    static constexpr int RPI = (256 / TEAM) * R;   // rows per block iteration
+    static constexpr int NT = 256;                 // threads per block
+    static constexpr int RPI = (NT / TEAM) * R;    // rows per block iteration
     static constexpr int PARTS = TEAM;             // partial sums per row
     static constexpr int NACC = R;                 // accumulators per lane
     static constexpr int UG = U;                   // groups per lane per step
@@ -190,9 +191,12 @@ struct Work {
     using XS = XStage;
     static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_layout(lds, K); }
     static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_bytes(K); }
-    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
+    // NTH: the threads of the block that stages (a staging kernel runs more than a GEMV block)
+    template <int NTH = NT, class After = brik::NoLoads>
+    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F,
+                                                 After after_first = After())
     {
-        brik::xstage<FMT, STAGE_TRIPS>(x, S, K, F);
+        brik::xstage<FMT, STAGE_TRIPS, NTH>(x, S, K, F, after_first);
     }
 
     __device__ __forceinline__ void init()
@@ -302,10 +306,11 @@ __device__ __forceinline__ void code_nibbles(const Grp<FMT>& d, uint32_t (&c)[4]
 //
 // P = 2 (GLU pairs): two matrices of equal shape on the same staged x. A team's R rows are then
 // RH = R / 2 rows of the first matrix (rs) followed by the same rows of the second (rs2): row r of
-// the team is row n0(p) + r % RH of matrix r / RH. NT: threads per block.
-template <int FMT, int TEAM, int R, int U, int P = 1, int NT = 256>
+// the team is row n0(p) + r % RH of matrix r / RH. NTB: threads per block.
+template <int FMT, int TEAM, int R, int U, int P = 1, int NTB = 256>
 struct WorkD {
     static_assert(P == 1 || (P == 2 && R % 2 == 0), "pair rows");
+    static constexpr int NT = NTB;                 // threads per block
     static constexpr int RPI = (NT / TEAM) * R;    // rows per block iteration, both matrices together
     static constexpr int RH = R / P;               // rows per team and matrix
     static constexpr int PARTS = TEAM;
@@ -320,9 +325,11 @@ struct WorkD {
     using XS = brik::XStageD;
     static __device__ __forceinline__ XS xs_layout(void* lds, int K) { return brik::xstage_d_layout(lds, K); }
     static __device__ __forceinline__ size_t xs_bytes(int K) { return brik::xstage_d_bytes(K); }
-    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F)
+    template <int NTH = NT, class After = brik::NoLoads>
+    static __device__ __forceinline__ void stage(const float* __restrict__ x, const XS& S, int K, const Fuse& F,
+                                                 After after_first = After())
     {
-        brik::xstage_d<FMT, STAGE_TRIPS>(x, S, K, F);
+        brik::xstage_d<FMT, STAGE_TRIPS, NTH>(x, S, K, F, after_first);
     }
 
     __device__ __forceinline__ void init()
@@ -403,13 +410,14 @@ using PairWork = WorkD<FMT, TEAM, R, U, 2, NT>;
 
 // Exact path for a row holding Inf/NaN: teams of 16 lanes (16 in a 256-thread block); in every row set
 // (rows base + [0, RPI), base = r0, r0 + rstep, ...) team t takes rows t, t + teams, ... (any RPI).
-template <int FMT, int RPI>
+template <int FMT, int RPI, int NT>
 __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, const Fuse& F, float inv,
                                                 const Planes& P, float* __restrict__ yrow,
                                                 const float* __restrict__ res, int K, int r0, int r1, int rstep)
 {
     const int lane = threadIdx.x % 16;
-    const int team = threadIdx.x / 16, nteams = blockDim.x / 16;
+    const int team = threadIdx.x / 16;
+    constexpr int nteams = NT / 16;
     for (int base = r0; base < r1; base += rstep) {
         for (int i = team; i < RPI; i += nteams) {
             const int n = base + i;         // uniform across the team's 16 lanes
@@ -425,40 +433,45 @@ __device__ __forceinline__ void gemv_rows_exact(const float* __restrict__ x, con
 
 // Copy a staged x image of `bytes` bytes (a multiple of 8) from global memory into LDS at `lds`:
 // direct global->LDS loads, 1 KiB per wave instruction, 16 bytes per lane.
+template <int NT>
 __device__ __forceinline__ void stage_copy(const unsigned char* __restrict__ src, unsigned char* lds, uint32_t bytes)
 {
     const brsrc_t r = make_rsrc(src, bytes);
     const uint32_t lane = threadIdx.x & 63;
-    for (uint32_t c0 = (threadIdx.x >> 6) * 1024u; c0 < bytes; c0 += blockDim.x * 16u)
+    for (uint32_t c0 = (threadIdx.x >> 6) * 1024u; c0 < bytes; c0 += NT * 16u)
         if (c0 + 16u * lane < bytes)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (brik::lds_void_t*)(lds + c0), 16, c0 + 16u * lane, 0, 0, 0);
 }
 
-// The software pipeline of one team: D - 1 steps issued before x is staged, then a straight-line
+// The software pipeline of one team: D - 1 steps issued while x is staged, then a straight-line
 // loop (unrolled by D so buffer indices are static) issuing step i + D - 1 and consuming step i.
-// With a pre-staged image (`staged`, written by brik_gemv_stage_<fmt> or by a GLU pair launch) the
-// block copies it into LDS, issued ahead of the first weight loads so that waiting for it does not
-// wait for them. Returns true, before any step is consumed, if the row holds a value that is not
-// finite: the caller then runs the exact path.
+// Vector-memory loads complete in issue order, so whatever x comes from is loaded first and the D - 1
+// weight steps are issued behind it: staging then waits for x alone and runs while the weights are in
+// flight (issued first, they had to arrive before staging could start, and the two latencies added
+// up). In-block staging issues the weights after its first batch of x loads (xprep.h batched_in); with a
+// pre-staged image (`staged`, written by brik_gemv_stage_<fmt> or by a GLU pair launch) the block
+// copies it into LDS, then issues the weights. Returns true, before any step is consumed, if the row
+// holds a value that is not finite: the caller then runs the exact path.
 template <int FMT, class W, int D, bool EVEN>
 __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
                                          int K, int S, const unsigned char* __restrict__ staged, unsigned char* lds)
 {
     typename W::Data d[D];
     int ip = 0, bp = 0;                      // (p, b) of the next step to issue
-    if (staged) {
-        stage_copy(staged, lds, (uint32_t)((W::xs_bytes(K) + 15) & ~(size_t)15));
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    auto issue_ahead = [&] {
 #pragma unroll
-    for (int k = 0; k < D - 1; ++k) {
-        w.template issue<EVEN>(d[k], ip, bp);
-        const bool wrap = bp + 1 == w.B;
-        bp = wrap ? 0 : bp + 1;
-        ip += wrap;
-    }
+        for (int k = 0; k < D - 1; ++k) {
+            w.template issue<EVEN>(d[k], ip, bp);
+            const bool wrap = bp + 1 == w.B;
+            bp = wrap ? 0 : bp + 1;
+            ip += wrap;
+        }
+    };
     int flag;
     if (staged) {
+        stage_copy<W::NT>(staged, lds, (uint32_t)((W::xs_bytes(K) + 15) & ~(size_t)15));
+        __builtin_amdgcn_sched_barrier(0);
+        issue_ahead();
         // every load issued after the copy is one of the D - 1 weight steps above
         brik::wait_vmcnt<(D - 1) * W::NACC * W::UG * LoadsPerGroup<FMT>::v>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -466,9 +479,9 @@ __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const fl
         // a GLU pair launch writes the groups of an image but not its flag, which stays -1: each group
         // then carries its own marker (a stager writes the flag, 0 or 1)
         if constexpr (FMT != FMT_Q8)
-            if (flag < 0) flag = brik::image_bad(X);
+            if (flag < 0) flag = brik::image_bad<W::NT>(X);
     } else {
-        W::stage(x, X, K, F);
+        W::stage(x, X, K, F, issue_ahead);
         flag = *X.flag;
     }
     if (flag) return true;
@@ -503,6 +516,23 @@ __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const fl
     return false;
 }
 
+// The sums of `rows` rows of PARTS lane partials each (LDS, row-major: partial l of row q at
+// part[q * PARTS + l]): PARTS consecutive threads load one row's partials together and add them with
+// DPP steps (team_sum, within 16-lane rows, then across them), and the row's first lane calls
+// out(q, sum). Every row sums in the same order, whichever thread holds it. Called by every thread of
+// the block (NT threads, a multiple of PARTS); the partials must be complete (after a barrier).
+template <int PARTS, int NT, class Out>
+__device__ __forceinline__ void row_sums(const float* __restrict__ part, int rows, Out out)
+{
+    constexpr int per = NT / PARTS;                   // rows per pass
+    const int l = (int)threadIdx.x % PARTS;
+    for (int q0 = 0; q0 < rows; q0 += per) {          // the same trips for every thread: the DPP steps
+        const int q = q0 + (int)threadIdx.x / PARTS;  // see whole teams
+        const float v = team_sum<PARTS>(q < rows ? part[q * PARTS + l] : 0.f);
+        if (l == 0 && q < rows) out(q, v);
+    }
+}
+
 // Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
 // then the cross-lane sums of the LDS partials are written to y. The block owns row sets
 // p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
@@ -525,25 +555,20 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
                                 : pipeline<FMT, W, D, false>(w, X, x, F, K, S, staged, lds);
     if (exact) {
         // teams of 16 lanes over RPI rows per iteration
-        gemv_rows_exact<FMT, W::RPI>(x, F, *X.inv, P, yrow, res, K, r0, r1, rstep);
+        gemv_rows_exact<FMT, W::RPI, W::NT>(x, F, *X.inv, P, yrow, res, K, r0, r1, rstep);
         return;
     }
     __syncthreads();
-    // cross-lane sums: one thread per row, PARTS partials each (rows past r1 are skipped), times the
-    // RMSNorm factor of a fused input (1 otherwise: exact), which the staged image leaves out
-    constexpr int PARTS = W::PARTS;
+    // cross-lane sums (row_sums), times the RMSNorm factor of a fused input (1 otherwise: exact), which
+    // the staged image leaves out; rows past r1 are skipped
     const float inv = *X.inv;
-    for (int q = threadIdx.x; q < nsets * W::RPI; q += blockDim.x) {
+    row_sums<W::PARTS, W::NT>(w.part, nsets * W::RPI, [&](int q, float v) {
         const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
         if (n < r1) {
-            const float* pp = w.part + (size_t)q * PARTS;
-            float v = 0.f;
-#pragma unroll
-            for (int l = 0; l < PARTS; ++l) v += pp[(l + q) % PARTS];
             v *= inv;
             yrow[n] = res ? res[n] + v : v;
         }
-    }
+    });
 }
 
 // One matrix, one activation row per grid.y. `staged` (M = 1 only): the row's LDS image, written by
@@ -620,43 +645,32 @@ __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const 
                                 : pipeline<FMT, W, D, false>(w, X, jg.job.x, F, K, w.B, nullptr, lds);
     float* vals = (float*)lds;     // gate then up values of the set; the x image is not read any more
     if (exact) {
-        gemv_rows_exact<FMT, H>(jg.job.x, F, *X.inv, Pg, jg.job.y, jg.res, K, w.r0, w.r1, H);
-        gemv_rows_exact<FMT, H>(ju.job.x, F, *X.inv, Pu, ju.job.y, ju.res, K, w.r0, w.r1, H);
+        gemv_rows_exact<FMT, H, W::NT>(jg.job.x, F, *X.inv, Pg, jg.job.y, jg.res, K, w.r0, w.r1, H);
+        gemv_rows_exact<FMT, H, W::NT>(ju.job.x, F, *X.inv, Pu, ju.job.y, ju.res, K, w.r0, w.r1, H);
         __syncthreads();           // the rows just written are visible to the block
-        for (int q = threadIdx.x; q < 2 * H; q += blockDim.x) {
+        for (int q = threadIdx.x; q < 2 * H; q += W::NT) {
             const int n = r0 + q % H;
             vals[q] = n < N ? (q < H ? jg.job.y : ju.job.y)[n] : 0.f;
         }
     } else {
         __syncthreads();
-        const float inv = *X.inv;      // read by every thread before the values overwrite LDS
-        float v[2] = {0.f, 0.f};
-        int at[2] = {-1, -1};
-        // thread q sums partial row q = team * R + r: row i = team * RH + r % RH of matrix r / RH
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int q = (int)threadIdx.x + k * (int)blockDim.x;
-            if (q < W::RPI) {
-                const int r = q % R, m = r / RH, i = q / R * RH + r % RH;
-                const float* pp = w.part + (size_t)q * PARTS;
-                float s = 0.f;
-#pragma unroll
-                for (int l = 0; l < PARTS; ++l) s += pp[(l + i) % PARTS];
-                s *= inv;
-                const int n = r0 + i;
-                if (n < N) {
-                    const float* res = m ? ju.res : jg.res;
-                    s = res ? res[n] + s : s;
-                    (m ? ju.job.y : jg.job.y)[n] = s;
-                }
-                v[k] = s;
-                at[k] = m * H + i;
+        // read by every thread before the values overwrite LDS: a tiny row's image tail, inv included,
+        // lies under them (the partials do not: they start past the image, at 304 bytes or more)
+        const float inv = *X.inv;
+        __syncthreads();
+        // partial row q = team * R + r is row i = team * RH + r % RH of matrix r / RH; summed as the
+        // unpaired plans sum theirs (row_sums), so gate and up are bit-identical to those
+        row_sums<PARTS, W::NT>(w.part, W::RPI, [&](int q, float s) {
+            const int r = q % R, m = r / RH, i = q / R * RH + r % RH;
+            s *= inv;
+            const int n = r0 + i;
+            if (n < N) {
+                const float* res = m ? ju.res : jg.res;
+                s = res ? res[n] + s : s;
+                (m ? ju.job.y : jg.job.y)[n] = s;
             }
-        }
-        __syncthreads();           // (a tiny row's image tail, inv included, lies under the values)
-#pragma unroll
-        for (int k = 0; k < 2; ++k)
-            if (at[k] >= 0) vals[at[k]] = v[k];
+            vals[m * H + i] = s;
+        });
     }
     __syncthreads();
     // group g on lanes 0-31 of wave g, lane e holding element e
@@ -727,7 +741,7 @@ __device__ __forceinline__ void stage_input(const brik_stage_input* __restrict__
     using W = Work<FMT, 16, 2, 1>;
     const brik_stage_input e = in[blockIdx.x];
     const typename W::XS S = W::xs_layout(out + e.off, e.K);
-    W::stage(e.x, S, e.K, Fuse{e.gate, e.norm_w, e.eps, e.flags});
+    W::template stage<1024>(e.x, S, e.K, Fuse{e.gate, e.norm_w, e.eps, e.flags});
 }
 }  // namespace
 
@@ -737,7 +751,7 @@ template <int FMT>
 __device__ __forceinline__ void stage_row(const float* __restrict__ x, int K, unsigned char* __restrict__ out)
 {
     using W = Work<FMT, 16, 2, 1>;
-    W::stage(x, W::xs_layout(out, K), K, Fuse{nullptr, nullptr, 0.f, 0});
+    W::template stage<1024>(x, W::xs_layout(out, K), K, Fuse{nullptr, nullptr, 0.f, 0});
 }
 }  // namespace
 

@@ -100,18 +100,37 @@ struct RawIn {
     f32x4_t x[C], g[C], w[C];
 };
 
+// Buffer resources over the inputs of a staging pass (x, gate, RMSNorm gain: `bytes` each), built from
+// laundered pointers (launder_uniform) so that the loads keep their place in program order:
+// batched_in's hook relies on the x loads going out first.
+struct InRs {
+    brsrc_t x, g, w;
+};
+
+__device__ __forceinline__ InRs in_rsrc(const float* __restrict__ x, const Fuse& F, uint32_t bytes)
+{
+    const float* xl = launder_uniform(x);
+    return InRs{make_rsrc(xl, bytes), make_rsrc(F.gate ? launder_uniform(F.gate) : xl, F.gate ? bytes : 0u),
+                make_rsrc(F.norm_w ? launder_uniform(F.norm_w) : xl, F.norm_w ? bytes : 0u)};
+}
+
+__device__ __forceinline__ f32x4_t ld_f4(const brsrc_t& r, int k)
+{
+    return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)k * 4u, 0u, 0));
+}
+
 template <int C>
-__device__ __forceinline__ void load_in(RawIn<C>& r, const float* __restrict__ x, const Fuse& F, int k)
+__device__ __forceinline__ void load_in(RawIn<C>& r, const InRs& R, const Fuse& F, int k)
 {
 #pragma unroll
-    for (int c = 0; c < C; ++c) r.x[c] = *(const f32x4_t*)(x + k + 4 * c);
+    for (int c = 0; c < C; ++c) r.x[c] = ld_f4(R.x, k + 4 * c);
     if (F.gate) {
 #pragma unroll
-        for (int c = 0; c < C; ++c) r.g[c] = *(const f32x4_t*)(F.gate + k + 4 * c);
+        for (int c = 0; c < C; ++c) r.g[c] = ld_f4(R.g, k + 4 * c);
     }
     if (F.norm_w) {
 #pragma unroll
-        for (int c = 0; c < C; ++c) r.w[c] = *(const f32x4_t*)(F.norm_w + k + 4 * c);
+        for (int c = 0; c < C; ++c) r.w[c] = ld_f4(R.w, k + 4 * c);
     }
 }
 
@@ -138,29 +157,63 @@ __device__ __forceinline__ f32x4_t gain_in(const RawIn<C>& r, int c, const Fuse&
 
 __device__ __forceinline__ float sumsq4(f32x4_t v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
 
-// body(i, loads) for i = threadIdx.x, + blockDim.x, ... < n over chunks of 4C floats, in that order.
+// A staging call's hook for other loads (none by default).
+struct NoLoads {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+// body(i, loads) for i = threadIdx.x, + NT, ... < n over chunks of 4C floats, in that order (NT: the
+// block's threads, a compile-time constant: blockDim.x can cost a memory round trip to read).
 // The loads of SB consecutive trips are issued together before any is used, so a thread pays one
 // memory round trip per SB trips instead of one per trip (a K = 9728 row takes five trips of a
 // 256-thread block). Indices past n are clamped for the loads, which then stay in range, and their
-// trips run no body. Whole aligned lane groups enter each body together when n and blockDim are
+// trips run no body. Whole aligned lane groups enter each body together when n and NT are
 // multiples of the group size, as the DPP group reductions need.
-template <int SB, int C, class Body>
-__device__ __forceinline__ void batched_in(const float* __restrict__ x, const Fuse& F, int n, Body body)
+// after_first() runs once, right after the first batch's loads are issued (every thread calls it):
+// the GEMV issues its first weight loads there. Vector-memory loads complete in issue order, so the
+// first batch's bodies then wait for x only, with the weights still in flight behind it; issued
+// before x, the weights would have to arrive before staging could start.
+template <int SB, int C, int NT, class Body, class After = NoLoads>
+__device__ __forceinline__ void batched_in(const float* __restrict__ x, const Fuse& F, int n, Body body,
+                                           After after_first = After())
 {
-    const int bd = (int)blockDim.x, tid = (int)threadIdx.x;
-    for (int b = 0; b < n; b += SB * bd) {
-        RawIn<C> r[SB];
+    constexpr int bd = NT;
+    const int tid = (int)threadIdx.x;
+    const InRs R = in_rsrc(x, F, (uint32_t)n * 16u * C);
+    auto load = [&](RawIn<C> (&r)[SB], int b) {
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
             const int i = min(b + u * bd + tid, n - 1);
-            load_in<C>(r[u], x, F, 4 * C * i);
+            load_in<C>(r[u], R, F, 4 * C * i);
         }
+    };
+    auto run = [&](const RawIn<C> (&r)[SB], int b) {
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
             if (b + u * bd >= n) break;           // the same for every thread of the block
             const int i = b + u * bd + tid;
             if (i < n) body(i, r[u]);
         }
+    };
+    // The first batch is straight-line code (n > 0 always: K >= 32), so the compiler's wait before its
+    // bodies counts the hook's loads as still in flight; inside the loop under a condition, the
+    // branch-merged count had it wait for them.
+    {
+        RawIn<C> r[SB];
+        load(r, 0);
+        // keep the order: x loads, then the hook's loads (the empty asm orders memory operations in the
+        // compiler's IR, the scheduling barrier in the machine scheduler)
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        after_first();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        run(r, 0);
+    }
+    for (int b = SB * bd; b < n; b += SB * bd) {
+        RawIn<C> r[SB];
+        load(r, b);
+        run(r, b);
     }
 }
 
@@ -174,6 +227,7 @@ __device__ __forceinline__ void batched_in(const float* __restrict__ x, const Fu
 // the flag too: the exact path applies it per element, as the reference does. thread 0 wrote flag = 0
 // before the pass; the 1s are written after the first barrier, so they cannot race it. Ends with a
 // barrier after which flag and inv hold their final values.
+template <int NT>
 __device__ __forceinline__ void stage_finish(int* flag, float* inv, const Fuse& F, int K, float ss, int bad)
 {
     if (F.norm_w) {
@@ -187,7 +241,7 @@ __device__ __forceinline__ void stage_finish(int* flag, float* inv, const Fuse& 
         float f = 1.f;
         if (F.norm_w) {
             float t = 0.f;
-            for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += inv[1 + w];
+            for (int w = 0; w < NT / 64; ++w) t += inv[1 + w];
             f = 1.f / sqrtf(t / (float)K + F.eps);
             if (!(f > 0.f && f < __builtin_inff())) *flag = 1;
         }
@@ -207,8 +261,9 @@ __device__ __forceinline__ void split_limbs(float v, int sh, bool finite, int& h
 
 // Stage x[0..K) (16-byte aligned, K % 32 == 0). All threads of the block call it; ends with a barrier.
 // SB: loop trips whose loads a thread issues together (batched_in); more trips hold more registers.
-template <int FMT, int SB>
-__device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K, const Fuse& F)
+template <int FMT, int SB, int NT, class After = NoLoads>
+__device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage& S, int K, const Fuse& F,
+                                       After after_first = After())
 {
     static_assert(FMT == FMT_Q8, "q4 and q3 stage digit planes (xstage_d)");
     const int G = S.G;
@@ -220,9 +275,9 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
     const int nq = K >> 2;
     float ss = 0.f;
     int bad = 0;
-    // the 8 float4 chunks of a group sit in 8 consecutive lanes (blockDim % 8 == 0, nq % 8 == 0);
+    // the 8 float4 chunks of a group sit in 8 consecutive lanes (NT % 8 == 0, nq % 8 == 0);
     // every body is entered by whole 8-lane groups, so the DPP group reductions see full groups
-    batched_in<SB, 1>(x, F, nq, [&](int i, const RawIn<1>& r) {
+    batched_in<SB, 1, NT>(x, F, nq, [&](int i, const RawIn<1>& r) {
         f32x4_t v = apply_in<1>(r, 0, F);
         if (F.norm_w) {
             ss += sumsq4(v);
@@ -251,8 +306,8 @@ __device__ __forceinline__ void xstage(const float* __restrict__ x, const XStage
         *(uint32_t*)(base + pos) = pack(hh);
         *(uint32_t*)(base + 32 + pos) = pack(mm);
         *(uint32_t*)(base + 64 + pos) = pack(ll);
-    });
-    stage_finish(S.flag, S.inv, F, K, ss, bad);
+    }, after_first);
+    stage_finish<NT>(S.flag, S.inv, F, K, ss, bad);
 }
 
 // ---- q4: x as six signed 4-bit digit planes ---------------------------------------------------
@@ -400,19 +455,21 @@ __device__ __forceinline__ bool stage_group_d(f32x4_t v0, f32x4_t v1, int j, uns
 }
 
 // Stage x[0..K) (16-byte aligned, K % 32 == 0) as digit planes: one thread per 8 consecutive elements,
-// a quad of lanes per group. All threads of the block call it; ends with a barrier.
-template <int FMT, int SB>
-__device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XStageD& S, int K, const Fuse& F)
+// a quad of lanes per group. All threads of the block call it; ends with a barrier. after_first: as in
+// batched_in.
+template <int FMT, int SB, int NT, class After = NoLoads>
+__device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XStageD& S, int K, const Fuse& F,
+                                         After after_first = After())
 {
     const int G = S.G;
     if (threadIdx.x == 0) *S.flag = 0;
     if (threadIdx.x < 7) *(u32x4_t*)(S.base + 112 * G + 16 * threadIdx.x) = u32x4_t{0u, 0u, 0u, 0u};
     float ss = 0.f;
     int bad = 0;
-    // every body is entered by whole quads (blockDim % 4 == 0, K/8 % 4 == 0), so the DPP group
+    // every body is entered by whole quads (NT % 4 == 0, K/8 % 4 == 0), so the DPP group
     // reductions see full groups
     const int n8 = K >> 3;
-    batched_in<(SB > 1 ? SB - 1 : 1), 2>(x, F, n8, [&](int i, const RawIn<2>& r) {
+    batched_in<(SB > 1 ? SB - 1 : 1), 2, NT>(x, F, n8, [&](int i, const RawIn<2>& r) {
         f32x4_t v0 = apply_in<2>(r, 0, F), v1 = apply_in<2>(r, 1, F);
         if (F.norm_w) {
             ss += sumsq4(v0) + sumsq4(v1);
@@ -420,8 +477,8 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
             v1 = gain_in<2>(r, 1, F, v1);
         }
         bad |= !stage_group_d<FMT>(v0, v1, i & 3, S.base + 112 * (i >> 2));
-    });
-    stage_finish(S.flag, S.inv, F, K, ss, bad);
+    }, after_first);
+    stage_finish<NT>(S.flag, S.inv, F, K, ss, bad);
 }
 
 // The same group image from lanes 0-31 of one wave (all active), lane e holding element e: for a
@@ -482,10 +539,11 @@ __device__ __forceinline__ void stage_group_lanes(float v, unsigned char* gb)
 // Whether any of the G groups of a digit-plane image holds a value that is not finite (the marker
 // stage_group_d writes). Called by every thread of the block after the image is in LDS; the
 // block-wide OR ends with a barrier.
+template <int NT>
 __device__ __forceinline__ int image_bad(const XStageD& S)
 {
     int bad = 0;
-    for (int g = (int)threadIdx.x; g < S.G; g += (int)blockDim.x) bad |= *(const int*)(S.base + 112 * g + 108);
+    for (int g = (int)threadIdx.x; g < S.G; g += NT) bad |= *(const int*)(S.base + 112 * g + 108);
     return __syncthreads_or(bad);
 }
 

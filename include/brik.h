@@ -363,6 +363,16 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
                                     (each block then loops over several row sets) */
 int brik_set_option(brik_ctx *ctx, int key, int value);
 
+/* The path the last brik_matmul_t_* / brik_matmul_t_q4_noalloc / brik_moe_matmul_t_q4* call on this
+ * context enqueued (0 before any such call, or for K = 0). A diagnostic with no counterpart in the
+ * reference (whose dispatch is the fixed M thresholds of recMM, kernels.ts:1521-1567): it lets tests
+ * and tuning runs confirm the routing a shape took. */
+#define BRIK_PATH_GEMV 1         /* decode GEMV kernels, x staged in every block */
+#define BRIK_PATH_GEMV_STAGED 2  /* decode GEMV over an x image staged once per call (large M = 1) */
+#define BRIK_PATH_TILED 3        /* MFMA GEMM tiles over staged f16 rows (dense or expert-grouped) */
+#define BRIK_PATH_SPLITK 4       /* few-row split-K MFMA GEMM (partial tiles summed in slice order) */
+int brik_last_path(const brik_ctx *ctx);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,7 +6,8 @@ import numpy as np
 import pytest
 
 from brimkern_amd import synth
-from brimkern_amd.capi import BrikError, BRIK_EINVAL
+from brimkern_amd.capi import (BrikError, BRIK_EINVAL, BRIK_OPT_PATH, BRIK_PATH_GEMV, BRIK_PATH_SPLITK,
+                               BRIK_PATH_TILED, PATH_AUTO, PATH_GEMM)
 from helpers import Gpu
 
 pytestmark = pytest.mark.gpu
@@ -99,18 +100,32 @@ def test_capture_refuses_workspace_growth_and_copies(gpu):
 def test_replay_after_workspace_reallocation_is_refused(gpu):
     """A graph records the context workspace's address; an eager call that needs a larger workspace
     frees and reallocates it, after which replaying the old graph would touch freed memory. The
-    library refuses that launch (no GPU work is enqueued) and a graph recorded afterwards replays."""
+    library refuses that launch (no GPU work is enqueued) and a graph recorded afterwards replays. A
+    graph whose launches hold no workspace address (a GEMV) still replays after the reallocation."""
     ctx = gpu.ctx
     K, N, M = 256, 64, 16
     t = synth.q4_tensor(140, N, K)
     nib, sc, mn = gpu.planes("q4", t)
     xm = gpu.up(synth.normal(141, M * K))
     ym = gpu.up(np.zeros(M * N, np.float32))
-    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+    yg = gpu.up(np.zeros(M * N, np.float32))
+    # the MFMA GEMM path (staged rows in the context workspace) for the recorded call
+    ctx.set_option(BRIK_OPT_PATH, PATH_GEMM)
+    try:
+        ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+        assert ctx.last_path() in (BRIK_PATH_TILED, BRIK_PATH_SPLITK)
+        ctx.sync()
+        ctx.graph_begin()
+        ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+        old = ctx.graph_end()
+    finally:
+        ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
+    ctx.matmul_t_q4(xm, nib, sc, mn, yg, M, K, N)
+    assert ctx.last_path() == BRIK_PATH_GEMV
     ctx.sync()
     ctx.graph_begin()
-    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
-    old = ctx.graph_end()
+    ctx.matmul_t_q4(xm, nib, sc, mn, yg, M, K, N)
+    gemv_graph = ctx.graph_end()
     # 128 MiB of staged activation rows (M_big x K_big halves): more than any earlier call of the session
     M_big, K_big = 16384, 4096
     xb = gpu.up(np.zeros(M_big * K_big, np.float32))
@@ -122,13 +137,25 @@ def test_replay_after_workspace_reallocation_is_refused(gpu):
         with pytest.raises(BrikError) as e:
             old.launch()
         assert e.value.code == BRIK_EINVAL
+        eager = ctx.download(yg, np.float32, M * N)
+        ctx.h2d(yg, np.full(M * N, np.nan, np.float32))
+        gemv_graph.launch()
+        ctx.sync()
+        assert np.array_equal(ctx.download(yg, np.float32, M * N), eager)
     finally:
         old.destroy()
-    ctx.graph_begin()
-    ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
-    new = ctx.graph_end()
+        gemv_graph.destroy()
+    ctx.set_option(BRIK_OPT_PATH, PATH_GEMM)
     try:
+        ctx.graph_begin()
         ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+        new = ctx.graph_end()
+    finally:
+        ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
+    try:
+        ctx.set_option(BRIK_OPT_PATH, PATH_GEMM)
+        ctx.matmul_t_q4(xm, nib, sc, mn, ym, M, K, N)
+        ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
         ctx.sync()
         eager = ctx.download(ym, np.float32, M * N)
         ctx.h2d(ym, np.full(M * N, np.nan, np.float32))
