@@ -605,26 +605,37 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 }
 
 // GEMV variant for a launch over `rows` rows in total (one matrix or a plan's jobs) with shortest row
-// K (index into kGemvVariants).
-// q8 / q3: the 32-row sets of variant 0 need enough blocks to keep every CU's loads in flight; below
-// that the 16-row sets of variant 5 (32 lanes per row, pipeline depth 3) give twice the blocks, when
-// rows are long enough (K >= 2048) for 32 lanes. Measured on the Qwen3-4B shapes: N = 9728 and the
-// 216-matrix layer set are faster with variant 0, N <= 4096 and the K = 9728 down projection with
-// variant 5; the K = 896 q8 FFN shape with variant 4 (below).
-// q4: large launches (the 36-layer set: 98k rows) stream whole rows per step with variant 7 (16
-// lanes x 5 groups = a K = 2560 row, 2 rows per team); rows of K >= 8192 alone (a down projection)
-// the one-row-per-team whole-row form of variant 8 (10.4 us against 11.0 us with variant 5 for
-// Qwen3-4B's fused down launch); rows of K >= 4096 variant 5; launches of a layer's gate/up size
-// (8k-24k rows) variant 0; 4k-8k rows (a layer's q/k/v) variant 1 (7.3 us against 7.9 us with
-// variant 8); smaller ones variant 8, which gives twice the blocks of variant 7.
-// q3 is bound by its unpacking (2-bit and 1-bit planes merged to bytes, ~35 VALU per row and group):
-// large launches take variant 3 (4 rows per team share each staged x read); the q3 LM head (N = 151936, K = 2560)
-// measured 45 us against 47-51 us with variant 0 and 52-58 us with the whole-row variants.
-int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
+// K (index into kGemvVariants). `single`: one matrix at M = 1 (brik_matmul_t_*); `staged`: its blocks
+// copy an x image staged once per call (a large single matrix) or by a GLU pair (a plan's consumer).
+//
+// Single matrices below the staged size: a launch of a few hundred blocks reaches HBM rate only when
+// every block's loads go out at once, so the variant that gives at least ~256 blocks wins. Measured
+// under graph replay on the Qwen3-4B shapes (us per launch): rows >= 4096 the whole-row 16-row blocks of
+// variant 8 (q 4.37, gate 6.40 against 5.25 / 7.10 for the next best; q8 gate 9.01, q3 gate 6.63);
+// fewer rows the 4-row blocks of variant 6, 64 lanes per row (k/v 3.46 against 4.07; wo K = 4096 5.05
+// against 5.51; q8 k/v 3.44; q3 k/v 3.76); rows of K >= 8192 the 32-lane teams of variant 5 (down
+// 8.52 against 8.99 with variant 6 and 9.74 with variant 8); short q8 rows (K <= 1024, the cfg 1 FFN
+// shape K = 896: 28 groups) two groups per lane step, variant 4, which covers a row in one step (4.15
+// against 4.37).
+// Plans: large ones (the 36-layer set: 98k rows) stream whole rows per step with variant 7 (16 lanes x
+// 5 groups = a K = 2560 row, 2 rows per team); the consumer of a GLU pair, which copies its image and
+// so has no staging to amortize, takes the 4-row blocks of variant 6 (Qwen3-4B down, K = 9728: 640
+// blocks, 6.74 us against 7.66 with variant 8); rows of K >= 8192 alone (a self-staged down
+// projection) the one-row whole-row form of variant 8; rows of K >= 4096 (wo)
+// variant 5; 8k-24k rows (a layer's gate/up) variant 0; 4k-8k rows (q/k/v) variant 1; smaller ones
+// variant 8, which gives twice the blocks of variant 7.
+// q3 large launches take variant 3 (4 rows per team share each staged x read) and the staged LM head
+// variant 7 (42.8 us against 45 us with variant 3).
+int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged, bool single)
 {
     if (c->opt_variant > 0) return c->opt_variant - 1;
-    // with x staged once per call, q3 streams whole rows too (the q3 LM head: 42.8 us against 45 us)
+    if (staged && !single) return 6;
     if (staged && f == F_Q3) return 7;
+    if (single && rows < 96L * 256) {
+        if (f == F_Q8 && kmin <= 1024 && rows < 32L * 256) return 4;
+        if (kmin >= 8192) return 5;
+        return rows >= 4096 ? 8 : 6;
+    }
     if (f == F_Q4) {
         if (rows >= 96L * 256) return 7;
         if (kmin >= 8192) return 8;
@@ -633,8 +644,6 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged = false)
         return rows >= 16L * 256 ? 1 : 8;
     }
     if (f == F_Q3 && rows >= 96L * 256) return 3;
-    // short q8 rows (K <= 1024, the cfg 1 FFN shape K = 896: 28 groups) in a small launch: two groups
-    // per lane step cover a row in one step (4.7 us against 5.2 us with variant 0)
     if (f == F_Q8 && kmin <= 1024 && rows < 32L * 256) return 4;
     return rows >= 32L * 256 || kmin < 2048 ? 0 : 5;
 }
@@ -649,7 +658,7 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
     // block) and its blocks copy the image instead of each staging x themselves. q8 measured no gain.
     const bool stage1 = M == 1 && N >= kPrestageRows && f != F_Q8 && c->opt_path != 2;
     // GEMV launch shape: one block per row set of RPI rows, capped; the block also stages its results
-    const int v = gemv_variant(c, f, N, K, stage1);
+    const int v = gemv_variant(c, f, N, K, stage1, true);
     const int rpi = kGemvVariants[v].rpi();
     const unsigned sets = (unsigned)((N + rpi - 1) / rpi);
     // a launch that copies a staged image (stage1) runs 4 blocks per CU, each looping over its row sets
@@ -1439,7 +1448,7 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
     }
     long rows = 0;
     for (int j = 0; j < njobs; ++j) rows += jobs[j].job.N;
-    const int v = gemv_variant(c, f, rows, kmin);
+    const int v = gemv_variant(c, f, rows, kmin, image != nullptr, false);
     const int rpi = kGemvVariants[v].rpi();
     // Blocks of about equal cost: rows per block ~ kPlanGroupRows / (K/32), in whole row sets of rpi
     // rows, at most kPlanMaxSets sets (bounded by the LDS partials buffer). A small plan (a decoder

@@ -15,7 +15,7 @@ import pytest
 
 import oracle as O
 from brimkern_amd import synth
-from brimkern_amd.capi import BrikError, BRIK_EINVAL
+from brimkern_amd.capi import BrikError, BRIK_EINVAL, BRIK_OPT_GEMV_VARIANT
 from helpers import Gpu, PLANES, normwise_rel
 
 pytestmark = pytest.mark.gpu
@@ -68,14 +68,20 @@ class Ffn:
         return {n: c.download(b, np.float32, b.nbytes // 4) for n, b in out.items()}
 
     def run_linked(self, runs=1):
-        """The linked pair; "y_plain": the ordinary down plan on the pair's gate.y and up.y."""
+        """The linked pair; "y_plain": the ordinary down plan on the pair's gate.y and up.y, on the GEMV
+        variant the pair's consumer runs (variant 6: 4-row blocks, 64 lanes per row), so that the two differ only in where the staged image comes from. q8 has no pair kernel:
+        its "pair" is two ordinary plans, compared with an ordinary plan as it is."""
         jg, ju, jd, out = self.jobs()
         gu, dn = self.gpu.ctx.gemv_plan_glu(self.fmt, jg, ju, jd)
         for _ in range(runs):
             gu.run()
             dn.run()
         out["y_plain"] = self.gpu.up(np.full(self.D, np.nan, np.float32))
-        plain = self.gpu.ctx.gemv_plan(self.fmt, [dict(jd, y=out["y_plain"])])
+        self.gpu.ctx.set_option(BRIK_OPT_GEMV_VARIANT, 0 if self.fmt == "q8" else 1 + 6)
+        try:
+            plain = self.gpu.ctx.gemv_plan(self.fmt, [dict(jd, y=out["y_plain"])])
+        finally:
+            self.gpu.ctx.set_option(BRIK_OPT_GEMV_VARIANT, 0)
         plain.run()
         r = self.read(out)
         plain.destroy()
