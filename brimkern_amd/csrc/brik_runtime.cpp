@@ -119,6 +119,8 @@ int fmt_index(int f) { return f == F_Q8 ? 0 : f == F_Q4 ? 1 : 2; }
 
 }  // namespace
 
+static_assert(sizeof(brik_gemv_block) == 128, "block table entry");
+
 // A device buffer shared by the two plans of a GLU pair (the staged image of act(gate) * up), freed
 // with the last of them.
 struct SharedBuf {
@@ -128,8 +130,7 @@ struct SharedBuf {
 
 struct brik_gemv_plan {
     hipFunction_t kernel;
-    // grouped: [jobs (brik_gemv_job_ex) | block_start | rows_per_block | stage_off (njobs) | stage inputs];
-    // GLU pair: [gate job | up job]
+    // grouped: [block table (brik_gemv_block per launch block) | stage inputs]; GLU pair: [gate job | up job]
     void* dev = nullptr;
     int njobs = 0;
     unsigned blocks = 0;
@@ -1497,6 +1498,8 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
         const size_t need = gemv_lds(b.K, f) + kGemvVariants[v].extra_lds(rpbs[k]);
         lds = need > lds ? need : lds;
     }
+    if (start[njobs] == 0 || start[njobs] > (1u << 31))
+        return fail(c, BRIK_EINVAL, "gemv_plan: %u blocks is outside the launch range", start[njobs]);
     if (lds > kGemvMaxLds) return fail(c, BRIK_EINVAL, "gemv_plan: K=%d too large for LDS staging", kmax);
     // distinct input rows (x and the fused transform) and where each is staged
     std::vector<uint32_t> stage_off(njobs, 0);
@@ -1524,19 +1527,22 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
     }
     brik_gemv_plan* p = new (std::nothrow) brik_gemv_plan();
     if (!p) return BRIK_ENOMEM;
-    const size_t jb = sizeof(brik_gemv_job_ex) * (size_t)njobs;
-    const size_t tables = jb + sizeof(uint32_t) * (start.size() + rpbs.size() + stage_off.size());
-    const size_t inputs_off = (tables + 15) & ~(size_t)15;
+    // device tables: one brik_gemv_block per launch block (its job, rows and staged image), then the
+    // staging pass's input table
+    const size_t nblocks = start[njobs];
+    const size_t inputs_off = sizeof(brik_gemv_block) * nblocks;
     const size_t bytes = inputs_off + sizeof(brik_stage_input) * inputs.size();
     std::vector<unsigned char> host(bytes, 0);
-    unsigned char* h = host.data();
-    std::memcpy(h, sorted.data(), jb);
-    h += jb;
-    std::memcpy(h, start.data(), sizeof(uint32_t) * start.size());
-    h += sizeof(uint32_t) * start.size();
-    std::memcpy(h, rpbs.data(), sizeof(uint32_t) * rpbs.size());
-    h += sizeof(uint32_t) * rpbs.size();
-    std::memcpy(h, stage_off.data(), sizeof(uint32_t) * stage_off.size());
+    brik_gemv_block* bt = reinterpret_cast<brik_gemv_block*>(host.data());
+    for (int k = 0; k < njobs; ++k) {
+        for (uint32_t b = start[k]; b < start[k + 1]; ++b) {
+            brik_gemv_block& d = bt[b];
+            d.job = sorted[k];
+            d.r0 = (int32_t)((b - start[k]) * rpbs[k]);
+            d.r1 = std::min(sorted[k].job.N, d.r0 + (int32_t)rpbs[k]);
+            d.stage_off = stage_off[k];
+        }
+    }
     if (!inputs.empty()) std::memcpy(host.data() + inputs_off, inputs.data(), sizeof(brik_stage_input) * inputs.size());
     int r = brik_alloc(c, bytes, &p->dev);
     if (r == BRIK_OK) r = brik_h2d(c, p->dev, host.data(), bytes);
@@ -1665,12 +1671,8 @@ int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
         void* args[] = {&jobs, &img, &af};
         return launch_fn(c, p->kernel, p->blocks, 1, kGluThreads, p->lds, args);
     }
-    const brik_gemv_job_ex* jobs = (const brik_gemv_job_ex*)p->dev;
-    const uint32_t* start = (const uint32_t*)((const unsigned char*)p->dev + sizeof(brik_gemv_job_ex) * (size_t)p->njobs);
-    const uint32_t* rpbs = start + p->njobs + 1;
-    const uint32_t* stage_off = rpbs + p->njobs;
+    const brik_gemv_block* blocks = static_cast<const brik_gemv_block*>(p->dev);
     const unsigned char* stage = static_cast<const unsigned char*>(p->stage);
-    int nj = p->njobs;
     if (p->stager) {
         // one block per distinct input row; the GEMV launch that follows on the stream reads the images
         const brik_stage_input* inputs =
@@ -1679,7 +1681,7 @@ int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
         void* sargs[] = {&inputs, &stage_buf};
         HIP_TRY_RC(launch_fn(c, p->stager, (unsigned)p->ninputs, 1, kStageThreads, 0, sargs));
     }
-    void* args[] = {&jobs, &start, &rpbs, &nj, &stage, &stage_off};
+    void* args[] = {&blocks, &stage};
     return launch_fn(c, p->kernel, p->blocks, 1, 256, p->lds, args);
 }
 

@@ -586,32 +586,21 @@ __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uin
                            nullptr, N, K, blockIdx.x * RPI, N, gridDim.x * RPI, lds, staged);
 }
 
-// Grouped GEMV over a job table: block b runs rows [rb * rows_per_block[j], ...) of job j, where
-// block_start[j] <= b < block_start[j + 1] (a prefix over the jobs' block counts). With a stage buffer
-// (non-null stage_base) job j's x image is at stage_base + stage_off[j].
+// Grouped GEMV over a plan's block table: block b runs rows [r0, r1) of the job in blocks[b], in row
+// sets of RPI rows. With a stage buffer (non-null stage_base) the job's x image is at
+// stage_base + stage_off.
 template <int FMT, class W, int D>
-__device__ __forceinline__ void gemv_grouped_body(const brik_gemv_job_ex* __restrict__ jobs,
-                                                  const uint32_t* __restrict__ block_start,
-                                                  const uint32_t* __restrict__ rows_per_block, int njobs,
-                                                  const unsigned char* __restrict__ stage_base,
-                                                  const uint32_t* __restrict__ stage_off)
+__device__ __forceinline__ void gemv_grouped_body(const brik_gemv_block* __restrict__ blocks,
+                                                  const unsigned char* __restrict__ stage_base)
 {
     extern __shared__ __align__(16) unsigned char lds[];
     constexpr int RPI = W::RPI;
-    const uint32_t b = blockIdx.x;
-    int lo = 0, hi = njobs - 1;          // last j with block_start[j] <= b
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (block_start[mid] <= b) lo = mid; else hi = mid - 1;
-    }
-    const brik_gemv_job_ex je = jobs[lo];
+    const brik_gemv_block bd = blocks[blockIdx.x];
+    const brik_gemv_job_ex& je = bd.job;
     const brik_gemv_job& job = je.job;
     const Planes P{(const uint8_t*)job.p0, (const uint8_t*)job.p1, job.scales, job.mins};
-    const int rpb = (int)rows_per_block[lo];
-    const int r0 = (int)(b - block_start[lo]) * rpb;
-    const int r1 = min(job.N, r0 + rpb);
-    gemv_matrix<FMT, W, D>(job.x, Fuse{je.gate, je.norm_w, je.eps, je.flags}, P, job.y, je.res, job.N, job.K, r0, r1,
-                           RPI, lds, stage_base ? stage_base + stage_off[lo] : nullptr);
+    gemv_matrix<FMT, W, D>(job.x, Fuse{je.gate, je.norm_w, je.eps, je.flags}, P, job.y, je.res, job.N, job.K, bd.r0,
+                           bd.r1, RPI, lds, stage_base ? stage_base + bd.stage_off : nullptr);
 }
 
 // GLU pair (brik_gemv_plan_create_glu): rows [r0, r0 + H) of gate (jobs jg) and up (ju), H = RPI / 2,
@@ -692,12 +681,9 @@ __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const 
         gemv_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(x, p0, p1, sc, mn, y, K, N, staged);            \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void brik_gemvg_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
-        const brik_gemv_job_ex* __restrict__ jobs, const uint32_t* __restrict__ block_start,        \
-        const uint32_t* __restrict__ rows_per_block, int njobs,                                      \
-        const unsigned char* __restrict__ stage_base, const uint32_t* __restrict__ stage_off)        \
+        const brik_gemv_block* __restrict__ blocks, const unsigned char* __restrict__ stage_base)    \
     {                                                                                               \
-        gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(jobs, block_start, rows_per_block, njobs,   \
-                                                           stage_base, stage_off);                   \
+        gemv_grouped_body<FMT, Work<FMT, TEAM, RR, UU>, DD>(blocks, stage_base);                    \
     }
 
 // The variant table of the runtime (brik_runtime.cpp, kGemvVariants) lists these in this order.
