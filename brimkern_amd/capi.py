@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_PKG, "libbrik.so")
 BRIK_OK, BRIK_EINVAL, BRIK_EALIGN, BRIK_EHIP, BRIK_ENOMEM, BRIK_ENODEV, BRIK_EMODULE = 0, -1, -2, -3, -4, -5, -6
 BRIK_EVALID = -7
 BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT = 1, 2
-BRIK_GEMV_VARIANTS = 9
+BRIK_GEMV_VARIANTS = 11
 BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES = 3, 23
 BRIK_OPT_PLAN_STAGE, BRIK_OPT_PLAN_SETS, BRIK_OPT_SPLITK, BRIK_OPT_GEMV_BLOCKS = 4, 5, 6, 7
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2

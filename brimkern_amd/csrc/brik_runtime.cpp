@@ -61,7 +61,7 @@ struct GemvVariant {
 };
 constexpr GemvVariant kGemvVariants[] = {{16, 2, 1, 2}, {16, 2, 1, 3}, {16, 2, 1, 4}, {16, 4, 1, 2},
                                          {16, 2, 2, 2}, {32, 2, 1, 3}, {64, 1, 1, 3}, {16, 2, 5, 2},
-                                         {16, 1, 5, 2}};
+                                         {16, 1, 5, 2}, {16, 1, 2, 2}, {32, 1, 1, 2}};
 constexpr int kNumGemvVariants = sizeof(kGemvVariants) / sizeof(kGemvVariants[0]);
 const char* const kFmtNames[3] = {"q8", "q4", "q3"};
 // GLU pair kernels brik_gemvp_<fmt>_t16_r2_u1_d2_n512 (q4, q3): 512-thread blocks of 32 teams of 16
@@ -615,9 +615,9 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
 // variant 8 (q 4.37, gate 6.40 against 5.25 / 7.10 for the next best; q8 gate 9.01, q3 gate 6.63);
 // fewer rows the 4-row blocks of variant 6, 64 lanes per row (k/v 3.46 against 4.07; wo K = 4096 5.05
 // against 5.51; q8 k/v 3.44; q3 k/v 3.76); rows of K >= 8192 the 32-lane teams of variant 5 (down
-// 8.52 against 8.99 with variant 6 and 9.74 with variant 8); short q8 rows (K <= 1024, the cfg 1 FFN
-// shape K = 896: 28 groups) two groups per lane step, variant 4, which covers a row in one step (4.15
-// against 4.37).
+// 8.52 against 8.99 with variant 6 and 9.74 with variant 8); q8 rows of K <= 1024 (the cfg 1 FFN shape
+// K = 896: 28 groups, one step of 32 lanes) and q8 launches of 4096 rows or more the 8-row blocks of
+// variant 10 (cfg 1 3.95 us against 4.13 with the 32-row blocks of variant 4; gate 8.13 against 8.99).
 // Plans: large ones (the 36-layer set: 98k rows) stream whole rows per step with variant 7 (16 lanes x
 // 5 groups = a K = 2560 row, 2 rows per team); the consumer of a GLU pair, which copies its image and
 // so has no staging to amortize, takes the 4-row blocks of variant 6 (Qwen3-4B down, K = 9728: 640
@@ -633,9 +633,10 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged, bool sing
     if (staged && !single) return 6;
     if (staged && f == F_Q3) return 7;
     if (single && rows < 96L * 256) {
-        if (f == F_Q8 && kmin <= 1024 && rows < 32L * 256) return 4;
+        if (f == F_Q8 && kmin <= 1024 && rows < 32L * 256) return 10;
         if (kmin >= 8192) return 5;
-        return rows >= 4096 ? 8 : 6;
+        if (rows < 4096) return 6;
+        return f == F_Q8 ? 10 : 8;
     }
     if (f == F_Q4) {
         if (rows >= 96L * 256) return 7;

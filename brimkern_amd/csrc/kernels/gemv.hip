@@ -696,7 +696,9 @@ __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const 
     BRIK_GEMV(FMTN, FMT, 32, 2, 1, 3) \
     BRIK_GEMV(FMTN, FMT, 64, 1, 1, 3) \
     BRIK_GEMV(FMTN, FMT, 16, 2, 5, 2) \
-    BRIK_GEMV(FMTN, FMT, 16, 1, 5, 2)
+    BRIK_GEMV(FMTN, FMT, 16, 1, 5, 2) \
+    BRIK_GEMV(FMTN, FMT, 16, 1, 2, 2) \
+    BRIK_GEMV(FMTN, FMT, 32, 1, 1, 2)
 
 BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)

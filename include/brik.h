@@ -344,7 +344,7 @@ int brik_timer_end(brik_ctx *ctx, float *ms);
 /* Kernel-selection overrides, for tests and tuning sweeps (0 restores automatic choice). */
 #define BRIK_OPT_PATH 1        /* 0 auto, 1 force GEMV (any M), 2 force MFMA GEMM (any M) */
 #define BRIK_OPT_GEMV_VARIANT 2  /* 0 auto, else 1 + index of a GEMV tiling variant (see brik_runtime.cpp) */
-#define BRIK_GEMV_VARIANTS 9
+#define BRIK_GEMV_VARIANTS 11
 #define BRIK_OPT_GEMM_TILE 3     /* 0 auto, else 1 + index of an MFMA GEMM block tile (rows x columns):
                                     1 128x256, 2 128x128, 3 128x384, 4 64x256, 5 64x128, 6 64x384,
                                     7 32x256, 8 32x128, 9 32x384, 10 96x256, 11 96x128, 12 96x384
