@@ -119,6 +119,37 @@ def time_loop_min(ctx, fn, steps, warmup, min_ms=MIN_TIMED_MS):
     return ms
 
 
+def time_graph(ctx, fn, count, min_calls=256, min_ms=MIN_TIMED_MS):
+    """fn(i), i = 0 .. n-1 (n >= count, so every weight copy appears), recorded into one graph and
+    replayed until at least min_ms of GPU time; returns ms per call. This is the GPU-side rate of
+    back-to-back launches, as a decode step recorded once and replayed issues them (the reference
+    records a layer's matmuls into one command encoder); a Python loop of calls is bound by the host
+    for launches this short."""
+    n = max(count, min_calls)
+    fn(0)
+    ctx.sync()              # workspaces at their size before the capture (which refuses growth)
+    ctx.graph_begin()
+    for i in range(n):
+        fn(i)
+    g = ctx.graph_end()
+    try:
+        g.launch()
+        ctx.sync()
+        ctx.timer_begin()
+        g.launch()
+        one = ctx.timer_end()
+        reps = max(2, int(math.ceil(min_ms / max(one, 1e-3))))
+        ctx.sync()
+        ctx.timer_begin()
+        for _ in range(reps):
+            g.launch()
+        ms = ctx.timer_end()
+        ctx.sync()
+    finally:
+        g.destroy()
+    return ms / (reps * n)
+
+
 def settle(ctx, fn, seconds):
     """Run ``fn`` untimed until ``seconds`` of wall time have passed (GPU clocks reach steady state)."""
     if seconds <= 0:
@@ -132,12 +163,20 @@ def settle(ctx, fn, seconds):
         ctx.sync()
 
 
+HEAD_X_SEED = {2560: 101, 9728: 102}     # the headline's activation rows by K (shared with cpu_baseline)
+
+
+def head_x(K):
+    from brimkern_amd import synth
+    return synth.normal(HEAD_X_SEED[K], K)
+
+
 def build_layer_plan(ctx, layers):
     """One grouped GEMV plan over ``layers`` distinct copies of the Qwen3-4B q4 layer set."""
     from brimkern_amd import synth
     reps, jobs, nbytes = {}, [], 0
-    xa = ctx.upload(synth.normal(101, 2560))
-    xd = ctx.upload(synth.normal(102, 9728))
+    xa = ctx.upload(head_x(2560))
+    xd = ctx.upload(head_x(9728))
     ybuf = ctx.alloc(4 * layers * sum(n for _, _, n in QWEN3_4B))
     yo = 0
     for si, (name, K, N) in enumerate(QWEN3_4B):
@@ -158,6 +197,8 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
     reps, xa, xd, ybuf, nbytes = b["reps"], b["xa"], b["xd"], b["ybuf"], b["nbytes"]
     settle(ctx, lambda i: plan.run(), settle_s)
     ms = time_loop(ctx, lambda i: plan.run(), steps, warmup)
+    # the last timed step's outputs: all 216 matrices, checked against the CPU reference later
+    y_head = ctx.download(ybuf, np.float32, ybuf.nbytes // 4)
     plan.destroy()
     # per-shape single launches and small-M calls, each rotating over distinct weight copies totalling
     # at least twice the 256 MB last-level cache (so every call streams its weights from HBM)
@@ -173,22 +214,12 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
         def one(i, M=1, r=extra, yb=yb, K=K, N=N, count=count):
             nib, sc, mn = r.planes(i % count)
             ctx.matmul_t_q4(x if M == 1 else xm, nib, sc, mn, yb, M, K, N)
-        lms = time_loop_min(ctx, one, max(4 * layers, count), count)
-        b = tb + 4 * K + 4 * N
-        single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(b / (lms * 1e-3) / 1e9, 1),
-                                       "copies": count}
-        for M in SMALL_M:
-            row = {}
-            for label, path, sk in (("auto", PATH_AUTO, 0), ("gemv", PATH_GEMV, 0), ("tiled", PATH_GEMM, 1),
-                                    ("splitk", PATH_GEMM, 2)):
-                ctx.set_option(BRIK_OPT_PATH, path)
-                ctx.set_option(BRIK_OPT_SPLITK, sk)
-                ms_m = time_loop_min(ctx, lambda i, M=M: one(i, M), count, count // 4)
-                row[label + "_us"] = round(ms_m * 1e3, 2)
-            ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
-            ctx.set_option(BRIK_OPT_SPLITK, 0)
-            row["weight_GBps"] = round(tb / (row["auto_us"] * 1e-6) / 1e9, 1)
-            small_m.setdefault(f"M{M}", {})[f"{name}_K{K}_N{N}"] = row
+        lms = time_graph(ctx, one, count)
+        ems = time_loop_min(ctx, one, max(4 * layers, count), count)
+        bb = tb + 4 * K + 4 * N
+        single[f"{name}_K{K}_N{N}"] = {"us": round(lms * 1e3, 2), "GBps": round(bb / (lms * 1e-3) / 1e9, 1),
+                                       "eager_us": round(ems * 1e3, 2), "copies": count}
+        small_m_rows(ctx, small_m, f"{name}_K{K}_N{N}", tb, count, one)
         if extra is not reps[name]:
             ctx.free(extra.buf)
         ctx.free(xm)
@@ -197,7 +228,49 @@ def gemv_layer_set(ctx, steps, warmup, layers, settle_s, graph_replay=True):
     for r in reps.values():
         ctx.free(r.buf)
     ctx.free(ybuf)
-    return ms, nbytes, single, fused, small_m
+    return ms, nbytes, single, fused, small_m, y_head
+
+
+def small_m_rows(ctx, small_m, key, tb, count, one):
+    """``one(i, M)`` at M in SMALL_M on each path (auto, GEMV, tiled, split-K), graph-replayed."""
+    for M in SMALL_M:
+        row = {}
+        for label, path, sk in (("auto", PATH_AUTO, 0), ("gemv", PATH_GEMV, 0), ("tiled", PATH_GEMM, 1),
+                                ("splitk", PATH_GEMM, 2)):
+            ctx.set_option(BRIK_OPT_PATH, path)
+            ctx.set_option(BRIK_OPT_SPLITK, sk)
+            try:
+                ms_m = time_graph(ctx, lambda i, M=M: one(i, M), count, min_calls=64)
+            finally:
+                ctx.set_option(BRIK_OPT_PATH, PATH_AUTO)
+                ctx.set_option(BRIK_OPT_SPLITK, 0)
+            row[label + "_us"] = round(ms_m * 1e3, 2)
+        row["weight_GBps"] = round(tb / (row["auto_us"] * 1e-6) / 1e9, 1)
+        small_m.setdefault(f"M{M}", {})[key] = row
+
+
+def small_m_formats(ctx):
+    """The few-row lines for q8 and q3 weights at three Qwen3-4B shapes (k/v, gate, down), graph-replayed."""
+    from brimkern_amd import synth
+    out = {}
+    for fmt in ("q8", "q3"):
+        rows = {}
+        for name, K, N in (("k", 2560, 1024), ("gate", 2560, 9728), ("down", 9728, 2560)):
+            t = synth.tensor(fmt, 250, N, K)
+            tb = q_bytes(fmt, N, K)
+            count = max(2, -(-ROTATE_BYTES // tb))
+            r = Replicas(ctx, fmt, t, count)
+            xm = ctx.upload(synth_rows(K, max(SMALL_M)))
+            yb = ctx.alloc(4 * N * max(SMALL_M))
+            fn = {"q8": ctx.matmul_t_q8, "q3": ctx.matmul_t_q3}[fmt]
+
+            def one(i, M, r=r, xm=xm, yb=yb, K=K, N=N, count=count, fn=fn):
+                fn(xm, *r.planes(i % count), yb, M, K, N)
+            small_m_rows(ctx, rows, f"{name}_K{K}_N{N}", tb, count, one)
+            for bb in (r.buf, xm, yb):
+                ctx.free(bb)
+        out[fmt] = rows
+    return out
 
 
 def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
@@ -265,12 +338,15 @@ def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
     x = ctx.upload(synth.normal(seed + 1, K))
     y = ctx.alloc(4 * N)
     fn = {"q8": ctx.matmul_t_q8, "q4": ctx.matmul_t_q4, "q3": ctx.matmul_t_q3}[fmt]
-    ms = time_loop_min(ctx, lambda i: fn(x, *r.planes(i % copies), y, 1, K, N), max(steps, copies), copies)
+    call = lambda i: fn(x, *r.planes(i % copies), y, 1, K, N)   # noqa: E731
+    ms = time_graph(ctx, call, copies)
+    ems = time_loop_min(ctx, call, max(steps, copies), copies)
     b = tb + 4 * K + 4 * N
     for bb in (r.buf, x, y):
         ctx.free(bb)
     return {"us": round(ms * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
-            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+            "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "eager_us": round(ems * 1e3, 2),
+            "copies": copies, "timing": "graph-replayed back-to-back calls (eager_us: a Python loop of calls)"}
 
 
 def lm_head_topk_cfg3(ctx, steps, warmup, gemv_us, cache_bytes=768 << 20):
@@ -446,36 +522,59 @@ def cpu_model():
 
 def cpu_baseline(target_s=15.0):
     """JS restatement of the reference CPU matmul (oracle/cpuref.js) on one Qwen3-4B q4 layer set (M=1),
-    single-threaded under node. A first pass times the layer set once; the sample then repeats each
-    matrix so the whole sample takes about ``target_s`` seconds, and the value is the mean rate."""
+    single-threaded under node, on the headline's own inputs (the same weight tensors and activation
+    rows). A first pass times the layer set once and keeps its outputs; the sample then repeats each
+    matrix so the whole sample takes about ``target_s`` seconds, and the value is the mean rate.
+    Returns (the cpu_baseline object, the reference outputs by shape name) or (None, None)."""
     node = shutil.which("node")
     if node is None:
-        return None
+        return None, None
     from brimkern_amd import synth, layout
+    refs = {}
 
     def run(reps):
         total_ms, nbytes = 0.0, 0
         with tempfile.TemporaryDirectory() as d:
             for si, (name, K, N) in enumerate(QWEN3_4B):
                 t = synth.q4_tensor(200 + si, N, K)
-                x = synth.normal(500 + si, K)
                 inp, out = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
                 with open(inp, "wb") as f:
-                    f.write(x.tobytes())
+                    f.write(head_x(K).tobytes())
                     f.write(layout.pack("q4", t).tobytes())
                 res = json.loads(subprocess.check_output([node, os.path.join(ROOT, "oracle", "cpuref.js"), "q4", "1",
                                                           str(K), str(N), inp, out, str(reps)]))
                 total_ms += res["total_ms"]
                 nbytes += reps * (q_bytes("q4", N, K) + 4 * K + 4 * N)
+                if name not in refs:
+                    refs[name] = np.fromfile(out, np.float32, N)
         return total_ms, nbytes
 
     t1, _ = run(1)
     reps = max(1, min(200, int(round(target_s * 1e3 / max(t1, 1.0)))))
     total_ms, nbytes = run(reps)
-    return {"value": round(nbytes / (total_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"one Qwen3-4B q4 layer set (6 matrices, M=1, {nbytes / reps / 1e6:.1f} MB) x {reps} passes, "
-                      f"{total_ms / 1e3:.1f} s, node {subprocess.check_output([node, '--version']).decode().strip()} "
-                      f"single-threaded, {cpu_model()}"}
+    return ({"value": round(nbytes / (total_ms * 1e-3) / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+             "sample": f"one Qwen3-4B q4 layer set (6 matrices, M=1, {nbytes / reps / 1e6:.1f} MB) x {reps} passes, "
+                       f"{total_ms / 1e3:.1f} s, node {subprocess.check_output([node, '--version']).decode().strip()} "
+                       f"single-threaded, {cpu_model()}; the headline's inputs"}, refs)
+
+
+def verify_headline(y_head, refs, layers, tol=1e-5):
+    """The headline's last timed step against the CPU reference's outputs on the same inputs: every
+    layer's copy of each of the six matrices (all 216 outputs, every row), normwise relative error
+    max|y - r| / max|r|. The layer copies hold the same weights, so one reference per shape serves all."""
+    if refs is None:
+        return {"verified": None, "note": "node absent: no CPU reference outputs"}
+    worst, where, off = 0.0, None, 0
+    for l in range(layers):
+        for name, K, N in QWEN3_4B:
+            y, r = y_head[off:off + N], refs[name]
+            err = float(np.max(np.abs(y.astype(np.float64) - r)) / max(np.max(np.abs(r)), 1e-30))
+            if not np.isfinite(err) or err > worst:
+                worst, where = err if np.isfinite(err) else float("inf"), f"layer {l} {name}"
+            off += N
+    return {"verified": bool(worst <= tol), "max_normwise_rel": worst, "worst": where, "tol": tol,
+            "outputs": layers * len(QWEN3_4B),
+            "against": "oracle/cpuref.js (the cpu_baseline run) on the same weights and x"}
 
 
 # ---- HBM traffic of the dominant kernel (two rocprofv3 counter passes in child processes) ---------
@@ -666,15 +765,17 @@ def main():
     from brimkern_amd import Context
     ctx = Context(0)
     log("bench: q4 GEMV layer set")
-    ms, nbytes, single, fused, small_m = gemv_layer_set(ctx, args.steps, args.warmup, args.layers, args.settle,
-                                                        not args.no_graph)
+    ms, nbytes, single, fused, small_m, y_head = gemv_layer_set(ctx, args.steps, args.warmup, args.layers,
+                                                                args.settle, not args.no_graph)
     value = nbytes / (ms * 1e-3) / 1e9
     extra = {"per_matrix_single_launch": single, "f3_decode_layers_fused_qwen3_4b": fused,
              "small_m_qwen3_4b": dict(small_m, note="matmul_t_q4 at M rows per call (the reference's "
                                       "matmul_t_q4_tiled range 2 <= M < 16): the routed path (auto), the GEMV "
-                                      "re-streaming W per row, the tiled MFMA GEMM and the split-K MFMA GEMM; "
-                                      "weight_GBps = W bytes (read once) / auto time")}
+                                      "re-streaming W per row, the tiled MFMA GEMM and the split-K MFMA GEMM, "
+                                      "graph-replayed; weight_GBps = W bytes (read once) / auto time")}
     if not args.no_extra:
+        log("bench: q8 / q3 small-M")
+        extra["small_m_q8_q3_qwen3_4b"] = small_m_formats(ctx)
         log("bench: cfg1 q8 GEMV")
         extra["cfg1_q8_gemv_K896_N4864"] = gemv_single_cfg(ctx, "q8", 896, 4864, 600, args.steps, args.warmup)
         log("bench: cfg3 q3 LM head")
@@ -692,13 +793,18 @@ def main():
         extra["f4_matmul_t_f16w_K2560_N9728"] = f16w_f4(ctx, args.steps, args.warmup)
         log("bench: F1 encoders")
         extra["f1_quantize_f32_to_planes_N9728_K2560"] = quantize_f1(ctx, args.steps, args.warmup)
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu, refs = (None, None) if args.no_cpu else cpu_baseline()
+    check = verify_headline(y_head, refs, args.layers) if not args.no_cpu else {"verified": None,
+                                                                               "note": "--no-cpu"}
     line = {
         "metric": "q4 GEMV HBM GB/s (% of peak) at Qwen3-4B shapes; prefill q4 GEMM TFLOP/s",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "settle_s": args.settle, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic (seeded SplitMix64), random q4 weights of the Qwen3-4B shapes",
+        "dtype": "f32", "x_staging": "per 32-element group as 24-bit block floating point (exact int32 dot "
+                                     "products with the codes, one f32 rescale per group), f32 accumulation",
+        "data": "synthetic (seeded SplitMix64), random q4 weights of the Qwen3-4B shapes",
+        "verified": check.get("verified"), "verification": check,
         "config": {"workload": f"matmul_t_q4 decode GEMV, Qwen3-4B layer set x {args.layers} layers "
                                f"(216 matrices, M=1), grouped plan: one staging + one GEMV launch per step",
                    "bytes_per_step": nbytes, "layers": args.layers},

@@ -405,16 +405,19 @@ int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*&
     return BRIK_OK;
 }
 
-// M >= 2 (dense): the cheapest of three paths by a cost model fitted on the Qwen3-4B q4 shapes at
-// M = 2..64 (us per call, launches included):
+// M >= 2 (dense): the cheapest of three paths by a cost model fitted per format on the Qwen3-4B shapes
+// (k/v, gate, down for q8 and q3; all six for q4) at M = 2, 4, 8, 15, each path timed as graph-replayed
+// back-to-back calls (us per call, launches included; W bytes = the packed planes):
 // GEMV (grid.y = M: every activation row streams W again, rows after the first mostly from the 256 MB
-// last-level cache): 5 + M * W bytes / 7.5 TB/s (q3: 4.5, bound by its unpacking).
-// Tiled GEMM: 5 + max(0.65 us per 128-deep K step, which is what its few-row tiles spend in issue
-// latency on one wave per SIMD, 2MNK at 1 PFLOP/s).
-// Split-K (few rows, below): ~9 us of launches (x staging, the kernel, the slice sum), 0.15 us per K step,
-// W at about 2.5 TB/s and 0.15 us per row, fitted on the same shapes at M = 2..64; it beats the tiled GEMM
-// at every such point (e.g. M = 32, K = 9728, N = 2560: 30 us against 94), and the GEMV for M >= 8-16
-// except on small matrices (N = 1024 up to M ~ 32). The tiled GEMM keeps M > 64.
+// last-level cache): 3.5 + M (0.35 min(1, N / 1024) + W bytes / (7.8 TB/s q4, 6.0 q8 / q3)); the
+// per-row latency term is that of rows whose blocks fill the chip (N >= 1024), smaller rows overlap.
+// Tiled GEMM: 5 + max(c per 128-deep K step, which is what its few-row tiles spend in issue latency on
+// one wave per SIMD (c = 0.70 us q4, 0.83 q8, 0.86 q3), 2MNK at 1 PFLOP/s).
+// Split-K (few rows, below): 7.7 us of launches (x staging, the kernel, the slice sum), 0.15 us per K step,
+// W at 3.4 TB/s (q4), 4.8 (q8), 2.4 (q3; its unpacking), 0.15 us per row.
+// Over the 66 measured points the choice costs 0.9 us in total against the fastest path (the q4-only fit
+// it replaces, which took the tiled GEMM for q8 / q3 gate shapes at M = 4-15: 38.8 us). M = 32,
+// K = 9728, N = 2560: split-K 30 us against 94 tiled (eager timing). The tiled GEMM keeps M > 64.
 enum SmallMPath { SM_GEMV, SM_SPLITK, SM_TILED };
 constexpr long kSplitKMaxRows = 64;
 
@@ -424,9 +427,12 @@ SmallMPath small_m_path(Fmt f, long M, long K, long N)
     const double wbytes = f == F_Q4 ? nk * (0.5 + 4.0 / kGroup) : f == F_Q8 ? nk * (1.0 + 2.0 / kGroup)
                                                                             : nk * (0.375 + 4.0 / kGroup);
     const double steps = (double)((K + 2 * 128 - 1) / (2 * 128) * 2);
-    const double gemv_us = 5.0 + (double)M * wbytes / (f == F_Q3 ? 4.5e6 : 7.5e6);
-    const double tiled_us = 5.0 + std::max(0.65 * steps, 2.0 * M * nk / 1e9);
-    const double sk_us = M <= kSplitKMaxRows ? 9.0 + 0.15 * steps + wbytes / 2.5e6 + 0.15 * M : 1e30;
+    const double gemv_bw = f == F_Q4 ? 7.8e6 : 6.0e6;                   // bytes per us
+    const double tiled_step = f == F_Q4 ? 0.70 : f == F_Q8 ? 0.83 : 0.86;
+    const double sk_bw = f == F_Q4 ? 3.4e6 : f == F_Q8 ? 4.8e6 : 2.4e6;
+    const double gemv_us = 3.5 + (double)M * (0.35 * std::min(1.0, N / 1024.0) + wbytes / gemv_bw);
+    const double tiled_us = 5.0 + std::max(tiled_step * steps, 2.0 * M * nk / 1e9);
+    const double sk_us = M <= kSplitKMaxRows ? 7.7 + 0.15 * steps + wbytes / sk_bw + 0.15 * M : 1e30;
     if (gemv_us <= sk_us && gemv_us <= tiled_us) return SM_GEMV;
     return sk_us <= tiled_us ? SM_SPLITK : SM_TILED;
 }
