@@ -3,10 +3,15 @@
 The multiply loop issues its LDS reads as inline asm (gemm.hip: ds_read_b128 / ds_read_u16, then
 lds_wait and tie), so the compiler does not know that their destination registers are written
 asynchronously. Correctness then rests on register allocation: no instruction may read or write a
-destination register of such a read before the next `s_waitcnt lgkmcnt(0)`. This script disassembles the
-built code object (llvm-objdump, our own build) and checks that, scanning each kernel's instructions in
-address order across branches (conservative: a wait reached on any path ends the window only when it is
-also the next wait in address order).
+destination register of such a read before an `s_waitcnt lgkmcnt(0)` has retired it.
+
+This script disassembles the built code object (llvm-objdump, our own build) and checks exactly that
+on every path through each checked kernel: it builds the kernel's control-flow graph from the branch
+instructions (targets from their 16-bit word offsets; a conditional branch also falls through, an
+unconditional one and s_endpgm do not) and propagates the set of registers still pending from an
+asm LDS read forward to a fixed point, the union over all predecessors, so a read issued at the bottom
+of a loop is still pending at the loop's head on the back edge. An instruction that touches a pending
+register is reported.
 
 Usage: python -m brimkern_amd.check_lds_reads <code object>   (exit status 1 on a violation)
 """
@@ -36,41 +41,101 @@ def _checked(fn: str) -> bool:
     return fn.startswith(("brik_gemm_", "brik_gemmg_")) and not fn.startswith(("brik_gemm_sk_", "brik_gemm_f16w"))
 
 
-def check(disasm: str) -> list:
-    """Violations in `disasm` (llvm-objdump -d text) of the kernels _checked selects."""
-    out = []
-    fn = None
-    pending = {}
+def _kernels(disasm: str) -> dict:
+    """{kernel: [(address or None, instruction text)]} from llvm-objdump -d output (the address is the
+    one in the trailing comment)."""
+    out, fn = {}, None
     for raw in disasm.split("\n"):
         m = re.match(r"^[0-9a-f]+ <([^>]+)>:", raw)
         if m:
-            fn, pending = m.group(1), {}
+            fn = m.group(1)
+            out[fn] = []
             continue
-        if fn is None or not _checked(fn):
+        if fn is None:
             continue
         line = raw.split("//")[0].strip()
         if not line:
             continue
-        if line.startswith("s_waitcnt") and "lgkmcnt(0)" in line:
-            pending = {}
+        am = re.search(r"//\s*([0-9A-Fa-f]+):", raw)
+        out[fn].append((int(am.group(1), 16) if am else None, line))
+    return out
+
+
+def _successors(code: list) -> list:
+    """Successor indices of every instruction (branch targets from the SOPP word offset)."""
+    at = {a: i for i, (a, _) in enumerate(code) if a is not None}
+    succ = []
+    for i, (a, line) in enumerate(code):
+        op = line.split(None, 1)[0]
+        nxt = [i + 1] if i + 1 < len(code) else []
+        if op == "s_endpgm":
+            succ.append([])
             continue
+        if op == "s_branch" or op.startswith("s_cbranch"):
+            tgt = None
+            m = re.match(r"\S+\s+(-?\d+)", line)
+            if m and a is not None:
+                off = int(m.group(1))
+                off = off - 65536 if off >= 32768 else off
+                tgt = at.get(a + 4 + 4 * off)
+            if op == "s_branch":
+                succ.append([tgt] if tgt is not None else nxt)
+            else:
+                succ.append(nxt + ([tgt] if tgt is not None else []))
+            continue
+        succ.append(nxt)
+    return succ
+
+
+def _check_kernel(fn: str, code: list) -> list:
+    n = len(code)
+    succ = _successors(code)
+    parsed = []
+    for _, line in code:
         parts = line.split(None, 1)
         ops = [o.strip().split()[0] for o in parts[1].split(",") if o.strip()] if len(parts) > 1 else []
         used = set()
         for o in ops:
             used |= _regs(o)
-        hit = used & set(pending)
-        if hit and not parts[0].startswith("ds_read"):
-            out.append(f"{fn}: '{line}' touches v{sorted(hit)} before the LDS read that writes it has been waited for")
-        if parts[0] in ASM_READS and ops:
-            for r in _regs(ops[0]):
-                pending[r] = line
+        clears = parts[0] == "s_waitcnt" and "lgkmcnt(0)" in line
+        writes = _regs(ops[0]) if parts[0] in ASM_READS and ops else set()
+        parsed.append((parts[0], used, clears, writes))
+    pend_in = [None] * n                       # pending registers at entry (None: not reached yet)
+    pend_in[0] = frozenset() if n else None
+    work = [0] if n else []
+    while work:
+        i = work.pop()
+        op, used, clears, writes = parsed[i]
+        out = frozenset() if clears else (pend_in[i] | writes)
+        for j in succ[i]:
+            new = out if pend_in[j] is None else pend_in[j] | out
+            if new != pend_in[j]:
+                pend_in[j] = new
+                work.append(j)
+    bad = []
+    for i, (op, used, clears, writes) in enumerate(parsed):
+        if pend_in[i] is None or op.startswith("ds_read"):
+            continue
+        hit = used & pend_in[i]
+        if hit:
+            bad.append(f"{fn}: '{code[i][1]}' touches v{sorted(hit)} before the LDS read that writes it has "
+                       f"been waited for")
+    return bad
+
+
+def check(disasm: str) -> list:
+    """Violations in `disasm` (llvm-objdump -d text) of the kernels _checked selects."""
+    out = []
+    for fn, code in _kernels(disasm).items():
+        if _checked(fn):
+            out += _check_kernel(fn, code)
     return out
 
 
 def check_file(path: str) -> list:
     if not os.path.exists(OBJDUMP):
-        return []
+        raise RuntimeError(f"{OBJDUMP} is missing: the LDS-read register check of the GEMM kernels cannot run "
+                           "(set ROCM_PATH to a ROCm install with llvm-objdump)")
     text = subprocess.run([OBJDUMP, "-d", "--mcpu=gfx950", path], capture_output=True, text=True,
                           check=True).stdout
     return check(text)

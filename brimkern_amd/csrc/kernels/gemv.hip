@@ -20,8 +20,11 @@
 //     the pattern HBM serves fastest;
 //   * each lane reads a group's x limbs from LDS once and applies them to its R rows;
 //   * software pipeline: a lane's work is a sequence of steps of U groups x R rows; the loads of
-//     step i + 1 are issued before step i is consumed, and the first step's loads before x is staged;
-//   * team partial sums are reduced with cross-lane shuffles; lane 0 writes y.
+//     step i + D - 1 are issued before step i is consumed, and the first D - 1 steps' loads right after
+//     the loads of x, so staging x overlaps their latency;
+//   * each lane stores its running partial sum of a row to LDS every step (branch-free loop body); after
+//     the loop, the TEAM partials of a row are loaded by TEAM lanes at once and added with DPP steps
+//     (row_sums), and the row's first lane writes y.
 #include "common.h"
 #include "xprep.h"
 #include "stage_abi.h"

@@ -49,6 +49,26 @@ def componentwise_ok(y, r, absden, tol=REL_TOL):
     return bool(np.all(np.abs(y - r) <= tol * d + 1e-30))
 
 
+def moe_oracle_abs(x, row_off, t, E, K, N):
+    """The expert-grouped q4 reference (per expert, the reference matmul of its rows and its [N, K]
+    planes, as oracle.moe_matmul_t_q4 computes it) with the componentwise denominator sum |x w| of every
+    output: (y [R, N], den [R, N])."""
+    import oracle as O
+    x = np.asarray(x, np.float32).reshape(-1, K)
+    R = int(row_off[E])
+    y = np.zeros((R, N), np.float32)
+    den = np.zeros((R, N), np.float64)
+    gq = N * K // 32
+    for e in range(E):
+        a, b = int(row_off[e]), int(row_off[e + 1])
+        if b == a:
+            continue
+        ye, de = O.matmul_t_q4(np.ascontiguousarray(x[a:b]), t["nib"][e * N * K // 2:(e + 1) * N * K // 2],
+                               t["sc"][e * gq:(e + 1) * gq], t["mn"][e * gq:(e + 1) * gq], b - a, K, N, absden=True)
+        y[a:b], den[a:b] = ye, de
+    return y, den
+
+
 class Gpu:
     """Upload planes / run the C-ABI matmuls on one context."""
 

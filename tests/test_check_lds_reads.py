@@ -43,3 +43,47 @@ def test_window_spans_branches_and_other_kernels_are_skipped():
     ])
     bad = check(text)
     assert len(bad) == 1 and bad[0].startswith("brik_gemm_q8_64x1")
+
+
+def at(lines, base=0x1000):
+    """Instructions 4 bytes apart (branch offsets count 4-byte words from the next instruction)."""
+    return "".join(f"\t{l}  // {base + 4 * i:012X}: 00000000\n" for i, l in enumerate(lines))
+
+
+def test_loop_back_edge_is_followed():
+    """A read at the bottom of a loop whose register is used at the loop head, reached only by the back
+    edge (address order alone never sees the use after the read)."""
+    text = HEAD.format("brik_gemm_q4_64x1") + at([
+        "v_add_u32_e32 v20, v7, v3",              # 0x1000: loop head, uses v7
+        "ds_read_b128 v[6:9], v1",                # 0x1004
+        "s_cbranch_scc1 65533",                   # 0x1008: -3 words -> 0x1000
+        "s_waitcnt lgkmcnt(0)",                   # 0x100c
+        "s_endpgm",
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and "v[7]" in bad[0] and "v_add_u32" in bad[0]
+
+
+def test_wait_on_every_path_is_clean():
+    text = HEAD.format("brik_gemm_q4_64x1") + at([
+        "s_waitcnt lgkmcnt(0)",                   # 0x1000: loop head waits first
+        "v_add_u32_e32 v20, v7, v3",
+        "ds_read_b128 v[6:9], v1",
+        "s_cbranch_scc1 65532",                   # 0x100c: -4 words -> 0x1000
+        "s_waitcnt lgkmcnt(0)",
+        "v_mov_b32_e32 v7, 0",
+        "s_endpgm",
+    ])
+    assert check(text) == []
+
+
+def test_unconditional_branch_skips_fallthrough():
+    text = HEAD.format("brik_gemm_q4_64x1") + at([
+        "ds_read_b128 v[6:9], v1",                # 0x1000
+        "s_branch 1",                             # 0x1004: +1 word -> 0x100c
+        "v_mov_b32_e32 v7, 0",                    # 0x1008: never reached
+        "s_waitcnt lgkmcnt(0)",                   # 0x100c
+        "v_mov_b32_e32 v7, 0",
+        "s_endpgm",
+    ])
+    assert check(text) == []

@@ -10,7 +10,7 @@ import pytest
 import oracle as O
 from brimkern_amd import synth
 from brimkern_amd.capi import BrikError, BRIK_OPT_GEMM_TILE, BRIK_OPT_SPLITK, BRIK_GEMM_TILES
-from helpers import Gpu, normwise_rel, REL_TOL
+from helpers import Gpu, componentwise_ok, moe_oracle_abs, normwise_rel, REL_TOL
 
 pytestmark = pytest.mark.gpu
 
@@ -55,7 +55,10 @@ def test_x2_benchmark_layer(gpu):
     assert same_bits(ya, sa) and same_bits(yb, sb)
     for y, t in ((ya, ta), (yb, tb)):
         r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, H, F)
+        ra, den = moe_oracle_abs(x, row_off, t, E, H, F)
+        assert np.array_equal(ra, r)
         assert normwise_rel(y, r) <= REL_TOL
+        assert componentwise_ok(y, r, den), "componentwise bound violated"
 
 
 @pytest.mark.parametrize("tile", range(0, BRIK_GEMM_TILES + 1))
@@ -69,8 +72,10 @@ def test_x2_every_tile(gpu, tile):
     gpu.ctx.set_option(BRIK_OPT_GEMM_TILE, tile)
     (ya, yb), (sa, sb) = run_pair(gpu, x, row_off, ta, tb, E, K, N)
     assert same_bits(ya, sa) and same_bits(yb, sb)
-    r = O.moe_matmul_t_q4(x, row_off, tb["nib"], tb["sc"], tb["mn"], E, K, N)
-    assert normwise_rel(yb, r) <= REL_TOL
+    for y, t in ((ya, ta), (yb, tb)):
+        r, den = moe_oracle_abs(x, row_off, t, E, K, N)
+        assert normwise_rel(y, r) <= REL_TOL
+        assert componentwise_ok(y, r, den), "componentwise bound violated"
 
 
 def test_x2_forced_splitk(gpu):
@@ -83,8 +88,10 @@ def test_x2_forced_splitk(gpu):
     gpu.ctx.set_option(BRIK_OPT_SPLITK, 2)
     (ya, yb), (sa, sb) = run_pair(gpu, x, row_off, ta, tb, E, K, N)
     assert same_bits(ya, sa) and same_bits(yb, sb)
-    r = O.moe_matmul_t_q4(x, row_off, ta["nib"], ta["sc"], ta["mn"], E, K, N)
-    assert normwise_rel(ya, r) <= REL_TOL
+    for y, t in ((ya, ta), (yb, tb)):
+        r, den = moe_oracle_abs(x, row_off, t, E, K, N)
+        assert normwise_rel(y, r) <= REL_TOL
+        assert componentwise_ok(y, r, den), "componentwise bound violated"
 
 
 def test_x2_malformed_row_table(gpu):

@@ -12,7 +12,7 @@ import oracle as O
 from brimkern_amd import synth, layout
 from brimkern_amd.capi import (BrikError, BRIK_EINVAL, BRIK_EALIGN, BRIK_OPT_PATH, BRIK_OPT_GEMV_VARIANT,
                                BRIK_GEMV_VARIANTS, BRIK_OPT_GEMM_TILE, BRIK_GEMM_TILES)
-from helpers import Gpu, load_golden, normwise_rel, componentwise_ok, PLANES, REL_TOL
+from helpers import Gpu, load_golden, normwise_rel, componentwise_ok, moe_oracle_abs, PLANES, REL_TOL
 
 pytestmark = pytest.mark.gpu
 GEMV_TOL = 1e-5
@@ -232,7 +232,9 @@ def test_moe_e64(gpu, which):
     gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
     y = gpu.ctx.download(yb, np.float32, R * N)
     r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
-    assert normwise_rel(y, r) <= REL_TOL
+    ra, den = moe_oracle_abs(x, row_off, t, E, K, N)
+    assert np.array_equal(ra, r)
+    check(y, r, den, REL_TOL)
 
 
 @pytest.mark.parametrize("tile", range(0, BRIK_GEMM_TILES + 1))
@@ -250,8 +252,8 @@ def test_moe_every_tile(gpu, tile):
     yb = gpu.up(np.full(R * N, np.nan, np.float32))
     gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, R, K, N)
     y = gpu.ctx.download(yb, np.float32, R * N)
-    r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
-    assert normwise_rel(y, r) <= REL_TOL
+    r, den = moe_oracle_abs(x, row_off, t, E, K, N)
+    check(y, r, den, REL_TOL)
 
 
 @pytest.mark.parametrize("tile", range(0, BRIK_GEMM_TILES + 1))
@@ -266,8 +268,8 @@ def test_moe_empty_experts(gpu, tile):
     yb = gpu.up(np.full(9 * N, np.nan, np.float32))
     gpu.ctx.moe_matmul_t_q4(xb, rb, *planes, yb, E, 9, K, N)
     y = gpu.ctx.download(yb, np.float32, 9 * N)
-    r = O.moe_matmul_t_q4(x, row_off, t["nib"], t["sc"], t["mn"], E, K, N)
-    assert normwise_rel(y, r) <= REL_TOL
+    r, den = moe_oracle_abs(x, row_off, t, E, K, N)
+    check(y, r, den, REL_TOL)
 
 
 # ---- edge cases and error behaviour --------------------------------------------------------

@@ -50,3 +50,21 @@ def test_gated_activations():
         assert np.all(np.diff(pos.astype(np.float64)) >= 0)
     # the up factor multiplies
     np.testing.assert_allclose(O.swiglu(v, 2 * one), 2 * O.swiglu(v, one), rtol=1e-6)
+
+
+def test_gated_activations_against_torch():
+    """SiLU and tanh-GELU against independent implementations (torch, computed in float64): a wrong
+    slope (e.g. sigmoid(2v)), erf-GELU in place of the reference's tanh form, or a wrong cubic
+    coefficient each miss these by far more than the tolerance, which only covers the float32 store."""
+    torch = __import__("pytest").importorskip("torch")
+    v = np.linspace(-12, 12, 4801).astype(np.float32)
+    up = np.random.default_rng(7).standard_normal(v.size).astype(np.float32)
+    tv, tu = torch.from_numpy(v.astype(np.float64)), torch.from_numpy(up.astype(np.float64))
+    silu = (torch.nn.functional.silu(tv) * tu).numpy()
+    gelu = (torch.nn.functional.gelu(tv, approximate="tanh") * tu).numpy()
+    # atol: for v << 0 both evaluate 0.5 v (1 + tanh(u)) with 1 + tanh(u) cancelling to ~1e-16 noise
+    for got, want in ((O.swiglu(v, up), silu), (O.geglu(v, up), gelu)):
+        np.testing.assert_allclose(got.astype(np.float64), want, rtol=2e-7, atol=1e-12)
+    # the two forms the tests above cannot tell apart from the reference's: erf-GELU differs here
+    erf = (torch.nn.functional.gelu(tv, approximate="none") * tu).numpy()
+    assert np.abs(O.geglu(v, up).astype(np.float64) - erf).max() > 1e-4
