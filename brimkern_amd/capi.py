@@ -37,6 +37,7 @@ SIGNATURES = {
     "brik_h2d": (_I, [_P, _P, _P, _Z]),
     "brik_d2h": (_I, [_P, _P, _P, _Z]),
     "brik_d2d": (_I, [_P, _P, _P, _Z]),
+    "brik_h2d_async": (_I, [_P, _P, _P, _Z]),
     "brik_sync": (_I, [_P]),
     "brik_fence_record": (_I, [_P, ctypes.POINTER(_P)]),
     "brik_fence_d2h": (_I, [_P, _P, _P, _Z]),
@@ -79,6 +80,7 @@ SIGNATURES = {
 }
 BRIK_TOPK_MAX = 64
 BRIK_NOALLOC_SCRATCH_BYTES = 16 << 20
+BRIK_STAGING_RING_BYTES = 32 << 20
 
 FMT_CODES = {"q8": 8, "q4": 4, "q3": 3}
 
@@ -218,6 +220,12 @@ class Context:
         a = np.ascontiguousarray(arr)
         self._check(self.lib.brik_h2d(self.handle, _P(int(_addr(dst).value or 0) + dst_offset),
                                       _P(a.ctypes.data), a.nbytes))
+
+    def h2d_async(self, dst, arr: np.ndarray, dst_offset: int = 0):
+        """Upload without waiting for earlier work (brik_h2d_async): ``arr`` may change on return."""
+        a = np.ascontiguousarray(arr)
+        self._check(self.lib.brik_h2d_async(self.handle, _P(int(_addr(dst).value or 0) + dst_offset),
+                                            _P(a.ctypes.data), a.nbytes))
 
     def download(self, src, dtype, count: int, src_offset: int = 0) -> np.ndarray:
         out = np.empty(count, dtype=dtype)

@@ -467,6 +467,21 @@ napi_value H2D(napi_env env, napi_callback_info info)
     return undefined(env);
 }
 
+// h2dAsync(ctx, dstPtr, src): the bytes are staged at once (src may be reused on return) and the copy is
+// enqueued without waiting for earlier work (brik_h2d_async; the reference's queue.writeBuffer)
+napi_value H2DAsync(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 3)) return nullptr;
+    brik_ctx* ctx;
+    void* dst;
+    void* src;
+    size_t len;
+    if (!get_ctx(env, a.v[0], &ctx) || !get_ptr(env, a.v[1], &dst) || !get_bytes(env, a.v[2], &src, &len)) return nullptr;
+    if (check(env, ctx, brik_h2d_async(ctx, dst, src, len))) return nullptr;
+    return undefined(env);
+}
+
 // d2h(ctx, srcPtr, bytes) -> ArrayBuffer
 napi_value D2H(napi_env env, napi_callback_info info)
 {
@@ -888,6 +903,92 @@ napi_value GemvPlanDestroy(napi_env env, napi_callback_info info)
     return undefined(env);
 }
 
+// ---- recorded launches ---------------------------------------------------------------------------
+// graphBegin(ctx); ... library calls ...; graphEnd(ctx) -> graph; graphLaunch(graph); graphDestroy(graph).
+// The graph is also destroyed by its finalizer if the handle is dropped.
+constexpr uint32_t kGraphMagic = 0x62726b67;   // "brkg": the handle kind, checked before use
+
+struct GraphBox {
+    uint32_t magic;
+    CtxBox* box;
+    brik_graph* graph;
+};
+
+void graph_finalize(napi_env, void* data, void*)
+{
+    GraphBox* g = static_cast<GraphBox*>(data);
+    if (g->graph) brik_graph_destroy(g->box->ctx, g->graph);
+    box_release(g->box);
+    delete g;
+}
+
+bool get_graph(napi_env env, napi_value v, GraphBox** out)
+{
+    void* p = nullptr;
+    if (napi_get_value_external(env, v, &p) != napi_ok || !p || static_cast<GraphBox*>(p)->magic != kGraphMagic) {
+        napi_throw_type_error(env, "BRIK_EINVAL", "expected a recorded graph");
+        return false;
+    }
+    *out = static_cast<GraphBox*>(p);
+    if (!(*out)->graph) {
+        napi_throw_error(env, "BRIK_EINVAL", "graph was destroyed");
+        return false;
+    }
+    return true;
+}
+
+napi_value GraphBegin(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    brik_ctx* ctx;
+    if (!get_ctx(env, a.v[0], &ctx)) return nullptr;
+    if (check(env, ctx, brik_graph_begin(ctx))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GraphEnd(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    CtxBox* box;
+    if (!get_box(env, a.v[0], &box)) return nullptr;
+    brik_graph* g = nullptr;
+    if (check(env, box->ctx, brik_graph_end(box->ctx, &g))) return nullptr;
+    GraphBox* gb = new GraphBox{kGraphMagic, box, g};
+    ++box->refs;
+    napi_value ext;
+    if (napi_create_external(env, gb, graph_finalize, nullptr, &ext) != napi_ok) {
+        graph_finalize(env, gb, nullptr);
+        napi_throw_error(env, "BRIK_NAPI", "napi_create_external failed");
+        return nullptr;
+    }
+    return ext;
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    GraphBox* g;
+    if (!get_graph(env, a.v[0], &g)) return nullptr;
+    if (check(env, g->box->ctx, brik_graph_launch(g->box->ctx, g->graph))) return nullptr;
+    return undefined(env);
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info)
+{
+    Args a;
+    if (!get_args(env, info, a, 1)) return nullptr;
+    void* p = nullptr;
+    if (napi_get_value_external(env, a.v[0], &p) != napi_ok || !p || static_cast<GraphBox*>(p)->magic != kGraphMagic)
+        return undefined(env);
+    GraphBox* g = static_cast<GraphBox*>(p);
+    if (g->graph) brik_graph_destroy(g->box->ctx, g->graph);
+    g->graph = nullptr;
+    return undefined(env);
+}
+
 napi_value Init(napi_env env, napi_value exports)
 {
     const napi_property_descriptor props[] = {
@@ -896,6 +997,11 @@ napi_value Init(napi_env env, napi_value exports)
         {"alloc", nullptr, Alloc, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"free", nullptr, Free, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"h2d", nullptr, H2D, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"h2dAsync", nullptr, H2DAsync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"graphBegin", nullptr, GraphBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"graphEnd", nullptr, GraphEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"graphLaunch", nullptr, GraphLaunch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+        {"graphDestroy", nullptr, GraphDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"d2h", nullptr, D2H, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"sync", nullptr, Sync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
         {"setOption", nullptr, SetOption, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <new>
 #include <vector>
 #include <algorithm>
@@ -194,6 +195,17 @@ struct brik_ctx {
     size_t cws_bytes = 0;
     void* pws = nullptr;   // split-K partial tiles [slice][row][column] f32 (grow-only)
     size_t pws_bytes = 0;
+
+    // pinned staging ring of brik_h2d_async (allocated on first use): uploads in flight as
+    // {offset, bytes, event} in issue order; events are recycled through a free list
+    struct Upload {
+        size_t off, len;
+        hipEvent_t ev;
+    };
+    void* ring = nullptr;
+    size_t ring_head = 0;
+    std::deque<Upload> ring_inflight;
+    std::vector<hipEvent_t> ring_events;
 
     // the device's fixed scratch array (brik_scratch.hip), resolved at creation; scratch_err holds the
     // hipError_t of a failed resolution, which only the no-allocation entry point reports
@@ -1028,6 +1040,9 @@ void brik_destroy(brik_ctx* c)
     // best-effort teardown: errors here have no caller to report to
     if (c->device >= 0) (void)hipSetDevice(c->device);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (const brik_ctx::Upload& u : c->ring_inflight) (void)hipEventDestroy(u.ev);
+    for (hipEvent_t e : c->ring_events) (void)hipEventDestroy(e);
+    if (c->ring) (void)hipHostFree(c->ring);
     if (c->ev_begin) (void)hipEventDestroy(c->ev_begin);
     if (c->ev_end) (void)hipEventDestroy(c->ev_end);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -1074,6 +1089,64 @@ static int copy(brik_ctx* c, void* dst, const void* src, size_t n, hipMemcpyKind
 }
 
 int brik_h2d(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyHostToDevice); }
+
+int brik_h2d_async(brik_ctx* c, void* dst, const void* src, size_t n)
+{
+    if (!c) return BRIK_EINVAL;
+    if (n == 0) return BRIK_OK;
+    if (!dst || !src) return fail(c, BRIK_EINVAL, "h2d_async: null pointer");
+    if (c->graph_capturing) return fail(c, BRIK_EINVAL, "copy: not allowed while a graph capture is open");
+    constexpr size_t ring_bytes = BRIK_STAGING_RING_BYTES;
+    if (n > ring_bytes / 2) return copy(c, dst, src, n, hipMemcpyHostToDevice);
+    HIP_TRY(c, hipSetDevice(c->device));
+    if (!c->ring) {
+        HIP_TRY(c, hipHostMalloc(&c->ring, ring_bytes, hipHostMallocDefault));
+    }
+    // the slot: at the head, or at the start of the ring if it does not fit before the end
+    size_t off = c->ring_head;
+    if (off + n > ring_bytes) off = 0;
+    // uploads still in flight that overlap [off, off + n): wait for the newest of them (events complete
+    // in stream order, so every older upload has completed too) and retire them all up to it
+    size_t last = 0;
+    bool any = false;
+    for (size_t i = 0; i < c->ring_inflight.size(); ++i) {
+        const brik_ctx::Upload& u = c->ring_inflight[i];
+        if (u.off < off + n && off < u.off + u.len) {
+            last = i;
+            any = true;
+        }
+    }
+    if (any) {
+        HIP_TRY(c, hipEventSynchronize(c->ring_inflight[last].ev));
+        for (size_t i = 0; i <= last; ++i) {          // all complete
+            c->ring_events.push_back(c->ring_inflight.front().ev);
+            c->ring_inflight.pop_front();
+        }
+    }
+    // retire uploads found complete at the front, without waiting
+    while (!c->ring_inflight.empty() && hipEventQuery(c->ring_inflight.front().ev) == hipSuccess) {
+        c->ring_events.push_back(c->ring_inflight.front().ev);
+        c->ring_inflight.pop_front();
+    }
+    hipEvent_t ev = nullptr;
+    if (!c->ring_events.empty()) {
+        ev = c->ring_events.back();
+        c->ring_events.pop_back();
+    } else {
+        HIP_TRY(c, hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    }
+    unsigned char* slot = static_cast<unsigned char*>(c->ring) + off;
+    std::memcpy(slot, src, n);
+    hipError_t e = hipMemcpyAsync(dst, slot, n, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+    if (e != hipSuccess) {
+        c->ring_events.push_back(ev);
+        return fail(c, BRIK_EHIP, "h2d_async: %s", hipGetErrorString(e));
+    }
+    c->ring_inflight.push_back(brik_ctx::Upload{off, n, ev});
+    c->ring_head = (off + n + 255) & ~(size_t)255;
+    return BRIK_OK;
+}
 int brik_d2h(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyDeviceToHost); }
 int brik_d2d(brik_ctx* c, void* dst, const void* src, size_t n) { return copy(c, dst, src, n, hipMemcpyDeviceToDevice); }
 

@@ -9,8 +9,12 @@
 //   matmulQ4Tiled / matmulQ4Shared      :1055-1075  aliases of matmulQ4 (one entry picks the kernel by m)
 //   matmulQ3(a, lo, hi, sc, mn, m, k, n):1080-1087  engine.matmulQ3(...)
 //   matmulQ8(a, codes, sc, m, k, n)     :1140-1147  engine.matmulQ8(...), matmulQ8Tiled / Shared aliases
-//   recMM(enc, trash, a, w, m, k, n)    :1562-1567  engine.mm(a, w, m, k, n[, out]) (device resident,
-//                                                    dispatch on the handle's shape: q3 / nib / codes)
+//   recMM(enc, trash, a, w, m, k, n)    :1562-1567  engine.recMM(trash, a, w, m, k, n) / mm(a, w, m, k, n[, out])
+//                                                    (device resident, dispatch on the handle's shape:
+//                                                    q3 / nib / codes; pooled output put on trash)
+//   storage / release / releaseGpu /    :903-956,   engine.storage(bytes), release(bufs), releaseGpu(bufs),
+//   trimPool / readGpu                  :1434-1458  trimPool(keep), readGpu(buf, n)
+//   queue.writeBuffer                   :231-235    engine.writeBuffer(buf, data[, offset]) (no wait)
 //   dequantGpuQ4/Q3/Q8 Q4W/Q3W/Q8W path  model.ts:214-270  engine.weightFromBlob(fmt, blob, nElems)
 //   destroyWeight(b)                     model.ts:274-280  engine.destroyWeight(w)
 //   decodeTopKQ8 head + sampling passes :1934-1968  engine.lmHeadTopK(x, w, d, vocab, recent, penalty, softcap, K)
@@ -101,6 +105,11 @@ class Engine {
   constructor(device) {
     this.native = loadNative();
     this.ctx = this.native.createContext(device === undefined ? 0 : device);
+    // scratch pool by exact byte size, as the reference's storage() / release() (kernels.ts:903-956):
+    // buffers return to it after use and are handed out again; stream order makes the reuse safe (a
+    // call enqueued later runs after every earlier reader of the buffer)
+    this._pool = new Map();
+    this._pooled = new WeakSet();
   }
 
   static deviceCount() { return loadNative().deviceCount(); }
@@ -125,6 +134,90 @@ class Engine {
   }
 
   uploadGpu(f32) { return this.uploadGpuRaw(f32); }
+
+  // ---- scratch pool (kernels.ts:903-956, 1418-1458) ----------------------------------------------
+  // A device buffer of `bytes` from the pool (or a new one): the reference's storage().
+  storage(bytes) {
+    const free = this._pool.get(bytes);
+    if (free && free.length) {
+      const b = free.pop();
+      this._pooled.delete(b);
+      return b;
+    }
+    const b = this.alloc(bytes);
+    b._poolSize = bytes;
+    return b;
+  }
+
+  // Return buffers: pooled scratch (from storage) goes back to the pool, anything else is destroyed; a
+  // buffer already in the pool is skipped (a double release would hand it out twice).
+  release(buffers) {
+    for (const b of buffers) {
+      if (!b) continue;
+      if (b._poolSize !== undefined) {
+        if (this._pooled.has(b) || b.ptr === null) continue;
+        this._pooled.add(b);
+        let list = this._pool.get(b._poolSize);
+        if (!list) { list = []; this._pool.set(b._poolSize, list); }
+        list.push(b);
+        continue;
+      }
+      if (typeof b.destroy === 'function') b.destroy();
+    }
+  }
+
+  releaseGpu(buffers) { this.release(buffers); }
+
+  // Shrink the pool to about keepBytes, largest buffers first (trimPool, kernels.ts:1440-1455).
+  trimPool(keepBytes) {
+    const keep = keepBytes === undefined ? 64 * 1024 * 1024 : keepBytes;
+    let kept = 0;
+    this._pool.forEach(function (list, size) { kept += size * list.length; });
+    const sizes = Array.from(this._pool.keys()).sort(function (a, b) { return b - a; });
+    for (const size of sizes) {
+      const list = this._pool.get(size);
+      while (list.length && kept > keep) {
+        const b = list.pop();
+        this._pooled.delete(b);
+        b.destroy();
+        kept -= size;
+      }
+    }
+  }
+
+  // Bytes held by the pool's free buffers.
+  poolBytes() {
+    let n = 0;
+    this._pool.forEach(function (list, size) { n += size * list.length; });
+    return n;
+  }
+
+  // Read nElems f32 of a device buffer back (readGpu, kernels.ts:1434).
+  readGpu(buf, nElems) { return this.readBackAsync(buf, nElems * 4); }
+
+  // Upload without waiting for earlier work (queue.writeBuffer, kernels.ts:231-235): the bytes are
+  // staged at once, so `data` may be reused when this returns.
+  writeBuffer(buf, data, offset) {
+    const b = toBytes(data);
+    const ptr = (typeof buf === 'bigint' ? buf : buf.ptr) + BigInt(offset || 0);
+    if (b.byteLength) this.native.h2dAsync(this.ctx, ptr, b);
+  }
+
+  // ---- recorded launches ---------------------------------------------------------------------------
+  // record(fn): the library calls fn() makes (plan runs, mm, ...) captured once into a HIP graph, not
+  // run; the returned {launch(), destroy()} replays them, as the reference records a decode step into
+  // one command encoder and submits it. Workspaces must already have their size (run fn() once before).
+  record(fn) {
+    const nat = this.native;
+    nat.graphBegin(this.ctx);
+    let g = null;
+    try {
+      fn();
+    } finally {
+      g = nat.graphEnd(this.ctx);
+    }
+    return { launch: function () { nat.graphLaunch(g); }, destroy: function () { nat.graphDestroy(g); } };
+  }
 
   readBack(buf, bytes) {
     const ptr = typeof buf === 'bigint' ? buf : buf.ptr;
@@ -165,21 +258,21 @@ class Engine {
   }
 
   // ---- readback ops (reference signatures) -----------------------------------------------------
-  // Upload a, enqueue the matmul and read y back without blocking the JS thread; a bad argument or a
-  // library error rejects the promise. The temporary buffers are freed after the readback (freeing
-  // them earlier would wait for the stream).
+  // Upload a, enqueue the matmul and read y back without blocking the JS thread: the upload is staged
+  // and enqueued without waiting for earlier work (writeBuffer), the readback resolves through a fence.
+  // A bad argument or a library error rejects the promise. x and y come from the scratch pool and go
+  // back to it once the readback has completed.
   async _readback(fn, a, planeArgs, m, k, n) {
     const x = a instanceof Float32Array ? a : Float32Array.from(a);
     if (x.length !== m * k) throw einval('activation has ' + x.length + ' floats, expected m*k = ' + m * k);
-    const xb = this.alloc(x.byteLength);
-    const yb = this.alloc(m * n * 4);
+    const xb = this.storage(Math.max(x.byteLength, 4));
+    const yb = this.storage(Math.max(m * n * 4, 4));
     try {
-      if (x.byteLength) this.native.h2d(this.ctx, xb.ptr, x);
+      this.writeBuffer(xb, x);
       fn.apply(this.native, [this.ctx, xb.ptr].concat(planeArgs, [yb.ptr, m, k, n]));
       return await this.readBackAsync(yb, m * n * 4);
     } finally {
-      xb.destroy();
-      yb.destroy();
+      this.release([xb, yb]);
     }
   }
 
@@ -205,8 +298,22 @@ class Engine {
   }
 
   // ---- recorded (device-resident) form: recMM ---------------------------------------------------
-  mm(a, w, m, k, n, out) {
-    const y = out || this.alloc(m * n * 4);
+  // recMM(trash, a, w, m, k, n) (kernels.ts:1521-1567): the output comes from the scratch pool and is
+  // pushed onto `trash`; release(trash) returns it once the caller is done (the reference releases its
+  // trash after the submit). mm(a, w, m, k, n[, out[, trash]]): into `out`, else a pooled buffer put
+  // on `trash` if one is given, else a new buffer the caller owns.
+  recMM(trash, a, w, m, k, n) { return this.mm(a, w, m, k, n, null, trash); }
+
+  mm(a, w, m, k, n, out, trash) {
+    let y = out;
+    if (!y) {
+      if (trash) {
+        y = this.storage(Math.max(m * n * 4, 4));
+        trash.push(y);
+      } else {
+        y = this.alloc(m * n * 4);
+      }
+    }
     if (w && w.q3) this.native.matmulQ3(this.ctx, a, w.lo, w.hi, w.sc, w.mn, y, m, k, n);
     else if (w && w.nib) this.native.matmulQ4(this.ctx, a, w.nib, w.sc, w.mn, y, m, k, n);
     else if (w && w.codes) this.native.matmulQ8(this.ctx, a, w.codes, w.sc, y, m, k, n);

@@ -64,6 +64,15 @@ int brik_free(brik_ctx *ctx, void *dptr);
 int brik_h2d(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
 int brik_d2h(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
 int brik_d2d(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Upload without waiting, as the reference's queue.writeBuffer (kernels.ts:231-235, used by the
+ * readback ops at :1046-1053): the bytes are copied at once into a context-owned pinned staging ring
+ * and the device copy is enqueued on the context stream, ordered before any later call; the call
+ * returns without waiting for earlier work, and `src` may be reused when it returns. A ring slot is
+ * reused only after its copy has completed (an event per upload; the call waits for one only when the
+ * ring has wrapped onto a copy still in flight). Uploads larger than BRIK_STAGING_RING_BYTES / 2 take
+ * the blocking brik_h2d path. Not allowed while a graph capture is open. */
+#define BRIK_STAGING_RING_BYTES (32u << 20)
+int brik_h2d_async(brik_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Wait for all work enqueued on the context's stream. */
 int brik_sync(brik_ctx *ctx);
 

@@ -2,7 +2,9 @@
 // GPU checks of the JavaScript host's asynchronous surface and buffer lifetime (brimkern_amd/js over
 // the N-API addon): readbacks resolve through stream fences off the JS thread, results of concurrent
 // calls land in their own promises, bad arguments reject instead of throwing, dropped DeviceBuffers
-// are freed by their finalizers (and keep their context alive until then), and selfValidate passes.
+// are freed by their finalizers (and keep their context alive until then), selfValidate passes; the
+// scratch pool (storage / release / trimPool), recMM's pooled outputs, recorded launches, and readback
+// ops that neither allocate per call nor wait for earlier work before returning.
 // Run with --expose-gc; prints one JSON line, exit code 0 iff every check passed.
 const path = require('path');
 const root = path.join(__dirname, '..', '..');
@@ -126,9 +128,14 @@ async function main() {
     engine.destroyWeight(w.h);
   }
 
-  // 5. temporaries of the readback ops are freed: the live count returns to where it was
+  // 5. temporaries of the readback ops go back to the scratch pool: the live count is the base plus the
+  // pool's free buffers, and trimming the pool returns it to the base
   {
-    check('readback ops free their temporaries', engine.liveBuffers() === base,
+    const pooled = engine.liveBuffers() - base;
+    check('readback temporaries are pooled', pooled >= 2 && engine.poolBytes() > 0,
+      { live: engine.liveBuffers(), base: base, poolBytes: engine.poolBytes() });
+    engine.trimPool(0);
+    check('trimPool(0) frees the pooled temporaries', engine.liveBuffers() === base && engine.poolBytes() === 0,
       { live: engine.liveBuffers(), base: base });
   }
 
@@ -165,6 +172,132 @@ async function main() {
     handle = null;
     await collect();           // the last reference goes: the context is destroyed here
     check('buffer outlives its dropped engine', err === null, { err: err });
+  }
+
+  // 8. the scratch pool (storage / release, kernels.ts:903-956): exact-size reuse, a double release
+  // does not hand one buffer out twice, release destroys what is not pooled, trimPool frees
+  {
+    const a = engine.storage(4096);
+    engine.release([a]);
+    const b = engine.storage(4096);
+    check('storage reuses a released buffer of the same size', a === b, {});
+    engine.release([b, b]);
+    const c1 = engine.storage(4096), c2 = engine.storage(4096);
+    check('a double release is ignored', c1 !== c2 && c1 === b, {});
+    const d = engine.storage(8192);
+    check('another size is another buffer', d !== c1 && d !== c2, {});
+    const own = engine.alloc(256);
+    engine.release([c1, c2, d, own, null]);
+    check('release destroys a buffer that is not pooled', own.ptr === null, {});
+    check('the pool holds the released sizes', engine.poolBytes() === 2 * 4096 + 8192, { bytes: engine.poolBytes() });
+    engine.trimPool(4096);
+    check('trimPool drops the largest first down to keepBytes', engine.poolBytes() <= 4096, { bytes: engine.poolBytes() });
+    engine.trimPool(0);
+    check('trimPool(0) empties the pool', engine.poolBytes() === 0 && engine.liveBuffers() === base,
+      { live: engine.liveBuffers(), base: base });
+  }
+
+  // 9. recMM(trash, ...): a pooled output on the trash, equal to the readback op; after release the next
+  // call gets the same buffer, so a decode loop allocates nothing after its first step
+  {
+    const K = 2560, N = 1024;
+    const w = await makeWeight(engine, 21, N, K);
+    const xh = randn(rng(22), K);
+    const x = engine.uploadGpu(xh);
+    const ref = await engine.matmulQ4(xh, w.h.nib, w.h.sc, w.h.mn, 1, K, N);
+    let trash = [];
+    const y0 = engine.recMM(trash, x, w.h, 1, K, N);
+    const got = await engine.readGpu(y0, N);
+    check('recMM output is on the trash', trash.length === 1 && trash[0] === y0, {});
+    check('recMM equals the readback op', normwise(got, ref) === 0, { rel: normwise(got, ref) });
+    engine.release(trash);
+    const live0 = engine.liveBuffers();
+    let same = true;
+    for (let i = 0; i < 100; i++) {
+      trash = [];
+      const y = engine.recMM(trash, x, w.h, 1, K, N);
+      same = same && y === y0;
+      engine.release(trash);
+    }
+    check('recMM reuses its pooled output across steps', same && engine.liveBuffers() === live0,
+      { live: engine.liveBuffers(), live0: live0 });
+    // the readback ops reuse their pooled temporaries the same way
+    const live1 = engine.liveBuffers();
+    for (let i = 0; i < 20; i++) await engine.matmulQ4(xh, w.h.nib, w.h.sc, w.h.mn, 1, K, N);
+    check('readback ops allocate nothing per call', engine.liveBuffers() === live1,
+      { live: engine.liveBuffers(), live1: live1 });
+    x.destroy();
+    engine.destroyWeight(w.h);
+    engine.trimPool(0);
+  }
+
+  // 10. record(): launches captured once and replayed give the eager results (with the inputs changed
+  // between replays: the graph keeps addresses, not contents)
+  {
+    const K = 1024, N = 768;
+    const w = await makeWeight(engine, 23, N, K);
+    const x = engine.alloc(4 * K), y = engine.alloc(4 * N);
+    engine.writeBuffer(x, randn(rng(24), K));
+    engine.mm(x, w.h, 1, K, N, y);                 // workspaces at size before the capture
+    const g = engine.record(function () { engine.mm(x, w.h, 1, K, N, y); });
+    let ok = true;
+    for (let rep = 0; rep < 3; rep++) {
+      const xh = randn(rng(30 + rep), K);
+      engine.writeBuffer(x, xh);
+      engine.writeBuffer(y, new Float32Array(N).fill(NaN));
+      g.launch();
+      const got = await engine.readGpu(y, N);
+      const ref = await engine.matmulQ4(xh, w.h.nib, w.h.sc, w.h.mn, 1, K, N);
+      ok = ok && normwise(got, ref) === 0;
+    }
+    g.destroy();
+    check('recorded launches replay to the eager result', ok, {});
+    [x, y].forEach(function (b) { b.destroy(); });
+    engine.destroyWeight(w.h);
+    engine.trimPool(0);
+  }
+
+  // 11. a readback op issued behind a long queue of work returns at once: the upload is staged and
+  // enqueued without waiting (queue.writeBuffer), and the promise resolves after the queue drains
+  {
+    const K = 4096, N = 4096, M = 512;
+    const big = await makeWeight(engine, 25, N, K);
+    const xb = engine.uploadGpu(randn(rng(26), M * K));
+    const yb = engine.alloc(M * N * 4);
+    const w = await makeWeight(engine, 27, 512, 512);
+    const xs = randn(rng(28), 512);
+    await engine.matmulQ4(xs, w.h.nib, w.h.sc, w.h.mn, 1, 512, 512);   // pool and staging ring warm
+    engine.mm(xb, big.h, M, K, N, yb);
+    await engine.readGpu(yb, 4);
+    const g = engine.record(function () { for (let i = 0; i < 100; i++) engine.mm(xb, big.h, M, K, N, yb); });
+    for (let attempt = 0; attempt < 2; attempt++) {
+      const t0 = process.hrtime.bigint();
+      g.launch();
+      g.launch();
+      const t1 = process.hrtime.bigint();
+      const p = engine.matmulQ4(xs, w.h.nib, w.h.sc, w.h.mn, 1, 512, 512);
+      const t2 = process.hrtime.bigint();
+      let ticks = 0, done = false;
+      setImmediate(function spin() { if (!done) { ticks++; setImmediate(spin); } });
+      const y = await p;
+      done = true;
+      const t3 = process.hrtime.bigint();
+      const issue = Number(t2 - t1) / 1e6, total = Number(t3 - t0) / 1e6;
+      const ref = cpuQ4(w.bytes, xs, 1, 512, 512);
+      const rel = normwise(y, ref);
+      if (attempt === 1 || (total > 4 && issue < 0.1 * total)) {
+        check('matmulQ4 behind a long queue returns without waiting', total > 4 && issue < 0.1 * total,
+          { issue_ms: issue, queue_ms: total });
+        check('the event loop turns while it is pending', ticks >= 1, { ticks: ticks });
+        check('its result is correct', rel <= 1e-5, { rel: rel });
+        break;
+      }
+    }
+    g.destroy();
+    [xb, yb].forEach(function (b) { b.destroy(); });
+    engine.destroyWeight(big.h);
+    engine.destroyWeight(w.h);
+    engine.trimPool(0);
   }
 
   const failed = results.filter(function (r) { return !r.ok; }).length;

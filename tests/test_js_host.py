@@ -25,7 +25,8 @@ EXPORTS = ["deviceCount", "createContext", "alloc", "free", "h2d", "d2h", "sync"
            "timerEnd", "matmulQ8", "matmulQ4", "matmulQ3", "moeMatmulQ4", "dequantQ8", "dequantQ4", "dequantQ3",
            "gemvPlanCreate", "gemvPlanCreateGlu", "gemvPlanRun", "gemvPlanDestroy", "logitsTopK", "lmHeadTopK", "quantize",
            "f16ToF32", "conv2d", "matmulF16W", "allocBuffer", "bufferPtr", "freeBuffer", "liveBuffers",
-           "readbackAsync", "selfValidate", "moeMatmulQ4x2"]
+           "readbackAsync", "selfValidate", "moeMatmulQ4x2", "h2dAsync", "graphBegin", "graphEnd", "graphLaunch",
+           "graphDestroy"]
 
 
 def node(script, timeout=120):
@@ -68,9 +69,10 @@ def test_js_engine_parity_on_gpu():
 @pytest.mark.gpu
 def test_js_engine_async_and_lifetime_on_gpu():
     """Readbacks through fences off the JS thread, rejection instead of throwing, finalizers freeing
-    dropped device buffers (and keeping their context alive), selfValidate passing."""
+    dropped device buffers (and keeping their context alive), selfValidate passing, the scratch pool and
+    recMM's pooled outputs, recorded launches, readback ops issued behind a long queue returning at once."""
     r = subprocess.run([NODE, "--expose-gc", os.path.join(ROOT, "tests", "js", "engine_async.js")], cwd=ROOT,
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     res = json.loads(r.stdout.strip().splitlines()[-1])
-    assert res["failed"] == 0 and res["checks"] >= 14
+    assert res["failed"] == 0 and res["checks"] >= 30
