@@ -558,6 +558,20 @@ def cpu_baseline(target_s=15.0):
                        f"single-threaded, {cpu_model()}; the headline's inputs"}, refs)
 
 
+def node_host_timing(timeout=240):
+    """The JavaScript host's per-call costs (brimkern_amd/js/host_timing.js under node, a child process
+    with its own context): mm, a fused decoder layer's plan runs and an awaited readback op, eager and
+    replayed from a recorded graph."""
+    node = shutil.which("node")
+    if node is None:
+        return {"skipped": "node absent"}
+    r = subprocess.run([node, os.path.join(ROOT, "brimkern_amd", "js", "host_timing.js")], cwd=ROOT,
+                       capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        return {"failed": r.stderr[-500:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def verify_headline(y_head, refs, layers, tol=1e-5):
     """The headline's last timed step against the CPU reference's outputs on the same inputs: every
     layer's copy of each of the six matrices (all 216 outputs, every row), normwise relative error
@@ -793,6 +807,8 @@ def main():
         extra["f4_matmul_t_f16w_K2560_N9728"] = f16w_f4(ctx, args.steps, args.warmup)
         log("bench: F1 encoders")
         extra["f1_quantize_f32_to_planes_N9728_K2560"] = quantize_f1(ctx, args.steps, args.warmup)
+        log("bench: JS host (node) per-call costs")
+        extra["js_host_node"] = node_host_timing()
     cpu, refs = (None, None) if args.no_cpu else cpu_baseline()
     check = verify_headline(y_head, refs, args.layers) if not args.no_cpu else {"verified": None,
                                                                                "note": "--no-cpu"}
