@@ -119,13 +119,18 @@ def time_loop_min(ctx, fn, steps, warmup, min_ms=MIN_TIMED_MS):
     return ms
 
 
+GRAPHS = True     # False under --no-graph: the graph-replayed lines are timed eagerly instead
+
+
 def time_graph(ctx, fn, count, min_calls=256, min_ms=MIN_TIMED_MS):
     """fn(i), i = 0 .. n-1 (n >= count, so every weight copy appears), recorded into one graph and
     replayed until at least min_ms of GPU time; returns ms per call. This is the GPU-side rate of
     back-to-back launches, as a decode step recorded once and replayed issues them (the reference
     records a layer's matmuls into one command encoder); a Python loop of calls is bound by the host
-    for launches this short."""
+    for launches this short. With GRAPHS off (--no-graph, for profiler runs) the calls run eagerly."""
     n = max(count, min_calls)
+    if not GRAPHS:
+        return time_loop_min(ctx, fn, n, count)
     fn(0)
     ctx.sync()              # workspaces at their size before the capture (which refuses growth)
     ctx.graph_begin()
@@ -743,12 +748,14 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--no-graph", action="store_true",
-                    help="time the fused decoder layers eagerly only (rocprofv3's kernel trace has crashed in "
-                         "hipGraphLaunch on the box)")
+                    help="no graph replay: time the fused decoder layers and the single-launch lines eagerly "
+                         "(rocprofv3's kernel trace has crashed in hipGraphLaunch on the box)")
     ap.add_argument("--only", choices=sorted(ONLY),
                     help="run one workload alone and print its result (for profiler runs; not the bench line)")
     ap.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    global GRAPHS
+    GRAPHS = not args.no_graph
     if args.probe:
         probe(args.layers)
         return
