@@ -6,6 +6,9 @@
 3. ``csrc/brik_runtime.cpp`` + ``csrc/brik_embed.S`` (embeds the code object) + that object ->
    ``libbrik.so`` (the C ABI declared in ``include/brik.h``)
 4. ``csrc/brik_napi.cc`` -> ``js/brik.node`` (Node N-API addon over libbrik.so, rpath $ORIGIN/..)
+5. ``tests/native/host_sanitize.cpp`` + the runtime sources, host code built with AddressSanitizer and
+   UndefinedBehaviorSanitizer -> ``tests/native/host_sanitize`` (a test driver, not part of the library;
+   skipped when g++ cannot link the sanitizer runtimes)
 
 Run ``python -m brimkern_amd.build`` or call :func:`build`.
 """
@@ -26,6 +29,8 @@ HSACO = os.path.join(BUILD, "brik_gfx950.hsaco")
 SCRATCH_OBJ = os.path.join(BUILD, "brik_scratch.o")
 LIB = os.path.join(PKG, "libbrik.so")
 ADDON = os.path.join(PKG, "js", "brik.node")
+SANITIZE_SRC = os.path.join(ROOT, "tests", "native", "host_sanitize.cpp")
+SANITIZE_BIN = os.path.join(ROOT, "tests", "native", "host_sanitize")
 
 # Device flags. packed-fp32-ops is switched off: the compiler would otherwise fuse pairs of f32
 # operations into v_pk_* forms.
@@ -84,6 +89,28 @@ def build_addon(verbose=False):
     return ADDON
 
 
+def build_host_sanitize(verbose=False):
+    """The runtime's host code with ASan + UBSan (g++, host only; the kernels stay the ordinary code
+    object), linked with the driver that exercises every entry point (tests/test_host_sanitize.py)."""
+    if not os.path.exists(SANITIZE_SRC):
+        return None
+    tmp = SANITIZE_BIN + ".tmp"
+    try:
+        _run(["g++", "-O1", "-g", "-std=c++17", "-Wall", "-Wextra", "-fno-omit-frame-pointer",
+              "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined", "-static-libasan",
+              "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"), "-I", os.path.join(ROOT, "include"),
+              f'-DBRIK_HSACO_PATH="{HSACO}"', SANITIZE_SRC,
+              os.path.join(CSRC, "brik_runtime.cpp"), os.path.join(CSRC, "brik_embed.S"), SCRATCH_OBJ,
+              "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+              "-o", tmp], verbose)
+    except (subprocess.CalledProcessError, OSError):
+        if verbose:
+            print("+ host sanitizer driver skipped: g++ could not build it", flush=True)
+        return None
+    os.replace(tmp, SANITIZE_BIN)
+    return SANITIZE_BIN
+
+
 def check_hsaco(verbose=False):
     """The GEMM kernels' inline-asm LDS reads must be waited for before their registers are touched
     (check_lds_reads.py); a violation fails the build."""
@@ -101,6 +128,7 @@ def build(verbose=False):
     build_scratch(verbose)
     build_lib(verbose)
     build_addon(verbose)
+    build_host_sanitize(verbose)
 
 
 if __name__ == "__main__":
