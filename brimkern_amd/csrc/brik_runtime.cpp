@@ -72,6 +72,9 @@ constexpr GemvVariant kGluVariant = {16, 2, 1, 2};
 constexpr int kGluThreads = 512;
 constexpr int kGluRows = 32;   // rows of each matrix per block
 static_assert(kGluThreads / kGluVariant.team * kGluVariant.r == 2 * kGluRows, "GLU block rows");
+// the pair launch's blocks past the whole groups: 8 teams of 64 lanes, one row of each matrix per team
+constexpr int kGluTailRows = 8;
+static_assert(kGluThreads / 64 * kGluVariant.r == 2 * kGluTailRows, "GLU tail block rows");
 
 constexpr int kGroup = 32;
 // GEMM block tiles (BM rows x 32 TN NW columns, NW waves), in the order of BRIK_GEMM_FMT in gemm.hip:
@@ -145,6 +148,7 @@ struct brik_gemv_plan {
     // staged input (stage = image->ptr, no stager)
     bool glu = false;
     int act_flags = 0;
+    int glu_full = 0;             // producer blocks that write whole groups of the image
     SharedBuf* image = nullptr;
 };
 
@@ -1510,9 +1514,11 @@ static int check_jobs(brik_ctx* c, Fmt f, const brik_gemv_job_ex* jobs, int njob
 }
 
 // A grouped plan over `jobs`. With `image` (the consumer of a GLU pair: one job), the blocks copy that
-// staged image of the job's input instead of staging it, and the plan holds a reference to it.
+// staged image of the job's input instead of staging it, and the plan holds a reference to it; with
+// img_groups > 0 the producer writes only the image's first img_groups groups and the blocks stage the
+// others themselves.
 static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int njobs, brik_gemv_plan** out,
-                       SharedBuf* image)
+                       SharedBuf* image, int img_groups = 0)
 {
     if (!c || !out) return BRIK_EINVAL;
     *out = nullptr;
@@ -1621,6 +1627,7 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
             d.r0 = (int32_t)((b - start[k]) * rpbs[k]);
             d.r1 = std::min(sorted[k].job.N, d.r0 + (int32_t)rpbs[k]);
             d.stage_off = stage_off[k];
+            d.img_groups = image ? (uint32_t)img_groups : 0u;
         }
     }
     if (!inputs.empty()) std::memcpy(host.data() + inputs_off, inputs.data(), sizeof(brik_stage_input) * inputs.size());
@@ -1687,9 +1694,19 @@ int brik_gemv_plan_create_glu(brik_ctx* c, int fmt, const brik_gemv_job_ex* gate
     int r = check_jobs(c, f, both, 2);
     if (r == BRIK_OK) r = check_jobs(c, f, down, 1);
     if (r != BRIK_OK) return r;
+    // The launch's blocks of whole groups (32 rows of each matrix, 8 waves) are equal units: with
+    // 9728 rows (304 groups) on 256 CUs, 48 CUs ran two of them while the others ran one (12.0 us
+    // against 9.7 us for the unlinked gate/up plan). When the groups exceed a whole number of rounds
+    // of CUs by at most half a round, the remainder runs in blocks of 8 rows of each matrix that write
+    // act(gate) * up of their rows after the image, and the consumer stages those groups itself (the
+    // same code on the same values as its own staging, so its input stays bit-identical).
+    const int groups = g.N / kGroup;
+    const int rem = groups % (int)kCUs;
+    const int nfull = groups > (int)kCUs && rem > 0 && rem <= (int)kCUs / 2 ? groups - rem : groups;
     // the image of down's input: zero groups (group G stays the zero group), then the flag -1 (read the
-    // groups' own markers) and the RMSNorm factor 1
+    // groups' own markers) and the RMSNorm factor 1; then the values of the groups past nfull
     const size_t ib = (gemv_lds(d.K, f) + 15) & ~(size_t)15;
+    const size_t tail_bytes = sizeof(float) * kGroup * (size_t)(groups - nfull);
     std::vector<unsigned char> host(ib, 0);
     const size_t tail = (size_t)112 * (d.K / kGroup + 1);
     const int32_t scan = -1;
@@ -1703,7 +1720,7 @@ int brik_gemv_plan_create_glu(brik_ctx* c, int fmt, const brik_gemv_job_ex* gate
         delete p;
         return BRIK_ENOMEM;
     }
-    r = brik_alloc(c, ib, &img->ptr);
+    r = brik_alloc(c, ib + tail_bytes, &img->ptr);
     if (r == BRIK_OK) r = brik_h2d(c, img->ptr, host.data(), ib);
     if (r == BRIK_OK) r = brik_alloc(c, sizeof both, &p->dev);
     if (r == BRIK_OK) r = brik_h2d(c, p->dev, both, sizeof both);
@@ -1717,13 +1734,14 @@ int brik_gemv_plan_create_glu(brik_ctx* c, int fmt, const brik_gemv_job_ex* gate
     p->glu = true;
     p->kernel = c->gemvp[fmt_index(f)];
     p->njobs = 2;
-    p->blocks = (unsigned)(g.N / kGluRows);
+    p->glu_full = nfull;
+    p->blocks = (unsigned)(nfull + (groups - nfull) * (kGroup / kGluTailRows));
     p->lds = gemv_lds(g.K, f) + kGluVariant.extra_lds(2 * kGluRows);
     p->act_flags = down->flags & BRIK_JOB_ACT_GELU;
     p->stage = img->ptr;
     p->image = img;
     img->refs = 1;
-    r = plan_create(c, fmt, down, 1, down_plan, img);
+    r = plan_create(c, fmt, down, 1, down_plan, img, nfull < groups ? nfull : 0);
     if (r != BRIK_OK) {
         brik_gemv_plan_destroy(c, p);
         return r;
@@ -1748,7 +1766,8 @@ int brik_gemv_plan_run(brik_ctx* c, const brik_gemv_plan* p)
         const brik_gemv_job_ex* jobs = (const brik_gemv_job_ex*)p->dev;
         void* img = p->stage;
         int af = p->act_flags;
-        void* args[] = {&jobs, &img, &af};
+        int nfull = p->glu_full;
+        void* args[] = {&jobs, &img, &af, &nfull};
         return launch_fn(c, p->kernel, p->blocks, 1, kGluThreads, p->lds, args);
     }
     const brik_gemv_block* blocks = static_cast<const brik_gemv_block*>(p->dev);

@@ -453,11 +453,15 @@ __device__ __forceinline__ void stage_copy(const unsigned char* __restrict__ src
 // flight (issued first, they had to arrive before staging could start, and the two latencies added
 // up). In-block staging issues the weights after its first batch of x loads (xprep.h batched_in); with a
 // pre-staged image (`staged`, written by brik_gemv_stage_<fmt> or by a GLU pair launch) the block
-// copies it into LDS, then issues the weights. Returns true, before any step is consumed, if the row
-// holds a value that is not finite: the caller then runs the exact path.
+// copies it into LDS, then issues the weights. An image that holds only groups [0, img_groups) (a GLU
+// pair launch that wrote those; 0: the whole image) is copied as far as it goes and the block stages the
+// remaining groups itself, issuing the weights after the first batch of those loads. Returns true,
+// before any step is consumed, if the row holds a value that is not finite: the caller then runs the
+// exact path.
 template <int FMT, class W, int D, bool EVEN>
 __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const float* __restrict__ x, const Fuse& F,
-                                         int K, int S, const unsigned char* __restrict__ staged, unsigned char* lds)
+                                         int K, int S, const unsigned char* __restrict__ staged, unsigned char* lds,
+                                         int img_groups = 0)
 {
     typename W::Data d[D];
     int ip = 0, bp = 0;                      // (p, b) of the next step to issue
@@ -472,10 +476,27 @@ __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const fl
     };
     int flag;
     if (staged) {
-        stage_copy<W::NT>(staged, lds, (uint32_t)((W::xs_bytes(K) + 15) & ~(size_t)15));
-        __builtin_amdgcn_sched_barrier(0);
-        issue_ahead();
-        // every load issued after the copy is one of the D - 1 weight steps above
+        bool part = false;
+        if constexpr (FMT != FMT_Q8) part = img_groups > 0 && img_groups < X.G;
+        if (part) {
+            // the tail's loads first, then the copy and the weights: the LDS writes of the tail's groups
+            // come after every load is issued (the compiler waits for a direct global->LDS load before
+            // any later LDS write, so a copy issued first would hold back the tail's loads)
+            // the producer's values of the remaining groups follow its image in the same buffer
+            if constexpr (FMT != FMT_Q8)
+                brik::xstage_d_tail<FMT, W::STAGE_TRIPS, W::NT>(
+                    (const float*)(staged + ((W::xs_bytes(K) + 15) & ~(size_t)15)), X, img_groups, [&] {
+                    stage_copy<W::NT>(staged, lds, 112u * (uint32_t)img_groups);
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue_ahead();
+                });
+        } else {
+            stage_copy<W::NT>(staged, lds, (uint32_t)((W::xs_bytes(K) + 15) & ~(size_t)15));
+            __builtin_amdgcn_sched_barrier(0);
+            issue_ahead();
+        }
+        // every load issued after the copy (and the staged tail's loads) is one of the D - 1 weight
+        // steps above
         brik::wait_vmcnt<(D - 1) * W::NACC * W::UG * LoadsPerGroup<FMT>::v>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         flag = *X.flag;
@@ -543,7 +564,7 @@ template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Fuse& F, const Planes& P,
                                             float* __restrict__ yrow, const float* __restrict__ res,
                                             int N, int K, int r0, int r1, int rstep, unsigned char* lds,
-                                            const unsigned char* __restrict__ staged)
+                                            const unsigned char* __restrict__ staged, int img_groups = 0)
 {
     W w;
     w.G = K / BRIK_GROUP;
@@ -554,8 +575,8 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     const int S = nsets * w.B;                                            // steps per lane
     const typename W::XS X = W::xs_layout(lds, K);
     w.part = (float*)(lds + W::xs_bytes(K));
-    const bool exact = w.even() ? pipeline<FMT, W, D, true>(w, X, x, F, K, S, staged, lds)
-                                : pipeline<FMT, W, D, false>(w, X, x, F, K, S, staged, lds);
+    const bool exact = w.even() ? pipeline<FMT, W, D, true>(w, X, x, F, K, S, staged, lds, img_groups)
+                                : pipeline<FMT, W, D, false>(w, X, x, F, K, S, staged, lds, img_groups);
     if (exact) {
         // teams of 16 lanes over RPI rows per iteration
         gemv_rows_exact<FMT, W::RPI, W::NT>(x, F, *X.inv, P, yrow, res, K, r0, r1, rstep);
@@ -591,7 +612,7 @@ __device__ __forceinline__ void gemv_body(const float* __restrict__ x, const uin
 
 // Grouped GEMV over a plan's block table: block b runs rows [r0, r1) of the job in blocks[b], in row
 // sets of RPI rows. With a stage buffer (non-null stage_base) the job's x image is at
-// stage_base + stage_off.
+// stage_base + stage_off, whole or (img_groups > 0) its first img_groups groups.
 template <int FMT, class W, int D>
 __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_block* __restrict__ blocks,
                                                   const unsigned char* __restrict__ stage_base)
@@ -603,7 +624,7 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_block* __restr
     const brik_gemv_job& job = je.job;
     const Planes P{(const uint8_t*)job.p0, (const uint8_t*)job.p1, job.scales, job.mins};
     gemv_matrix<FMT, W, D>(job.x, Fuse{je.gate, je.norm_w, je.eps, je.flags}, P, job.y, je.res, job.N, job.K, bd.r0,
-                           bd.r1, RPI, lds, stage_base ? stage_base + bd.stage_off : nullptr);
+                           bd.r1, RPI, lds, stage_base ? stage_base + bd.stage_off : nullptr, (int)bd.img_groups);
 }
 
 // GLU pair (brik_gemv_plan_create_glu): rows [r0, r0 + H) of gate (jobs jg) and up (ju), H = RPI / 2,
@@ -615,12 +636,16 @@ __device__ __forceinline__ void gemv_grouped_body(const brik_gemv_block* __restr
 // uses the same lane partials, summed in the same order (a rotation by the row index), as the
 // single-matrix path with the same TEAM and U, so gate and up, and with them the image, are
 // bit-identical to those of unpaired plans.
-template <int FMT, class W, int D>
+// IMG = false: the pair launch's blocks past the whole groups it writes images for (H any whole number
+// of team rows): gate.y, up.y and act(gate) * up of rows n >= tail0 at index n - tail0 of the values
+// that follow the image in the same buffer, which the consumer stages itself.
+template <int FMT, class W, int D, bool IMG = true>
 __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const brik_gemv_job_ex& ju, int r0,
-                                              unsigned char* __restrict__ img, int act_flags, unsigned char* lds)
+                                              unsigned char* __restrict__ img, int act_flags, unsigned char* lds,
+                                              int tail0 = 0)
 {
     constexpr int H = W::RPI / 2, RH = W::RH, R = W::NACC, PARTS = W::PARTS;
-    static_assert(H % BRIK_GROUP == 0 && R == 2 * RH, "whole groups per block");
+    static_assert((!IMG || H % BRIK_GROUP == 0) && R == 2 * RH, "whole groups per block");
     const int K = jg.job.K, N = jg.job.N;
     const Fuse F{jg.gate, jg.norm_w, jg.eps, jg.flags};
     const Planes Pg{(const uint8_t*)jg.job.p0, (const uint8_t*)jg.job.p1, jg.job.scales, jg.job.mins};
@@ -665,6 +690,12 @@ __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const 
         });
     }
     __syncthreads();
+    if constexpr (!IMG) {
+        float* tail = (float*)(img + ((W::xs_bytes(N) + 15) & ~(size_t)15));
+        const int q = (int)threadIdx.x;
+        if (q < H && r0 + q < N) tail[r0 + q - tail0] = brik::act(vals[q], act_flags) * vals[H + q];
+        return;
+    }
     // group g on lanes 0-31 of wave g, lane e holding element e
     const int g = threadIdx.x >> 6, e = threadIdx.x & 63;
     if (g < H / BRIK_GROUP && e < BRIK_GROUP) {
@@ -707,16 +738,28 @@ BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)
 BRIK_GEMV_FMT(q3, FMT_Q3)
 
-// GLU pair launch: jobs[0] = gate, jobs[1] = up; block b (NT threads) runs rows [H b, H b + H) of both,
-// H = RPI / 2, and writes their groups of the image of act(gate) * up to img (act_flags:
-// BRIK_JOB_ACT_GELU or 0). The runtime table (brik_runtime.cpp, kGluVariant) names this shape.
+// GLU pair launch: jobs[0] = gate, jobs[1] = up. Block b < nfull (NT threads, teams of TEAM lanes)
+// runs rows [H b, H b + H) of both, H = RPI / 2 = 32 (one quantization group of down's input), and
+// writes that group of the image of act(gate) * up to img (act_flags: BRIK_JOB_ACT_GELU or 0). Blocks
+// past nfull run 8 rows of both each (teams of 64 lanes) from row 32 nfull on and write gate.y, up.y
+// and act(gate) * up of their rows after the image: the runtime keeps nfull at a whole number of
+// blocks per CU when the groups exceed the CUs by a small remainder, and the consumer stages those
+// last groups itself from those values, so no CU runs two of the 64-row blocks while others run one.
+// The runtime table (brik_runtime.cpp, kGluVariant) names this shape.
 #define BRIK_GEMV_PAIR(FMTN, FMT, TEAM, RR, UU, DD, NT)                                                   \
     extern "C" __global__ __launch_bounds__(NT) void brik_gemvp_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD##_n##NT( \
-        const brik_gemv_job_ex* __restrict__ jobs, unsigned char* __restrict__ img, int act_flags)      \
+        const brik_gemv_job_ex* __restrict__ jobs, unsigned char* __restrict__ img, int act_flags, int nfull) \
     {                                                                                                   \
         extern __shared__ __align__(16) unsigned char lds[];                                            \
         using W_ = PairWork<FMT, TEAM, RR, UU, NT>;                                                     \
-        gemv_glu_pair<FMT, W_, DD>(jobs[0], jobs[1], (int)blockIdx.x * (W_::RPI / 2), img, act_flags, lds); \
+        using WB_ = PairWork<FMT, 64, RR, 1, NT>;                                                       \
+        const int b = (int)blockIdx.x;                                                                  \
+        if (b < nfull)                                                                                  \
+            gemv_glu_pair<FMT, W_, DD>(jobs[0], jobs[1], b * (W_::RPI / 2), img, act_flags, lds);       \
+        else                                                                                            \
+            gemv_glu_pair<FMT, WB_, DD, false>(jobs[0], jobs[1],                                        \
+                                               nfull * (W_::RPI / 2) + (b - nfull) * (WB_::RPI / 2), img, \
+                                               act_flags, lds, nfull * (W_::RPI / 2));                  \
     }
 BRIK_GEMV_PAIR(q4, FMT_Q4, 16, 2, 1, 2, 512)
 BRIK_GEMV_PAIR(q3, FMT_Q3, 16, 2, 1, 2, 512)

@@ -19,13 +19,15 @@ typedef struct brik_stage_input {
     uint32_t off;          // byte offset of the staged image in the stage buffer (16-byte aligned)
 } brik_stage_input;
 
-// One block of a grouped GEMV launch: its job, the rows [r0, r1) of that job it computes and the byte
-// offset of the job's staged input image in the plan's stage buffer. Block b reads entry b, so
+// One block of a grouped GEMV launch: its job, the rows [r0, r1) of that job it computes, the byte
+// offset of the job's staged input image in the plan's stage buffer, and how many groups of that image
+// a producer wrote (0: all of them; else the block stages the rest itself). Block b reads entry b, so
 // everything it needs arrives with one scalar load round trip; a lookup of the job by block index
 // (a search over per-job block counts, then the job record) took several dependent ones.
 typedef struct brik_gemv_block {
     brik_gemv_job_ex job;
     int32_t r0, r1;
     uint32_t stage_off;
-    uint32_t pad[7];       // 128 bytes
+    uint32_t img_groups;
+    uint32_t pad[6];       // 128 bytes
 } brik_gemv_block;

@@ -481,6 +481,28 @@ __device__ __forceinline__ void xstage_d(const float* __restrict__ x, const XSta
     stage_finish<NT>(S.flag, S.inv, F, K, ss, bad);
 }
 
+// Groups [g0, G) of an input row for a block whose LDS already receives groups [0, g0) from a
+// producer's image (a GLU pair launch that wrote only those): `src` holds the row's values from
+// element 32 g0 on, as the producer wrote them (act(gate) * up, rounded), and they are staged by the
+// same group code as xstage_d's, with the zero group after them. The flag is set to -1 (the caller
+// then reads every group's own non-finite marker) and the RMSNorm factor to 1: such an input has no
+// RMSNorm. No barrier: the caller's follows. after_first: as in batched_in.
+template <int FMT, int SB, int NT, class After = NoLoads>
+__device__ __forceinline__ void xstage_d_tail(const float* __restrict__ src, const XStageD& S, int g0,
+                                              After after_first = After())
+{
+    const int G = S.G;
+    if (threadIdx.x == 0) {
+        *S.flag = -1;
+        *S.inv = 1.f;
+    }
+    if (threadIdx.x < 7) *(u32x4_t*)(S.base + 112 * G + 16 * threadIdx.x) = u32x4_t{0u, 0u, 0u, 0u};
+    const Fuse none{nullptr, nullptr, 0.f, 0};
+    batched_in<(SB > 1 ? SB - 1 : 1), 2, NT>(src, none, 4 * (G - g0), [&](int i, const RawIn<2>& r) {
+        (void)stage_group_d<FMT>(r.x[0], r.x[1], i & 3, S.base + 112 * (g0 + (i >> 2)));
+    }, after_first);
+}
+
 // The same group image from lanes 0-31 of one wave (all active), lane e holding element e: for a
 // producer that writes a single group at the end of its block, with the group reductions as DPP steps
 // and two lane reads instead of the 8-element-per-lane work of stage_group_d. Every value is

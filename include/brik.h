@@ -212,9 +212,11 @@ int brik_gemv_plan_create_ex(brik_ctx *ctx, int fmt, const brik_gemv_job_ex *job
  * gate = gate.y, x = up.y}: *gate_up runs both projections in one launch, each block computing rows of
  * the same indices of gate and up (32 of each, one quantization group of down's input), and writes the
  * staged input image of act(gate.y) * up.y for those rows; *down_plan copies that image instead of
- * each of its blocks transforming the whole row. down.y is bit-identical to the unlinked down plan's
- * for the same gate.y and up.y; gate.y and up.y equal the unlinked plan's within f32 rounding (the
- * RMSNorm factor and the row sums are added up in another order).
+ * each of its blocks transforming the whole row. When the groups exceed the device's CUs by a small
+ * remainder, the last groups run in smaller blocks that write act(gate.y) * up.y itself, which
+ * *down_plan's blocks stage (so no CU runs two whole groups). down.y is bit-identical to the unlinked
+ * down plan's for the same gate.y and up.y; gate.y and up.y equal the unlinked plan's within f32
+ * rounding (the RMSNorm factor and the row sums are added up in another order).
  *   gate, up: equal x, K, N and input fusion (gate, norm_w, eps, flags), distinct y.
  *   down: down.gate == gate.y, down.x == up.y, down.K == N; no norm_w; flags 0 or BRIK_JOB_ACT_GELU
  *         (the activation of the image); res allowed.

@@ -6,7 +6,9 @@ Against the two ordinary plans {gate, up} and {down with gate = gate.y, x = up.y
 half of recordLayerKV, kernels.ts:1726-1741), whose own parity against the oracle is tested in
 test_gpu_fused.py: down.y must be bit-identical to the ordinary down plan's on the same gate.y and
 up.y (the image equals the consumer's own staging), and gate.y / up.y equal the ordinary plan's within
-f32 rounding (the pair block has 8 waves, so the RMSNorm factor is summed in another order). One case
+f32 rounding (the pair block has 8 waves, so the RMSNorm factor is summed in another order). Past 256
+groups of down's input the pair launch writes the image of whole groups for the first multiple of 256
+and the consumer stages the rest from the values the launch's 8-row blocks write (shapes below). One case
 also checks the chain against the oracle directly. Non-finite gate / up outputs must send down through
 the exact path, as the self-staged input does.
 """
@@ -120,7 +122,10 @@ def check_pair(a, b):
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q3", "q8"])
-@pytest.mark.parametrize("shape", [(2560, 9728), (256, 96), (64, 32), (512, 1024)])
+# (2560, 9728): 304 groups of down's input on 256 CUs, so the pair launch writes the image of the first
+# 256 and runs the last 48 in 8-row blocks that the consumer stages itself; (256, 8448) and
+# (128, 8224): 264 and 257 groups, a remainder of 8 and of 1
+@pytest.mark.parametrize("shape", [(2560, 9728), (256, 96), (64, 32), (512, 1024), (256, 8448), (128, 8224)])
 def test_glu_matches_ordinary_plans(gpu, fmt, shape):
     D, F = shape
     f = Ffn(gpu, fmt, D, F, 300)
@@ -152,17 +157,19 @@ def test_glu_against_oracle(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q3"])
-@pytest.mark.parametrize("where", ["gate_row", "input"])
+@pytest.mark.parametrize("where", ["gate_row", "input", "tail_gate_row"])
 def test_glu_non_finite(gpu, fmt, where):
     """An infinite scale in one gate row (one group of down's input non-finite) or an Inf in the shared
     input (every gate / up output non-finite) must put down on the exact path, as with a self-staged
-    input: the same outputs, NaN and Inf included, as the unlinked plans."""
-    D, F = 512, 1024
+    input: the same outputs, NaN and Inf included, as the unlinked plans. tail_gate_row: the row lies
+    in the groups the consumer stages itself (F = 9728: groups 256-303)."""
+    D, F = 512, 9728 if where == "tail_gate_row" else 1024
     t = {n: synth.tensor(fmt, 330 + i, N, K) for i, (n, K, N) in enumerate([("gate", D, F), ("up", D, F),
                                                                             ("down", F, D)])}
-    if where == "gate_row":
+    if where != "input":
+        row = 9000 if where == "tail_gate_row" else 77
         sc = t["gate"]["sc"].copy()
-        sc[(77 * D) // 32 + 3] = 0x7C00          # +Inf scale in row 77 of gate
+        sc[(row * D) // 32 + 3] = 0x7C00         # +Inf scale in one row of gate
         t["gate"]["sc"] = sc
     f = Ffn(gpu, fmt, D, F, 330, tensors=t)
     if where == "input":
