@@ -135,9 +135,10 @@ def test_glu_matches_ordinary_plans(gpu, fmt, shape):
 
 @pytest.mark.parametrize("fmt", ["q4", "q3"])
 @pytest.mark.parametrize("variant", ["geglu", "no_norm_no_res"])
-def test_glu_variants_match(gpu, fmt, variant):
-    f = Ffn(gpu, fmt, 1024, 2048, 310, norm=variant != "no_norm_no_res", gelu=variant == "geglu",
-            res=variant != "no_norm_no_res")
+@pytest.mark.parametrize("F", [2048, 8448])     # 8448: 264 groups, the last 8 staged by the consumer
+def test_glu_variants_match(gpu, fmt, variant, F):
+    f = Ffn(gpu, fmt, 1024 if F == 2048 else 256, F, 310, norm=variant != "no_norm_no_res",
+            gelu=variant == "geglu", res=variant != "no_norm_no_res")
     a, b = f.run_linked(), f.run_plain()
     check_pair(a, b)
 
@@ -157,22 +158,23 @@ def test_glu_against_oracle(gpu, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["q4", "q3"])
-@pytest.mark.parametrize("where", ["gate_row", "input", "tail_gate_row"])
+@pytest.mark.parametrize("where", ["gate_row", "input", "tail_gate_row", "tail_input"])
 def test_glu_non_finite(gpu, fmt, where):
     """An infinite scale in one gate row (one group of down's input non-finite) or an Inf in the shared
     input (every gate / up output non-finite) must put down on the exact path, as with a self-staged
     input: the same outputs, NaN and Inf included, as the unlinked plans. tail_gate_row: the row lies
-    in the groups the consumer stages itself (F = 9728: groups 256-303)."""
-    D, F = 512, 9728 if where == "tail_gate_row" else 1024
+    in the groups the consumer stages itself (F = 9728: groups 256-303); tail_input: the Inf input at
+    that size (the exact path of the pair launch's 8-row blocks too)."""
+    D, F = 512, 9728 if where.startswith("tail") else 1024
     t = {n: synth.tensor(fmt, 330 + i, N, K) for i, (n, K, N) in enumerate([("gate", D, F), ("up", D, F),
                                                                             ("down", F, D)])}
-    if where != "input":
+    if where in ("gate_row", "tail_gate_row"):
         row = 9000 if where == "tail_gate_row" else 77
         sc = t["gate"]["sc"].copy()
         sc[(row * D) // 32 + 3] = 0x7C00         # +Inf scale in one row of gate
         t["gate"]["sc"] = sc
     f = Ffn(gpu, fmt, D, F, 330, tensors=t)
-    if where == "input":
+    if where in ("input", "tail_input"):
         f.x[5] = np.inf
         f.xb = gpu.up(f.x)
     a, b = f.run_linked(), f.run_plain()
