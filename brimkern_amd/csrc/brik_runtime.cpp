@@ -1043,6 +1043,12 @@ void brik_destroy(brik_ctx* c)
     if (!c) return;
     // best-effort teardown: errors here have no caller to report to
     if (c->device >= 0) (void)hipSetDevice(c->device);
+    if (c->stream && c->graph_capturing) {
+        // a capture left open: end it (nothing recorded in it ran) so the stream can be synchronized
+        hipGraph_t dropped = nullptr;
+        if (hipStreamEndCapture(c->stream, &dropped) == hipSuccess && dropped) (void)hipGraphDestroy(dropped);
+        c->graph_capturing = false;
+    }
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     for (const brik_ctx::Upload& u : c->ring_inflight) (void)hipEventDestroy(u.ev);
     for (hipEvent_t e : c->ring_events) (void)hipEventDestroy(e);
@@ -1851,7 +1857,12 @@ int brik_graph_end(brik_ctx* c, brik_graph** out)
     if (!c->graph_capturing) return fail(c, BRIK_EINVAL, "graph_end: no capture is open");
     c->graph_capturing = false;
     brik_graph* g = new (std::nothrow) brik_graph();
-    if (!g) return BRIK_ENOMEM;
+    if (!g) {
+        // close the capture all the same, so the stream works again
+        hipGraph_t dropped = nullptr;
+        if (hipStreamEndCapture(c->stream, &dropped) == hipSuccess && dropped) (void)hipGraphDestroy(dropped);
+        return BRIK_ENOMEM;
+    }
     hipError_t e = hipStreamEndCapture(c->stream, &g->graph);
     if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
     if (e != hipSuccess) {

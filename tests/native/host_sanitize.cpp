@@ -471,6 +471,15 @@ int main(int argc, char** argv)
         brik_destroy(ctx);
         ctx = nullptr;
     }
+    // a context destroyed while a capture is still open, then a fresh one
+    brik_ctx* c2 = nullptr;
+    CHECK(brik_create(0, &c2) == BRIK_OK, "create for the open-capture case");
+    if (c2) {
+        CHECK(brik_graph_begin(c2) == BRIK_OK, "graph_begin");
+        brik_destroy(c2);
+    }
+    CHECK(brik_create(0, &c2) == BRIK_OK, "create after destroying an open capture");
+    if (c2) brik_destroy(c2);
     std::printf("device checks done: %d failure(s)\n", fails);
     return fails ? 1 : 0;
 }
