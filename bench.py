@@ -330,8 +330,9 @@ def decode_layers_fused(ctx, reps, layers, steps, warmup, graph_replay=True):
     return {"us_per_layer": round(ms * 1e3 / layers, 2), "weight_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "replay": replay,
             "eager_us_per_layer": round(ms_eager * 1e3 / layers, 2), "launches_per_layer": 4, "layers": layers,
-            "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up (+ staged swiglu image), "
-                     "down (copies the image) + residual"}
+            "fused": "rmsnorm -> q/k/v, wo + residual, rmsnorm -> gate/up (+ staged swiglu image of the "
+                     "first 256 groups, swiglu values of the rest), down (copies the image, stages the rest) "
+                     "+ residual"}
 
 
 def gemv_single_cfg(ctx, fmt, K, N, seed, steps, warmup, cache_bytes=768 << 20):
