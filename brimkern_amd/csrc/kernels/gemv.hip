@@ -24,7 +24,7 @@
 //     the loads of x, so staging x overlaps their latency;
 //   * each lane stores its running partial sum of a row to LDS every step (branch-free loop body); after
 //     the loop, the TEAM partials of a row are loaded by TEAM lanes at once and added with DPP steps
-//     (row_sums), and the row's first lane writes y.
+//     within 16-lane rows and lane exchanges across rows (row_sums), and the row's first lane writes y.
 #include "common.h"
 #include "xprep.h"
 #include "stage_abi.h"
@@ -542,8 +542,8 @@ __device__ __forceinline__ bool pipeline(W& w, const typename W::XS& X, const fl
 
 // The sums of `rows` rows of PARTS lane partials each (LDS, row-major: partial l of row q at
 // part[q * PARTS + l]): PARTS consecutive threads load one row's partials together and add them with
-// DPP steps (team_sum, within 16-lane rows, then across them), and the row's first lane calls
-// out(q, sum). Every row sums in the same order, whichever thread holds it. Called by every thread of
+// DPP steps within 16-lane rows and __shfl_xor exchanges across them (team_sum), and the row's first
+// lane calls out(q, sum). Every row sums in the same order, whichever thread holds it. Called by every thread of
 // the block (NT threads, a multiple of PARTS); the partials must be complete (after a barrier).
 template <int PARTS, int NT, class Out>
 __device__ __forceinline__ void row_sums(const float* __restrict__ part, int rows, Out out)
