@@ -111,6 +111,11 @@ constexpr unsigned kStageThreads = 1024;       // threads of a staging block (la
 constexpr double kPrestageGroupRows = 8192;
 constexpr long kPrestageMaxSets = 4;
 constexpr long kPrestageMinSets = 2;
+// The last jobs of a pre-staged plan of many blocks run in single-set blocks, about this many of them
+// (whole jobs): the launch's drain, where fewer blocks than the CUs hold remain, then ends on short
+// blocks (36-layer q4 set, 3 rounds of alternating processes: 298.6-298.9 us per step with none,
+// 297.9-298.2 with 256 or 768, 298.2-298.3 with 1536; two-set tail blocks were slower, 299.2-300.3 us).
+constexpr long kPrestageTailBlocks = 512;
 constexpr long kPlanMinBlocks = 1024;          // grouped-plan blocks, at least (while sets > 1)
 
 enum Fmt { F_Q8 = 8, F_Q4 = 4, F_Q3 = 3 };
@@ -1579,6 +1584,15 @@ static int plan_create(brik_ctx* c, int fmt, const brik_gemv_job_ex* jobs, int n
         }
         if (blocks >= kPlanMinBlocks || maxsets == 1) break;
         for (int k = 0; k < njobs; ++k) sets[k] = (sets[k] + 1) / 2;
+    }
+    long nblk = 0;
+    for (int k = 0; k < njobs; ++k) nblk += (sorted[k].job.N + sets[k] * rpi - 1) / (sets[k] * rpi);
+    if (prestage && nblk >= 8 * kPrestageTailBlocks) {   // plans of many blocks only: the tail stays short
+        long tail = kPrestageTailBlocks;
+        for (int k = njobs - 1; k >= 0 && tail > 0; --k) {
+            sets[k] = 1;
+            tail -= (sorted[k].job.N + rpi - 1) / rpi;
+        }
     }
     if (c->opt_plan_sets > 0)
         for (int k = 0; k < njobs; ++k) sets[k] = c->opt_plan_sets < maxsets ? c->opt_plan_sets : maxsets;
