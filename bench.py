@@ -376,7 +376,8 @@ def lm_head_topk_cfg3(ctx, steps, warmup, gemv_us, cache_bytes=768 << 20):
         ctx.free(bb)
     return {"us": round(ms * 1e3, 2), "passes_alone_us": round(ms_p * 1e3, 2),
             "over_gemv_us": round(ms * 1e3 - gemv_us, 2), "readback_bytes": 8 * k,
-            "launches": "brik_gemv_q3 + brik_topk_prep + brik_topk_select"}
+            "launches": "brik_gemv_stage1_q3 + brik_gemvh_q3 (head GEMV, softcap / penalty / 16-logit maxima "
+                        "in its epilogue) + brik_topk_select; passes_alone: brik_topk_prep + brik_topk_select"}
 
 
 def quantize_f1(ctx, steps, warmup):

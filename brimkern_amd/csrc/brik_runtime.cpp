@@ -76,6 +76,10 @@ static_assert(kGluThreads / kGluVariant.team * kGluVariant.r == 2 * kGluRows, "G
 constexpr int kGluTailRows = 8;
 static_assert(kGluThreads / 64 * kGluVariant.r == 2 * kGluTailRows, "GLU tail block rows");
 
+// the variant of the LM-head kernels brik_gemvh_<fmt>_t16_r2_u5_d2 (the one a staged single q4 / q3
+// matrix runs)
+constexpr int kHeadVariant = 7;
+
 constexpr int kGroup = 32;
 // GEMM block tiles (BM rows x 32 TN NW columns, NW waves), in the order of BRIK_GEMM_FMT in gemm.hip:
 // brik_gemm_<fmt>_<BM>x<TN> (NW = 4) and brik_gemm_<fmt>_<BM>x<TN>w8 (NW = 8).
@@ -180,6 +184,7 @@ struct brik_ctx {
     hipFunction_t gemv[3][kNumGemvVariants] = {};
     hipFunction_t gemvg[3][kNumGemvVariants] = {};
     hipFunction_t gemvp[3] = {};                 // GLU pair kernels (q4, q3; q8 has none)
+    hipFunction_t gemvh[3] = {};                 // LM heads with the top-k pre-work (q4, q3; variant kHeadVariant)
     hipFunction_t gemm[3][kNumGemmTiles] = {};
     hipFunction_t gemmg[kNumGemmTiles] = {};    // expert-grouped q4 kernels (brik_gemmg_q4_*)
     hipFunction_t gemmg_adapt[2] = {};           // brik_gemmg_q4_64a (4 waves), brik_gemmg_q4_64aw8 (8 waves)
@@ -678,8 +683,21 @@ int gemv_variant(brik_ctx* c, Fmt f, long rows, int kmin, bool staged, bool sing
 }
 
 
+// The sampling pre-work an LM head can run in its epilogue (brik_gemvh_*): the arguments of
+// brik_topk_prep. `done` tells the caller whether the head ran it (else the caller runs the passes).
+struct HeadArgs {
+    float cap;
+    int pen;
+    float penalty;
+    const int32_t* recent;
+    int n_recent;
+    uint32_t* maxima;
+    bool done;
+};
+
 int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, const void* sc,
-           const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr)
+           const void* mn, float* y, int M, int K, int N, const Scratch* fixed = nullptr,
+           HeadArgs* head = nullptr)
 {
     c->last_path = 0;
     if (K == 0) return fill_zero(c, y, (size_t)M * N);   // empty sums, whatever the path
@@ -718,8 +736,20 @@ int matmul(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, c
             void* sargs[] = {&x, &Ki, &img};
             HIP_TRY_RC(launch(c, f == F_Q4 ? K_GEMV_STAGE1_Q4 : K_GEMV_STAGE1_Q3, 1, 1, kStageThreads, 0, sargs));
         }
-        void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged};
         c->last_path = stage1 ? BRIK_PATH_GEMV_STAGED : BRIK_PATH_GEMV;
+        if (head && stage1 && v == kHeadVariant) {
+            // the LM head with the top-k pre-work in its epilogue: its LDS adds the row sums of a block
+            // and a bitmap of its rows
+            const long rows = (long)rpi * ((sets + gx - 1) / gx);
+            const size_t hlds = lds + sizeof(float) * (size_t)rows + sizeof(uint32_t) * (size_t)((rows + 31) / 32);
+            if (hlds <= kGemvMaxLds) {
+                void* hargs[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged, &head->cap, &head->pen,
+                                 &head->penalty, &head->recent, &head->n_recent, &head->maxima};
+                head->done = true;
+                return launch_fn(c, c->gemvh[fmt_index(f)], gx, 1, 256, hlds, hargs);
+            }
+        }
+        void* args[] = {&x, &p0, &p1, &sc, &mn, &y, &Ki, &Ni, &staged};
         return launch_fn(c, c->gemv[fmt_index(f)][v], gx, (unsigned)M, 256, lds, args);
     }
     return gemm(c, f, x, p0, p1, sc, mn, y, M, K, N, nullptr, 0, fixed);
@@ -749,6 +779,14 @@ int check_topk(brik_ctx* c, const char* who, int n, const int32_t* recent, int n
     return BRIK_OK;
 }
 
+// brik_topk_select over m lane maxima (one per 16 logits) in the top-k workspace.
+int topk_select(brik_ctx* c, float* logits, int n, int m, int k, int32_t* ids, float* vals)
+{
+    uint32_t* maxima = static_cast<uint32_t*>(c->tws);
+    void* args[] = {&logits, &n, &k, &maxima, &m, &ids, &vals};
+    return launch(c, K_TOPK_SELECT, 1, 1, 1024, 0, args);
+}
+
 // The passes over a device logits vector (modified in place); the top-k workspace is ensured by the
 // caller. Two launches: brik_topk_prep (softcap, penalty, lane maxima), brik_topk_select (one block:
 // bound, candidates, sort, output).
@@ -761,9 +799,7 @@ int topk_passes(brik_ctx* c, float* logits, int n, const int32_t* recent, int n_
         void* args[] = {&logits, &n, &softcap, &recent, &n_recent, &penalty, &peni, &maxima};
         HIP_TRY_RC(launch(c, K_TOPK_PREP, (unsigned)topk_blocks(n), 1, 256, 0, args));
     }
-    int m = (int)topk_maxima(n);
-    void* args[] = {&logits, &n, &k, &maxima, &m, &ids, &vals};
-    return launch(c, K_TOPK_SELECT, 1, 1, 1024, 0, args);
+    return topk_select(c, logits, n, (int)topk_maxima(n), k, ids, vals);
 }
 
 int ensure_topk_ws(brik_ctx* c, size_t bytes) { return ensure_buf(c, c->tws, c->tws_bytes, bytes); }
@@ -778,7 +814,11 @@ int lm_head_topk(brik_ctx* c, const char* who, Fmt f, const float* x, const void
     HIP_TRY_RC(ensure_topk_ws(c, topk_logits_off(vocab) + (size_t)vocab * 4));
     float* logits = reinterpret_cast<float*>(static_cast<char*>(c->tws) + topk_logits_off(vocab));
     HIP_TRY_RC(check_mm(c, who, x, p0, p1, sc, mn, logits, 1, K, vocab, f));
-    HIP_TRY_RC(matmul(c, f, x, p0, p1, sc, mn, logits, 1, K, vocab));
+    // a q4 / q3 head staged once per call runs the pre-work in its epilogue (no pass over the logits);
+    // any other takes the separate prep launch
+    HeadArgs head{softcap, pen ? 1 : 0, penalty, recent, n_recent, static_cast<uint32_t*>(c->tws), false};
+    HIP_TRY_RC(matmul(c, f, x, p0, p1, sc, mn, logits, 1, K, vocab, nullptr, &head));
+    if (head.done) return topk_select(c, logits, vocab, (vocab + 15) / 16, k, ids, vals);
     return topk_passes(c, logits, vocab, recent, n_recent, penalty, softcap, k, ids, vals, pen);
 }
 
@@ -995,6 +1035,9 @@ int brik_create(int device, brik_ctx** out)
         snprintf(name, sizeof name, "brik_gemvp_%s_t%d_r%d_u%d_d%d_n%d", kFmtNames[f], gv.team, gv.r, gv.u, gv.d,
                  kGluThreads);
         if (hipModuleGetFunction(&c->gemvp[f], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
+        const GemvVariant& hv = kGemvVariants[kHeadVariant];
+        snprintf(name, sizeof name, "brik_gemvh_%s_t%d_r%d_u%d_d%d", kFmtNames[f], hv.team, hv.r, hv.u, hv.d);
+        if (hipModuleGetFunction(&c->gemvh[f], c->module, name) != hipSuccess) return bail(BRIK_EMODULE);
     }
     for (int f = 0; f < 3; ++f)
         for (int t = 0; t < kNumGemmTiles; ++t) {

@@ -46,6 +46,15 @@ __device__ __forceinline__ brsrc_t make_rsrc(const void* p, uint32_t bytes)
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, BRIK_BUF_DWORD3);
 }
 
+// Order-preserving map of f32 to u32 (larger float -> larger key); NaN -> 0 (ranks below every
+// number). The top-k passes compare logits through it.
+__device__ __forceinline__ uint32_t order_key(float v)
+{
+    if (v != v) return 0u;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // p, with its provenance hidden from the compiler (an empty asm on a uniform value). Loads through a
 // restrict-qualified const pointer are treated as reads of constant memory, which the compiler may
 // reorder freely; through the laundered pointer they stay in program order relative to other memory
@@ -92,6 +101,15 @@ __device__ __forceinline__ float sum16(float v)
     v = BRIK_DPP_ADD(v, DPP_QUAD_2301);
     v = BRIK_DPP_ADD(v, DPP_ROW_ROR4);
     return BRIK_DPP_ADD(v, DPP_ROW_ROR8);
+}
+
+// Unsigned maximum over aligned groups of 16 lanes (one DPP row); every lane receives the result.
+__device__ __forceinline__ uint32_t max16u(uint32_t v)
+{
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_1032, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_QUAD_2301, 0xF, 0xF, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_ROW_ROR4, 0xF, 0xF, false));
+    return max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, DPP_ROW_ROR8, 0xF, 0xF, false));
 }
 
 // Wait until at most N vector-memory loads of this wave are in flight (direct global->LDS loads count;

@@ -557,14 +557,68 @@ __device__ __forceinline__ void row_sums(const float* __restrict__ part, int row
     }
 }
 
+// The sampling pre-work of an LM head (topk.hip, brik_topk_prep) applied to the head's own output
+// rows as they are written: softcap, then the repetition penalty for rows listed in `recent`, and the
+// maximum order key of every 16 consecutive logits into maxima[n / 16] (the layout brik_topk_select
+// reads), so the logits are not read back by a separate pass.
+struct HeadEpi {
+    float cap;                 // softcap when > 0
+    int pen;                   // penalty applies
+    float penalty;
+    const int32_t* recent;     // n_recent ids
+    int n_recent;
+    uint32_t* maxima;          // one per 16 logits
+};
+
+// Rows of the block (q = p RPI + i: row r0 + p rstep + i) given their sums v[q] in LDS: the head's
+// transforms, the logits written, the 16-row maxima. RPI and the set starts are multiples of 16, so 16
+// consecutive q are one chunk of 16 consecutive rows. marks: a bitmap of the block's rows (LDS, zeroed
+// by the caller's earlier pass). Every thread of the block calls it.
+template <int RPI, int NT>
+__device__ __forceinline__ void head_finish(const HeadEpi& h, const float* __restrict__ v, uint32_t* marks,
+                                            float* __restrict__ yrow, int N, int r0, int rstep, int nsets)
+{
+    static_assert(RPI % 16 == 0 && NT % 16 == 0, "16-row chunks");
+    const int rows = nsets * RPI;
+    if (h.pen) {
+        // ids outside [0, N) are skipped, as brik_topk_prep does
+        for (int r = (int)threadIdx.x; r < h.n_recent; r += NT) {
+            const int id = h.recent[r];
+            const int d = id - r0;
+            if (id >= 0 && id < N && d >= 0) {
+                const int p = d / rstep, i = d % rstep;
+                if (p < nsets && i < RPI) atomicOr(&marks[(p * RPI + i) >> 5], 1u << ((p * RPI + i) & 31));
+            }
+        }
+        __syncthreads();
+    }
+    for (int q0 = 0; q0 < rows; q0 += NT) {              // the same trips for every thread (DPP below)
+        const int q = q0 + (int)threadIdx.x;
+        const int n = r0 + (q / RPI) * rstep + q % RPI;
+        uint32_t key = 0u;
+        if (q < rows && n < N) {
+            float t = v[q];
+            const bool p = h.pen && ((marks[q >> 5] >> (q & 31)) & 1u);
+            if (h.cap > 0.f) t = h.cap * tanhf(t / h.cap);
+            if (p) t = t > 0.f ? t / h.penalty : t * h.penalty;
+            yrow[n] = t;
+            key = order_key(t);
+        }
+        key = max16u(key);
+        if ((q & 15) == 0 && q < rows && n < N) h.maxima[n >> 4] = key;
+    }
+}
+
 // Rows [r0, r1) of one N x K matrix in steps of rstep: first loads, x staging, the pipelined steps,
 // then the cross-lane sums of the LDS partials are written to y. The block owns row sets
-// p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI).
-template <int FMT, class W, int D>
+// p = 0 .. nsets-1 with rows r0 + p * rstep + [0, RPI). With a head epilogue (HEAD, he), the sums go
+// through head_finish instead: its LDS (the sums, the penalty bitmap) follows the partials.
+template <int FMT, class W, int D, bool HEAD = false>
 __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const Fuse& F, const Planes& P,
                                             float* __restrict__ yrow, const float* __restrict__ res,
                                             int N, int K, int r0, int r1, int rstep, unsigned char* lds,
-                                            const unsigned char* __restrict__ staged, int img_groups = 0)
+                                            const unsigned char* __restrict__ staged, int img_groups = 0,
+                                            const HeadEpi* he = nullptr)
 {
     W w;
     w.G = K / BRIK_GROUP;
@@ -577,9 +631,22 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
     w.part = (float*)(lds + W::xs_bytes(K));
     const bool exact = w.even() ? pipeline<FMT, W, D, true>(w, X, x, F, K, S, staged, lds, img_groups)
                                 : pipeline<FMT, W, D, false>(w, X, x, F, K, S, staged, lds, img_groups);
+    float* hv = w.part + (size_t)nsets * W::RPI * W::PARTS;           // HEAD: the row sums
+    uint32_t* marks = (uint32_t*)(hv + nsets * W::RPI);               // HEAD: the penalty bitmap
+    if constexpr (HEAD)
+        for (int i = (int)threadIdx.x; i < (nsets * W::RPI + 31) / 32; i += W::NT) marks[i] = 0u;
     if (exact) {
         // teams of 16 lanes over RPI rows per iteration
         gemv_rows_exact<FMT, W::RPI, W::NT>(x, F, *X.inv, P, yrow, res, K, r0, r1, rstep);
+        if constexpr (HEAD) {
+            __syncthreads();       // the rows just written are visible to the block
+            for (int q = (int)threadIdx.x; q < nsets * W::RPI; q += W::NT) {
+                const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
+                hv[q] = n < r1 ? yrow[n] : 0.f;
+            }
+            __syncthreads();
+            head_finish<W::RPI, W::NT>(*he, hv, marks, yrow, r1, r0, rstep, nsets);
+        }
         return;
     }
     __syncthreads();
@@ -590,9 +657,15 @@ __device__ __forceinline__ void gemv_matrix(const float* __restrict__ x, const F
         const int n = r0 + (q / W::RPI) * rstep + q % W::RPI;
         if (n < r1) {
             v *= inv;
-            yrow[n] = res ? res[n] + v : v;
+            v = res ? res[n] + v : v;
+            if constexpr (HEAD) hv[q] = v;
+            else yrow[n] = v;
         }
     });
+    if constexpr (HEAD) {
+        __syncthreads();
+        head_finish<W::RPI, W::NT>(*he, hv, marks, yrow, r1, r0, rstep, nsets);
+    }
 }
 
 // One matrix, one activation row per grid.y. `staged` (M = 1 only): the row's LDS image, written by
@@ -737,6 +810,26 @@ __device__ __forceinline__ void gemv_glu_pair(const brik_gemv_job_ex& jg, const 
 BRIK_GEMV_FMT(q4, FMT_Q4)
 BRIK_GEMV_FMT(q8, FMT_Q8)
 BRIK_GEMV_FMT(q3, FMT_Q3)
+
+// An LM head with the sampling pre-work in its epilogue (HeadEpi, head_finish): the q4 / q3 variant of
+// single matrices whose x image is staged once per call (whole rows, two rows per team). The runtime
+// (brik_runtime.cpp, lm_head_topk) then runs brik_topk_select on the maxima it writes.
+#define BRIK_GEMV_HEAD(FMTN, FMT, TEAM, RR, UU, DD)                                                      \
+    extern "C" __global__ __launch_bounds__(256) void brik_gemvh_##FMTN##_t##TEAM##_r##RR##_u##UU##_d##DD( \
+        const float* __restrict__ x, const uint8_t* __restrict__ p0, const uint8_t* __restrict__ p1,      \
+        const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn, float* __restrict__ y, int K,   \
+        int N, const unsigned char* __restrict__ staged, float cap, int pen, float penalty,              \
+        const int32_t* __restrict__ recent, int n_recent, uint32_t* __restrict__ maxima)                 \
+    {                                                                                                    \
+        extern __shared__ __align__(16) unsigned char lds[];                                             \
+        using W_ = Work<FMT, TEAM, RR, UU>;                                                              \
+        const HeadEpi he{cap, pen, penalty, recent, n_recent, maxima};                                  \
+        gemv_matrix<FMT, W_, DD, true>(x, Fuse{nullptr, nullptr, 0.f, 0}, Planes{p0, p1, sc, mn}, y,     \
+                                       nullptr, N, K, (int)blockIdx.x * W_::RPI, N,                      \
+                                       (int)gridDim.x * W_::RPI, lds, staged, 0, &he);                   \
+    }
+BRIK_GEMV_HEAD(q4, FMT_Q4, 16, 2, 5, 2)
+BRIK_GEMV_HEAD(q3, FMT_Q3, 16, 2, 5, 2)
 
 // GLU pair launch: jobs[0] = gate, jobs[1] = up. Block b < nfull (NT threads, teams of TEAM lanes)
 // runs rows [H b, H b + H) of both, H = RPI / 2 = 32 (one quantization group of down's input), and

@@ -9,7 +9,9 @@
 // id (smaller first), on a (value, id) key that is unique per element. Two launches:
 //   a. brik_topk_prep: each block takes 4096 logits, applies the softcap and the penalty (the recent
 //      ids of its range are marked in an LDS bitmap), writes them back, and every lane writes the
-//      maximum of its 16 ("lane maxima", one per 16 logits).
+//      maximum of its 16 consecutive logits ("lane maxima": maximum q covers logits [16q, 16q + 16)).
+//      A q4 / q3 LM head staged once per call runs these passes in its own epilogue instead
+//      (gemv.hip, brik_gemvh_*), with the same maxima layout.
 //   b. brik_topk_select, one block: folds the lane maxima into 256 maxima of disjoint element sets and
 //      takes the k-th largest of those as a bound (k distinct elements reach it, so it is at most the
 //      vector's k-th largest; for logits only a few more elements than k pass it). An element at or
@@ -27,13 +29,8 @@ constexpr int TOPK_MAX = 64;
 constexpr int TOPK_CAP = 8192;      // candidate list capacity (keys)
 constexpr int TOPK_BLOCK = 4096;    // logits per block: 4 waves x 64 lanes x 16
 
-// Order-preserving map of f32 to u32 (larger float -> larger key); NaN -> 0.
-__device__ __forceinline__ uint32_t okey(float v)
-{
-    if (v != v) return 0u;
-    const uint32_t b = __builtin_bit_cast(uint32_t, v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
+// The order key of common.h (NaN -> 0).
+__device__ __forceinline__ uint32_t okey(float v) { return order_key(v); }
 
 __device__ __forceinline__ float okey_inv(uint32_t k)
 {
@@ -66,15 +63,15 @@ __device__ __forceinline__ void bitonic_desc(K* s, int P)
 
 }  // namespace
 
-// Block b: logits [4096 b, 4096 b + 4096); wave w, lane l, step j: element 4096 b + 1024 w + 64 j + l.
-// Lane maximum q = 256 b + 64 w + l.
+// Block b: logits [4096 b, 4096 b + 4096); thread t: the 16 consecutive logits 4096 b + 16 t + j and
+// lane maximum q = 256 b + t.
 extern "C" __global__ __launch_bounds__(256) void brik_topk_prep(float* __restrict__ logits, int n, float cap,
                                                                  const int32_t* __restrict__ recent, int n_recent,
                                                                  float penalty, int pen,
                                                                  uint32_t* __restrict__ maxima)
 {
     __shared__ uint32_t marks[TOPK_BLOCK / 32];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const long base = (long)blockIdx.x * TOPK_BLOCK;
     if (pen) {
         for (int i = tid; i < TOPK_BLOCK / 32; i += 256) marks[i] = 0u;
@@ -89,17 +86,29 @@ extern "C" __global__ __launch_bounds__(256) void brik_topk_prep(float* __restri
         }
         __syncthreads();
     }
-    // all 16 loads of a thread first (one memory round trip; four at a time took four)
+    // all 16 loads of a thread first (one memory round trip; four at a time took four): four 16-byte
+    // buffer loads of a whole chunk (the logits need only 4-byte alignment), else one at a time
     float raw[16];
+    const long c0 = base + 16 * tid;
+    if (c0 + 16 <= n) {
+        const brsrc_t r = make_rsrc(logits, (uint32_t)n * 4u);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const long i = base + 1024 * wave + 64 * j + lane;
-        raw[j] = i < n ? logits[i] : 0.f;
+        for (int u = 0; u < 4; ++u) {
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(c0 + 4 * u) * 4u, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t w = v[e];      // a scalar first: bit_cast of v[e] itself read element 0
+                raw[4 * u + e] = __builtin_bit_cast(float, w);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) raw[j] = c0 + j < n ? logits[c0 + j] : 0.f;
     }
     uint32_t m = 0u;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const int o = 1024 * wave + 64 * j + lane;
+        const int o = 16 * tid + j;
         const long i = base + o;
         if (i < n) {
             float v = raw[j];
@@ -116,7 +125,8 @@ extern "C" __global__ __launch_bounds__(256) void brik_topk_prep(float* __restri
 constexpr int TOPK_LANES = 2048;    // lanes read back by the select block, at most
 constexpr int TOPK_STAGE = 16384;   // lane maxima staged in LDS (vectors of up to 262144 logits)
 
-// One block of 1024 threads; m = the number of lane maxima (256 per prep block).
+// One block of 1024 threads; m = the number of lane maxima (256 per prep block, or one per 16 logits
+// from a fused LM head), maximum q covering logits [16 q, 16 q + 16).
 extern "C" __global__ __launch_bounds__(1024) void brik_topk_select(const float* __restrict__ logits, int n, int k,
                                                                     const uint32_t* __restrict__ maxima, int m,
                                                                     int32_t* __restrict__ out_ids,
@@ -186,7 +196,7 @@ extern "C" __global__ __launch_bounds__(1024) void brik_topk_select(const float*
     if (!overflow) {
         for (uint32_t e = tid; e < nl * 16u; e += 1024) {
             const uint32_t q = lanes[e >> 4], j = e & 15u;
-            const long i = (long)(q >> 8) * TOPK_BLOCK + 1024 * ((q >> 6) & 3) + 64 * j + (q & 63);
+            const long i = 16L * q + j;
             if (i < n) {
                 const uint32_t key = okey(logits[i]);
                 if (key >= bound) {

@@ -148,3 +148,56 @@ def test_lm_head_topk(gpu, fmt):
     # the GPU logits agree with the oracle's to ~1e-6, so near-ties may swap: the reference's own rule
     reference_rule(ids, vals, ref, rids)
     assert len(set(ids.tolist())) == k
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q3"])
+@pytest.mark.parametrize("vocab,cap,penalty", [(151936, 30.0, 1.15), (24583, 0.0, 1.3), (32768, 25.0, 1.0)])
+def test_lm_head_topk_fused_epilogue(gpu, fmt, vocab, cap, penalty):
+    """A q4 / q3 head of at least 24576 rows runs the softcap, the penalty and the 16-logit maxima in
+    its GEMV epilogue (brik_gemvh_*): its ids and values must be bit-identical to the same head's
+    logits (brik_matmul_t_*, the same GEMV variant) passed through brik_logits_topk."""
+    K, k = 256, 64
+    t = synth.tensor(fmt, 710, vocab, K)
+    x = synth.normal(711, K)
+    planes = gpu.planes(fmt, t)
+    recent = sorted({0, 15, 16, 31, 32, 777, vocab // 2, vocab - 17, vocab - 16, vocab - 1}
+                    | set((synth.uniform(712, 40) * vocab).astype(np.int64).tolist()))
+    xb, rb = gpu.up(x), gpu.up(np.asarray(recent, np.int32))
+    ob = gpu.up(np.zeros(2 * k, np.int32))
+    print(f"fused head: fmt={fmt} vocab={vocab} cap={cap} penalty={penalty}", flush=True)
+    gpu.ctx.lm_head_topk(fmt, xb, planes, K, vocab, rb, len(recent), penalty, cap, k, ob, ob.offset(4 * k))
+    ids = gpu.ctx.download(ob, np.int32, k)
+    vals = gpu.ctx.download(ob, np.float32, k, src_offset=4 * k)
+    yb = gpu.up(np.zeros(vocab, np.float32))
+    getattr(gpu.ctx, f"matmul_t_{fmt}")(xb, *planes, yb, 1, K, vocab)
+    gpu.ctx.sync()
+    plain = gpu.ctx.download(yb, np.float32, vocab)
+    pids, pvals, _ = run_topk(gpu, plain, recent, penalty, cap, k)
+    assert np.array_equal(ids, pids)
+    assert np.array_equal(vals.view(np.uint32), pvals.view(np.uint32))
+    ref, rids, _ = oracle_passes(plain, recent, penalty, cap, k)
+    reference_rule(ids, vals, ref, rids)
+
+
+@pytest.mark.parametrize("fmt", ["q4", "q3"])
+def test_lm_head_topk_fused_non_finite_input(gpu, fmt):
+    """An Inf in x sends the fused head through its exact path; the epilogue then reads the rows back:
+    the same ids and values as the unfused form."""
+    K, vocab, k = 128, 24576, 8
+    t = synth.tensor(fmt, 720, vocab, K)
+    x = synth.normal(721, K)
+    x[3] = np.inf
+    planes = gpu.planes(fmt, t)
+    recent = [1, 2, 24575]
+    xb, rb = gpu.up(x), gpu.up(np.asarray(recent, np.int32))
+    ob = gpu.up(np.zeros(2 * k, np.int32))
+    gpu.ctx.lm_head_topk(fmt, xb, planes, K, vocab, rb, len(recent), 1.2, 20.0, k, ob, ob.offset(4 * k))
+    ids = gpu.ctx.download(ob, np.int32, k)
+    vals = gpu.ctx.download(ob, np.float32, k, src_offset=4 * k)
+    yb = gpu.up(np.zeros(vocab, np.float32))
+    getattr(gpu.ctx, f"matmul_t_{fmt}")(xb, *planes, yb, 1, K, vocab)
+    gpu.ctx.sync()
+    plain = gpu.ctx.download(yb, np.float32, vocab)
+    pids, pvals, _ = run_topk(gpu, plain, recent, 1.2, 20.0, k)
+    assert np.array_equal(ids, pids)
+    assert np.array_equal(vals.view(np.uint32), pvals.view(np.uint32))
