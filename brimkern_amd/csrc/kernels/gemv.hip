@@ -301,15 +301,26 @@ __device__ __forceinline__ void code_nibbles(const Grp<FMT>& d, uint32_t (&c)[4]
 }
 
 // q4 and q3 on v_dot8_i32_i4: x as signed 4-bit digit planes (xprep.h, xstage_d), codes as signed
-// nibbles (code_nibbles). Per (row, group): 24 dot8 run the Horner chain over the six digit planes
-// (most significant first, shifting by 4 between planes; for q4 the last shift also adds the staged
-// 8 * sum X that undoes the -8), then one conversion, one exact rescale and two FMAs.
-// The dot products use the clamping form: no partial sum can overflow, so the value is the same,
-// and the compiler keeps the chain as written instead of splitting it into six sums.
+// nibbles (code_nibbles). Per (row, group): 24 dot8 over the six digit planes d_5 .. d_0 in Horner
+// chains, then one conversion, one exact rescale and two FMAs. With DigitChains<FMT> = C chains,
+// chain k takes planes 5 - k, 5 - k - C, ... (most significant first, shifting by 4C bits between
+// them), and sum X q = sum_k chain_k * 16^(C - 1 - k) (+ for q4 the staged 8 * sum X that undoes the
+// -8), an exact int32 in wrapping arithmetic (no chain's partial sum can overflow: each is below
+// 2048 * (1 + 2^(4C) + ...) < 2^28). The chains of a group's R rows are independent, so 3 chains
+// give 3R dot8 sequences to interleave where one serial chain of 24 waits for each result: q4 decode
+// launches of one or two waves per SIMD (Qwen3-4B, graph-replayed) q 4.35 -> 4.10 us, gate 6.40 ->
+// 6.20, down 8.44 -> 8.20, k/v 3.45 -> 3.34, the fused decoder layer 30.9 -> 30.2 us, the 36-layer
+// set 296.4 -> 295.5 us per step. The q3 LM head, whose code assembly already supplies independent
+// work and which runs 4 waves per SIMD, measured 37.3 us with one chain against 37.6 with three, so
+// q3 keeps one. The dot products use the clamping form: no partial sum overflows, so the value is
+// the same, and the compiler keeps each chain as written instead of splitting it into sums.
 //
 // P = 2 (GLU pairs): two matrices of equal shape on the same staged x. A team's R rows are then
 // RH = R / 2 rows of the first matrix (rs) followed by the same rows of the second (rs2): row r of
 // the team is row n0(p) + r % RH of matrix r / RH. NTB: threads per block.
+template <int FMT> struct DigitChains { static constexpr int v = FMT == FMT_Q4 ? 3 : 1; };
+static_assert(6 % DigitChains<FMT_Q4>::v == 0 && 6 % DigitChains<FMT_Q3>::v == 0, "whole chains");
+
 template <int FMT, int TEAM, int R, int U, int P = 1, int NTB = 256>
 struct WorkD {
     static_assert(P == 1 || (P == 2 && R % 2 == 0), "pair rows");
@@ -381,19 +392,31 @@ struct WorkD {
 #pragma unroll
             for (int n = 0; n < 6; ++n) L[n] = *(const u32x4_t*)(a + 16 * n);
             const i32x4_t xs = *(const i32x4_t*)(a + 96);                   // {sum x, e - 22, 8 sum X, 0}
+            uint32_t c[R][4];
+#pragma unroll
+            for (int r = 0; r < R; ++r) code_nibbles<FMT>(d[u][r], c[r]);
+            constexpr int CH = DigitChains<FMT>::v;
+            int ch[CH][R];
+#pragma unroll
+            for (int t = 0; t < 6 / CH; ++t) {
+#pragma unroll
+                for (int k = 0; k < CH; ++k)
+#pragma unroll
+                    for (int r = 0; r < R; ++r) ch[k][r] = t == 0 ? 0 : ch[k][r] << (4 * CH);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int k = 0; k < CH; ++k)
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            ch[k][r] = __builtin_amdgcn_sdot8((int)c[r][j], (int)L[5 - k - CH * t][j], ch[k][r], true);
+            }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                uint32_t c[4];
-                code_nibbles<FMT>(d[u][r], c);
-                int v = 0;
+                uint32_t vu = FMT == FMT_Q4 ? (uint32_t)xs.z : 0u;
 #pragma unroll
-                for (int n = 5; n >= 0; --n) {
-                    if (n == 0 && FMT == FMT_Q4) v = (v << 4) + xs.z;
-                    else if (n != 5) v <<= 4;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) v = __builtin_amdgcn_sdot8((int)c[j], (int)L[n][j], v, true);
-                }
-                const float pr = ldexpf((float)v, xs.y);                       // exact rescale
+                for (int k = 0; k < CH; ++k) vu += (uint32_t)ch[k][r] << (4 * (CH - 1 - k));
+                const float pr = ldexpf((float)(int)vu, xs.y);                // exact rescale
                 acc[r] = __builtin_fmaf(f16_bits_to_f32(d[u][r].s), pr, acc[r]);
                 acc[r] = __builtin_fmaf(f16_bits_to_f32(d[u][r].m), __builtin_bit_cast(float, xs.x), acc[r]);
             }
