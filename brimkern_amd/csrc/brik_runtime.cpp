@@ -351,6 +351,14 @@ int gemm_tile(brik_ctx* c, long M, long N, long K, int E)
     double blocks = 0;
     int best = pick(true, blocks);
     if (blocks < kCUs) best = pick(false, blocks);
+    // One round of 128 x 256 tiles that fills most of the CUs beats more blocks of fewer rows: a
+    // 128-row block runs its tile at about 1.37x the per-CU rate of a 96-row one (x fragments and
+    // dequantized codes each feed more MFMAs). Measured at K = 2560, N = 9728 (graph-free calls, 8 weight
+    // copies): M = 512 42.7-43.0 us against 44.1-44.3 (96 x 256); M = 640 47.3 against 55-59 (model's
+    // pick) and 72.5 (96 x 256); M = 768 52.5 against 52.5-54 and 74; at 76-114 blocks (M = 256, 384)
+    // the smaller tiles stay ahead (28-35 us against 37-40).
+    const double b128 = (double)gemm_tiles(M, 128) * gemm_tiles(N, 256);
+    if (b128 >= 0.55 * kCUs && b128 <= kCUs) return find(128, 1, 8);
     const GemmTile& g = kGemmTiles[best];
     return g.tn == 2 ? find(g.bm, 1, 8) : best;     // the 8-wave form of a 256-column tile
 }
