@@ -3,15 +3,19 @@
 The multiply loop issues its LDS reads as inline asm (gemm.hip: ds_read_b128 / ds_read_u16, then
 lds_wait and tie), so the compiler does not know that their destination registers are written
 asynchronously. Correctness then rests on register allocation: no instruction may read or write a
-destination register of such a read before an `s_waitcnt lgkmcnt(0)` has retired it.
+destination register of such a read before an `s_waitcnt lgkmcnt` has retired it.
 
 This script disassembles the built code object (llvm-objdump, our own build) and checks exactly that
 on every path through each checked kernel: it builds the kernel's control-flow graph from the branch
 instructions (targets from their 16-bit word offsets; a conditional branch also falls through, an
-unconditional one and s_endpgm do not) and propagates the set of registers still pending from an
-asm LDS read forward to a fixed point, the union over all predecessors, so a read issued at the bottom
-of a loop is still pending at the loop's head on the back edge. An instruction that touches a pending
-register is reported.
+unconditional one and s_endpgm do not) and propagates the registers still pending from an LDS read
+forward to a fixed point, so a read issued at the bottom of a loop is still pending at the loop's head
+on the back edge. The disassembly does not tell the asm reads from the compiler's own, so every
+ds_read_b128 / ds_read_u16 is tracked. A pending register carries its age, the number of LGKM-counted
+operations (LDS, scalar memory) issued after its read, and at a join the smaller age of the paths:
+LDS operations complete in issue order, so `s_waitcnt lgkmcnt(N)` retires the reads of age N or more,
+unless a scalar memory load may be in flight (those complete out of order, and then only lgkmcnt(0)
+retires anything). An instruction that touches a pending register is reported.
 
 Usage: python -m brimkern_amd.check_lds_reads <code object>   (exit status 1 on a violation)
 """
@@ -25,6 +29,7 @@ import sys
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 OBJDUMP = os.path.join(ROCM, "llvm", "bin", "llvm-objdump")
 ASM_READS = ("ds_read_b128", "ds_read_u16")
+MAX_AGE = 16          # lgkmcnt holds at most 15 on gfx9: an older read is retired by any lgkmcnt wait
 
 
 def _regs(op: str) -> set:
@@ -87,6 +92,39 @@ def _successors(code: list) -> list:
     return succ
 
 
+def _lgkm_wait(line: str):
+    """N of an s_waitcnt that names lgkmcnt(N), else None."""
+    m = re.search(r"lgkmcnt\((\d+)\)", line)
+    return int(m.group(1)) if m else None
+
+
+def _join(a, b):
+    """Pending states (frozenset of (register, age), scalar load in flight): union, smaller age."""
+    if a is None:
+        return b
+    ages = dict(a[0])
+    for r, g in b[0]:
+        ages[r] = min(g, ages.get(r, g))
+    return frozenset(ages.items()), a[1] or b[1]
+
+
+def _step(state, op: str, wait, writes):
+    regs, smem = state
+    if op == "s_waitcnt" and wait is not None:
+        if wait == 0:
+            return frozenset(), False
+        if smem:
+            return regs, smem
+        return frozenset((r, g) for r, g in regs if g < wait), smem
+    lgkm = op.startswith("ds_") or op.startswith(("s_load", "s_buffer_load", "s_memtime", "s_memrealtime"))
+    if not lgkm:
+        return state
+    aged = {r: min(g + 1, MAX_AGE) for r, g in regs}
+    for r in writes:
+        aged[r] = 0
+    return frozenset(aged.items()), smem or op.startswith(("s_load", "s_buffer_load", "s_memtime", "s_memrealtime"))
+
+
 def _check_kernel(fn: str, code: list) -> list:
     n = len(code)
     succ = _successors(code)
@@ -97,26 +135,27 @@ def _check_kernel(fn: str, code: list) -> list:
         used = set()
         for o in ops:
             used |= _regs(o)
-        clears = parts[0] == "s_waitcnt" and "lgkmcnt(0)" in line
+        wait = _lgkm_wait(line) if parts[0] == "s_waitcnt" else None
         writes = _regs(ops[0]) if parts[0] in ASM_READS and ops else set()
-        parsed.append((parts[0], used, clears, writes))
-    pend_in = [None] * n                       # pending registers at entry (None: not reached yet)
-    pend_in[0] = frozenset() if n else None
+        parsed.append((parts[0], used, wait, writes))
+    pend_in = [None] * n                       # pending state at entry (None: not reached yet)
+    if n:
+        pend_in[0] = (frozenset(), False)
     work = [0] if n else []
     while work:
         i = work.pop()
-        op, used, clears, writes = parsed[i]
-        out = frozenset() if clears else (pend_in[i] | writes)
+        op, used, wait, writes = parsed[i]
+        out = _step(pend_in[i], op, wait, writes)
         for j in succ[i]:
-            new = out if pend_in[j] is None else pend_in[j] | out
+            new = _join(pend_in[j], out)
             if new != pend_in[j]:
                 pend_in[j] = new
                 work.append(j)
     bad = []
-    for i, (op, used, clears, writes) in enumerate(parsed):
+    for i, (op, used, wait, writes) in enumerate(parsed):
         if pend_in[i] is None or op.startswith("ds_read"):
             continue
-        hit = used & pend_in[i]
+        hit = used & {r for r, _ in pend_in[i][0]}
         if hit:
             bad.append(f"{fn}: '{code[i][1]}' touches v{sorted(hit)} before the LDS read that writes it has "
                        f"been waited for")

@@ -250,7 +250,8 @@ struct Tile {
     static constexpr int C_BYTES = 32 * CLD * 4;          // one 32-row block
     static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 2 && TM % 2 == 0 ? 2 : 1;
     static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
-    static constexpr int SMEM = MAIN > RF * C_BYTES ? MAIN : RF * C_BYTES;
+    static constexpr int RS_OFF = MAIN;                   // the tile's row scales (BM floats)
+    static constexpr int SMEM = MAIN + 4 * BM_ > RF * C_BYTES ? MAIN + 4 * BM_ : RF * C_BYTES;
     // vector-memory loads per step: W codes, then the x chunks
     static constexpr int W_OPS = (FMT == FMT_Q4 ? 2 : FMT == FMT_F16 ? 8 : 4) * TN_;
     // loads a wave may still have in flight once the x of the next step has landed: the W and x of the
@@ -741,6 +742,9 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
     ld.h = lane >> 5; ld.G = G; ld.lds = smem;
     ld.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = ld.h, wave = ld.wave;
+    // the row scales the epilogue applies, into LDS now: their load's latency hides behind the
+    // prologue's instead of opening the epilogue (rows past the tile's end repeat a live row)
+    if (tid < T::BM) reinterpret_cast<float*>(smem + T::RS_OFF)[tid] = rscale[min(m0 + tid, m_end - 1)];
     // x staging: this lane's chunk of each direct-load instruction (row 4 (NW i + wave) + (lane >> 4),
     // stored chunk lane & 15, which holds logical chunk (lane & 15) ^ (row & 15))
 #pragma unroll
@@ -860,14 +864,40 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
     }
     // the clamped loads of the last steps may still be writing LDS, which the epilogue reuses
     wait_vm<0>();
+    if (!trans) {
+        // Row-major y: every lane stores its accumulators straight from registers (D layout of a
+        // 32x32 tile: lane holds column lane & 31, register r row 8 (r >> 2) + 4 h + (r & 3)), times
+        // the row scale read from LDS, 4 rows per 16-byte read. One store instruction covers two rows
+        // of 32 consecutive columns (two 128-byte runs). Staging the tile through LDS for 16-byte
+        // stores cost two barriers per round of row blocks and let no store start before the whole
+        // round was staged.
+        const float* const rs = reinterpret_cast<const float*>(smem + T::RS_OFF);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r0 = 32 * i + 8 * q + 4 * h;
+                const f32x4_t s4 = *reinterpret_cast<const f32x4_t*>(rs + r0);
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int n = n0 + wn + 32 * j + (lane & 31);
+                    if (n >= N) continue;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int m = m0 + r0 + e;
+                        if (m < m_end) y[(size_t)m * N + n] = acc[i][j][4 * q + e] * s4[e];
+                    }
+                }
+            }
+        return;
+    }
     lds_barrier();
 
-    // Epilogue, RF row blocks per round: the accumulators are staged in LDS (D layout of a 32x32
-    // tile: lane holds column lane & 31, register r row 8 (r >> 2) + 4 h + (r & 3)), then every thread
-    // scales 4 consecutive columns of one row by rscale and stores them with one 16-byte store
-    // (N % 4 == 0) or four 4-byte stores.
+    // Epilogue of the transposed store (y [N, M], the convolution's layout), RF row blocks per round:
+    // the accumulators are staged in LDS (the D layout above), then every thread scales 4 consecutive
+    // rows of one column by rscale, adds the column's bias and stores them with one 16-byte store
+    // (M % 4 == 0) or four 4-byte stores.
     float* const Cs = reinterpret_cast<float*>(smem);
-    constexpr int CH = BN / 4;                      // 4-column chunks per row
 #pragma unroll
     for (int i0 = 0; i0 < TM; i0 += T::RF) {
         if (i0) lds_barrier();                      // the previous round's reads are done
@@ -879,42 +909,25 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
                 for (int r = 0; r < 16; ++r)
                     Cs[(ii * 32 + 8 * (r >> 2) + 4 * h + (r & 3)) * T::CLD + wn + 32 * j + (lane & 31)] = acc[i0 + ii][j][r];
         lds_barrier();
-        if (trans) {
-            // y is [N, M]: y[n, m] = C[m, n] rscale[m] + tbias[n] (one rounding, the product being exact),
-            // 4 consecutive rows of one column per thread and store
-            constexpr int RB = T::RF * 32 / 4;
-            for (int c = tid; c < BN * RB; c += NT) {
-                const int col = c / RB, row = (c % RB) * 4;
-                const int m = m0 + i0 * 32 + row, n = n0 + col;
-                if (m >= m_end || n >= N) continue;
-                const float b = tbias ? tbias[n] : 0.f;
-                f32x4_t v;
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    v[k] = m + k < m_end ? Cs[(row + k) * T::CLD + col] * rscale[m + k] + b : 0.f;
-                float* dst = y + (size_t)n * M + m;
-                if ((M & 3) == 0 && m + 3 < m_end) {
-                    *(f32x4_t*)dst = v;
-                } else {
-#pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        if (m + k < m_end) dst[k] = v[k];
-                }
-            }
-            continue;
-        }
-        for (int c = tid; c < T::RF * 32 * CH; c += NT) {
-            const int row = c / CH, col = (c % CH) * 4;
+        // y[n, m] = C[m, n] rscale[m] + tbias[n] (one rounding, the product being exact), 4 consecutive
+        // rows of one column per thread and store
+        constexpr int RB = T::RF * 32 / 4;
+        for (int c = tid; c < BN * RB; c += NT) {
+            const int col = c / RB, row = (c % RB) * 4;
             const int m = m0 + i0 * 32 + row, n = n0 + col;
             if (m >= m_end || n >= N) continue;
-            const f32x4_t v = *(const f32x4_t*)(Cs + row * T::CLD + col) * rscale[m];
-            float* dst = y + (size_t)m * N + n;
-            if ((N & 3) == 0) {
+            const float b = tbias ? tbias[n] : 0.f;
+            f32x4_t v;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                v[k] = m + k < m_end ? Cs[(row + k) * T::CLD + col] * rscale[m + k] + b : 0.f;
+            float* dst = y + (size_t)n * M + m;
+            if ((M & 3) == 0 && m + 3 < m_end) {
                 *(f32x4_t*)dst = v;
             } else {
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
-                    if (n + k < N) dst[k] = v[k];
+                    if (m + k < m_end) dst[k] = v[k];
             }
         }
     }

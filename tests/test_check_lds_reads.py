@@ -87,3 +87,46 @@ def test_unconditional_branch_skips_fallthrough():
         "s_endpgm",
     ])
     assert check(text) == []
+
+
+def test_counted_wait_retires_older_reads_only():
+    """LDS reads complete in order: lgkmcnt(1) retires every read but the last one issued."""
+    text = HEAD.format("brik_gemm_q4_128x1w8") + body([
+        "ds_read_b128 v[66:69], v0",
+        "ds_read_b128 v[50:53], v1",
+        "s_waitcnt lgkmcnt(1)",
+        "v_mad_i64_i32 v[66:67], s[2:3], v0, s10, 0",   # the older read has landed
+        "v_mul_f32_e32 v1, v54, v50",                   # the newer one may not have
+        "s_waitcnt lgkmcnt(0)",
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and "v[50]" in bad[0] and "v_mul_f32" in bad[0]
+
+
+def test_counted_wait_with_a_scalar_load_in_flight_retires_nothing():
+    """A scalar load may complete before an earlier LDS read, so lgkmcnt(1) then guarantees nothing."""
+    text = HEAD.format("brik_gemm_q4_128x1w8") + body([
+        "ds_read_b128 v[66:69], v0",
+        "s_load_dwordx2 s[4:5], s[0:1], 0x0",
+        "s_waitcnt lgkmcnt(1)",
+        "v_mov_b32_e32 v66, 0",
+        "s_waitcnt lgkmcnt(0)",
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and "v[66]" in bad[0]
+
+
+def test_join_keeps_the_younger_age():
+    """Paths that meet with the same read at different ages: the wait after the join must cover the
+    path on which fewer operations followed it."""
+    text = HEAD.format("brik_gemm_q4_64x1") + at([
+        "ds_read_b128 v[6:9], v1",                # 0x1000
+        "s_cbranch_scc1 1",                       # 0x1004: -> 0x100c, the read still at age 0
+        "ds_read_b128 v[10:13], v1",              # 0x1008: the read at age 1 on this path
+        "s_waitcnt lgkmcnt(1)",                   # 0x100c
+        "v_mov_b32_e32 v7, 0",                    # not retired on the branch path
+        "s_waitcnt lgkmcnt(0)",
+        "s_endpgm",
+    ])
+    bad = check(text)
+    assert len(bad) == 1 and "v[7]" in bad[0]
