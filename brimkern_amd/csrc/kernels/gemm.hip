@@ -23,7 +23,8 @@
 //      FMA then give the dequantized pair (q s + m), rounded once to f16 whatever the scale; the
 //      code pairs (j, j + 4) this produces from 8 packed codes fix the
 //      [0 4 1 5 2 6 3 7] order. Scales and mins are staged in LDS a few steps at a time by coalesced
-//      loads. The epilogue multiplies by rscale[m] (exact) and stores y through LDS with 16-byte stores.
+//      loads. The epilogue multiplies by rscale[m] (exact, staged in LDS at the prologue) and stores y
+//      straight from the accumulator registers (the transposed convolution store goes through LDS).
 // f16 (not bf16) operands: 11-bit significands keep the normwise error near 3e-4, inside the 1e-3
 // bar; with bf16's 8 bits the same products measure 2e-3 to 3e-3 (tests/test_operand_precision.py).
 // The row scaling removes f16's range limit on activations.
@@ -246,7 +247,7 @@ struct Tile {
     static constexpr int SBUF = PLANES * SPLANE;          // one scale chunk
     static constexpr int NSD = PLANES * SPLANE / 1024 / NW_;   // scale-chunk load instructions per wave
     static constexpr int S_OFF = A_BYTES;                 // scale chunks follow the x buffers
-    static constexpr int CLD = BN + 4;                    // epilogue staging row stride (floats)
+    static constexpr int CLD = BN + 4;                    // transposed-store staging row stride (floats)
     static constexpr int C_BYTES = 32 * CLD * 4;          // one 32-row block
     static constexpr int RF = (A_BYTES / C_BYTES) >= TM ? TM : (A_BYTES / C_BYTES) >= 2 && TM % 2 == 0 ? 2 : 1;
     static constexpr int MAIN = A_BYTES + 2 * SBUF + 64;  // + a pad for reads of dead groups
