@@ -392,12 +392,14 @@ struct WorkD {
 #pragma unroll
             for (int n = 0; n < 6; ++n) L[n] = *(const u32x4_t*)(a + 16 * n);
             const i32x4_t xs = *(const i32x4_t*)(a + 96);                   // {sum x, e - 22, 8 sum X, 0}
-            // q4: the six plane reads issue together, so one LDS round trip per group is waited for
-            // (left to itself the compiler reads each plane just before its dot products, six waits per
-            // group): the fused decoder layer 30.2 -> 29.8 us per layer on one box, the 36-layer set
-            // unchanged. q3 keeps the compiler's order: the batched reads take its LM head from 84 to
-            // 152 VGPRs, 4 to 3 waves per SIMD, 38.2 -> 39.4 us.
-            if constexpr (FMT == FMT_Q4) __builtin_amdgcn_sched_barrier(0);
+            // The six plane reads issue together, so one LDS round trip per group is waited for (left to
+            // itself the compiler reads each plane just before its dot products, six waits per group),
+            // on the q4 variants of one group per lane step whose teams are 16 or 64 lanes: the fused
+            // decoder layer 30.3 -> 29.9 us per layer in alternating processes on one box. The others
+            // keep the compiler's order: there the batched reads cost registers and time (the 36-layer
+            // set 296.2 -> 297.4 us, the single q and gate launches +1 %, down on 32-lane teams 8.23 ->
+            // 8.38 us, the q3 LM head 84 -> 152 VGPRs, 4 -> 3 waves per SIMD, 38.2 -> 39.4 us).
+            if constexpr (FMT == FMT_Q4 && U == 1 && TEAM != 32) __builtin_amdgcn_sched_barrier(0);
             uint32_t c[R][4];
 #pragma unroll
             for (int r = 0; r < R; ++r) code_nibbles<FMT>(d[u][r], c[r]);
