@@ -1412,14 +1412,14 @@ static int conv2d(brik_ctx* c, Fmt f, const char* who, const float* inp, const v
     else if (c->opt_path == 2 && gemm_ok) use_gemm = true;
     int Ci = Cin, Hi = H, Wi = W, Co = Cout, khi = kh, kwi = kw, si = stride, pi = pad, OHi = OH, OWi = OW;
     if (!use_gemm) {
-        const long long n = M * Cout, blocks = (n + 255) / 256;
-        const unsigned gx = (unsigned)(blocks < 65536 ? blocks : 65536);
+        // 256 output pixels x 16 output channels per block (conv.hip, conv_direct)
+        const unsigned gx = (unsigned)((M + 255) / 256), gy = (unsigned)((Cout + 15) / 16);
         if (f == F_Q8) {
             void* args[] = {&inp, &p0, &sc, &bias, &out, &Ci, &Hi, &Wi, &Co, &khi, &kwi, &si, &pi, &OHi, &OWi};
-            return launch(c, K_CONV_Q8, gx, 1, 256, 0, args);
+            return launch(c, K_CONV_Q8, gx, gy, 256, 0, args);
         }
         void* args[] = {&inp, &p0, &sc, &mn, &bias, &out, &Ci, &Hi, &Wi, &Co, &khi, &kwi, &si, &pi, &OHi, &OWi};
-        return launch(c, K_CONV_Q4, gx, 1, 256, 0, args);
+        return launch(c, K_CONV_Q4, gx, gy, 256, 0, args);
     }
     const int rows = (int)M, Kint = (int)K;
     long Kp;

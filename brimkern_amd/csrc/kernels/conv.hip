@@ -12,8 +12,12 @@
 //     (one per output pixel, K taps) as scaled f16 rows, the way brik_xprep_f16 stages matmul
 //     activations, the MFMA GEMM of gemm.hip computes Y[pixels, Cout] = X . deq(W)^T, and
 //     brik_conv_out transposes Y to [Cout, pixels] adding the bias;
-//   * direct, for any shape: brik_conv2d_direct_<fmt>, one output per thread accumulating in f32 in
-//     the reference's (ci, ky, kx) order, each weight dequantized as dequantizeQ8 / Q4 do.
+//   * direct, for any shape: brik_conv2d_direct_<fmt>, every output accumulated in f32 in the
+//     reference's (ci, ky, kx) order over the in-image taps, each weight dequantized as dequantizeQ8 /
+//     Q4 do. A block owns 256 output pixels x 16 output channels: it dequantizes the weights of its
+//     channels into LDS a chunk of 256 (ci, ky, kx) taps at a time, and every thread runs the 16
+//     channels of its pixel, so each input value it loads feeds 16 FMAs and each weight is dequantized
+//     once per block instead of once per output.
 #include "common.h"
 
 namespace {
@@ -30,30 +34,148 @@ __device__ __forceinline__ float conv_weight(const void* __restrict__ p0, const 
     return fmaf((float)q, s, f16_bits_to_f32(mn[i >> 5]));
 }
 
+constexpr int DC_PIX = 256;     // output pixels per block (one per thread)
+constexpr int DC_CO = 16;       // output channels per block (accumulators per thread)
+constexpr int DC_TAPS = 256;    // (ci, ky, kx) taps of a weight chunk in LDS
+constexpr int DC_LD = 20;       // LDS row stride of a tap's 16 weights (floats; 16-byte aligned rows)
+constexpr int DC_U = 8;         // taps whose input loads a thread issues together
+
+// Block (bx, by): pixels p = 256 bx + t (p = oy OW + ox), channels 16 by + j. For each chunk of 256 taps
+// k = (ci kh + ky) kw + kx (the flat weight order within a channel), the block dequantizes the 16 x 256
+// weights into LDS, then every thread walks the chunk's taps in order and adds x * w to its 16 sums. The
+// walk's position (ci, ky, kx) is the same for every thread (scalar registers); a thread's input offset
+// is its origin plus ci H W + ky W + kx, and a tap is inside the image when bit ky of its row mask and
+// bit kx of its column mask are set (kernels of up to 32 x 32; larger ones test the coordinates). When
+// every weight of the chunk is finite an outside tap reads x = 0 (an offset past the end of a buffer
+// resource) and its FMA adds a signed zero, so the walk has no branch per tap; a chunk holding an
+// infinite or NaN weight skips the outside taps one by one as the reference does (0 * inf is NaN).
 template <int FMT>
 __device__ __forceinline__ void conv_direct(const float* __restrict__ inp, const void* __restrict__ p0,
                                             const uint16_t* __restrict__ sc, const uint16_t* __restrict__ mn,
                                             const float* __restrict__ bias, float* __restrict__ out, int Cin, int H,
                                             int W, int Cout, int kh, int kw, int stride, int pad, int OH, int OW)
 {
-    const long np = (long)OH * OW;
-    for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < (long)Cout * np; idx += (long)gridDim.x * 256) {
-        const int ox = (int)(idx % OW), oy = (int)((idx / OW) % OH), co = (int)(idx / np);
-        float acc = bias ? bias[co] : 0.f;
-        for (int ci = 0; ci < Cin; ++ci) {
-            const float* ib = inp + (size_t)ci * H * W;
-            const uint32_t wb = (uint32_t)(((size_t)co * Cin + ci) * kh * kw);
-            for (int ky = 0; ky < kh; ++ky) {
-                const int iy = oy * stride + ky - pad;
-                if (iy < 0 || iy >= H) continue;
-                for (int kx = 0; kx < kw; ++kx) {
-                    const int ix = ox * stride + kx - pad;
-                    if (ix < 0 || ix >= W) continue;
-                    acc = fmaf(ib[(size_t)iy * W + ix], conv_weight<FMT>(p0, sc, mn, wb + ky * kw + kx), acc);
+    __shared__ __attribute__((aligned(16))) float wl[DC_TAPS * DC_LD];
+    const int t = threadIdx.x;
+    const int M = OH * OW;
+    const int p = (int)blockIdx.x * DC_PIX + t;
+    const int co0 = (int)blockIdx.y * DC_CO;
+    const bool live = p < M;
+    const int oy = live ? p / OW : 0, ox = live ? p % OW : 0;
+    const int y0 = oy * stride - pad, x0 = ox * stride - pad;
+    const int taps = kh * kw, K = Cin * taps;
+    const bool masks = kh <= 32 && kw <= 32;
+    uint32_t rmask = 0u, cmask = 0u;
+    if (masks && live) {
+        for (int ky = 0; ky < kh; ++ky) rmask |= (y0 + ky >= 0 && y0 + ky < H) ? 1u << ky : 0u;
+        for (int kx = 0; kx < kw; ++kx) cmask |= (x0 + kx >= 0 && x0 + kx < W) ? 1u << kx : 0u;
+    }
+    const long origin = (long)y0 * W + x0;         // may be negative; only in-image taps are read
+    // the branch-free walk reads the input through a buffer resource (32-bit byte offsets)
+    const bool fast = masks && (long)Cin * H * W < (1L << 30);
+    const brsrc_t rin = make_rsrc(inp, fast ? (uint32_t)((long)Cin * H * W * 4) : 0u);
+    float acc[DC_CO];
+#pragma unroll
+    for (int j = 0; j < DC_CO; ++j) acc[j] = bias && co0 + j < Cout ? bias[co0 + j] : 0.f;
+    // the walk's position, the same for every thread
+    int ci = 0, ky = 0, kx = 0;
+    long uoff = 0;                                   // ci H W + ky W
+    for (int k0 = 0; k0 < K; k0 += DC_TAPS) {
+        const int nk = min(DC_TAPS, K - k0);
+        __syncthreads();                          // the previous chunk's reads are done
+        bool fin = true;
+        const int nkp = (nk + DC_U - 1) / DC_U * DC_U;    // rows past nk (the last chunk) hold zeros
+        for (int e = t; e < nkp * DC_CO; e += DC_PIX) {
+            const int kk = e % nkp, j = e / nkp, co = co0 + j;
+            const float w = co < Cout && kk < nk ? conv_weight<FMT>(p0, sc, mn, (uint32_t)((size_t)co * K + k0 + kk))
+                                                  : 0.f;
+            fin = fin && __builtin_isfinite(w);
+            wl[kk * DC_LD + j] = w;
+        }
+        // every weight of the chunk finite: an outside tap then adds x = 0 times a finite weight, a
+        // signed zero, which leaves every sum as skipping the tap does (up to the sign of a zero sum),
+        // so the taps need no branch; otherwise they are skipped one by one
+        const bool all_fin = __syncthreads_and(fin);
+        if (all_fin && fast) {
+            // the input loads of the next DC_U taps go out before the sums of these
+            auto fetch = [&](float (&xv)[DC_U], int kb) {
+#pragma unroll
+                for (int u = 0; u < DC_U; ++u) {
+                    const bool ok = (((rmask >> ky) & (cmask >> kx) & 1u) != 0u) & (kb + u < nk);
+                    // an offset past the resource's end reads 0: no branch and no select per tap
+                    const uint32_t off = ok ? (uint32_t)(origin + uoff + kx) * 4u : 0xFFFFFFF0u;
+                    xv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rin, off, 0u, 0));
+                    if (++kx == kw) {
+                        kx = 0;
+                        uoff += W;
+                        if (++ky == kh) {
+                            ky = 0;
+                            ++ci;
+                            uoff = (long)ci * H * W;
+                        }
+                    }
+                }
+            };
+            float xa[DC_U], xb[DC_U];
+            fetch(xa, 0);
+            for (int k = 0; k < nk; k += DC_U) {
+                if (k + DC_U < nk) fetch(xb, k + DC_U);
+#pragma unroll
+                for (int u = 0; u < DC_U; ++u) {
+                    const f32x4_t* wr = reinterpret_cast<const f32x4_t*>(wl + (k + u) * DC_LD);
+#pragma unroll
+                    for (int q = 0; q < DC_CO / 4; ++q) {
+                        const f32x4_t w = wr[q];
+                        acc[4 * q + 0] = fmaf(xa[u], w.x, acc[4 * q + 0]);
+                        acc[4 * q + 1] = fmaf(xa[u], w.y, acc[4 * q + 1]);
+                        acc[4 * q + 2] = fmaf(xa[u], w.z, acc[4 * q + 2]);
+                        acc[4 * q + 3] = fmaf(xa[u], w.w, acc[4 * q + 3]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < DC_U; ++u) xa[u] = xb[u];
+            }
+            continue;
+        }
+        for (int k = 0; k < nk; k += DC_U) {
+            float xv[DC_U];
+            bool in[DC_U];
+#pragma unroll
+            for (int u = 0; u < DC_U; ++u) {
+                bool ok;
+                if (masks) ok = ((rmask >> ky) & (cmask >> kx) & 1u) != 0u;
+                else ok = live && y0 + ky >= 0 && y0 + ky < H && x0 + kx >= 0 && x0 + kx < W;
+                in[u] = ok && k + u < nk;
+                xv[u] = inp[in[u] ? origin + uoff + kx : 0];
+                if (++kx == kw) {
+                    kx = 0;
+                    uoff += W;
+                    if (++ky == kh) {
+                        ky = 0;
+                        ++ci;
+                        uoff = (long)ci * H * W;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < DC_U; ++u) {
+                if (!in[u]) continue;
+                const f32x4_t* wr = reinterpret_cast<const f32x4_t*>(wl + (k + u) * DC_LD);
+#pragma unroll
+                for (int q = 0; q < DC_CO / 4; ++q) {
+                    const f32x4_t w = wr[q];
+                    acc[4 * q + 0] = fmaf(xv[u], w.x, acc[4 * q + 0]);
+                    acc[4 * q + 1] = fmaf(xv[u], w.y, acc[4 * q + 1]);
+                    acc[4 * q + 2] = fmaf(xv[u], w.z, acc[4 * q + 2]);
+                    acc[4 * q + 3] = fmaf(xv[u], w.w, acc[4 * q + 3]);
                 }
             }
         }
-        out[idx] = acc;
+    }
+    if (live) {
+#pragma unroll
+        for (int j = 0; j < DC_CO; ++j)
+            if (co0 + j < Cout) out[(size_t)(co0 + j) * M + p] = acc[j];
     }
 }
 

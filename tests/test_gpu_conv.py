@@ -134,3 +134,33 @@ def test_engine_conv2d_session_form(ctx):
         check(y, ref, den, Cin * 9, 1)
     with pytest.raises(BrikError):
         eng.conv2d(x, QWeight({"q3": True, "lo": 0, "hi": 0, "sc": 0, "mn": 0}), b, Cin, H, W, Cout, 3, 3, 1, 1)
+
+
+@pytest.mark.parametrize("fmt", ["q8", "q4"])
+def test_direct_skips_outside_taps_with_infinite_weights(gpu, fmt):
+    """A weight group with an infinite scale (channel 1 of a 1x1 conv padded by 1): the reference skips
+    the taps outside the image, so the outputs on the padding ring are exactly the bias while the
+    interior ones are not finite. The direct kernel's branch-free walk (x = 0 at outside taps) would make
+    the ring NaN (0 * inf), so a chunk holding a non-finite weight must take the skipping walk."""
+    shape = (32, 5, 5, 4, 1, 1, 1, 1)
+    Cin, H, W, Cout, kh, kw, st, pd = shape
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal(Cin * H * W).astype(np.float32)
+    w = (rng.standard_normal(Cout * Cin) * 0.2).astype(np.float32)
+    b = rng.standard_normal(Cout).astype(np.float32)
+    parts = list(getattr(O, f"quantize_{fmt}")(w))
+    sc = np.array(parts[1], np.uint16).copy()
+    sc[1] = 0x7C00                                   # channel 1's group (K = 32): scale +inf
+    parts[1] = sc
+    blob = getattr(O, f"pack_{fmt}")(*parts)
+    deq = getattr(O, f"dequant_{fmt}")(*parts)
+    ref, den = O.conv2d(x, deq, b, Cin, H, W, Cout, kh, kw, st, pd, return_absden=True)
+    y = run(gpu, fmt, x, blob, w.size, b, shape, 1)
+    ring = np.ones((H + 2, W + 2), bool)
+    ring[1:-1, 1:-1] = False
+    assert np.array_equal(y[1][ring], np.full(ring.sum(), b[1], np.float32))
+    assert not np.isfinite(y[1][~ring]).any()
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(y), fin)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    check(np.where(fin, y, 0), np.where(fin, ref, 0), np.where(fin, den, 0), Cin, 1)
