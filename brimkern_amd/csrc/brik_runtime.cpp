@@ -439,6 +439,14 @@ int gemm_stage_ws(brik_ctx* c, int rows, int K, long& Kp, uint16_t*& xh, float*&
     return BRIK_OK;
 }
 
+// Grid of brik_xprep_f16 (gemm.hip): one 256-thread block per row, or per four rows when a staged
+// row holds at most 2048 halves (one wave per row); at most 65536 blocks, which loop over the rest.
+unsigned xprep_grid(long rows, long Kp)
+{
+    const long blocks = Kp <= 2048 ? (rows + 3) / 4 : rows;
+    return (unsigned)(blocks < 65536 ? blocks : 65536);
+}
+
 // M >= 2 (dense): the cheapest of three paths by a cost model fitted per format on the Qwen3-4B shapes
 // (k/v, gate, down for q8 and q3; all six for q4) at M = 2, 4, 8, 15, each path timed as graph-replayed
 // back-to-back calls (us per call, launches included; W bytes = the packed planes):
@@ -639,8 +647,8 @@ int gemm(brik_ctx* c, Fmt f, const float* x, const void* p0, const void* p1, con
     HIP_TRY_RC(gemm_stage_ws(c, rows, K, Kp, xh, rscale, fixed));
     int Mi = rows, Ki = K, Kpi = (int)Kp;
     {
-        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};   // one block per row, at most 65536 blocks
-        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)(rows < 65536 ? rows : 65536), 1, 256, 0, args));
+        void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};
+        HIP_TRY_RC(launch(c, K_XPREP, xprep_grid(rows, Kp), 1, 256, 0, args));
     }
     return gemm_run(c, f, xh, rscale, p0, p1, sc, mn, y, rows, K, N, row_off, E, fixed, pair);
 }
@@ -1507,7 +1515,7 @@ int brik_matmul_t_f16w(brik_ctx* c, const float* x, const uint16_t* w, float* y,
     int Kpi = (int)Kp;
     {
         void* args[] = {&x, &xh, &rscale, &Mi, &Ki, &Kpi};
-        HIP_TRY_RC(launch(c, K_XPREP, (unsigned)(M < 65536 ? M : 65536), 1, 256, 0, args));
+        HIP_TRY_RC(launch(c, K_XPREP, xprep_grid(M, Kp), 1, 256, 0, args));
     }
     if (K % kGroup == 0) {
         // the tiled MFMA GEMM with f16 weights (TN = 1 tiles): a forced tile, or the one of fewest
