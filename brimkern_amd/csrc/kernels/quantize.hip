@@ -43,15 +43,11 @@ __device__ __forceinline__ uint32_t f16_encode(double v)
     return sign | ((uint32_t)exp << 10) | (r & 0x3ffu);
 }
 
-// f16BitsToF32 for the bits f16_encode produces (no subnormals): the exact value as a double.
-__device__ __forceinline__ double f16_decode(uint32_t h)
+// f16BitsToF32 for the bits f16_encode produces (no subnormals, no NaN; the infinity bits decode to
+// infinity): the exact value, through the hardware conversion (every f16 value is an f32 value).
+__device__ __forceinline__ float f16_decode(uint32_t h)
 {
-    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-    double v;
-    if (e == 0u) v = 0.0;
-    else if (e == 31u) v = m ? __builtin_nan("") : __builtin_inf();
-    else v = ldexp(1.0 + m / 1024.0, (int)e - 15);
-    return (h >> 15) ? -v : v;
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // JavaScript's `v || 1e-8` for a number: 0 and NaN are falsy.
@@ -89,24 +85,35 @@ __device__ __forceinline__ int cvt_i32(float v)
     return r;
 }
 
-// The same code in f32, without a division: d = x - m and t = d * r (r = 1 / s rounded to f32) are
-// each rounded once in f32, so t is within 3 * 2^-24 (|x| + |m|) / s of the exact (x - m) / s, and
-// JavaScript's f64 quotient is closer still (and rounds half up exactly as the exact quotient does).
-// With the margin e = (|x| + |m|) * r * 2^-20, five times that bound, plus the rounding of t + 1/2
-// (which the compiler may fuse with the product, removing one rounding): when t + 1/2 is farther than
-// e from every integer, floor(t + 1/2) is JavaScript's Math.round.
-// Otherwise `unsure` is set and the caller redoes the group with code_exact (rare for weights: exact
-// ties, values within about 2^-20 of one, or groups far from zero relative to their spread). NaN
-// gives 0 and infinities saturate before the clamp, as the reference's stores and clamp do.
-// `er` is r * 2^-20 and `am` is |m|, both per group.
-__device__ __forceinline__ int code_fast(float x, float m, float r, float er, float am, int lo, int hi, bool& unsure)
+// The same code in f32, without a division. Per group: r = 1 / s to within 2^-23 relative (v_rcp_f32),
+// c = 1/2 - m r (two f32 roundings). Per value, u = x r + c with one rounding: against the exact
+// U = (x - m) / s + 1/2, |u - U| <= 5 * 2^-24 (|x| + |m|) / s + 2^-24 (the r error on both products,
+// the roundings of m r, of c and of u, and |U| <= (|x| + |m|) / s + 1/2). JavaScript's f64 quotient,
+// rounded half up, is floor of a value within 2^-52 (|x| + |m|) / s + 2^-53 of U. The margin
+// e = (|x| + |m|) r 2^-20, about 16 * 2^-24 (|x| + |m|) / s, covers both whenever u lies near an
+// integer (then |x - m| / s >= 1/2, so the absolute terms are at most 4 * 2^-24 (|x| + |m|) / s);
+// far from one, when (|x| + |m|) / s < 1/11, u is within 0.1 of 1/2. So when u is farther than e
+// from every integer, floor(u) is JavaScript's Math.round. Otherwise `unsure` is set and the caller
+// redoes the group with code_exact (rare for weights: exact ties, values within about 2^-20 of one,
+// or groups far from zero relative to their spread).
+// NaN gives 0 and infinities saturate before the clamp, as the reference's stores and clamp do. For
+// lo = 0 the truncating conversion gives the clamped floor (they differ only below 0), so no floor
+// is taken. Per group: `c`, `er` = r 2^-20 and `h0` = 1/2 - |m| er; then 1/2 - e = h0 - |x| er.
+template <int LO, int HI>
+__device__ __forceinline__ int code_fast(float x, float r, float c, float er, float h0, bool& unsure)
 {
-    const float t = (x - m) * r;
-    const float e = (fabsf(x) + am) * er;
-    const float u = t + 0.5f, fu = floorf(u);
-    unsure |= fabsf((u - fu) - 0.5f) >= 0.5f - e;
-    const int q = cvt_i32(fu);
-    return q < lo ? lo : q > hi ? hi : q;
+    const float u = fmaf(x, r, c);
+    const float h = fmaf(-fabsf(x), er, h0);
+    int q;
+    if constexpr (LO == 0) {
+        unsure |= fabsf(__builtin_amdgcn_fractf(u) - 0.5f) >= h;
+        q = cvt_i32(u);
+    } else {
+        const float fu = floorf(u);
+        unsure |= fabsf((u - fu) - 0.5f) >= h;
+        q = cvt_i32(fu);
+    }
+    return q < LO ? LO : q > HI ? HI : q;
 }
 
 constexpr int ENC_GROUPS = 32;           // groups per wave iteration (two lanes each)
@@ -195,15 +202,31 @@ __device__ __forceinline__ void min_max(const float* half, bool second, float& m
 // result).
 template <int L>
 __device__ __forceinline__ void asym_header(const float* half, bool second, uint32_t& sh, uint32_t& mh, double& s,
-                                            double& m, double& r)
+                                            double& m)
 {
     float mn, mx;
     min_max(half, second, mn, mx);
     sh = f16_encode(or_tiny(((double)mx - (double)mn) / (double)L));
     mh = f16_encode((double)mn);
-    s = or_tiny(f16_decode(sh));
-    m = f16_decode(mh);
-    r = 1.0 / s;
+    s = or_tiny((double)f16_decode(sh));
+    m = (double)f16_decode(mh);
+}
+
+// The per-group constants of code_fast for scale s and min m. A non-finite c (m infinite) marks the
+// group unsure.
+struct FastConst {
+    float r, c, er, h0;
+};
+__device__ __forceinline__ FastConst fast_const(double s, double m, bool& unsure)
+{
+    FastConst k;
+    const float mf = (float)m;
+    k.r = __builtin_amdgcn_rcpf((float)s);
+    k.c = 0.5f - mf * k.r;
+    k.er = k.r * 0x1p-20f;
+    k.h0 = 0.5f - fabsf(mf) * k.er;
+    unsure = !(fabsf(k.c) <= 3.4028235e38f);
+    return k;
 }
 
 // The wave's staging and loop, shared by the encoders: `encode(g, half, second)` encodes the half of
@@ -254,10 +277,10 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q8(const f32x4_t* 
         amax = first_max(amax, second);
         const uint32_t sh = f16_encode(or_tiny((double)amax / 127.0));
         if (!second) scales[g] = (uint16_t)sh;
-        const double s = or_tiny(f16_decode(sh));
-        const float r = (float)(1.0 / s), er = r * 0x1p-20f;
+        const double s = or_tiny((double)f16_decode(sh));
+        bool unsure;
+        const FastConst fk = fast_const(s, 0.0, unsure);
         uint32_t* out = codes + g * 8 + (second ? 4 : 0);
-        bool unsure = false;
 #pragma unroll 1
         for (int k = 0; k < 4; ++k) {
             const f32x4_t w = row4(half, k);
@@ -265,7 +288,7 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q8(const f32x4_t* 
             uint32_t word = 0u;
 #pragma unroll
             for (int b = 0; b < 4; ++b)
-                word |= ((uint32_t)code_fast(e[b], 0.f, r, er, 0.f, -127, 127, unsure) & 0xffu) << (8 * b);
+                word |= ((uint32_t)code_fast<-127, 127>(e[b], fk.r, fk.c, fk.er, fk.h0, unsure) & 0xffu) << (8 * b);
             out[k] = word;
         }
         if (unsure || pair_u32(unsure)) {
@@ -288,22 +311,22 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q4(const f32x4_t* 
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
     encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
         uint32_t sh, mh;
-        double s, m, r;
-        asym_header<15>(half, second, sh, mh, s, m, r);
+        double s, m;
+        asym_header<15>(half, second, sh, mh, s, m);
         if (!second) {
             scales[g] = (uint16_t)sh;
             mins[g] = (uint16_t)mh;
         }
-        const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
+        bool unsure;
+        const FastConst fk = fast_const(s, m, unsure);
         uint32_t* out = nibbles + g * 4 + (second ? 2 : 0);
-        bool unsure = false;
 #pragma unroll 1
         for (int k = 0; k < 2; ++k) {         // element 8 k + b of the half is nibble b of word k (low nibble = even)
             const f32x4_t a = row4(half, 2 * k), c = row4(half, 2 * k + 1);
             const float e[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
             uint32_t word = 0u;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) word |= (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 15, unsure) << (4 * b);
+            for (int b = 0; b < 8; ++b) word |= (uint32_t)code_fast<0, 15>(e[b], fk.r, fk.c, fk.er, fk.h0, unsure) << (4 * b);
             out[k] = word;
         }
         if (unsure || pair_u32(unsure)) {
@@ -326,14 +349,14 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q3(const f32x4_t* 
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
     encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
         uint32_t sh, mh;
-        double s, m, r;
-        asym_header<7>(half, second, sh, mh, s, m, r);
+        double s, m;
+        asym_header<7>(half, second, sh, mh, s, m);
         if (!second) {
             scales[g] = (uint16_t)sh;
             mins[g] = (uint16_t)mh;
         }
-        const float rf = (float)r, er = rf * 0x1p-20f, mf = (float)m, am = fabsf(mf);
-        bool unsure = false;
+        bool unsure;
+        const FastConst fk = fast_const(s, m, unsure);
         // this half: lo word `second` (2 low bits each) and hi bits [16 second, 16 second + 16)
         uint32_t l = 0u, hb = 0u;
 #pragma unroll
@@ -342,7 +365,7 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q3(const f32x4_t* 
             const float e[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
-                const uint32_t q = (uint32_t)code_fast(e[b], mf, rf, er, am, 0, 7, unsure);
+                const uint32_t q = (uint32_t)code_fast<0, 7>(e[b], fk.r, fk.c, fk.er, fk.h0, unsure);
                 l |= (q & 3u) << (2 * (4 * c + b));
                 hb |= (q >> 2) << (4 * c + b);
             }
