@@ -27,20 +27,16 @@ namespace {
 // f32ToF16Bits: the value rounded to f32, then sign | exponent | 10-bit mantissa rounded half up on
 // the first dropped bit; exponents below the normal range give +-0, above it +-65504 (0x7bff), and a
 // mantissa carry out of exponent 30 gives the infinity bits, as the reference's conversion does.
+// Branch-free: the rounded mantissa is added to the shifted exponent, so a carry out of the mantissa
+// (r = 0x400) increments the exponent and clears the mantissa bits.
 __device__ __forceinline__ uint32_t f16_encode(double v)
 {
     const uint32_t x = __builtin_bit_cast(uint32_t, (float)v);
     const uint32_t sign = (x >> 16) & 0x8000u;
-    int exp = (int)((x >> 23) & 0xffu) - 127 + 15;
+    const int exp = (int)((x >> 23) & 0xffu) - 127 + 15;
     const uint32_t mant = x & 0x7fffffu;
-    if (exp <= 0) return sign;
-    if (exp >= 31) return sign | 0x7bffu;
-    uint32_t r = (mant >> 13) + ((mant >> 12) & 1u);
-    if (r == 0x400u) {
-        r = 0u;
-        exp += 1;
-    }
-    return sign | ((uint32_t)exp << 10) | (r & 0x3ffu);
+    const uint32_t body = ((uint32_t)exp << 10) + (mant >> 13) + ((mant >> 12) & 1u);
+    return sign | (exp <= 0 ? 0u : exp >= 31 ? 0x7bffu : body);
 }
 
 // f16BitsToF32 for the bits f16_encode produces (no subnormals, no NaN; the infinity bits decode to
@@ -178,7 +174,10 @@ __device__ __forceinline__ float first_max(float own, bool second)
 // min and max of the group as the reference's loop finds them: NaN never replaces a value, and of
 // equal values (+0 and -0) the first stays. Each lane scans its 16 elements in order; the pair then
 // keeps the first half's value unless the second half's is strictly beyond it, which is what the
-// scan over all 32 gives.
+// scan over all 32 gives. The first pass takes v_min / v_max of the quieted values (NaN never
+// replaces a value there either), which may pick either zero of a +0 / -0 tie: a group whose minimum
+// or maximum is zero is scanned again with the reference's compares (both lanes of the pair see the
+// same combined values, so they take that branch together).
 __device__ __forceinline__ void min_max(const float* half, bool second, float& mn, float& mx)
 {
     mn = __builtin_inff();
@@ -189,12 +188,29 @@ __device__ __forceinline__ void min_max(const float* half, bool second, float& m
         const float e[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (e[j] < mn) mn = e[j];
-            if (e[j] > mx) mx = e[j];
+            const float c = __builtin_canonicalizef(e[j]);
+            mn = fminf(mn, c);
+            mx = fmaxf(mx, c);
         }
     }
     mn = first_min(mn, second);
     mx = first_max(mx, second);
+    if (mn == 0.f || mx == 0.f) {
+        mn = __builtin_inff();
+        mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4_t w = row4(half, i);
+            const float e[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (e[j] < mn) mn = e[j];
+                if (e[j] > mx) mx = e[j];
+            }
+        }
+        mn = first_min(mn, second);
+        mx = first_max(mx, second);
+    }
 }
 
 // The asymmetric (q4 / q3) group header: f16 scale (max - min) / L || 1e-8 and min, their decoded
@@ -263,16 +279,15 @@ extern "C" __global__ __launch_bounds__(256) void brik_encode_q8(const f32x4_t* 
 {
     __shared__ __attribute__((aligned(16))) float lds[4 * ENC_GROUPS * ENC_ROW];
     encode_groups(src, groups, lds, [&](size_t g, const float* half, bool second) {
+        // v_max of the quieted magnitudes: NaN never replaces a value, and equal magnitudes have one
+        // bit pattern (|-0| = +0), so the order of the scan does not matter
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const f32x4_t w = row4(half, i);
             const float e[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float a = fabsf(e[j]);
-                if (a > amax) amax = a;
-            }
+            for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(__builtin_canonicalizef(e[j])));
         }
         amax = first_max(amax, second);
         const uint32_t sh = f16_encode(or_tiny((double)amax / 127.0));
