@@ -166,6 +166,28 @@ def test_gemm_parity(gpu, fmt, M, K, N):
     check(gpu.matmul(fmt, x, planes, M, K, N), r, den, REL_TOL)
 
 
+@pytest.mark.parametrize("K", [256, 1024, 1056, 2048, 2080, 2560])
+def test_gemm_staged_row_scales(gpu, K):
+    """Rows of very different magnitudes through the MFMA path's x staging: one wave per row for
+    staged rows of at most 2048 halves (two or four 8-element chunks per lane), one block per row
+    above. Each row's power-of-two scale brings its maximum into f16 range, so rows near 1e-30, 1e30
+    and past f16's maximum meet the componentwise bound, and a zero row gives exact zeros."""
+    M, N = 9, 160
+    t = synth.tensor("q4", 40 + K, N, K)
+    x = synth.normal(41 + K, M * K).reshape(M, K)
+    x[1] *= 1e-30
+    x[2] *= 1e30
+    x[3] = 0.0
+    x[4] *= 3e4
+    x[5, ::7] = 0.0
+    planes = gpu.planes("q4", t)
+    r, den = oracle_mm("q4", x.ravel(), t, M, K, N)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
+    y = gpu.matmul("q4", x.ravel(), planes, M, K, N)
+    check(y, r, den, REL_TOL)
+    assert not np.any(y[3])
+
+
 @pytest.mark.parametrize("M", [2, 3, 4, 8, 15, 16, 32])
 @pytest.mark.parametrize("K,N", [(2560, 4096), (2560, 9728), (9728, 2560), (2560, 1024)])
 def test_small_m_routing(gpu, M, K, N):
