@@ -71,8 +71,10 @@ __device__ __forceinline__ void conv_direct(const float* __restrict__ inp, const
         for (int kx = 0; kx < kw; ++kx) cmask |= (x0 + kx >= 0 && x0 + kx < W) ? 1u << kx : 0u;
     }
     const long origin = (long)y0 * W + x0;         // may be negative; only in-image taps are read
-    // the branch-free walk reads the input through a buffer resource (32-bit byte offsets)
-    const bool fast = masks && (long)Cin * H * W < (1L << 30);
+    // the branch-free walk reads the input through a buffer resource (32-bit byte offsets); with fewer
+    // than 2^29 elements its range is below 2^31 bytes, so the offset 2^32 - 16 given to the taps
+    // outside the image lies past it
+    const bool fast = masks && (long)Cin * H * W < (1L << 29);
     const brsrc_t rin = make_rsrc(inp, fast ? (uint32_t)((long)Cin * H * W * 4) : 0u);
     float acc[DC_CO];
 #pragma unroll
