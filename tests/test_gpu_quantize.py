@@ -37,7 +37,8 @@ def engine(ctx):
 
 
 def oracle_bytes(fmt, x):
-    return getattr(O, f"pack_{fmt}")(*getattr(O, f"quantize_{fmt}")(np.asarray(x, np.float32)))
+    with np.errstate(invalid="ignore"):          # signalling NaNs widened to f64 by the oracle
+        return getattr(O, f"pack_{fmt}")(*getattr(O, f"quantize_{fmt}")(np.asarray(x, np.float32)))
 
 
 def adversarial(seed, groups):
@@ -67,6 +68,14 @@ def adversarial(seed, groups):
     x[448:480] = 2.5
     x[452], x[470] = -3.0, -3.0
     x[n - 32:] = rng.standard_normal(32).astype(np.float32) * 1e4
+    if n >= 1024:
+        # signalling NaNs (the encoders take v_min / v_max of quieted values: an unquieted one would
+        # become the group's extreme): among values, as a group's first element, with either sign,
+        # and a group of nothing else but one value
+        xb = x.view(np.uint32)
+        xb[512], xb[517], xb[522] = 0x7F800001, 0xFFA00000, 0x7FBFFFFF
+        xb[544:576] = 0x7F800001
+        x[560] = 1.5
     return x
 
 
