@@ -684,6 +684,17 @@ __device__ __forceinline__ void wait_vm()
 // global->LDS load in flight (it counts them as LDS writes), including the ones issued for two steps
 // ahead; the LDS reads of this wave are waited for here, its direct loads by wait_vm before the call.
 // The memory clobber keeps LDS accesses on their side of the barrier.
+// The row scale of one tile row into LDS for the epilogue. An ordinary store here is an LDS write the
+// compiler orders after every direct global->LDS load before it, and it had waited for the scale's own
+// load before the first of them was issued: a memory round trip ahead of the prologue's weight and x
+// loads. As asm the store only waits for its value (the compiler's own wait on the loaded register);
+// the step barriers that follow (each waits for this wave's LDS operations) make it visible to the
+// epilogue's readers in the other waves.
+__device__ __forceinline__ void store_rscale(uint32_t addr, float v)
+{
+    asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v));
+}
+
 __device__ __forceinline__ void step_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -799,9 +810,10 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
     ld.h = lane >> 5; ld.G = G; ld.lds = smem;
     ld.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = ld.h, wave = ld.wave;
-    // the row scales the epilogue applies, into LDS now: their load's latency hides behind the
-    // prologue's instead of opening the epilogue (rows past the tile's end repeat a live row)
-    if (tid < T::BM) reinterpret_cast<float*>(smem + T::RS_OFF)[tid] = rscale[min(m0 + tid, m_end - 1)];
+    // the row scales the epilogue applies: loaded first, so their latency hides behind the prologue's
+    // instead of opening the epilogue (rows past the tile's end repeat a live row), and written into LDS
+    // after the prologue's loads are issued (store_rscale)
+    const float rs_row = tid < T::BM ? rscale[min(m0 + tid, m_end - 1)] : 0.f;
     // x staging: this lane's chunk of each direct-load instruction (row 4 (NW i + wave) + (lane >> 4),
     // stored chunk lane & 15, which holds logical chunk (lane & 15) ^ (row & 15))
 #pragma unroll
@@ -873,6 +885,7 @@ __device__ __forceinline__ void gemm_tile_run(unsigned char* smem, const uint16_
     // x step 0 (and scale chunk 0) landed: at most x step 1 and the PF - 1 later (W, x) pairs in flight
     wait_vm<XI + (T::PF - 1) * (T::W_OPS + XI)>();
     step_barrier();
+    if (tid < T::BM) store_rscale(lds_addr(smem + T::RS_OFF) + 4 * (uint32_t)tid, rs_row);
     if constexpr (FMT != FMT_F16) ld.read_scales(wr[0], 0, T::S_OFF, lane);
     const DeqConst dk = DeqConst::make();
     read_a<TM>(a[0], lds_addr(smem) + aoff[0]);
