@@ -680,21 +680,22 @@ __device__ __forceinline__ void wait_vm()
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Barrier between pipeline steps. A fence here would make the compiler wait for every direct
-// global->LDS load in flight (it counts them as LDS writes), including the ones issued for two steps
-// ahead; the LDS reads of this wave are waited for here, its direct loads by wait_vm before the call.
-// The memory clobber keeps LDS accesses on their side of the barrier.
-// The row scale of one tile row into LDS for the epilogue. An ordinary store here is an LDS write the
-// compiler orders after every direct global->LDS load before it, and it had waited for the scale's own
-// load before the first of them was issued: a memory round trip ahead of the prologue's weight and x
-// loads. As asm the store only waits for its value (the compiler's own wait on the loaded register);
-// the step barriers that follow (each waits for this wave's LDS operations) make it visible to the
+// The row scale of one tile row into LDS for the epilogue. Written as an ordinary store at the top of
+// the prologue, it is an LDS write the compiler keeps ahead of the direct global->LDS loads that follow
+// (it counts them as LDS writes too), so the code waited for the scale's own load before issuing the
+// first of them: a memory round trip ahead of the prologue's weight and x loads. As asm after the
+// prologue's loads it only waits for its value (the compiler's own wait on the loaded register); the
+// step barriers that follow (each waits for this wave's LDS operations) make it visible to the
 // epilogue's readers in the other waves.
 __device__ __forceinline__ void store_rscale(uint32_t addr, float v)
 {
     asm volatile("ds_write_b32 %0, %1" ::"v"(addr), "v"(v));
 }
 
+// Barrier between pipeline steps. A fence here would make the compiler wait for every direct
+// global->LDS load in flight (it counts them as LDS writes), including the ones issued for two steps
+// ahead; the LDS reads of this wave are waited for here, its direct loads by wait_vm before the call.
+// The memory clobber keeps LDS accesses on their side of the barrier.
 __device__ __forceinline__ void step_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
