@@ -188,6 +188,20 @@ def test_gemm_staged_row_scales(gpu, K):
     assert not np.any(y[3])
 
 
+@pytest.mark.parametrize("M,K", [(262150, 64), (65541, 2560)])
+def test_gemm_staging_grid_loops(gpu, M, K):
+    """More rows than the x staging grid's 65536 blocks cover: one wave per row (K <= 2048, four rows
+    per block: past 262144 rows) and one block per row (past 65536 rows), so its blocks loop over the
+    rest; the MFMA path's result against the oracle on every row."""
+    N = 8
+    t = synth.tensor("q4", 50 + K, N, K)
+    x = synth.normal(51 + K, M * K)
+    planes = gpu.planes("q4", t)
+    r, den = oracle_mm("q4", x, t, M, K, N)
+    gpu.ctx.set_option(BRIK_OPT_PATH, 2)
+    check(gpu.matmul("q4", x, planes, M, K, N), r, den, REL_TOL)
+
+
 @pytest.mark.parametrize("M", [2, 3, 4, 8, 15, 16, 32])
 @pytest.mark.parametrize("K,N", [(2560, 4096), (2560, 9728), (9728, 2560), (2560, 1024)])
 def test_small_m_routing(gpu, M, K, N):
